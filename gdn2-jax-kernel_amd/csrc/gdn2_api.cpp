@@ -1,0 +1,200 @@
+// C ABI of libgdn2_hip.so: validation, workspace sizing and dispatch to the
+// templated gfx950 launchers.  Declared in include/gdn2.h.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gdn2.h"
+#include "gdn2_layout.h"
+
+namespace gdn2 {
+
+typedef __bf16 bf16_t;
+
+template <typename T, typename TG, int BT, int D>
+hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
+                      const void* v, const void* w, const void* b, const void* g,
+                      const float* h0, float scale, float* out, float* h_final, char* ws,
+                      float* a_dbg);
+
+template <typename T, typename TG, int BT, int D>
+hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
+                      const void* v, const void* w, const void* b, const void* g,
+                      const float* h0, float scale, const float* dout, const float* dh_final,
+                      void* dq, void* dk, void* dv, void* dw, void* db, void* dg, float* dh0,
+                      const char* fws, char* ws);
+
+size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t elem);
+
+static size_t elem_size(int dtype) { return dtype == GDN2_F32 ? 4 : 2; }
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static int check_ptrs(std::initializer_list<const void*> ps) {
+  for (const void* p : ps) {
+    if (!p) return GDN2_ERR_NULL;
+    if (!aligned16(p)) return GDN2_ERR_ALIGN;
+  }
+  return GDN2_OK;
+}
+static int check_opt(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (p && !aligned16(p)) return GDN2_ERR_ALIGN;
+  return GDN2_OK;
+}
+
+static size_t nchunks(int B, int T, int H, int BT) { return (size_t)B * H * (size_t)(T / BT); }
+
+// Dispatch on (in dtype, g dtype, BT, D).
+template <template <typename, typename, int, int> class F, typename... A>
+static int dispatch(int in_dtype, int g_dtype, int BT, int D, A... args) {
+#define GDN2_CASE(T, TG, BT_, D_)                                                   \
+  if (BT == BT_ && D == D_) return F<T, TG, BT_, D_>::run(args...);
+  if (in_dtype == GDN2_F32 && g_dtype == GDN2_F32) {
+    GDN2_CASE(float, float, 64, 64)
+    GDN2_CASE(float, float, 64, 128)
+  } else if (in_dtype == GDN2_BF16 && g_dtype == GDN2_F32) {
+    GDN2_CASE(bf16_t, float, 64, 64)
+    GDN2_CASE(bf16_t, float, 64, 128)
+    GDN2_CASE(bf16_t, float, 128, 64)
+    GDN2_CASE(bf16_t, float, 128, 128)
+  } else if (in_dtype == GDN2_BF16 && g_dtype == GDN2_BF16) {
+    GDN2_CASE(bf16_t, bf16_t, 64, 64)
+    GDN2_CASE(bf16_t, bf16_t, 64, 128)
+    GDN2_CASE(bf16_t, bf16_t, 128, 64)
+    GDN2_CASE(bf16_t, bf16_t, 128, 128)
+  }
+#undef GDN2_CASE
+  return GDN2_ERR_CHUNK;
+}
+
+template <typename T, typename TG, int BT, int D>
+struct FwdRun {
+  static int run(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
+                 const void* v, const void* w, const void* b, const void* g, const float* h0,
+                 float scale, float* out, float* h_final, char* ws, float* a_dbg) {
+    hipError_t e = launch_fwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale, out,
+                                            h_final, ws, a_dbg);
+    return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+  }
+};
+
+template <typename T, typename TG, int BT, int D>
+struct BwdRun {
+  static int run(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
+                 const void* v, const void* w, const void* b, const void* g, const float* h0,
+                 float scale, const float* dout, const float* dh_final, void* dq, void* dk,
+                 void* dv, void* dw, void* db, void* dg, float* dh0, const char* fws,
+                 char* ws) {
+    hipError_t e = launch_bwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale, dout,
+                                            dh_final, dq, dk, dv, dw, db, dg, dh0, fws, ws);
+    return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+  }
+};
+
+}  // namespace gdn2
+
+using namespace gdn2;
+
+extern "C" {
+
+const char* gdn2_version(void) { return "0.1.0"; }
+
+const char* gdn2_strerror(int code) {
+  switch (code) {
+    case GDN2_OK: return "ok";
+    case GDN2_ERR_HEAD_DIM: return "head dim D must be 64 or 128";
+    case GDN2_ERR_SEQ_LEN: return "sequence length T must be divisible by the chunk size BT";
+    case GDN2_ERR_CHUNK: return "chunk size BT must be 64 or 128 (128 needs bfloat16 inputs)";
+    case GDN2_ERR_DTYPE: return "unsupported dtype (inputs: float32 or bfloat16; g: float32, or bfloat16 with bfloat16 inputs)";
+    case GDN2_ERR_NULL: return "required pointer is NULL";
+    case GDN2_ERR_ALIGN: return "pointer is not 16-byte aligned";
+    case GDN2_ERR_WORKSPACE: return "workspace too small";
+    case GDN2_ERR_SHAPE: return "invalid shape (B and H must be >= 1, T >= 0)";
+    case GDN2_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown error";
+  }
+}
+
+int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype) {
+  if (B < 1 || H < 1 || T < 0) return GDN2_ERR_SHAPE;
+  if (in_dtype != GDN2_F32 && in_dtype != GDN2_BF16) return GDN2_ERR_DTYPE;
+  if (g_dtype != GDN2_F32 && g_dtype != GDN2_BF16) return GDN2_ERR_DTYPE;
+  if (in_dtype == GDN2_F32 && g_dtype != GDN2_F32) return GDN2_ERR_DTYPE;
+  if (D != 64 && D != 128) return GDN2_ERR_HEAD_DIM;
+  if (BT != 64 && BT != 128) return GDN2_ERR_CHUNK;
+  if (BT == 128 && in_dtype == GDN2_F32) return GDN2_ERR_CHUNK;
+  if (T % BT != 0) return GDN2_ERR_SEQ_LEN;
+  if ((double)B * T * H * D > 9.0e15) return GDN2_ERR_SHAPE;
+  return GDN2_OK;
+}
+
+size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {
+  if (gdn2_validate(B, T, H, D, BT, in_dtype, in_dtype) != GDN2_OK &&
+      gdn2_validate(B, T, H, D, BT, in_dtype, GDN2_F32) != GDN2_OK)
+    return 0;
+  return fwd_layout(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype)).total;
+}
+
+static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
+                      int g_dtype, const void* q, const void* k, const void* v, const void* w,
+                      const void* b, const void* g, const float* h0, float scale, float* out,
+                      float* h_final, void* ws, size_t ws_bytes, float* a_dbg) {
+  int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
+  if (rc) return rc;
+  if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, out}))) return rc;
+  if ((rc = check_ptrs({h_final}))) return rc;
+  if ((rc = check_opt({h0, a_dbg}))) return rc;
+  const size_t need = fwd_layout(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype)).total;
+  if (need > 0 && (rc = check_ptrs({ws}))) return rc;
+  if (ws_bytes < need) return GDN2_ERR_WORKSPACE;
+  return dispatch<FwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, B, T, H, q, k, v, w,
+                          b, g, h0, scale, out, h_final, (char*)ws, a_dbg);
+}
+
+int gdn2_fwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
+             const void* q, const void* k, const void* v, const void* w, const void* b,
+             const void* g, const float* h0, float scale, float* out, float* h_final,
+             void* ws, size_t ws_bytes) {
+  return fwd_common(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale,
+                    out, h_final, ws, ws_bytes, nullptr);
+}
+
+int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
+                   int g_dtype, const void* q, const void* k, const void* v, const void* w,
+                   const void* b, const void* g, const float* h0, float scale, float* out,
+                   float* h_final, void* ws, size_t ws_bytes, float* a_out) {
+  if (!a_out && T > 0) return GDN2_ERR_NULL;
+  return fwd_common(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale,
+                    out, h_final, ws, ws_bytes, a_out);
+}
+
+size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {
+  if (gdn2_validate(B, T, H, D, BT, in_dtype, in_dtype) != GDN2_OK &&
+      gdn2_validate(B, T, H, D, BT, in_dtype, GDN2_F32) != GDN2_OK)
+    return 0;
+  return bwd_ws_bytes(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype));
+}
+
+int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
+             const void* q, const void* k, const void* v, const void* w, const void* b,
+             const void* g, const float* h0, float scale, const float* dout,
+             const float* dh_final, void* dq, void* dk, void* dv, void* dw, void* db, void* dg,
+             float* dh0, const void* fwd_ws, size_t fwd_ws_bytes, void* ws,
+             size_t ws_bytes) {
+  int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
+  if (rc) return rc;
+  if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, dout, dq, dk, dv, dw, db, dg}))) return rc;
+  if ((rc = check_ptrs({dh0}))) return rc;
+  if ((rc = check_opt({h0, dh_final}))) return rc;
+  const size_t nc = nchunks(B, T, H, BT);
+  const size_t fneed = fwd_layout(nc, BT, D, elem_size(in_dtype)).total;
+  const size_t bneed = bwd_ws_bytes(nc, BT, D, elem_size(in_dtype));
+  if (fneed > 0 && (rc = check_ptrs({fwd_ws}))) return rc;
+  if (bneed > 0 && (rc = check_ptrs({ws}))) return rc;
+  if (fwd_ws_bytes < fneed || ws_bytes < bneed) return GDN2_ERR_WORKSPACE;
+  return dispatch<BwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, B, T, H, q, k, v, w,
+                          b, g, h0, scale, dout, dh_final, dq, dk, dv, dw, db, dg, dh0,
+                          (const char*)fwd_ws, (char*)ws);
+}
+
+}  // extern "C"

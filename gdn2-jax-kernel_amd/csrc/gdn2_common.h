@@ -1,0 +1,160 @@
+// Device-side building blocks shared by the gfx950 GDN-2 kernels.
+//
+// MFMA tile conventions (64-lane wavefront, lane = 16*lg + li):
+//   * An operand fragment is the 16-byte slice a lane feeds one k-group of a
+//     16x16 MFMA: lane (li, lg) supplies row li of the left operand X and row
+//     li of the right operand Y, at the k positions owned by lane-group lg.
+//     The product of one k-group is D[m][n] += sum_k X[m][k] * Y[n][k].
+//   * float32 k-group = 16 k positions, 4 instructions v_mfma_f32_16x16x4_f32;
+//     lane-group lg owns k = 4*lg + e (e = 0..3) of each group.
+//     bfloat16 k-group = 32 k positions, 1 instruction v_mfma_f32_16x16x32_bf16;
+//     lane-group lg owns k = 8*lg + e (e = 0..7).  Which k a lane-group owns
+//     only has to agree between the two operands, so either layout is a
+//     16-byte contiguous slice of a row (byte offset 64*j + 16*lg in k-group j).
+//   * The 16x16 fp32 result sits in "C layout": lane holds D[4*lg + r][li],
+//     r = 0..3.  Feeding a C-layout tile back as an operand therefore uses the
+//     k positions {4*lg + r} (fp32: exactly the owned set) or, for bf16, the
+//     two tiles 2p, 2p+1 give k = {32p + 4lg + r} U {32p + 16 + 4lg + r}; the
+//     other operand is then read with the matching "chained" pattern.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gdn2 {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16_t;
+
+// Reference saturation constant, gdn2_fwd.py:33.
+constexpr float kClip = 1e4f;
+
+// nan -> 0, +-inf -> +-kClip, clip to [-kClip, kClip]: gdn2_fwd.py:42-44.
+__device__ __forceinline__ float sanitize(float x) {
+  x = (x != x) ? 0.f : x;
+  return fminf(fmaxf(x, -kClip), kClip);
+}
+
+template <typename T> struct Tr;
+template <> struct Tr<float> {
+  static constexpr int KC = 4;     // elements per lane per k-group
+  static constexpr int KS = 16;    // k positions per k-group
+  using Op = f32x4;
+};
+template <> struct Tr<bf16_t> {
+  static constexpr int KC = 8;
+  static constexpr int KS = 32;
+  using Op = bf16x8;
+};
+
+__device__ __forceinline__ void mma(f32x4& acc, const f32x4& x, const f32x4& y) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[0], y[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[1], y[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[2], y[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[3], y[3], acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x4& acc, const bf16x8& x, const bf16x8& y) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ float to_f(float x) { return x; }
+__device__ __forceinline__ float to_f(bf16_t x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f(float x);
+template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16_t from_f<bf16_t>(float x) { return (bf16_t)x; }
+
+// 16-byte operand fragment from KC floats.
+__device__ __forceinline__ f32x4 make_op(const float* x, f32x4*) {
+  return f32x4{x[0], x[1], x[2], x[3]};
+}
+__device__ __forceinline__ bf16x8 make_op(const float* x, bf16x8*) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16_t)x[e];
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ typename Tr<T>::Op op_from(const float* x) {
+  return make_op(x, (typename Tr<T>::Op*)nullptr);
+}
+template <typename T>
+__device__ __forceinline__ typename Tr<T>::Op op_zero() {
+  typename Tr<T>::Op r;
+#pragma unroll
+  for (int e = 0; e < Tr<T>::KC; ++e) r[e] = (T)0.f;
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ typename Tr<T>::Op op_load(const T* p) {
+  return *reinterpret_cast<const typename Tr<T>::Op*>(p);
+}
+
+// Load N consecutive elements of type X as floats (N*sizeof(X) a multiple of 16).
+template <int N>
+__device__ __forceinline__ void load_f(const float* p, float* out) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+    f32x4 t = *reinterpret_cast<const f32x4*>(p + i);
+    out[i] = t[0]; out[i + 1] = t[1]; out[i + 2] = t[2]; out[i + 3] = t[3];
+  }
+}
+template <int N>
+__device__ __forceinline__ void load_f(const bf16_t* p, float* out) {
+#pragma unroll
+  for (int i = 0; i < N; i += 8) {
+    bf16x8 t = *reinterpret_cast<const bf16x8*>(p + i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[i + e] = (float)t[e];
+  }
+}
+
+// Store 4 consecutive values of a C/R-layout row.
+__device__ __forceinline__ void store4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+__device__ __forceinline__ void store4(bf16_t* p, f32x4 v) {
+  bf16x4 r = {(bf16_t)v[0], (bf16_t)v[1], (bf16_t)v[2], (bf16_t)v[3]};
+  *reinterpret_cast<bf16x4*>(p) = r;
+}
+__device__ __forceinline__ f32x4 load4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ f32x4 load4f(const bf16_t* p) {
+  bf16x4 t = *reinterpret_cast<const bf16x4*>(p);
+  return f32x4{(float)t[0], (float)t[1], (float)t[2], (float)t[3]};
+}
+
+// Operand read from memory in the pattern that matches a C-layout chained
+// operand (see header comment).  `p` points at k = 32p (bf16) / 16a (fp32).
+__device__ __forceinline__ f32x4 op_chained(const float* p, int lg) {
+  return *reinterpret_cast<const f32x4*>(p + 4 * lg);
+}
+__device__ __forceinline__ bf16x8 op_chained(const bf16_t* p, int lg) {
+  bf16x4 lo = *reinterpret_cast<const bf16x4*>(p + 4 * lg);
+  bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16 + 4 * lg);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+// C-layout tiles as the other operand of a chained product.
+__device__ __forceinline__ f32x4 op_from_c(const f32x4& t0, const f32x4&, f32x4*) { return t0; }
+__device__ __forceinline__ bf16x8 op_from_c(const f32x4& t0, const f32x4& t1, bf16x8*) {
+  bf16x8 r;
+  r[0] = (bf16_t)t0[0]; r[1] = (bf16_t)t0[1]; r[2] = (bf16_t)t0[2]; r[3] = (bf16_t)t0[3];
+  r[4] = (bf16_t)t1[0]; r[5] = (bf16_t)t1[1]; r[6] = (bf16_t)t1[2]; r[7] = (bf16_t)t1[3];
+  return r;
+}
+
+// Copy `rows` rows of `cols` elements (row pitch `gpitch` in global, `lpitch`
+// in LDS) with 16-byte transactions spread over the workgroup.
+template <typename T, int NT>
+__device__ __forceinline__ void g2s(T* lds, int lpitch, const T* g, size_t gpitch, int rows,
+                                    int cols, int tid) {
+  constexpr int EPV = 16 / sizeof(T);
+  const int cpr = cols / EPV;
+  const int total = rows * cpr;
+  for (int i = tid; i < total; i += NT) {
+    const int r = i / cpr, cc = (i - r * cpr) * EPV;
+    *reinterpret_cast<uint4*>(lds + r * lpitch + cc) =
+        *reinterpret_cast<const uint4*>(g + r * gpitch + cc);
+  }
+}
+
+}  // namespace gdn2

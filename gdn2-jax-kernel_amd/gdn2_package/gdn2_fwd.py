@@ -1,0 +1,189 @@
+"""GDN-2 forward on MI355X: drop-in for the reference's gdn2_fwd.py API.
+
+    out, h_final = gdn2_pallas_forward(q, k, v, w, b, g, scale, h0=None)
+
+Same argument order and meaning as gdn2_fwd.py:400 (q,k,v,w,b,g of shape
+(B,T,H,D); ``scale`` a Python float; optional float32 ``h0`` (B,H,D,D)).
+``out`` (B,T,H,D) and ``h_final`` (B,H,D,D) are float32 (gdn2_fwd.py:163-165,342).
+Tensors are torch tensors on the ROCm device; the compute runs in the gfx950
+HIP library libgdn2_hip.so (kernels fwd_prep / fwd_state / fwd_out).  There
+is no CPU fallback: without the library every call raises.
+
+Chunk size.  ``BT`` below plays the role of gdn2_fwd.py:29 but is read at call
+time, so overriding it also reaches the backward (the reference binds it by
+value at import, gdn2_bwd.py:23).  ``None`` picks 128 for bfloat16 inputs and
+64 for float32; 64 and 128 are accepted (128 only with bfloat16 inputs).
+Results do not depend on the chunk size beyond rounding.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+# Reference constants, gdn2_fwd.py:29-33.  BC/N_SUB/MB describe the reference's
+# own sub-blocking and are kept for API compatibility; this implementation
+# always works on 16-token sub-blocks.
+BT = None
+BC = 64
+N_SUB = 2
+MB = 16
+CLIP = 1e4
+
+_SUPPORTED_IN = (torch.float32, torch.bfloat16)
+
+
+class GDN2Error(RuntimeError):
+    """A libgdn2_hip call failed."""
+
+
+class GDN2ShapeError(GDN2Error, AssertionError, ValueError):
+    """Invalid shape (the reference raises AssertionError at trace time,
+    gdn2_fwd.py:145-146)."""
+
+
+def _raise(code: int, what: str):
+    msg = f"{what}: {_lib.strerror(code)} (code {code})"
+    if code in (_lib.ERR_HEAD_DIM, _lib.ERR_SEQ_LEN, _lib.ERR_CHUNK, _lib.ERR_SHAPE):
+        raise GDN2ShapeError(msg)
+    raise GDN2Error(msg)
+
+
+def _dtype_code(dt):
+    return _lib.GDN2_F32 if dt == torch.float32 else _lib.GDN2_BF16
+
+
+def chunk_size_for(dtype, chunk_size=None) -> int:
+    bt = chunk_size if chunk_size is not None else BT
+    if bt is None:
+        return 128 if dtype == torch.bfloat16 else 64
+    return int(bt)
+
+
+class _Prepared:
+    """Inputs normalised for the C ABI (contiguous, supported dtypes)."""
+
+    def __init__(self, q, k, v, w, b, g, scale, h0, chunk_size):
+        xs = (q, k, v, w, b, g)
+        for x in xs:
+            if not isinstance(x, torch.Tensor):
+                raise TypeError("gdn2: q,k,v,w,b,g must be torch tensors on the ROCm device")
+        if q.dim() != 4:
+            raise GDN2ShapeError(f"gdn2: expected (B,T,H,D) inputs, got shape {tuple(q.shape)}")
+        for x in xs[1:]:
+            if x.shape != q.shape:
+                raise GDN2ShapeError(
+                    f"gdn2: all inputs must share shape {tuple(q.shape)}; got {tuple(x.shape)}")
+        dev = q.device
+        if dev.type != "cuda":
+            raise GDN2Error("gdn2: inputs must live on the ROCm device (torch 'cuda'); "
+                            "this library has no CPU path")
+        in_dt = q.dtype if q.dtype in _SUPPORTED_IN else torch.float32
+        if any(x.dtype != in_dt for x in (k, v, w, b)):
+            in_dt = torch.float32
+        g_dt = torch.float32
+        if in_dt == torch.bfloat16 and g.dtype == torch.bfloat16:
+            g_dt = torch.bfloat16
+        self.in_dtypes = tuple(x.dtype for x in xs)
+        self.q, self.k, self.v, self.w, self.b = (x.to(in_dt).contiguous() for x in xs[:5])
+        self.g = g.to(g_dt).contiguous()
+        self.in_dt, self.g_dt = in_dt, g_dt
+        self.B, self.T, self.H, self.D = q.shape
+        self.scale = float(scale)
+        self.BT = chunk_size_for(in_dt, chunk_size)
+        self.h0 = None if h0 is None else h0.to(device=dev, dtype=torch.float32).contiguous()
+        if self.h0 is not None and self.h0.shape != (self.B, self.H, self.D, self.D):
+            raise GDN2ShapeError(f"gdn2: h0 must be (B,H,D,D); got {tuple(self.h0.shape)}")
+        self.device = dev
+        self.args = (self.B, self.T, self.H, self.D, self.BT, _dtype_code(in_dt),
+                     _dtype_code(g_dt))
+        rc = _lib.lib().gdn2_validate(*self.args)
+        if rc:
+            _raise(rc, f"gdn2 (B,T,H,D)={tuple(q.shape)}, BT={self.BT}")
+
+    def stream(self):
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    @staticmethod
+    def ptr(x):
+        return None if x is None else x.data_ptr()
+
+
+def _run_forward(p: _Prepared, debug_a: bool = False):
+    L = _lib.lib()
+    nbytes = L.gdn2_fwd_workspace_bytes(*p.args[:6])
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=p.device)
+    out = torch.empty((p.B, p.T, p.H, p.D), dtype=torch.float32, device=p.device)
+    h_final = torch.empty((p.B, p.H, p.D, p.D), dtype=torch.float32, device=p.device)
+    common = (p.stream(), *p.args, p.ptr(p.q), p.ptr(p.k), p.ptr(p.v), p.ptr(p.w), p.ptr(p.b),
+              p.ptr(p.g), p.ptr(p.h0), p.scale, out.data_ptr(), h_final.data_ptr(),
+              ws.data_ptr(), nbytes)
+    a_out = None
+    if debug_a:
+        N = p.T // p.BT
+        a_out = torch.empty((p.B, p.H, N, p.BT, p.BT), dtype=torch.float32, device=p.device)
+        rc = L.gdn2_fwd_debug(*common, a_out.data_ptr())
+    else:
+        rc = L.gdn2_fwd(*common)
+    if rc:
+        _raise(rc, "gdn2_fwd")
+    return out, h_final, ws, a_out
+
+
+def gdn2_pallas_forward(q, k, v, w, b, g, scale, h0=None, debug_tag="", chunk_size=None):
+    """Forward A->B->C->D (gdn2_fwd.py:400-424) on the gfx950 library.
+
+    ``debug_tag`` is accepted for signature compatibility (the reference uses
+    it only in GDN2_FWD_DIAG prints, gdn2_fwd.py:47-76).
+    """
+    p = _Prepared(q, k, v, w, b, g, scale, h0, chunk_size)
+    out, h_final, _, _ = _run_forward(p)
+    return out, h_final
+
+
+def _residual_views(p: _Prepared, ws: torch.Tensor):
+    """Workspace tensors as (B,H,N,...) views in the reference's layouts."""
+    B, H, D, BT = p.B, p.H, p.D, p.BT
+    N = p.T // BT
+    es = 4 if p.in_dt == torch.float32 else 2
+    NC = B * H * N
+    sizes = [("W", NC * BT * D * es), ("UT", NC * D * BT * 4), ("KgT", NC * D * BT * es),
+             ("Qg", NC * BT * D * es), ("Aqk", NC * BT * BT * es), ("GL", NC * D * 4),
+             ("HT", NC * D * D * es), ("VnT", NC * D * BT * es)]
+    off, views = 0, {}
+    for name, nb in sizes:
+        dt = torch.float32 if name in ("UT", "GL") else p.in_dt
+        views[name] = ws[off:off + nb].view(dt)
+        off = (off + nb + 255) // 256 * 256
+    f = lambda x: x.float()
+    shp = (B, H, N)
+    idx = torch.arange(BT, device=p.device)
+    causal = (idx[:, None] >= idx[None, :])
+    return {
+        "w_pseudo": f(views["W"].view(*shp, BT, D)),
+        "u": f(views["UT"].view(*shp, D, BT).transpose(-1, -2)),
+        "kg": f(views["KgT"].view(*shp, D, BT).transpose(-1, -2)),
+        "qg": f(views["Qg"].view(*shp, BT, D)),
+        "Aqk": torch.where(causal, f(views["Aqk"].view(*shp, BT, BT)), 0.0),
+        "gc_last": f(views["GL"].view(*shp, D)),
+        "h_pre_all": f(views["HT"].view(*shp, D, D).transpose(-1, -2)),
+        "v_new_all": f(views["VnT"].view(*shp, D, BT).transpose(-1, -2)),
+    }
+
+
+def gdn2_pallas_forward_with_residuals(q, k, v, w, b, g, scale, h0=None, debug_tag="",
+                                       chunk_size=None):
+    """gdn2_fwd.py:427-457: forward plus the per-chunk intermediates.
+
+    Residual keys follow the reference (:452-456), all float32 in (B,H,N,...)
+    layout: Aqk, Akk, A, h_pre_all, v_new_all, w_pseudo, u, kg, qg, gc_last.
+    ``Akk`` is not materialised by the kernels; it is recovered here as
+    strict_tril(A^{-1}) for inspection.
+    """
+    p = _Prepared(q, k, v, w, b, g, scale, h0, chunk_size)
+    out, h_final, ws, a_out = _run_forward(p, debug_a=True)
+    res = _residual_views(p, ws)
+    res["A"] = a_out
+    eye = torch.eye(p.BT, device=p.device, dtype=torch.float64)
+    res["Akk"] = torch.tril(torch.linalg.inv(a_out.double()) - eye, -1).float()
+    return out, h_final, res

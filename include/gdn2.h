@@ -1,0 +1,101 @@
+/*
+ * gdn2.h -- C ABI of the MI355X (gfx950) GDN-2 chunked linear-attention library
+ * (libgdn2_hip.so).
+ *
+ * The library replaces the device side of the reference's Python API:
+ *   gdn2_pallas_forward(q,k,v,w,b,g,scale,h0=None)          gdn2_fwd.py:400-424
+ *   gdn2_pallas_forward_trainable(q,k,v,w,b,g,scale,h0=None) gdn2_pipeline.py:143-159
+ * whose forward is kernels A-D (gdn2_fwd.py:142-397) and whose custom_vjp
+ * backward is B1-B5 (gdn2_bwd.py:32-375, assembled at gdn2_pipeline.py:70-137).
+ *
+ * Conventions
+ *  - Tensors are dense row-major.  q,k,v,w,b,g,out and all gradients are
+ *    (B, T, H, D); states h0, h_final, dh_final, dh0 are (B, H, D, D) indexed
+ *    [b][h][dk][dv] (gdn2_fwd.py:342,355-357).  out, h_final, dh0 are float32
+ *    (gdn2_fwd.py:163-165,342); gradients come back in the input dtype
+ *    (gdn2_pipeline.py:129-135).
+ *  - Every pointer is caller-owned device memory, 16-byte aligned.  No entry
+ *    point allocates: the caller sizes the workspace with the *_workspace_bytes
+ *    functions.  Work is enqueued on `stream` (a hipStream_t; NULL = default
+ *    stream) and the call returns without synchronising.
+ *  - Return value 0 on success, a negative GDN2_ERR_* code otherwise;
+ *    gdn2_strerror() names it.  Invalid shapes are rejected before any launch.
+ *  - No mutable global state: calls on different streams may run concurrently
+ *    provided their workspaces do not overlap.
+ */
+#ifndef GDN2_H_
+#define GDN2_H_
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (in_dtype applies to q,k,v,w,b and the gradients). */
+#define GDN2_F32  0
+#define GDN2_BF16 1
+
+/* Error codes. */
+#define GDN2_OK                0
+#define GDN2_ERR_HEAD_DIM     -1  /* D not in {64,128}; ref asserts D==128, gdn2_fwd.py:145 */
+#define GDN2_ERR_SEQ_LEN      -2  /* T % BT != 0; ref asserts, gdn2_fwd.py:146 */
+#define GDN2_ERR_CHUNK        -3  /* BT not in {64,128}, or BT=128 with float32 inputs */
+#define GDN2_ERR_DTYPE        -4  /* unknown dtype code */
+#define GDN2_ERR_NULL         -5  /* required pointer is NULL */
+#define GDN2_ERR_ALIGN        -6  /* pointer not 16-byte aligned */
+#define GDN2_ERR_WORKSPACE    -7  /* workspace smaller than *_workspace_bytes() */
+#define GDN2_ERR_SHAPE        -8  /* B<1, H<1, T<0, or sizes overflow */
+#define GDN2_ERR_LAUNCH       -9  /* HIP launch failure */
+
+/* Library version string, e.g. "0.1.0". */
+const char* gdn2_version(void);
+
+/* Static description of an error code (never NULL). */
+const char* gdn2_strerror(int code);
+
+/* Host-only shape/dtype check (no GPU needed).  Mirrors the reference's
+ * trace-time assertions gdn2_fwd.py:145-146 and gdn2_bwd.py:348-349. */
+int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype);
+
+/* Bytes of workspace gdn2_fwd needs.  The workspace afterwards holds the
+ * per-chunk residuals (WY factors, chunk states, v_new) that gdn2_bwd reads. */
+size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype);
+
+/* Forward: replaces gdn2_pallas_forward (gdn2_fwd.py:400-424), kernels A-D.
+ * h0 may be NULL (zero initial state, gdn2_fwd.py:403-404).  out (B,T,H,D)
+ * and h_final (B,H,D,D) are float32. */
+int gdn2_fwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
+             const void* q, const void* k, const void* v, const void* w, const void* b,
+             const void* g, const float* h0, float scale, float* out, float* h_final,
+             void* ws, size_t ws_bytes);
+
+/* Test hook: as gdn2_fwd, and additionally writes A = (I + Akk)^{-1}
+ * (kernel B's output, gdn2_fwd.py:246-260) as float32 (B,H,N,BT,BT) to a_out. */
+int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
+                   int g_dtype, const void* q, const void* k, const void* v,
+                   const void* w, const void* b, const void* g, const float* h0,
+                   float scale, float* out, float* h_final, void* ws, size_t ws_bytes,
+                   float* a_out);
+
+/* Bytes of workspace gdn2_bwd needs in addition to the forward workspace. */
+size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype);
+
+/* Backward: replaces _gdn2_core_bwd (gdn2_pipeline.py:70-137), kernels B1-B5.
+ * fwd_ws must hold the residuals of a gdn2_fwd call on the same inputs, h0 and
+ * scale (the reference recomputes them, gdn2_pipeline.py:77-83; a caller that
+ * kept no residuals re-runs gdn2_fwd first).  dh_final and h0 may be NULL
+ * (zero).  dq,dk,dv,dw,db are in_dtype, dg is g_dtype, dh0 is float32
+ * (B,H,D,D); all gradients are sanitized as gdn2_pipeline.py:129-135. */
+int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
+             const void* q, const void* k, const void* v, const void* w, const void* b,
+             const void* g, const float* h0, float scale, const float* dout,
+             const float* dh_final, void* dq, void* dk, void* dv, void* dw, void* db,
+             void* dg, float* dh0, const void* fwd_ws, size_t fwd_ws_bytes, void* ws,
+             size_t ws_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN2_H_ */
