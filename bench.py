@@ -1,0 +1,216 @@
+#!/usr/bin/env python3
+"""GDN-2 chunked linear attention on one MI355X -- the headline benchmark.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload (the metric's shape): B=8, T=8192, H=6,
+D=128, bfloat16 q,k,v,w,b, float32 g, float32 state/accumulators, chunk 128.
+A step is one ``gdn2_pallas_forward`` call on resident synthetic inputs;
+``value`` is forward tokens/s (B*T per step).  The same line carries the
+training-path figure (configs[3]: float32, forward + backward) when the
+backward library entry point is available, per-kernel HIP-event times, the
+roofline of the dominant kernel and a CPU baseline (the numpy restatement of
+the reference's chunked algorithm, timed on a bounded sample of the same
+shape on this host).
+
+Inputs are synthetic with the BASELINE.json distributions (torch generator,
+seed 0): q,k ~ N(0,1) L2-normalised over D, v ~ N(0,1), w,b = sigmoid(N(0,1)),
+g = -softplus(N(0,1)).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "gdn2-jax-kernel_amd"))
+sys.path.insert(0, str(ROOT))
+
+B, T, H, D = 8, 8192, 6, 128
+CHUNK = 128
+HBM_PEAK = 8.0e12            # MI355X HBM3E, bytes/s
+MFMA_PEAK = {"bf16": 2.5e15, "f32": 157.3e12}
+
+
+def make_inputs(dtype, seed=0, g_scale=1.0):
+    import torch
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    shape = (B, T, H, D)
+    r = lambda: torch.randn(shape, generator=gen, device="cuda", dtype=torch.float32)
+    q, k, v, w, b, g = r(), r(), r(), r(), r(), r()
+    q = q / q.norm(dim=-1, keepdim=True)
+    k = k / k.norm(dim=-1, keepdim=True)
+    w, b = torch.sigmoid(w), torch.sigmoid(b)
+    g = -torch.nn.functional.softplus(g) * g_scale
+    return [x.to(dtype) for x in (q, k, v, w, b)] + [g]
+
+
+def kernel_table(dtype_bytes, chunk):
+    """Algorithmic HBM bytes and flops per token-head for each kernel.
+
+    bytes: what the kernel must read and write given the layout (inputs read
+    once, each workspace tensor written once and read once); flops: the
+    chunked algorithm's MACs x2 with triangular products at half.
+    """
+    s, C = dtype_bytes, chunk
+    return {
+        "fwd_prep": {"bytes": 5 * D * s + D * 4 + 3 * D * s + C * s + D * 4 + 4 * D / C,
+                     "flops": 4 * C * D + C * C / 3},
+        "fwd_state": {"bytes": 2 * D * s + D * 4 + 4 * D / C + D * D * s / C + D * s,
+                      "flops": 4 * D * D},
+        "fwd_out": {"bytes": 2 * D * s + C * s + D * D * s / C + D * 4,
+                    "flops": 2 * D * D + C * D},
+    }
+
+
+def time_forward(gp, xs, steps, warmup, chunk):
+    import torch
+    from gdn2_package import _lib
+    L = _lib.lib()
+    scale = D ** -0.5
+    for _ in range(warmup):
+        gp.gdn2_pallas_forward(*xs, scale, chunk_size=chunk)
+    stream = torch.cuda.current_stream()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4 * steps)]
+    for e in evs:
+        e.record(stream)                      # creates the underlying hipEvent_t
+    handles = [(ctypes_vp(evs[4 * i + j].cuda_event)) for i in range(steps) for j in range(4)]
+    import ctypes
+    arrs = [(ctypes.c_void_p * 4)(*handles[4 * i:4 * i + 4]) for i in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        L.gdn2_set_launch_events(arrs[i], 4)
+        gp.gdn2_pallas_forward(*xs, scale, chunk_size=chunk)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    names = ["fwd_prep", "fwd_state", "fwd_out"]
+    per = {n: sum(evs[4 * i + j].elapsed_time(evs[4 * i + j + 1]) for i in range(steps)) / steps
+           for j, n in enumerate(names)}
+    return (t1 - t0) / steps * 1e3, per
+
+
+def ctypes_vp(x):
+    import ctypes
+    return ctypes.c_void_p(int(x))
+
+
+def time_train(gp, xs, steps, warmup):
+    import torch
+    scale = D ** -0.5
+    xs = [x.detach().requires_grad_(True) for x in xs]
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    dout = torch.randn((B, T, H, D), generator=gen, device="cuda")
+
+    def step():
+        out, hf = gp.gdn2_pallas_forward_trainable(*xs, scale)
+        torch.autograd.backward([out], [dout])
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+def cpu_baseline(sample_T=4096, sample_H=H):
+    """The numpy restatement of the reference's chunked forward (kernels A-D
+    with the 3-D decay tensor, float32) on a bounded sample of the workload."""
+    import numpy as np
+    from oracle import gdn2_oracle as O
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max(i.get("num_threads", 1) for i in threadpool_info()) or 1
+    except Exception:
+        cores = os.cpu_count() or 1
+    xs = O.make_inputs(1, sample_T, sample_H, D, seed=0)
+    t0 = time.perf_counter()
+    O.chunked_fwd(*xs, D ** -0.5, BT=CHUNK, clip=True, dtype=np.float32)
+    dt = time.perf_counter() - t0
+    return {"value": sample_T / dt, "unit": "tokens/s", "cores": int(cores), "kind": "port",
+            "sample": f"forward B=1 T={sample_T} H={sample_H} D={D} BT={CHUNK} float32, numpy "
+                      f"restatement of gdn2_fwd.py kernels A-D (oracle.chunked_fwd), "
+                      f"{dt:.1f} s; tokens/s comparable to value (same H, D)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-train", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the op shards over (batch, head) "
+              "pairs with no communication); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import gdn2_package as gp
+
+    xs = make_inputs(torch.bfloat16)
+    torch.cuda.synchronize()
+    ms, per = time_forward(gp, xs, args.steps, args.warmup, CHUNK)
+    tokens = B * T
+    value = tokens / (ms * 1e-3)
+
+    tab = kernel_table(2, CHUNK)
+    dom = max(per, key=per.get)
+    th = B * T * H
+    kb = tab[dom]["bytes"] * th
+    kf = tab[dom]["flops"] * th
+    t_hbm, t_mfma = kb / HBM_PEAK, kf / MFMA_PEAK["bf16"]
+    ksec = per[dom] * 1e-3
+    if t_hbm >= t_mfma:
+        roof = {"bound": "hbm", "achieved": kb / ksec / 1e9, "peak": HBM_PEAK / 1e9,
+                "unit": "GB/s"}
+    else:
+        roof = {"bound": "mfma", "achieved": kf / ksec / 1e12, "peak": MFMA_PEAK["bf16"] / 1e12,
+                "unit": "TFLOP/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof["kernel"] = dom
+    roof["traffic"] = None
+    pmc = ROOT / "profiles" / f"traffic_{dom}_b8t8192h6d128_bf16.json"
+    if pmc.exists():
+        roof["traffic"] = json.loads(pmc.read_text()).get("bytes_per_launch")
+
+    del xs
+    torch.cuda.empty_cache()
+    train = None
+    if not args.no_train:
+        try:
+            xs32 = make_inputs(torch.float32)
+            tms = time_train(gp, xs32, max(1, args.steps // 4), max(1, args.warmup // 2))
+            train = {"config": "B8 T8192 H6 D128 float32, forward + backward (trainable)",
+                     "ms_per_step": tms, "tokens_per_s": tokens / (tms * 1e-3)}
+            del xs32
+        except Exception as e:  # backward entry point not available in this build
+            train = {"error": f"{type(e).__name__}: {e}"[:200]}
+
+    line = {
+        "metric": "fwd & fwd+bwd ms, tokens/s at B8 T8192 H6 D128; % MFMA/HBM roofline",
+        "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "gdn2_pallas_forward B8 T8192 H6 D128 bf16 inputs, fp32 g/state, "
+                               "chunk 128 (BASELINE configs[2])",
+                   "B": B, "T": T, "H": H, "D": D, "chunk": CHUNK},
+        "kernels_ms": per,
+        "roofline": roof,
+        "train": train,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

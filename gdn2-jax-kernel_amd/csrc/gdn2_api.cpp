@@ -4,11 +4,10 @@
 #include <stdint.h>
 
 #include "gdn2.h"
+#include "gdn2_common.h"
 #include "gdn2_layout.h"
 
 namespace gdn2 {
-
-typedef __bf16 bf16_t;
 
 template <typename T, typename TG, int BT, int D>
 hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
@@ -93,11 +92,27 @@ struct BwdRun {
 
 }  // namespace gdn2
 
+namespace gdn2 {
+thread_local LaunchEvents g_launch_events;
+}
+
 using namespace gdn2;
+
+namespace {
+// Clears the per-thread timing request when an entry point returns.
+struct EventScope {
+  ~EventScope() { g_launch_events = LaunchEvents{}; }
+};
+}  // namespace
 
 extern "C" {
 
 const char* gdn2_version(void) { return "0.1.0"; }
+
+int gdn2_set_launch_events(void* const* events, int n) {
+  g_launch_events = LaunchEvents{events, n > 0 ? n : 0, 0};
+  return 0;
+}
 
 const char* gdn2_strerror(int code) {
   switch (code) {
@@ -139,6 +154,7 @@ static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_d
                       int g_dtype, const void* q, const void* k, const void* v, const void* w,
                       const void* b, const void* g, const float* h0, float scale, float* out,
                       float* h_final, void* ws, size_t ws_bytes, float* a_dbg) {
+  EventScope scope;
   int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, out}))) return rc;
@@ -181,6 +197,7 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
              const float* dh_final, void* dq, void* dk, void* dv, void* dw, void* db, void* dg,
              float* dh0, const void* fwd_ws, size_t fwd_ws_bytes, void* ws,
              size_t ws_bytes) {
+  EventScope scope;
   int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, dout, dq, dk, dv, dw, db, dg}))) return rc;

@@ -157,4 +157,19 @@ __device__ __forceinline__ void g2s(T* lds, int lpitch, const T* g, size_t gpitc
   }
 }
 
+// Per-thread timing request set by gdn2_set_launch_events (host side).
+struct LaunchEvents {
+  void* const* ev = nullptr;
+  int n = 0;
+  int i = 0;
+};
+extern thread_local LaunchEvents g_launch_events;
+
+// Record the next requested event on `st` (no-op without a request).
+inline void launch_mark(hipStream_t st) {
+  LaunchEvents& e = g_launch_events;
+  if (e.ev && e.i < e.n) (void)hipEventRecord((hipEvent_t)e.ev[e.i], st);
+  ++e.i;
+}
+
 }  // namespace gdn2

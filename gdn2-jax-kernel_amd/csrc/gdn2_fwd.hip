@@ -65,6 +65,8 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
   __shared__ __align__(16) float sA[BT * A_LD];
   __shared__ __align__(16) float sTot[NB * D];  // per-block sums of g
   __shared__ __align__(16) float sETot[NB * D]; // exp of those
+  __shared__ __align__(16) float sPre[NB * D];  // sum of the blocks before m
+  __shared__ __align__(16) float sSuf[NB * D];  // sum of the blocks after m
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int cid = blockIdx.x;
@@ -102,6 +104,16 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
   }
   __syncthreads();
   for (int i = tid; i < NB * D; i += 256) sETot[i] = __expf(sTot[i]);
+  if (tid < D) {
+    float run = 0.f;
+#pragma unroll
+    for (int m = 0; m < NB; ++m) { sPre[m * D + tid] = run; run += sTot[m * D + tid]; }
+    run = 0.f;
+#pragma unroll
+    for (int m = NB - 1; m >= 0; --m) { sSuf[m * D + tid] = run; run += sTot[m * D + tid]; }
+    a.GL[(size_t)cid * D + tid] = sPre[(NB - 1) * D + tid] + sTot[(NB - 1) * D + tid];
+  }
+  __syncthreads();
 
   // ---- 2. per-token factors, qg/kg/kbd/khat, diagonal score blocks ----------
   float aq[NBW][DQ], ak[NBW][DQ];
@@ -122,9 +134,7 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
 #pragma unroll
     for (int x = 0; x < DQ; ++x) {
       const int ch = chan(x);
-      float pre = 0.f, suf = 0.f;
-      for (int m = 0; m < I; ++m) pre += sTot[m * D + ch];
-      for (int m = I + 1; m < NB; ++m) suf += sTot[m * D + ch];
+      const float pre = sPre[I * D + ch], suf = sSuf[I * D + ch];
       const float tot = sTot[I * D + ch];
       const float lc = loc[i][x];
       const float lcm = __shfl(lc, 7, 16);
@@ -289,11 +299,6 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
     float* dst = a.a_dbg + (size_t)cid * BT * BT;
     for (int i = tid; i < BT * BT; i += 256) dst[i] = sA[(i / BT) * A_LD + (i % BT)];
   }
-  if (tid < D) {
-    float s = 0.f;
-    for (int m = 0; m < NB; ++m) s += sTot[m * D + tid];
-    a.GL[(size_t)cid * D + tid] = s;
-  }
 
   // ---- 6. w_pseudo = A (b k e^gc), u = A (w v) ------------------------------
 #pragma unroll
@@ -347,14 +352,17 @@ struct StateArgs {
 };
 
 // One workgroup = one (b,h) and 64 value columns; wave wv owns 16 columns.
+// The next chunk's W, kg^T (whole workgroup, registers) and u^T, gc_last
+// (per wave) are fetched while the current chunk is computed.
 template <typename T, int BT, int D>
 __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
   using Op = typename Tr<T>::Op;
   constexpr int NB = BT / 16, NDT = D / 16;
-  constexpr int PADT = 16 / sizeof(T);
-  constexpr int W_LD = D + PADT, K_LD = BT + PADT;
+  constexpr int EPV = 16 / sizeof(T);
+  constexpr int W_LD = D + EPV, K_LD = BT + EPV;
   constexpr int NVS = D / 64;
   constexpr bool F32 = sizeof(T) == 4;
+  constexpr int PW = BT * D / EPV / 256;  // uint4 per thread for W (same for kg^T)
   __shared__ __align__(16) T sW[BT * W_LD];
   __shared__ __align__(16) T sK[D * K_LD];
 
@@ -370,20 +378,51 @@ __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
     for (int r = 0; r < 4; ++r)
       h[at][r] = a.h0 ? sanitize(a.h0[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col]) : 0.f;
 
+  uint4 pw[PW], pk[PW];
+  f32x4 un[NB], gn[NDT];
+#define GDN2_STATE_FETCH(c_)                                                          \
+  {                                                                                   \
+    const size_t fcid = (size_t)bh * a.N + (c_);                                      \
+    const uint4* ws = reinterpret_cast<const uint4*>(a.W + fcid * BT * D);            \
+    const uint4* ks = reinterpret_cast<const uint4*>(a.KgT + fcid * D * BT);          \
+    _Pragma("unroll") for (int i = 0; i < PW; ++i) {                                  \
+      pw[i] = ws[tid + 256 * i];                                                      \
+      pk[i] = ks[tid + 256 * i];                                                      \
+    }                                                                                 \
+    const float* up = a.UT + fcid * D * BT + (size_t)col * BT;                        \
+    _Pragma("unroll") for (int it = 0; it < NB; ++it) un[it] = load4f(up + it * 16 + 4 * lg); \
+    const float* glc = a.GL + fcid * D;                                               \
+    _Pragma("unroll") for (int at = 0; at < NDT; ++at) gn[at] = load4f(glc + at * 16 + 4 * lg); \
+  }
+#define GDN2_STATE_COMMIT()                                                           \
+  {                                                                                   \
+    _Pragma("unroll") for (int i = 0; i < PW; ++i) {                                  \
+      const int iw = tid + 256 * i;                                                   \
+      const int rw = iw / (D / EPV), cw = iw % (D / EPV);                             \
+      *reinterpret_cast<uint4*>(&sW[rw * W_LD + cw * EPV]) = pw[i];                   \
+      const int rk = iw / (BT / EPV), ck = iw % (BT / EPV);                           \
+      *reinterpret_cast<uint4*>(&sK[rk * K_LD + ck * EPV]) = pk[i];                   \
+    }                                                                                 \
+  }
+  if (a.N > 0) {
+    GDN2_STATE_FETCH(0)
+    GDN2_STATE_COMMIT()
+  }
+  __syncthreads();
+
   for (int c = 0; c < a.N; ++c) {
     const size_t cid = (size_t)bh * a.N + c;
-    g2s<T, 256>(sW, W_LD, a.W + cid * BT * D, D, BT, D, tid);
-    g2s<T, 256>(sK, K_LD, a.KgT + cid * D * BT, BT, D, BT, tid);
-    __syncthreads();
+    f32x4 vn[NB], gl[NDT];
+#pragma unroll
+    for (int it = 0; it < NB; ++it) vn[it] = un[it];
+#pragma unroll
+    for (int at = 0; at < NDT; ++at) gl[at] = gn[at];
+    if (c + 1 < a.N) GDN2_STATE_FETCH(c + 1)
 
     T* hT = a.HT + cid * D * D + (size_t)col * D;
 #pragma unroll
     for (int at = 0; at < NDT; ++at) store4(hT + at * 16 + 4 * lg, h[at]);
 
-    f32x4 vn[NB];
-    const float* up = a.UT + cid * D * BT + (size_t)col * BT;
-#pragma unroll
-    for (int it = 0; it < NB; ++it) vn[it] = load4f(up + it * 16 + 4 * lg);
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -403,12 +442,10 @@ __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
 #pragma unroll
     for (int it = 0; it < NB; ++it) store4(vT + it * 16 + 4 * lg, vn[it]);
 
-    const float* glc = a.GL + cid * D;
 #pragma unroll
     for (int at = 0; at < NDT; ++at) {
-      const f32x4 gl4 = load4f(glc + at * 16 + 4 * lg);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) h[at][r] *= __expf(gl4[r]);
+      for (int r = 0; r < 4; ++r) h[at][r] *= __expf(gl[at][r]);
       if constexpr (F32) {
 #pragma unroll
         for (int it = 0; it < NB; ++it)
@@ -422,6 +459,8 @@ __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) h[at][r] = sanitize(h[at][r]);
     }
+    __syncthreads();
+    if (c + 1 < a.N) GDN2_STATE_COMMIT()
     __syncthreads();
   }
 #pragma unroll
@@ -516,17 +555,21 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   float* GL = reinterpret_cast<float*>(ws + L.GL);
   T* HT = reinterpret_cast<T*>(ws + L.HT);
   T* VnT = reinterpret_cast<T*>(ws + L.VnT);
+  launch_mark(st);
   if (NC > 0) {
     PrepArgs<T, TG> pa{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
                        (const TG*)g, T_len, H, N, scale, W, UT, KgT, Qg, Aqk, GL, a_dbg};
     hipLaunchKernelGGL((fwd_prep<T, TG, BT, D>), dim3(NC), dim3(256), 0, st, pa);
   }
+  launch_mark(st);
   StateArgs<T> sa{W, UT, KgT, GL, h0, N, HT, VnT, h_final};
   hipLaunchKernelGGL((fwd_state<T, BT, D>), dim3((size_t)B * H * (D / 64)), dim3(256), 0, st, sa);
+  launch_mark(st);
   if (NC > 0) {
     OutArgs<T> oa{Qg, Aqk, HT, VnT, T_len, H, N, scale, out};
     hipLaunchKernelGGL((fwd_out<T, BT, D>), dim3(NC), dim3(256), 0, st, oa);
   }
+  launch_mark(st);
   return hipGetLastError();
 }
 

@@ -9,6 +9,10 @@ import ctypes
 import os
 from pathlib import Path
 
+# torch first: its bundled HIP runtime carries the soname libamdhip64.so.7, so
+# the library below binds to that same runtime instead of loading a second one.
+import torch  # noqa: F401
+
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("GDN2_LIB", _HERE / "libgdn2_hip.so"))
 
@@ -38,6 +42,7 @@ SIGNATURES = {
     "gdn2_fwd": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7 + [_c_float, _vp, _vp, _vp, _c_size]),
     "gdn2_fwd_debug": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7
                        + [_c_float, _vp, _vp, _vp, _c_size, _vp]),
+    "gdn2_set_launch_events": (_c_int, [_vp, _c_int]),
     "gdn2_bwd": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7
                  + [_c_float, _vp, _vp] + [_vp] * 7 + [_vp, _c_size, _vp, _c_size]),
 }

@@ -74,32 +74,32 @@ class _Prepared:
             if x.shape != q.shape:
                 raise GDN2ShapeError(
                     f"gdn2: all inputs must share shape {tuple(q.shape)}; got {tuple(x.shape)}")
-        dev = q.device
-        if dev.type != "cuda":
-            raise GDN2Error("gdn2: inputs must live on the ROCm device (torch 'cuda'); "
-                            "this library has no CPU path")
         in_dt = q.dtype if q.dtype in _SUPPORTED_IN else torch.float32
         if any(x.dtype != in_dt for x in (k, v, w, b)):
             in_dt = torch.float32
         g_dt = torch.float32
         if in_dt == torch.bfloat16 and g.dtype == torch.bfloat16:
             g_dt = torch.bfloat16
-        self.in_dtypes = tuple(x.dtype for x in xs)
-        self.q, self.k, self.v, self.w, self.b = (x.to(in_dt).contiguous() for x in xs[:5])
-        self.g = g.to(g_dt).contiguous()
-        self.in_dt, self.g_dt = in_dt, g_dt
         self.B, self.T, self.H, self.D = q.shape
-        self.scale = float(scale)
         self.BT = chunk_size_for(in_dt, chunk_size)
-        self.h0 = None if h0 is None else h0.to(device=dev, dtype=torch.float32).contiguous()
-        if self.h0 is not None and self.h0.shape != (self.B, self.H, self.D, self.D):
-            raise GDN2ShapeError(f"gdn2: h0 must be (B,H,D,D); got {tuple(self.h0.shape)}")
-        self.device = dev
         self.args = (self.B, self.T, self.H, self.D, self.BT, _dtype_code(in_dt),
                      _dtype_code(g_dt))
         rc = _lib.lib().gdn2_validate(*self.args)
         if rc:
             _raise(rc, f"gdn2 (B,T,H,D)={tuple(q.shape)}, BT={self.BT}")
+        if h0 is not None and tuple(h0.shape) != (self.B, self.H, self.D, self.D):
+            raise GDN2ShapeError(f"gdn2: h0 must be (B,H,D,D); got {tuple(h0.shape)}")
+        dev = q.device
+        if dev.type != "cuda" or any(x.device != dev for x in xs):
+            raise GDN2Error("gdn2: inputs must live on one ROCm device (torch 'cuda'); "
+                            "this library has no CPU path")
+        self.in_dtypes = tuple(x.dtype for x in xs)
+        self.q, self.k, self.v, self.w, self.b = (x.to(in_dt).contiguous() for x in xs[:5])
+        self.g = g.to(g_dt).contiguous()
+        self.in_dt, self.g_dt = in_dt, g_dt
+        self.scale = float(scale)
+        self.h0 = None if h0 is None else h0.to(device=dev, dtype=torch.float32).contiguous()
+        self.device = dev
 
     def stream(self):
         return torch.cuda.current_stream(self.device).cuda_stream

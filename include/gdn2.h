@@ -20,7 +20,8 @@
  *    stream) and the call returns without synchronising.
  *  - Return value 0 on success, a negative GDN2_ERR_* code otherwise;
  *    gdn2_strerror() names it.  Invalid shapes are rejected before any launch.
- *  - No mutable global state: calls on different streams may run concurrently
+ *  - No mutable global state beyond the per-thread timing request of
+ *    gdn2_set_launch_events: calls on different streams may run concurrently
  *    provided their workspaces do not overlap.
  */
 #ifndef GDN2_H_
@@ -77,6 +78,13 @@ int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtyp
                    const void* w, const void* b, const void* g, const float* h0,
                    float scale, float* out, float* h_final, void* ws, size_t ws_bytes,
                    float* a_out);
+
+/* Timing hook.  For the next gdn2_fwd / gdn2_fwd_debug / gdn2_bwd call made
+ * on the calling host thread, record events[0] (hipEvent_t) on the call's
+ * stream before its first kernel and events[i] after its i-th kernel, for
+ * i < n.  The request is consumed by that call (also when it fails).
+ * gdn2_fwd launches 3 kernels (fwd_prep, fwd_state, fwd_out).  Returns 0. */
+int gdn2_set_launch_events(void* const* events, int n);
 
 /* Bytes of workspace gdn2_bwd needs in addition to the forward workspace. */
 size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype);

@@ -1,0 +1,119 @@
+"""The C ABI of libgdn2_hip.so (include/gdn2.h) -- CPU only: the library loads,
+exports every declared entry point, and its host-side checks reject bad input
+before any launch (the calls below never reach the GPU)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from gdn2_package import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "gdn2.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(gdn2_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared()
+    assert "gdn2_fwd" in names and "gdn2_bwd" in names
+    L = _lib.lib()
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table out of sync with gdn2.h"
+
+
+def test_version_and_strerror():
+    import gdn2_package
+    L = _lib.lib()
+    assert L.gdn2_version().decode() == gdn2_package.__version__
+    for code in range(0, -10, -1):
+        assert L.gdn2_strerror(code)
+    assert L.gdn2_strerror(-1234) == b"unknown error"
+
+
+F32, BF16 = _lib.GDN2_F32, _lib.GDN2_BF16
+
+
+@pytest.mark.parametrize("args,code", [
+    ((1, 512, 2, 64, 64, F32, F32), _lib.OK),
+    ((8, 8192, 6, 128, 128, BF16, F32), _lib.OK),
+    ((8, 8192, 6, 128, 128, BF16, BF16), _lib.OK),
+    ((1, 0, 2, 64, 64, F32, F32), _lib.OK),                 # empty sequence
+    ((1, 512, 2, 96, 64, F32, F32), _lib.ERR_HEAD_DIM),     # ref: D==128 assert, gdn2_fwd.py:145
+    ((1, 500, 2, 64, 64, F32, F32), _lib.ERR_SEQ_LEN),      # ref: L%BT assert, gdn2_fwd.py:146
+    ((1, 512, 2, 64, 256, BF16, F32), _lib.ERR_CHUNK),
+    ((1, 512, 2, 64, 128, F32, F32), _lib.ERR_CHUNK),       # fp32 needs BT=64
+    ((1, 512, 2, 64, 64, 7, F32), _lib.ERR_DTYPE),
+    ((1, 512, 2, 64, 64, F32, BF16), _lib.ERR_DTYPE),
+    ((0, 512, 2, 64, 64, F32, F32), _lib.ERR_SHAPE),
+    ((1, 512, 0, 64, 64, F32, F32), _lib.ERR_SHAPE),
+    ((1, -64, 2, 64, 64, F32, F32), _lib.ERR_SHAPE),
+])
+def test_validate(args, code):
+    assert _lib.lib().gdn2_validate(*args) == code
+
+
+def test_workspace_bytes():
+    L = _lib.lib()
+    # layout: 8 per-chunk tensors, each region 256-byte aligned
+    B, T, H, D, BT = 1, 512, 2, 64, 64
+    nc = B * H * (T // BT)
+    al = lambda x: (x + 255) // 256 * 256
+    s = 4
+    exp = sum(al(x) for x in [nc * BT * D * s, nc * D * BT * 4, nc * D * BT * s,
+                              nc * BT * D * s, nc * BT * BT * s, nc * D * 4,
+                              nc * D * D * s, nc * D * BT * s])
+    assert L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, F32) == exp
+    assert L.gdn2_fwd_workspace_bytes(1, 1024, 2, 64, 64, F32) > exp
+    assert L.gdn2_fwd_workspace_bytes(1, 512, 2, 96, 64, F32) == 0
+    assert L.gdn2_fwd_workspace_bytes(1, 0, 2, 64, 64, F32) == 0
+
+
+def _fwd(L, dims, ptrs, h0=None, out=None, hf=None, ws=None, wsb=0):
+    return L.gdn2_fwd(None, *dims, *ptrs, h0, 0.125, out, hf, ws, wsb)
+
+
+def test_fwd_rejects_before_launch():
+    L = _lib.lib()
+    good = (1, 512, 2, 64, 64, F32, F32)
+    fake = [0x100000 * (i + 1) for i in range(6)]          # never dereferenced
+    ws_need = L.gdn2_fwd_workspace_bytes(*good[:6])
+    # shape errors come first
+    assert _fwd(L, (1, 512, 2, 96, 64, F32, F32), fake, None, 0x1000, 0x2000) == _lib.ERR_HEAD_DIM
+    assert _fwd(L, (1, 500, 2, 64, 64, F32, F32), fake, None, 0x1000, 0x2000) == _lib.ERR_SEQ_LEN
+    # then pointers
+    assert _fwd(L, good, [None] + fake[1:], None, 0x1000, 0x2000, 0x3000, ws_need) == _lib.ERR_NULL
+    assert _fwd(L, good, fake, None, 0x1000, None, 0x3000, ws_need) == _lib.ERR_NULL
+    assert _fwd(L, good, [0x100008] + fake[1:], None, 0x1000, 0x2000, 0x3000, ws_need) \
+        == _lib.ERR_ALIGN
+    assert _fwd(L, good, fake, 0x1004, 0x1000, 0x2000, 0x3000, ws_need) == _lib.ERR_ALIGN
+    # then workspace size
+    assert _fwd(L, good, fake, None, 0x1000, 0x2000, 0x3000, ws_need - 1) == _lib.ERR_WORKSPACE
+    assert _fwd(L, good, fake, None, 0x1000, 0x2000, None, ws_need) == _lib.ERR_NULL
+
+
+def test_bwd_rejects_before_launch():
+    L = _lib.lib()
+    dims = (1, 512, 2, 64, 64, F32, F32)
+    fake = [0x100000 * (i + 1) for i in range(6)]
+    grads = [0x900000 * (i + 1) for i in range(6)]
+    fws = L.gdn2_fwd_workspace_bytes(*dims[:6])
+    bws = L.gdn2_bwd_workspace_bytes(*dims[:6])
+    call = lambda d, dout, fwsb: L.gdn2_bwd(None, *d, *fake, None, 0.125, dout, None, *grads,
+                                            0x5000, 0x6000, fwsb, 0x7000, bws)
+    assert call((1, 512, 2, 96, 64, F32, F32), 0x4000, fws) == _lib.ERR_HEAD_DIM
+    assert call(dims, None, fws) == _lib.ERR_NULL
+    assert call(dims, 0x4000, fws - 1) == _lib.ERR_WORKSPACE
+
+
+def test_launch_events_hook_is_host_only():
+    L = _lib.lib()
+    arr = (ctypes.c_void_p * 4)()
+    assert L.gdn2_set_launch_events(arr, 4) == 0
+    # a rejected call consumes the request without touching the events
+    assert _fwd(L, (1, 512, 2, 96, 64, F32, F32), [0] * 6) == _lib.ERR_HEAD_DIM
+    assert L.gdn2_set_launch_events(None, 0) == 0
