@@ -13,7 +13,7 @@ template <typename T, typename TG, int BT, int D>
 hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, float* out, float* h_final, char* ws,
-                      float* a_dbg);
+                      float* a_dbg, int flags);
 
 template <typename T, typename TG, int BT, int D>
 hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
@@ -70,9 +70,10 @@ template <typename T, typename TG, int BT, int D>
 struct FwdRun {
   static int run(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                  const void* v, const void* w, const void* b, const void* g, const float* h0,
-                 float scale, float* out, float* h_final, char* ws, float* a_dbg) {
+                 float scale, float* out, float* h_final, char* ws, float* a_dbg,
+                 int flags) {
     hipError_t e = launch_fwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale, out,
-                                            h_final, ws, a_dbg);
+                                            h_final, ws, a_dbg, flags);
     return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
   }
 };
@@ -153,7 +154,8 @@ size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
 static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
                       int g_dtype, const void* q, const void* k, const void* v, const void* w,
                       const void* b, const void* g, const float* h0, float scale, float* out,
-                      float* h_final, void* ws, size_t ws_bytes, float* a_dbg) {
+                      float* h_final, void* ws, size_t ws_bytes, float* a_dbg,
+                      int flags) {
   EventScope scope;
   int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
@@ -164,15 +166,15 @@ static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_d
   if (need > 0 && (rc = check_ptrs({ws}))) return rc;
   if (ws_bytes < need) return GDN2_ERR_WORKSPACE;
   return dispatch<FwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, B, T, H, q, k, v, w,
-                          b, g, h0, scale, out, h_final, (char*)ws, a_dbg);
+                          b, g, h0, scale, out, h_final, (char*)ws, a_dbg, flags);
 }
 
 int gdn2_fwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
              const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, const float* h0, float scale, float* out, float* h_final,
-             void* ws, size_t ws_bytes) {
+             void* ws, size_t ws_bytes, int flags) {
   return fwd_common(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale,
-                    out, h_final, ws, ws_bytes, nullptr);
+                    out, h_final, ws, ws_bytes, nullptr, flags);
 }
 
 int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
@@ -181,7 +183,7 @@ int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtyp
                    float* h_final, void* ws, size_t ws_bytes, float* a_out) {
   if (!a_out && T > 0) return GDN2_ERR_NULL;
   return fwd_common(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale,
-                    out, h_final, ws, ws_bytes, a_out);
+                    out, h_final, ws, ws_bytes, a_out, 0);
 }
 
 size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {
@@ -203,6 +205,7 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, dout, dq, dk, dv, dw, db, dg}))) return rc;
   if ((rc = check_ptrs({dh0}))) return rc;
   if ((rc = check_opt({h0, dh_final}))) return rc;
+  if (BT != 64) return GDN2_ERR_CHUNK;  // the backward kernels tile 64-token chunks
   const size_t nc = nchunks(B, T, H, BT);
   const size_t fneed = fwd_layout(nc, BT, D, elem_size(in_dtype)).total;
   const size_t bneed = bwd_ws_bytes(nc, BT, D, elem_size(in_dtype));

@@ -103,11 +103,21 @@ __device__ __forceinline__ void load_f(const float* p, float* out) {
 }
 template <int N>
 __device__ __forceinline__ void load_f(const bf16_t* p, float* out) {
+  static_assert(N % 4 == 0, "load_f reads groups of 4 or 8 elements");
+  if constexpr (N % 8 == 0) {
 #pragma unroll
-  for (int i = 0; i < N; i += 8) {
-    bf16x8 t = *reinterpret_cast<const bf16x8*>(p + i);
+    for (int i = 0; i < N; i += 8) {
+      bf16x8 t = *reinterpret_cast<const bf16x8*>(p + i);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[i + e] = (float)t[e];
+      for (int e = 0; e < 8; ++e) out[i + e] = (float)t[e];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      bf16x4 t = *reinterpret_cast<const bf16x4*>(p + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[i + e] = (float)t[e];
+    }
   }
 }
 

@@ -35,7 +35,7 @@ struct PrepArgs {
   T* Qg;
   T* Aqk;
   float* GL;
-  float* a_dbg;  // optional (BT x BT fp32 per chunk)
+  float* a_dbg;  // optional A = (I + Akk)^{-1} output (BT x BT fp32 per chunk)
 };
 
 // Own row blocks of wave `wv`: {wv} and, for 8 blocks, {7 - wv} -- equal work
@@ -543,7 +543,7 @@ template <typename T, typename TG, int BT, int D>
 hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, float* out, float* h_final, char* ws,
-                      float* a_dbg) {
+                      float* a_dbg, int flags) {
   const int N = T_len / BT;
   const size_t NC = (size_t)B * H * N;
   const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T));
@@ -558,7 +558,9 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   launch_mark(st);
   if (NC > 0) {
     PrepArgs<T, TG> pa{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
-                       (const TG*)g, T_len, H, N, scale, W, UT, KgT, Qg, Aqk, GL, a_dbg};
+                       (const TG*)g, T_len, H, N, scale, W, UT, KgT, Qg, Aqk, GL,
+                       a_dbg ? a_dbg : ((flags & 1) ? reinterpret_cast<float*>(ws + L.A)
+                                                    : nullptr)};
     hipLaunchKernelGGL((fwd_prep<T, TG, BT, D>), dim3(NC), dim3(256), 0, st, pa);
   }
   launch_mark(st);
@@ -577,7 +579,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   template hipError_t launch_fwd<T, TG, BT, D>(hipStream_t, int, int, int, const void*,     \
                                                const void*, const void*, const void*,       \
                                                const void*, const void*, const float*,      \
-                                               float, float*, float*, char*, float*);
+                                               float, float*, float*, char*, float*, int);
 
 GDN2_INST_FWD(float, float, 64, 64)
 GDN2_INST_FWD(float, float, 64, 128)

@@ -10,7 +10,15 @@
 //   GL   [cid][D]       f32   gc_last                        (gdn2_fwd.py:284)
 //   HT   [cid][D][D]    T     h_c^T: state entering chunk c, [dv][dk] (gdn2_fwd.py:391)
 //   VnT  [cid][D][BT]   T     v_new^T                         (gdn2_fwd.py:350)
+//   A    [cid][BT][BT]  f32   (I + Akk)^{-1}, written only for the backward
+//                             (GDN2_FWD_SAVE_A)               (gdn2_fwd.py:246-260)
 // T is float for float32 inputs and bfloat16 for bfloat16 inputs.
+//
+// Backward workspace (all f32, chunk-major, one region per name):
+//   DAQK [BT][BT] dAqk (causal)      DVPT [D][BT] (Aqk^T do)^T    QDOT [D][D] (scale qg^T do)^T
+//   DHT  [D][D]  dh_{c+1}^T           DVNT [D][BT] dv_new^T        KBD, WVM [BT][D] b k e^gc, w v
+//   DQG, DW, DKG, DKBD, DWV [BT][D]   DA, TMP, DAKK [BT][BT]
+//   RQ, RBK, RK [BT][D] off-diagonal score-gradient sums, DQD, DKD, DBKD [BT][D] diagonal ones
 #pragma once
 
 #include <stddef.h>
@@ -18,7 +26,7 @@
 namespace gdn2 {
 
 struct FwdLayout {
-  size_t W, UT, KgT, Qg, Aqk, GL, HT, VnT, total;
+  size_t W, UT, KgT, Qg, Aqk, GL, HT, VnT, A, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -35,6 +43,37 @@ inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem) {
   L.GL = take(nchunks * D * 4);
   L.HT = take(nchunks * D * D * elem);
   L.VnT = take(nchunks * D * BT * elem);
+  L.A = take(nchunks * BT * BT * 4);
+  L.total = off;
+  return L;
+}
+
+}  // namespace gdn2
+
+namespace gdn2 {
+
+enum BwdBuf {
+  B_DAQK, B_DVPT, B_QDOT, B_DHT, B_DVNT, B_KBD, B_WVM, B_DQG, B_DW, B_DKG, B_DKBD, B_DWV,
+  B_DA, B_TMP, B_DAKK, B_RQ, B_RBK, B_RK, B_DQD, B_DKD, B_DBKD, B_COUNT
+};
+
+struct BwdLayout {
+  size_t off[B_COUNT];
+  size_t elems[B_COUNT];  // per chunk
+  size_t total;
+};
+
+inline BwdLayout bwd_layout(size_t nchunks, int BT, int D) {
+  BwdLayout L;
+  const size_t tt = (size_t)BT * BT, td = (size_t)BT * D, dd = (size_t)D * D;
+  const size_t per[B_COUNT] = {tt, td, dd, dd, td, td, td, td, td, td, td,
+                               td, tt, tt, tt, td, td, td, td, td, td};
+  size_t off = 0;
+  for (int i = 0; i < B_COUNT; ++i) {
+    L.off[i] = off;
+    L.elems[i] = per[i];
+    off = align256(off + nchunks * per[i] * 4);
+  }
   L.total = off;
   return L;
 }

@@ -18,6 +18,7 @@ LIB_PATH = Path(os.environ.get("GDN2_LIB", _HERE / "libgdn2_hip.so"))
 
 GDN2_F32 = 0
 GDN2_BF16 = 1
+FWD_SAVE_A = 1
 
 OK = 0
 ERR_HEAD_DIM = -1
@@ -39,7 +40,8 @@ SIGNATURES = {
     "gdn2_validate": (_c_int, [_c_int] * 7),
     "gdn2_fwd_workspace_bytes": (_c_size, [_c_int] * 6),
     "gdn2_bwd_workspace_bytes": (_c_size, [_c_int] * 6),
-    "gdn2_fwd": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7 + [_c_float, _vp, _vp, _vp, _c_size]),
+    "gdn2_fwd": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7
+                 + [_c_float, _vp, _vp, _vp, _c_size, _c_int]),
     "gdn2_fwd_debug": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7
                        + [_c_float, _vp, _vp, _vp, _c_size, _vp]),
     "gdn2_set_launch_events": (_c_int, [_vp, _c_int]),

@@ -109,7 +109,7 @@ class _Prepared:
         return None if x is None else x.data_ptr()
 
 
-def _run_forward(p: _Prepared, debug_a: bool = False):
+def _run_forward(p: _Prepared, debug_a: bool = False, flags: int = 0):
     L = _lib.lib()
     nbytes = L.gdn2_fwd_workspace_bytes(*p.args[:6])
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=p.device)
@@ -124,7 +124,7 @@ def _run_forward(p: _Prepared, debug_a: bool = False):
         a_out = torch.empty((p.B, p.H, N, p.BT, p.BT), dtype=torch.float32, device=p.device)
         rc = L.gdn2_fwd_debug(*common, a_out.data_ptr())
     else:
-        rc = L.gdn2_fwd(*common)
+        rc = L.gdn2_fwd(*common, flags)
     if rc:
         _raise(rc, "gdn2_fwd")
     return out, h_final, ws, a_out

@@ -19,6 +19,9 @@ import torch
 from . import _lib
 from .gdn2_fwd import _Prepared, _raise, _run_forward
 
+# Chunk size of the trainable path (the backward kernels are written for 64).
+TRAIN_CHUNK = 64
+
 
 def _run_backward(p: _Prepared, ws: torch.Tensor, dout, dh_final):
     L = _lib.lib()
@@ -47,8 +50,10 @@ class _GDN2Core(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, w, b, g, h0, scale, chunk_size, recompute):
-        p = _Prepared(q, k, v, w, b, g, scale, h0, chunk_size)
-        out, h_final, ws, _ = _run_forward(p)
+        # the backward kernels tile 64-token chunks
+        p = _Prepared(q, k, v, w, b, g, scale, h0, TRAIN_CHUNK if chunk_size is None
+                      else chunk_size)
+        out, h_final, ws, _ = _run_forward(p, flags=_lib.FWD_SAVE_A)
         ctx.prep = p
         ctx.ws = None if recompute else ws
         ctx.h0_given = h0 is not None
@@ -60,7 +65,7 @@ class _GDN2Core(torch.autograd.Function):
         p = ctx.prep
         ws = ctx.ws
         if ws is None:
-            _, _, ws, _ = _run_forward(p)
+            _, _, ws, _ = _run_forward(p, flags=_lib.FWD_SAVE_A)
         if dout is None:
             dout = torch.zeros((p.B, p.T, p.H, p.D), dtype=torch.float32, device=p.device)
         dq, dk, dv, dw, db, dg, dh0 = _run_backward(p, ws, dout, dh_final)

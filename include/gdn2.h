@@ -63,13 +63,17 @@ int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype)
  * per-chunk residuals (WY factors, chunk states, v_new) that gdn2_bwd reads. */
 size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype);
 
+/* gdn2_fwd flags. */
+#define GDN2_FWD_SAVE_A 1  /* also keep A = (I + Akk)^{-1} in ws, needed by gdn2_bwd */
+
 /* Forward: replaces gdn2_pallas_forward (gdn2_fwd.py:400-424), kernels A-D.
  * h0 may be NULL (zero initial state, gdn2_fwd.py:403-404).  out (B,T,H,D)
- * and h_final (B,H,D,D) are float32. */
+ * and h_final (B,H,D,D) are float32.  flags: 0 for inference, GDN2_FWD_SAVE_A
+ * when gdn2_bwd will consume ws (the trainable forward, gdn2_pipeline.py:64-67). */
 int gdn2_fwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
              const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, const float* h0, float scale, float* out, float* h_final,
-             void* ws, size_t ws_bytes);
+             void* ws, size_t ws_bytes, int flags);
 
 /* Test hook: as gdn2_fwd, and additionally writes A = (I + Akk)^{-1}
  * (kernel B's output, gdn2_fwd.py:246-260) as float32 (B,H,N,BT,BT) to a_out. */
@@ -90,11 +94,13 @@ int gdn2_set_launch_events(void* const* events, int n);
 size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype);
 
 /* Backward: replaces _gdn2_core_bwd (gdn2_pipeline.py:70-137), kernels B1-B5.
- * fwd_ws must hold the residuals of a gdn2_fwd call on the same inputs, h0 and
- * scale (the reference recomputes them, gdn2_pipeline.py:77-83; a caller that
- * kept no residuals re-runs gdn2_fwd first).  dh_final and h0 may be NULL
- * (zero).  dq,dk,dv,dw,db are in_dtype, dg is g_dtype, dh0 is float32
- * (B,H,D,D); all gradients are sanitized as gdn2_pipeline.py:129-135. */
+ * fwd_ws must hold the residuals of a gdn2_fwd call with GDN2_FWD_SAVE_A on
+ * the same inputs, h0 and scale (the reference recomputes them,
+ * gdn2_pipeline.py:77-83; a caller that kept no residuals re-runs gdn2_fwd
+ * first).  BT must be 64.  dh_final and h0 may be NULL (zero).  dq,dk,dv,dw,db
+ * are in_dtype, dg is g_dtype, dh0 is float32 (B,H,D,D); all gradients are
+ * sanitized as gdn2_pipeline.py:129-135.  Computes in float32 throughout.
+ * Launches 16 kernels (see gdn2_set_launch_events). */
 int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
              const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, const float* h0, float scale, const float* dout,

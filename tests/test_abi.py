@@ -59,22 +59,22 @@ def test_validate(args, code):
 
 def test_workspace_bytes():
     L = _lib.lib()
-    # layout: 8 per-chunk tensors, each region 256-byte aligned
+    # layout: 9 per-chunk tensors (the last is A, float32), each region 256-byte aligned
     B, T, H, D, BT = 1, 512, 2, 64, 64
     nc = B * H * (T // BT)
     al = lambda x: (x + 255) // 256 * 256
     s = 4
     exp = sum(al(x) for x in [nc * BT * D * s, nc * D * BT * 4, nc * D * BT * s,
                               nc * BT * D * s, nc * BT * BT * s, nc * D * 4,
-                              nc * D * D * s, nc * D * BT * s])
+                              nc * D * D * s, nc * D * BT * s, nc * BT * BT * 4])
     assert L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, F32) == exp
     assert L.gdn2_fwd_workspace_bytes(1, 1024, 2, 64, 64, F32) > exp
     assert L.gdn2_fwd_workspace_bytes(1, 512, 2, 96, 64, F32) == 0
     assert L.gdn2_fwd_workspace_bytes(1, 0, 2, 64, 64, F32) == 0
 
 
-def _fwd(L, dims, ptrs, h0=None, out=None, hf=None, ws=None, wsb=0):
-    return L.gdn2_fwd(None, *dims, *ptrs, h0, 0.125, out, hf, ws, wsb)
+def _fwd(L, dims, ptrs, h0=None, out=None, hf=None, ws=None, wsb=0, flags=0):
+    return L.gdn2_fwd(None, *dims, *ptrs, h0, 0.125, out, hf, ws, wsb, flags)
 
 
 def test_fwd_rejects_before_launch():

@@ -1,0 +1,143 @@
+"""Backward parity on the GPU: gradients of gdn2_pallas_forward_trainable
+(torch.autograd through the gfx950 library) against the oracle's restatement
+of B1-B5 (float64), which tests/test_oracle.py pins to torch.autograd of the
+token recurrence.  Tolerance |got - ref| <= tol + tol*|ref|, tol = 1e-4 for
+float32 inputs and 2e-2 for bfloat16 inputs.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gdn2_oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+NAMES = ["dq", "dk", "dv", "dw", "db", "dg", "dh0"]
+
+
+def close(got, ref, tol):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float((np.abs(got - ref) - (tol + tol * np.abs(ref))).max()) <= 0.0, \
+        float(np.abs(got - ref).max())
+
+
+def gp():
+    import gdn2_package
+    return gdn2_package
+
+
+def run_grads(xs, scale, do, dh=None, h0=None, dtype=torch.float32, dev="cuda:0", **kw):
+    xt = [torch.tensor(np.asarray(x), device=dev).to(dtype if i < 5 else torch.float32)
+          .requires_grad_(True) for i, x in enumerate(xs)]
+    h0t = None if h0 is None else torch.tensor(h0, device=dev, requires_grad=True)
+    out, hf = gp().gdn2_pallas_forward_trainable(*xt, scale, h0=h0t, **kw)
+    loss = (out * torch.tensor(do, device=dev)).sum()
+    if dh is not None:
+        loss = loss + (hf * torch.tensor(dh, device=dev)).sum()
+    loss.backward()
+    grads = [x.grad.float().cpu().numpy() for x in xt]
+    grads.append(None if h0t is None else h0t.grad.cpu().numpy())
+    return (out, hf), grads, xt
+
+
+def check(grads, ref, tol, names=NAMES):
+    for n, g, r in zip(names, grads, ref):
+        if g is None:
+            continue
+        ok, e = close(g, r, tol)
+        assert ok, (n, e, float(np.abs(r).max()))
+
+
+def test_bwd_golden_fixture(dev):
+    with np.load(GOLD / "bwd_small.npz", allow_pickle=False) as z:
+        xs = [z[n] for n in "qkvwbg"]
+        (out, hf), grads, _ = run_grads(xs, float(z["scale"]), z["do"], z["dh"], h0=z["h0"],
+                                        dev=dev)
+        assert close(out.detach().cpu().numpy(), z["out"], 1e-4)[0]
+        assert close(hf.detach().cpu().numpy(), z["h_final"], 1e-4)[0]
+        check(grads, [z[n] for n in NAMES], 1e-4)
+
+
+@pytest.mark.parametrize("B,T,H,D,h0,dh,gs", [
+    (1, 256, 2, 64, False, False, 1.0),
+    (2, 256, 3, 128, True, True, 1.0),
+    (1, 512, 2, 128, True, True, 0.05),     # slow decay: state terms of dgc_last matter
+    (1, 128, 1, 64, False, True, 4.0),      # strong decay
+])
+def test_bwd_matches_oracle_fp32(dev, B, T, H, D, h0, dh, gs):
+    xs = O.make_inputs(B, T, H, D, seed=T + D + H, g_scale=gs)
+    rng = np.random.default_rng(11)
+    h0n = (0.2 * rng.standard_normal((B, H, D, D))).astype(np.float32) if h0 else None
+    do = rng.standard_normal((B, T, H, D)).astype(np.float32)
+    dhn = rng.standard_normal((B, H, D, D)).astype(np.float32) if dh else None
+    _, grads, _ = run_grads(xs, D ** -0.5, do, dhn, h0=h0n, dev=dev)
+    ref = O.chunked_bwd(*xs, D ** -0.5, do, dhn, h0=h0n, BT=64, clip=False)
+    check(grads, ref, 1e-4)
+
+
+def test_bwd_bf16_inputs(dev):
+    xs = O.make_inputs(1, 256, 2, 128, seed=21)
+    rng = np.random.default_rng(3)
+    do = rng.standard_normal(xs[0].shape).astype(np.float32)
+    _, grads, xt = run_grads(xs, 128 ** -0.5, do, dtype=torch.bfloat16, dev=dev)
+    for x in xt[:5]:
+        assert x.grad.dtype == torch.bfloat16
+    xin = [x.detach().float().cpu().numpy() for x in xt]
+    ref = O.chunked_bwd(*xin, 128 ** -0.5, do, BT=64, clip=False)
+    check(grads, ref, 2e-2)
+
+
+def test_bwd_recompute_matches_saved_residuals(dev):
+    xs = O.make_inputs(1, 256, 2, 64, seed=5)
+    do = np.random.default_rng(2).standard_normal(xs[0].shape).astype(np.float32)
+    _, g1, _ = run_grads(xs, 0.125, do, dev=dev)
+    _, g2, _ = run_grads(xs, 0.125, do, dev=dev, recompute=True)
+    for a, b in zip(g1[:6], g2[:6]):
+        assert np.array_equal(a, b)
+
+
+def test_config4_training_path_fp32(dev):
+    """(8,8192,6,128) fp32 forward + custom backward with an
+    N(0,1) cotangent on out and zero cotangent on h_final.  Two sampled
+    (batch, head) pairs are checked against the oracle (pairs are independent)."""
+    B, T, H, D = 8, 8192, 6, 128
+    gen = torch.Generator(device=dev).manual_seed(0)
+    r = lambda: torch.randn((B, T, H, D), generator=gen, device=dev)
+    q, k, v, w, b, g = r(), r(), r(), r(), r(), r()
+    q, k = q / q.norm(dim=-1, keepdim=True), k / k.norm(dim=-1, keepdim=True)
+    w, b, g = torch.sigmoid(w), torch.sigmoid(b), -torch.nn.functional.softplus(g)
+    xt = [x.detach().requires_grad_(True) for x in (q, k, v, w, b, g)]
+    do = torch.randn((B, T, H, D), generator=gen, device=dev)
+    out, hf = gp().gdn2_pallas_forward_trainable(*xt, D ** -0.5)
+    torch.autograd.backward([out], [do])
+    for x in xt:
+        assert torch.isfinite(x.grad).all()
+    for bb, hh in [(0, 0), (5, 4)]:
+        sl = [x.detach()[bb:bb + 1, :, hh:hh + 1].cpu().numpy() for x in xt]
+        ref = O.chunked_bwd(*sl, D ** -0.5, do[bb:bb + 1, :, hh:hh + 1].cpu().numpy(), BT=64,
+                            clip=False)
+        got = [x.grad[bb:bb + 1, :, hh:hh + 1].cpu().numpy() for x in xt]
+        check(got, ref[:6], 1e-4, NAMES[:6])
+
+
+def test_reference_all_ones_forward_backward(dev):
+    """tests/test_pallas.py:27-39: all-ones (2,512,4,128), scale 0.1, through the
+    trainable path; shapes and finiteness (values are saturation artefacts)."""
+    shape = (2, 512, 4, 128)
+    xs = [torch.ones(shape, device=dev, requires_grad=True) for _ in range(6)]
+    out, hf = gp().gdn2_pallas_forward_trainable(*xs, 0.1)
+    assert out.shape == shape and hf.shape == (2, 4, 128, 128)
+    (out.sum() + hf.sum()).backward()
+    for x in xs:
+        assert x.grad.shape == shape and torch.isfinite(x.grad).all()
+        assert x.grad.abs().max().item() <= 1e4
+
+
+def test_grad_of_h0_only_when_given(dev):
+    xs = O.make_inputs(1, 128, 2, 64, seed=1)
+    do = np.ones(xs[0].shape, dtype=np.float32)
+    _, grads, _ = run_grads(xs, 0.125, do, dev=dev)
+    assert grads[6] is None
