@@ -19,6 +19,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -152,6 +154,15 @@ __device__ __forceinline__ bf16x8 op_from_c(const f32x4& t0, const f32x4& t1, bf
   return r;
 }
 
+// 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane l's bytes land at lds_base + 16*l, so
+// `lds_base` must be the same for every lane of the wave.  Completion is
+// tracked by vmcnt.
+__device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds_base, 16,
+                                   0, 0);
+}
+
 // Copy `rows` rows of `cols` elements (row pitch `gpitch` in global, `lpitch`
 // in LDS) with 16-byte transactions spread over the workgroup.
 template <typename T, int NT>
@@ -165,6 +176,21 @@ __device__ __forceinline__ void g2s(T* lds, int lpitch, const T* g, size_t gpitc
     *reinterpret_cast<uint4*>(lds + r * lpitch + cc) =
         *reinterpret_cast<const uint4*>(g + r * gpitch + cc);
   }
+}
+
+// Compute units of the current device (host side; queried once per device).
+inline int num_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 // Per-thread timing request set by gdn2_set_launch_events (host side).

@@ -28,6 +28,7 @@ struct PrepArgs {
   const T *q, *k, *v, *w, *b;
   const TG* g;
   int T_len, H, N;
+  long long NC;   // number of chunks, B*H*N
   float scale;
   T* W;
   float* UT;
@@ -38,13 +39,37 @@ struct PrepArgs {
   float* a_dbg;  // optional A = (I + Akk)^{-1} output (BT x BT fp32 per chunk)
 };
 
-// Own row blocks of wave `wv`: {wv} and, for 8 blocks, {7 - wv} -- equal work
-// for the triangular loops.
+// Own row blocks of wave `wv` in fwd_out: {wv} and, for 8 blocks, {7 - wv} --
+// equal work for the triangular products.
 template <int NB>
 __device__ __forceinline__ int own_block(int wv, int i) {
   return i == 0 ? wv : NB - 1 - wv;
 }
 
+// Row-wise (16-lane) DPP helpers: inclusive prefix sum over lanes li = 0..15
+// (row_shr 1,2,4,8 with out-of-row sources reading 0) and broadcast of lane n
+// of each row (row_newbcast).
+template <int CTRL>
+__device__ __forceinline__ float row_shr_add(float x) {
+  return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                 0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float row_scan16(float x) {
+  x = row_shr_add<0x111>(x);
+  x = row_shr_add<0x112>(x);
+  x = row_shr_add<0x114>(x);
+  return row_shr_add<0x118>(x);
+}
+template <int N>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+             0, __builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, false));
+}
+
+// One 256-thread workgroup per chunk; wave wv owns the 16-token row blocks
+// {wv, NB-1-wv} (equal work for the triangular loops).  Per element four
+// exponentials are evaluated (e^{loc}, e^{T_I - loc} and the two diagonal-block
+// factors); the block-level factors e^{P_{I-1}}, e^{S_{I+1}} come from LDS.
 template <typename T, typename TG, int BT, int D>
 __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
   using Op = typename Tr<T>::Op;
@@ -55,18 +80,17 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
   constexpr int NKT = BT / KS;            // k-groups over tokens
   constexpr int DQ = NKD * KC;            // channels owned per lane (= D/4)
   constexpr int PADT = 16 / sizeof(T);
-  constexpr int KH_LD = D + PADT;         // sKh  [t][d]
-  constexpr int TT_LD = BT + PADT;        // sKbdT, sWVT [d][t]
-  constexpr int A_LD = BT + 4;            // sA   [t][s] fp32
+  constexpr int KH_LD = D + PADT;         // khat [t][d]
+  constexpr int TT_LD = BT + PADT;        // [d][t] tiles
+  constexpr int A_LD = BT + 4;            // A [t][s] fp32
   constexpr int R0 = (BT * KH_LD > D * TT_LD) ? BT * KH_LD : D * TT_LD;
 
   __shared__ __align__(16) T sR0[R0];         // khat [t][d]; later (w v)^T [d][t]
-  __shared__ __align__(16) T sKbdT[D * TT_LD];
+  __shared__ __align__(16) T sKbdT[D * TT_LD];  // (b k e^gc)^T [d][t]
   __shared__ __align__(16) float sA[BT * A_LD];
-  __shared__ __align__(16) float sTot[NB * D];  // per-block sums of g
-  __shared__ __align__(16) float sETot[NB * D]; // exp of those
-  __shared__ __align__(16) float sPre[NB * D];  // sum of the blocks before m
-  __shared__ __align__(16) float sSuf[NB * D];  // sum of the blocks after m
+  __shared__ __align__(16) float sTot[NB * D];  // T_m: per-block sums of g
+  __shared__ __align__(16) float sETot[NB * D]; // e^{T_m}
+  __shared__ __align__(16) float sF[2][NB * D]; // e^{P_{I-1}}, e^{S_{I+1}} per (block, channel)
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int cid = blockIdx.x;
@@ -76,102 +100,98 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
   auto rowp = [&](int t) { return tok0 + (size_t)t * HD; };
   auto chan = [&](int x) { return (x / KC) * KS + lg * KC + (x % KC); };
 
+  // all loads needed before the inverse, issued together
+  float loc[NBW][DQ];
+  Op qo[NBW][NKD], ko[NBW][NKD], bo[NBW][NKD];
+#pragma unroll
+  for (int i = 0; i < NBW; ++i) {
+    const size_t off = rowp(own_block<NB>(wv, i) * 16 + li);
+#pragma unroll
+    for (int j = 0; j < NKD; ++j) {
+      load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
+      qo[i][j] = op_load<T>(a.q + off + j * KS + lg * KC);
+      ko[i][j] = op_load<T>(a.k + off + j * KS + lg * KC);
+      bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
+    }
+  }
   for (int i = tid; i < BT * A_LD / 4; i += 256)
     reinterpret_cast<f32x4*>(sA)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // ---- 1. in-block inclusive cumsum of g (lanes li = tokens) ----------------
-  float loc[NBW][DQ];
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
     const int I = own_block<NB>(wv, i);
-    const size_t off = rowp(I * 16 + li);
 #pragma unroll
-    for (int j = 0; j < NKD; ++j) load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
-#pragma unroll
-    for (int x = 0; x < DQ; ++x) {
-      float s = loc[i][x];
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) {
-        float y = __shfl_up(s, o, 16);
-        if (li >= o) s += y;
-      }
-      loc[i][x] = s;
-    }
+    for (int x = 0; x < DQ; ++x) loc[i][x] = row_scan16(loc[i][x]);
     if (li == 15) {
 #pragma unroll
       for (int x = 0; x < DQ; ++x) sTot[I * D + chan(x)] = loc[i][x];
     }
   }
   __syncthreads();
-  for (int i = tid; i < NB * D; i += 256) sETot[i] = __expf(sTot[i]);
+  for (int i = tid; i < NB * D; i += 256) {
+    sETot[i] = __expf(sTot[i]);
+  }
   if (tid < D) {
     float run = 0.f;
 #pragma unroll
-    for (int m = 0; m < NB; ++m) { sPre[m * D + tid] = run; run += sTot[m * D + tid]; }
+    for (int m = 0; m < NB; ++m) { sF[0][m * D + tid] = __expf(run); run += sTot[m * D + tid]; }
+    a.GL[(size_t)cid * D + tid] = run;
     run = 0.f;
 #pragma unroll
-    for (int m = NB - 1; m >= 0; --m) { sSuf[m * D + tid] = run; run += sTot[m * D + tid]; }
-    a.GL[(size_t)cid * D + tid] = sPre[(NB - 1) * D + tid] + sTot[(NB - 1) * D + tid];
+    for (int m = NB - 1; m >= 0; --m) { sF[1][m * D + tid] = __expf(run); run += sTot[m * D + tid]; }
   }
   __syncthreads();
 
-  // ---- 2. per-token factors, qg/kg/kbd/khat, diagonal score blocks ----------
+  // ---- 2. per-token factors: qg, kbd, kg, khat; diagonal score blocks -------
   float aq[NBW][DQ], ak[NBW][DQ];
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
     const int I = own_block<NB>(wv, i);
     const int t = I * 16 + li;
-    const size_t off = rowp(t);
-    float qv[DQ], kv[DQ], bv[DQ];
-#pragma unroll
-    for (int j = 0; j < NKD; ++j) {
-      load_f<KC>(a.q + off + j * KS + lg * KC, &qv[j * KC]);
-      load_f<KC>(a.k + off + j * KS + lg * KC, &kv[j * KC]);
-      load_f<KC>(a.b + off + j * KS + lg * KC, &bv[j * KC]);
-    }
-    float dq[DQ], dk[DQ], db[DQ], qg[DQ];
     T* kgT = a.KgT + (size_t)cid * D * BT;
-#pragma unroll
-    for (int x = 0; x < DQ; ++x) {
-      const int ch = chan(x);
-      const float pre = sPre[I * D + ch], suf = sSuf[I * D + ch];
-      const float tot = sTot[I * D + ch];
-      const float lc = loc[i][x];
-      const float lcm = __shfl(lc, 7, 16);
-      const float egc = __expf(pre + lc);
-      const float eloc = __expf(lc);
-      const float bk = bv[x] * kv[x];
-      qg[x] = sanitize(qv[x] * egc);
-      sKbdT[ch * TT_LD + t] = from_f<T>(bk * egc);
-      kgT[(size_t)ch * BT + t] = from_f<T>(sanitize(kv[x] * __expf(suf + (tot - lc))));
-      sR0[t * KH_LD + ch] = from_f<T>(kv[x] * __expf(tot - lc));
-      aq[i][x] = qv[x] * eloc;
-      ak[i][x] = bk * eloc;
-      const float edq = __expf(lc - lcm), edk = __expf(lcm - lc);
-      dq[x] = qv[x] * edq;
-      db[x] = bk * edq;
-      dk[x] = kv[x] * edk;
-    }
     T* qgp = a.Qg + (size_t)cid * BT * D + (size_t)t * D;
-#pragma unroll
-    for (int j = 0; j < NKD; ++j) {
-      Op o = op_from<T>(&qg[j * KC]);
-      *reinterpret_cast<Op*>(qgp + j * KS + lg * KC) = o;
-    }
-    // diagonal block: X = k rows (j), Y = q / bk rows (i) -> lane holds [i=li][j=4lg+r]
     f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NKD; ++j) {
-      Op xo = op_from<T>(&dk[j * KC]);
-      mma(accq, xo, op_from<T>(&dq[j * KC]));
-      mma(acck, xo, op_from<T>(&db[j * KC]));
+      float qg[KC], kh[KC], dq[KC], dk[KC], db[KC];
+#pragma unroll
+      for (int e = 0; e < KC; ++e) {
+        const int x = j * KC + e, ch = chan(x);
+        const float qv = to_f(qo[i][j][e]), kv = to_f(ko[i][j][e]), bv = to_f(bo[i][j][e]);
+        const float lc = loc[i][x];
+        const float eloc = __expf(lc);
+        const float ekh = __expf(sTot[I * D + ch] - lc);
+        const float egc = eloc * sF[0][I * D + ch];
+        const float bk = bv * kv;
+        qg[e] = qv * egc;
+        sKbdT[ch * TT_LD + t] = from_f<T>(bk * egc);
+        kgT[(size_t)ch * BT + t] = from_f<T>(kv * ekh * sF[1][I * D + ch]);
+        kh[e] = kv * ekh;
+        aq[i][x] = qv * eloc;
+        ak[i][x] = bk * eloc;
+        // the diagonal-block factors keep their own exponentials: e^{loc} or
+        // e^{T_I-loc} may underflow where e^{loc-loc_m} e^{loc_m-loc'} does not
+        const float lm = row_bcast<7>(lc);
+        const float edq = __expf(lc - lm), edk = __expf(lm - lc);
+        dq[e] = qv * edq;
+        db[e] = bk * edq;
+        dk[e] = kv * edk;
+      }
+      *reinterpret_cast<Op*>(qgp + j * KS + lg * KC) = op_from<T>(qg);
+      *reinterpret_cast<Op*>(&sR0[t * KH_LD + j * KS + lg * KC]) = op_from<T>(kh);
+      // diagonal block, factorised around its 8th token: X = k rows (j),
+      // Y = q / bk rows (i) -> lane holds [i=li][j=4lg+r]
+      const Op xo = op_from<T>(dk);
+      mma(accq, xo, op_from<T>(dq));
+      mma(acck, xo, op_from<T>(db));
     }
     f32x4 sq, sk;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int jj = 4 * lg + r;
-      sq[r] = (jj <= li) ? sanitize(a.scale * accq[r]) : 0.f;
-      sk[r] = (jj < li) ? sanitize(acck[r]) : 0.f;
+      sq[r] = (jj <= li) ? a.scale * accq[r] : 0.f;
+      sk[r] = (jj < li) ? acck[r] : 0.f;
     }
     store4(a.Aqk + (size_t)cid * BT * BT + (size_t)t * BT + I * 16 + 4 * lg, sq);
     store4(&sA[t * A_LD + I * 16 + 4 * lg], sk);
@@ -196,23 +216,29 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
           yq[e] = aq[i][j * KC + e] * F[j * KC + e];
           yk[e] = ak[i][j * KC + e] * F[j * KC + e];
         }
-        Op xo = op_load<T>(&sR0[(J * 16 + li) * KH_LD + j * KS + lg * KC]);
+        const Op xo = op_load<T>(&sR0[(J * 16 + li) * KH_LD + j * KS + lg * KC]);
         mma(accq, xo, op_from<T>(yq));
         mma(acck, xo, op_from<T>(yk));
       }
-      f32x4 sq, sk;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sq[r] = sanitize(a.scale * accq[r]);
-        sk[r] = sanitize(acck[r]);
-      }
-      store4(a.Aqk + (size_t)cid * BT * BT + (size_t)t * BT + J * 16 + 4 * lg, sq);
-      store4(&sA[t * A_LD + J * 16 + 4 * lg], sk);
+      store4(a.Aqk + (size_t)cid * BT * BT + (size_t)t * BT + J * 16 + 4 * lg, accq * a.scale);
+      store4(&sA[t * A_LD + J * 16 + 4 * lg], acck);
 #pragma unroll
       for (int x = 0; x < DQ; ++x) F[x] *= sETot[J * D + chan(x)];
     }
   }
   __syncthreads();
+
+  // w, v: in flight during the inverse
+  Op wo[NBW][NKD], vo[NBW][NKD];
+#pragma unroll
+  for (int i = 0; i < NBW; ++i) {
+    const size_t off = rowp(own_block<NB>(wv, i) * 16 + li);
+#pragma unroll
+    for (int j = 0; j < NKD; ++j) {
+      wo[i][j] = op_load<T>(a.w + off + j * KS + lg * KC);
+      vo[i][j] = op_load<T>(a.v + off + j * KS + lg * KC);
+    }
+  }
 
   // ---- 4. A = (I + Akk)^{-1}: diagonal blocks by substitution ---------------
   if (lg < NBW) {
@@ -225,7 +251,7 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
       float s = (r == j) ? 1.f : 0.f;
 #pragma unroll
       for (int kk = 0; kk < r; ++kk) s -= blk[r * A_LD + kk] * x[kk];
-      x[r] = sanitize(s);
+      x[r] = s;
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) sA[(I * 16 + r) * A_LD + I * 16 + j] = x[r];
@@ -253,15 +279,12 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
             } else {
               y = X[i][K];
             }
-            const f32x4 xo = load4f(&sA[(I * 16 + li) * A_LD + K * 16 + 4 * lg]);
-            mma(S, xo, y);
+            mma(S, load4f(&sA[(I * 16 + li) * A_LD + K * 16 + 4 * lg]), y);
           }
         }
-        const f32x4 xii = load4f(&sA[(I * 16 + li) * A_LD + I * 16 + 4 * lg]);
         f32x4 R = {0.f, 0.f, 0.f, 0.f};
-        mma(R, xii, S);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) X[i][I][r] = sanitize(-R[r]);
+        mma(R, load4f(&sA[(I * 16 + li) * A_LD + I * 16 + 4 * lg]), S);
+        X[i][I] = -R;
       }
     }
   }
@@ -277,21 +300,15 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
       }
     }
   }
-  // ---- 5. (w v)^T into LDS ----------------------------------------------------
+  // ---- 5. (w v)^T into LDS (khat's region, free since step 3) ---------------
   T* sWVT = sR0;
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
-    const int I = own_block<NB>(wv, i);
-    const int t = I * 16 + li;
-    const size_t off = rowp(t);
-    float wv_[DQ], vv[DQ];
+    const int t = own_block<NB>(wv, i) * 16 + li;
 #pragma unroll
-    for (int j = 0; j < NKD; ++j) {
-      load_f<KC>(a.w + off + j * KS + lg * KC, &wv_[j * KC]);
-      load_f<KC>(a.v + off + j * KS + lg * KC, &vv[j * KC]);
-    }
-#pragma unroll
-    for (int x = 0; x < DQ; ++x) sWVT[chan(x) * TT_LD + t] = from_f<T>(wv_[x] * vv[x]);
+    for (int x = 0; x < DQ; ++x)
+      sWVT[chan(x) * TT_LD + t] =
+          from_f<T>(to_f(wo[i][x / KC][x % KC]) * to_f(vo[i][x / KC][x % KC]));
   }
   __syncthreads();
 
@@ -311,7 +328,7 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
       float tmp[KC];
 #pragma unroll
       for (int e = 0; e < KC; e += 4) {
-        f32x4 v4 = load4f(&sA[(I * 16 + li) * A_LD + kg * KS + lg * KC + e]);
+        const f32x4 v4 = load4f(&sA[(I * 16 + li) * A_LD + kg * KS + lg * KC + e]);
         tmp[e] = v4[0]; tmp[e + 1] = v4[1]; tmp[e + 2] = v4[2]; tmp[e + 3] = v4[3];
       }
       af[kg] = op_from<T>(tmp);
@@ -328,11 +345,8 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
           mma(accu, af[kg], op_load<T>(&sWVT[(dt * 16 + li) * TT_LD + kg * KS + lg * KC]));
         }
       }
-      f32x4 sw, su;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) { sw[r] = sanitize(accw[r]); su[r] = sanitize(accu[r]); }
-      store4(Wc + (size_t)(I * 16 + li) * D + dt * 16 + 4 * lg, sw);
-      store4(Uc + (size_t)(dt * 16 + li) * BT + I * 16 + 4 * lg, su);
+      store4(Wc + (size_t)(I * 16 + li) * D + dt * 16 + 4 * lg, accw);
+      store4(Uc + (size_t)(dt * 16 + li) * BT + I * 16 + 4 * lg, accu);
     }
   }
 }
@@ -352,24 +366,56 @@ struct StateArgs {
 };
 
 // One workgroup = one (b,h) and 64 value columns; wave wv owns 16 columns.
-// The next chunk's W, kg^T (whole workgroup, registers) and u^T, gc_last
-// (per wave) are fetched while the current chunk is computed.
+// W and kg^T of the next chunk stream into the other half of a double buffer
+// with global_load_lds_dwordx4 (no registers involved) while the current chunk
+// is computed; u^T rows are prefetched into registers.  Tiles are stored
+// unpadded with the 16-byte chunks of row r XOR-permuted by (r mod 16), so the
+// 16 rows an MFMA operand read touches land in distinct LDS banks.
 template <typename T, int BT, int D>
 __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
   using Op = typename Tr<T>::Op;
   constexpr int NB = BT / 16, NDT = D / 16;
-  constexpr int EPV = 16 / sizeof(T);
-  constexpr int W_LD = D + EPV, K_LD = BT + EPV;
   constexpr int NVS = D / 64;
   constexpr bool F32 = sizeof(T) == 4;
-  constexpr int PW = BT * D / EPV / 256;  // uint4 per thread for W (same for kg^T)
-  __shared__ __align__(16) T sW[BT * W_LD];
-  __shared__ __align__(16) T sK[D * K_LD];
+  constexpr int WBYTES = BT * D * (int)sizeof(T);   // one tile (W or kg^T)
+  constexpr int BUF = 2 * WBYTES;                    // W + kg^T
+  constexpr int PER_WAVE = BUF / 4 / 1024;           // 1 KB DMA instructions per wave
+  static_assert(BUF % 4096 == 0, "tiles must split into 1 KB pieces per wave");
+  __shared__ __align__(16) char sbuf[2 * BUF];
+  __shared__ __align__(16) float sGL[2 * D];
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int bh = blockIdx.x / NVS, vs = blockIdx.x % NVS;
   const int v0 = vs * 64 + wv * 16;
   const int col = v0 + li;
+
+  // element offset of logical (row r, element e) in a tile whose rows hold `re` elements
+  auto swz = [](int r, int e, int re) {
+    constexpr int EPC = 16 / sizeof(T);           // elements per 16-byte chunk
+    const int nchunk = re / EPC;
+    const int m = (nchunk < 16 ? nchunk : 16) - 1;
+    const int j = e / EPC;
+    return r * re + ((j ^ (r & m)) * EPC) + (e % EPC);
+  };
+  auto issue = [&](int c, int buf) {
+    const size_t cid = (size_t)bh * a.N + c;
+    char* base = sbuf + buf * BUF;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int o = (wv * PER_WAVE + i) * 1024;            // wave-uniform LDS offset
+      const int lo = o + lane * 16;                         // this lane's 16 bytes
+      const int tile = lo / WBYTES, ib = lo % WBYTES;
+      const int rowb = tile == 0 ? D * (int)sizeof(T) : BT * (int)sizeof(T);
+      const int r = ib / rowb, pch = (ib % rowb) / 16, nch = rowb / 16;
+      const int j = pch ^ (r & ((nch < 16 ? nch : 16) - 1));
+      const char* src = tile == 0
+          ? reinterpret_cast<const char*>(a.W + cid * BT * D)
+          : reinterpret_cast<const char*>(a.KgT + cid * D * BT);
+      lds_dma16(src + (size_t)r * rowb + j * 16, base + o);
+    }
+    if (wv == 0 && lane < D / 4)
+      lds_dma16(a.GL + cid * D + lane * 4, sGL + buf * D);
+  };
 
   f32x4 h[NDT];
 #pragma unroll
@@ -378,46 +424,29 @@ __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
     for (int r = 0; r < 4; ++r)
       h[at][r] = a.h0 ? sanitize(a.h0[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col]) : 0.f;
 
-  uint4 pw[PW], pk[PW];
-  f32x4 un[NB], gn[NDT];
-#define GDN2_STATE_FETCH(c_)                                                          \
-  {                                                                                   \
-    const size_t fcid = (size_t)bh * a.N + (c_);                                      \
-    const uint4* ws = reinterpret_cast<const uint4*>(a.W + fcid * BT * D);            \
-    const uint4* ks = reinterpret_cast<const uint4*>(a.KgT + fcid * D * BT);          \
-    _Pragma("unroll") for (int i = 0; i < PW; ++i) {                                  \
-      pw[i] = ws[tid + 256 * i];                                                      \
-      pk[i] = ks[tid + 256 * i];                                                      \
-    }                                                                                 \
-    const float* up = a.UT + fcid * D * BT + (size_t)col * BT;                        \
-    _Pragma("unroll") for (int it = 0; it < NB; ++it) un[it] = load4f(up + it * 16 + 4 * lg); \
-    const float* glc = a.GL + fcid * D;                                               \
-    _Pragma("unroll") for (int at = 0; at < NDT; ++at) gn[at] = load4f(glc + at * 16 + 4 * lg); \
-  }
-#define GDN2_STATE_COMMIT()                                                           \
-  {                                                                                   \
-    _Pragma("unroll") for (int i = 0; i < PW; ++i) {                                  \
-      const int iw = tid + 256 * i;                                                   \
-      const int rw = iw / (D / EPV), cw = iw % (D / EPV);                             \
-      *reinterpret_cast<uint4*>(&sW[rw * W_LD + cw * EPV]) = pw[i];                   \
-      const int rk = iw / (BT / EPV), ck = iw % (BT / EPV);                           \
-      *reinterpret_cast<uint4*>(&sK[rk * K_LD + ck * EPV]) = pk[i];                   \
-    }                                                                                 \
-  }
+  f32x4 un[NB];
   if (a.N > 0) {
-    GDN2_STATE_FETCH(0)
-    GDN2_STATE_COMMIT()
+    issue(0, 0);
+    const float* up = a.UT + (size_t)bh * a.N * D * BT + (size_t)col * BT;
+#pragma unroll
+    for (int it = 0; it < NB; ++it) un[it] = load4f(up + it * 16 + 4 * lg);
   }
-  __syncthreads();
-
   for (int c = 0; c < a.N; ++c) {
+    const int buf = c & 1;
     const size_t cid = (size_t)bh * a.N + c;
-    f32x4 vn[NB], gl[NDT];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // chunk c resident for every wave; buffer buf^1 no longer read
+    f32x4 vn[NB];
 #pragma unroll
     for (int it = 0; it < NB; ++it) vn[it] = un[it];
+    if (c + 1 < a.N) {
+      issue(c + 1, buf ^ 1);
+      const float* up = a.UT + (cid + 1) * D * BT + (size_t)col * BT;
 #pragma unroll
-    for (int at = 0; at < NDT; ++at) gl[at] = gn[at];
-    if (c + 1 < a.N) GDN2_STATE_FETCH(c + 1)
+      for (int it = 0; it < NB; ++it) un[it] = load4f(up + it * 16 + 4 * lg);
+    }
+    const T* sW = reinterpret_cast<const T*>(sbuf + buf * BUF);
+    const T* sK = reinterpret_cast<const T*>(sbuf + buf * BUF + WBYTES);
 
     T* hT = a.HT + cid * D * D + (size_t)col * D;
 #pragma unroll
@@ -426,15 +455,20 @@ __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      const int r = it * 16 + li;
       if constexpr (F32) {
 #pragma unroll
         for (int at = 0; at < NDT; ++at)
-          mma(acc, op_chained(&sW[(it * 16 + li) * W_LD + at * 16], lg), h[at]);
+          mma(acc, load4f(&sW[swz(r, at * 16 + 4 * lg, D)]), h[at]);
       } else {
 #pragma unroll
-        for (int p = 0; p < NDT / 2; ++p)
-          mma(acc, op_chained(&sW[(it * 16 + li) * W_LD + p * 32], lg),
+        for (int p = 0; p < NDT / 2; ++p) {
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&sW[swz(r, p * 32 + 4 * lg, D)]);
+          const bf16x4 hi =
+              *reinterpret_cast<const bf16x4*>(&sW[swz(r, p * 32 + 16 + 4 * lg, D)]);
+          mma(acc, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7),
               op_from_c(h[2 * p], h[2 * p + 1], (Op*)nullptr));
+        }
       }
       vn[it] -= acc;
     }
@@ -442,26 +476,30 @@ __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
 #pragma unroll
     for (int it = 0; it < NB; ++it) store4(vT + it * 16 + 4 * lg, vn[it]);
 
+    const float* glc = sGL + buf * D;
 #pragma unroll
     for (int at = 0; at < NDT; ++at) {
+      const f32x4 gl4 = load4f(glc + at * 16 + 4 * lg);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) h[at][r] *= __expf(gl[at][r]);
+      for (int r = 0; r < 4; ++r) h[at][r] *= __expf(gl4[r]);
+      const int r = at * 16 + li;
       if constexpr (F32) {
 #pragma unroll
         for (int it = 0; it < NB; ++it)
-          mma(h[at], op_chained(&sK[(at * 16 + li) * K_LD + it * 16], lg), vn[it]);
+          mma(h[at], load4f(&sK[swz(r, it * 16 + 4 * lg, BT)]), vn[it]);
       } else {
 #pragma unroll
-        for (int p = 0; p < NB / 2; ++p)
-          mma(h[at], op_chained(&sK[(at * 16 + li) * K_LD + p * 32], lg),
+        for (int p = 0; p < NB / 2; ++p) {
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&sK[swz(r, p * 32 + 4 * lg, BT)]);
+          const bf16x4 hi =
+              *reinterpret_cast<const bf16x4*>(&sK[swz(r, p * 32 + 16 + 4 * lg, BT)]);
+          mma(h[at], __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7),
               op_from_c(vn[2 * p], vn[2 * p + 1], (Op*)nullptr));
+        }
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) h[at][r] = sanitize(h[at][r]);
+      for (int r2 = 0; r2 < 4; ++r2) h[at][r2] = sanitize(h[at][r2]);
     }
-    __syncthreads();
-    if (c + 1 < a.N) GDN2_STATE_COMMIT()
-    __syncthreads();
   }
 #pragma unroll
   for (int at = 0; at < NDT; ++at)
@@ -558,7 +596,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   launch_mark(st);
   if (NC > 0) {
     PrepArgs<T, TG> pa{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
-                       (const TG*)g, T_len, H, N, scale, W, UT, KgT, Qg, Aqk, GL,
+                       (const TG*)g, T_len, H, N, (long long)NC, scale, W, UT, KgT, Qg, Aqk, GL,
                        a_dbg ? a_dbg : ((flags & 1) ? reinterpret_cast<float*>(ws + L.A)
                                                     : nullptr)};
     hipLaunchKernelGGL((fwd_prep<T, TG, BT, D>), dim3(NC), dim3(256), 0, st, pa);
