@@ -28,6 +28,7 @@ struct GMat {
   int ld;                   // row pitch of the stored matrix
   int trans;                // logical (r, k) stored at [k*ld + r] (1) or [r*ld + k] (0)
   int mask;                 // on stored (row, col): 1 keep col <= row, 2 keep col < row
+  int chained;              // bfloat16 columns stored in chained order (kpos)
 };
 struct GOut {
   float* p;
@@ -71,7 +72,8 @@ __device__ __forceinline__ void stage(float* dst, const GMat& m, size_t off, int
       if (i < total) {
         rr[u] = i / cq;
         cc[u] = (i - rr[u] * cq) * 4;
-        load4_any(m.p, m.bf16, off + (size_t)rr[u] * m.ld + cc[u], v[u]);
+        const int sc = m.chained ? kpos<bf16_t>(cc[u]) : cc[u];
+        load4_any(m.p, m.bf16, off + (size_t)rr[u] * m.ld + sc, v[u]);
       }
     }
 #pragma unroll
@@ -142,6 +144,7 @@ struct BStateArgs {
 };
 
 // dst[r][c] (pitch ld, f32) <- R x C tile of type T at src (pitch C), all loads first.
+// bfloat16 tiles (forward residuals W, kg^T) are stored in chained column order.
 template <typename T, int R, int C, int ld>
 __device__ __forceinline__ void stage_tile(float* dst, const T* src, int tid) {
   constexpr int Q = R * C / 4, PER = Q / 256;
@@ -150,7 +153,7 @@ __device__ __forceinline__ void stage_tile(float* dst, const T* src, int tid) {
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
     const int i = tid + 256 * u;
-    load_f<4>(src + (size_t)(i / (C / 4)) * C + (i % (C / 4)) * 4, v[u]);
+    load_f<4>(src + (size_t)(i / (C / 4)) * C + kpos<T>((i % (C / 4)) * 4), v[u]);
   }
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
@@ -481,7 +484,7 @@ __global__ void __launch_bounds__(128) bwd_combine(CombArgs<T, TG> a) {
   // exp(gl) * sum_dv dh'[d][dv] h[d][dv]  (gdn2_bwd.py:196-197)
   float sdh = 0.f;
   {
-    const T* ht = a.HT + (size_t)cid * D * D + d;
+    const T* ht = a.HT + (size_t)cid * D * D + kpos<T>(d);
     const float* dht = a.DHT + (size_t)cid * D * D + d;
     for (int dv = 0; dv < D; ++dv) sdh += dht[(size_t)dv * D] * to_f(ht[(size_t)dv * D]);
   }
@@ -541,6 +544,12 @@ GMat ch_mat(const void* p, int bf16, const Dims& d, int R, int C, int trans = 0,
   const long long tile = (long long)R * C;
   return GMat{p, bf16, (long long)d.H * d.N * tile, (long long)d.N * tile, tile, C, trans, mask};
 }
+// A forward residual tile (h^T, v_new^T): bfloat16 ones are in chained column order.
+GMat res_mat(const void* p, int bf16, const Dims& d, int R, int C, int trans = 0) {
+  GMat m = ch_mat(p, bf16, d, R, C, trans);
+  m.chained = bf16;
+  return m;
+}
 GOut ch_out(float* p, const Dims& d, int R, int C, float alpha = 1.f, int trans = 0,
             int mask = 0, int accum = 0) {
   const long long tile = (long long)R * C;
@@ -585,7 +594,7 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     }
     // B2: dAqk, Aqk^T do, scale qg^T do
     if (NC > 0) {
-      gemm(st, dm, tok_mat(dout, 0, dm), ch_mat(fVnT, tb, dm, D, BT),
+      gemm(st, dm, tok_mat(dout, 0, dm), res_mat(fVnT, tb, dm, D, BT),
            ch_out(buf(B_DAQK), dm, BT, BT, 1.f, 0, 1), BT, BT, D);
       gemm(st, dm, ch_mat(fAqk, tb, dm, BT, BT, 1, 1), tok_mat(dout, 0, dm),
            ch_out(buf(B_DVPT), dm, D, BT, 1.f, 1), BT, D, BT);
@@ -604,11 +613,11 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
       hipLaunchKernelGGL((bwd_elem<T, TG>), dim3(NC), dim3(D), 0, st, ea);
       launch_mark(st);
       // B3 products
-      gemm(st, dm, tok_mat(dout, 0, dm), ch_mat(fHT, tb, dm, D, D),
+      gemm(st, dm, tok_mat(dout, 0, dm), res_mat(fHT, tb, dm, D, D),
            ch_out(buf(B_DQG), dm, BT, D, scale), BT, D, D);
-      gemm(st, dm, ch_mat(buf(B_DVNT), 0, dm, D, BT, 1), ch_mat(fHT, tb, dm, D, D),
+      gemm(st, dm, ch_mat(buf(B_DVNT), 0, dm, D, BT, 1), res_mat(fHT, tb, dm, D, D),
            ch_out(buf(B_DW), dm, BT, D, -1.f), BT, D, D);
-      gemm(st, dm, ch_mat(fVnT, tb, dm, D, BT, 1), ch_mat(buf(B_DHT), 0, dm, D, D),
+      gemm(st, dm, res_mat(fVnT, tb, dm, D, BT, 1), ch_mat(buf(B_DHT), 0, dm, D, D),
            ch_out(buf(B_DKG), dm, BT, D), BT, D, D);
       gemm(st, dm, ch_mat(buf(B_DW), 0, dm, BT, D), ch_mat(buf(B_KBD), 0, dm, BT, D, 1),
            ch_out(buf(B_DA), dm, BT, BT, 1.f, 0, 2), BT, BT, D);

@@ -145,6 +145,21 @@ __device__ __forceinline__ bf16x8 op_chained(const bf16_t* p, int lg) {
   bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16 + 4 * lg);
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
+// Stored position of logical column c in the "chained order" used for bfloat16
+// tiles that the serial state pass contracts over: inside each 32-column
+// block, position 8*lg + 4*half + r holds column 16*half + 4*lg + r.  Then the
+// k positions a lane-group feeds from two C-layout tiles (header comment) are
+// one contiguous 16-byte run, and so are the values a lane holds of two
+// consecutive C-layout tiles.  float32 tiles keep the identity order.
+template <typename T>
+__host__ __device__ constexpr int kpos(int c) {
+  if constexpr (sizeof(T) == 4) {
+    return c;
+  } else {
+    return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3);
+  }
+}
+
 // C-layout tiles as the other operand of a chained product.
 __device__ __forceinline__ f32x4 op_from_c(const f32x4& t0, const f32x4&, f32x4*) { return t0; }
 __device__ __forceinline__ bf16x8 op_from_c(const f32x4& t0, const f32x4& t1, bf16x8*) {
@@ -161,6 +176,19 @@ __device__ __forceinline__ bf16x8 op_from_c(const f32x4& t0, const f32x4& t1, bf
 __device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds_base, 16,
                                    0, 0);
+}
+// 4 bytes per lane (global_load_lds_dword), lane l's bytes at lds_base + 4*l.
+__device__ __forceinline__ void lds_dma4(const void* gsrc, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds_base, 4,
+                                   0, 0);
+}
+
+// Wait until at most N vector memory instructions of this wave are in flight.
+// Loads complete in issue order, so this waits for all but the last N issued.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // Copy `rows` rows of `cols` elements (row pitch `gpitch` in global, `lpitch`

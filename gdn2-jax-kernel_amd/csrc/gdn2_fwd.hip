@@ -166,7 +166,7 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
         const float bk = bv * kv;
         qg[e] = qv * egc;
         sKbdT[ch * TT_LD + t] = from_f<T>(bk * egc);
-        kgT[(size_t)ch * BT + t] = from_f<T>(kv * ekh * sF[1][I * D + ch]);
+        kgT[(size_t)ch * BT + kpos<T>(t)] = from_f<T>(kv * ekh * sF[1][I * D + ch]);
         kh[e] = kv * ekh;
         aq[i][x] = qv * eloc;
         ak[i][x] = bk * eloc;
@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
           mma(accu, af[kg], op_load<T>(&sWVT[(dt * 16 + li) * TT_LD + kg * KS + lg * KC]));
         }
       }
-      store4(Wc + (size_t)(I * 16 + li) * D + dt * 16 + 4 * lg, accw);
+      store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dt * 16 + 4 * lg), accw);
       store4(Uc + (size_t)(dt * 16 + li) * BT + I * 16 + 4 * lg, accu);
     }
   }
@@ -365,30 +365,166 @@ struct StateArgs {
   float* h_final;
 };
 
-// One workgroup = one (b,h) and 64 value columns; wave wv owns 16 columns.
-// W and kg^T of the next chunk stream into the other half of a double buffer
-// with global_load_lds_dwordx4 (no registers involved) while the current chunk
-// is computed; u^T rows are prefetched into registers.  Tiles are stored
-// unpadded with the 16-byte chunks of row r XOR-permuted by (r mod 16), so the
-// 16 rows an MFMA operand read touches land in distinct LDS banks.
-template <typename T, int BT, int D>
-__global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
+// One workgroup = one (b,h) and 16*NW value columns: NW compute waves (16
+// columns each) and NP producer waves.  While the compute waves work on chunk
+// c, the producers stream chunk c+1 (W, kg^T, g_last and this workgroup's u^T
+// rows) into LDS with global_load_lds_dwordx4, wait for it and replace g_last
+// by e^{g_last}.  A wave
+// that issues that much memory traffic stalls at issue (at most 63 vector
+// memory instructions in flight per wave), so the compute waves issue none and
+// the traffic is split over several producers.  Two barriers per chunk: A
+// (chunk c resident, chunk c-1's buffers free) and B (u^T of chunk c copied to
+// registers, its buffer free).
+//
+// W / kg^T tiles are stored unpadded with the 16-byte chunks of row r
+// XOR-permuted by (r mod 16), so the 16 rows an MFMA operand read touches land
+// in distinct LDS banks.  u^T is gathered straight into the order the compute
+// lanes read it (one contiguous 1 KB block per wave and row block).  The two
+// halves of the W / kg^T double buffer are separate __shared__ arrays selected
+// at compile time (the chunk loop is unrolled by two), so the compiler can see
+// that reads of one half never alias the DMA into the other.
+template <typename T, int BT, int D, int NW, int NP>
+__global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
   using Op = typename Tr<T>::Op;
   constexpr int NB = BT / 16, NDT = D / 16;
-  constexpr int NVS = D / 64;
+  constexpr int NVS = D / (16 * NW);
   constexpr bool F32 = sizeof(T) == 4;
   constexpr int WBYTES = BT * D * (int)sizeof(T);   // one tile (W or kg^T)
   constexpr int BUF = 2 * WBYTES;                    // W + kg^T
-  constexpr int PER_WAVE = BUF / 4 / 1024;           // 1 KB DMA instructions per wave
-  static_assert(BUF % 4096 == 0, "tiles must split into 1 KB pieces per wave");
-  __shared__ __align__(16) char sbuf[2 * BUF];
-  __shared__ __align__(16) float sGL[2 * D];
+  constexpr int PIECES = BUF / 1024;                 // 1 KB DMA instructions per chunk
+  static_assert(BUF % 1024 == 0, "tiles must split into 1 KB pieces");
+  __shared__ __align__(16) char sbuf0[BUF];
+  __shared__ __align__(16) char sbuf1[BUF];
+  __shared__ __align__(16) f32x4 sU[NW * NB * 64];   // u^T in compute-lane order
+  __shared__ __align__(16) float sGL0[D];
+  __shared__ __align__(16) float sGL1[D];
+  __shared__ __align__(16) float sJunk[64];        // target of the L2 touches
 
-  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  const int bh = blockIdx.x / NVS, vs = blockIdx.x % NVS;
-  const int v0 = vs * 64 + wv * 16;
-  const int col = v0 + li;
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Workgroups are dealt round-robin over the 8 XCDs (XCD = id mod 8).  Place
+  // all NVS column slices of one (b,h) on the same XCD so the W / kg^T tiles
+  // they all stream are fetched into that XCD's L2 once.
+  int bh, vs;
+  {
+    const int nwg = gridDim.x, id = blockIdx.x;
+    const int per_xcd = nwg / 8;
+    if (nwg % 8 == 0 && per_xcd % NVS == 0) {
+      const int xcd = id % 8, slot = id / 8;
+      bh = xcd * (per_xcd / NVS) + slot / NVS;
+      vs = slot % NVS;
+    } else {
+      bh = id / NVS;
+      vs = id % NVS;
+    }
+  }
 
+  if (wv >= NW) {
+    // ---- producers ----------------------------------------------------------
+    // producer p moves W / kg^T pieces [p PP, (p+1) PP) and u^T blocks q = p mod NP
+    constexpr int ROWB_W = D * (int)sizeof(T), ROWB_K = BT * (int)sizeof(T);
+    constexpr int WPIECES = WBYTES / 1024;
+    constexpr int PP = PIECES / NP;
+    static_assert(PIECES % NP == 0 && (NW * NB) % NP == 0, "work must split evenly");
+    const int p = wv - NW;
+    auto issue = [&](int c, char* base, float* gl) __attribute__((always_inline)) {
+      const size_t cid = (size_t)bh * a.N + c;
+      const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
+      const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
+#pragma unroll
+      for (int i = 0; i < PP; ++i) {
+        const int piece = p * PP + i;                      // wave-uniform
+        char* dst = base + piece * 1024;
+        if (piece < WPIECES) {
+          const int ib = piece * 1024 + lane * 16;
+          const int r = ib / ROWB_W, pch = (ib % ROWB_W) / 16;
+          constexpr int NCH = ROWB_W / 16, M = (NCH < 16 ? NCH : 16) - 1;
+          lds_dma16(wsrc + (size_t)r * ROWB_W + ((pch ^ (r & M)) * 16), dst);
+        } else {
+          const int ib = (piece - WPIECES) * 1024 + lane * 16;
+          const int r = ib / ROWB_K, pch = (ib % ROWB_K) / 16;
+          constexpr int NCH = ROWB_K / 16, M = (NCH < 16 ? NCH : 16) - 1;
+          lds_dma16(ksrc + (size_t)r * ROWB_K + ((pch ^ (r & M)) * 16), dst);
+        }
+      }
+      if (p == NP - 1 && lane < D / 4) lds_dma16(a.GL + cid * D + lane * 4, gl);
+      // u^T[col][t] for compute wave w, row block it: lane (li, lg) of that
+      // wave reads u^T[16 w + li][16 it + 4 lg .. +3] from sU[(w NB + it) 64 + lane]
+      const float* usrc = a.UT + cid * D * BT + (size_t)(vs * 16 * NW + li) * BT + 4 * lg;
+#pragma unroll
+      for (int j = 0; j < NW * NB / NP; ++j) {
+        const int q = j * NP + p, w = q / NB, it = q % NB;
+        lds_dma16(usrc + (size_t)w * 16 * BT + it * 16, &sU[q * 64]);
+      }
+    };
+    // L2 touch of chunk c: one 4-byte DMA into a junk slot per 128-byte line of
+    // everything issue(c) will read, spread over the producers.  Issued one
+    // chunk ahead of the DMA, it turns the DMA's HBM latency into L2 latency.
+    constexpr int LINE = 128;
+    constexpr int LW = WBYTES / LINE;                       // lines per W / kg^T tile
+    constexpr int LUR = BT * 4 / LINE;                      // lines per u^T row
+    constexpr int LU = 16 * NW * LUR;                       // this workgroup's u^T rows
+    constexpr int LG = (D * 4 + LINE - 1) / LINE;           // g_last
+    constexpr int LTOT = 2 * LW + LU + LG;
+    constexpr int NTP = ((LTOT + 63) / 64 + NP - 1) / NP;   // touch instructions per producer
+    auto touch = [&](int c) __attribute__((always_inline)) {
+      const size_t cid = (size_t)bh * a.N + c;
+      const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
+      const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
+      const char* usrc = reinterpret_cast<const char*>(a.UT + cid * D * BT + (size_t)vs * 16 * NW * BT);
+      const char* gsrc = reinterpret_cast<const char*>(a.GL + cid * D);
+#pragma unroll
+      for (int j = 0; j < NTP; ++j) {
+        int l = (j * NP + p) * 64 + lane;
+        l = l < LTOT ? l : LTOT - 1;
+        const char* src = l < LW ? wsrc + l * LINE
+                        : l < 2 * LW ? ksrc + (l - LW) * LINE
+                        : l < 2 * LW + LU ? usrc + (l - 2 * LW) * LINE
+                        : gsrc + (l - 2 * LW - LU) * LINE;
+        lds_dma4(src, sJunk);
+      }
+    };
+    // In flight at the top of chunk c: issue(c), then touch(c+1) if c+1 < N.
+    auto wait_chunk = [&](int c) __attribute__((always_inline)) {
+      if (c + 1 < a.N) wait_vmcnt<NTP>();
+      else wait_vmcnt<0>();
+    };
+    // The producers' data ordering is the explicit vmcnt wait; a plain barrier
+    // (no fence) keeps the compiler from also waiting for the L2 touches.
+    auto barrier = []() __attribute__((always_inline)) {
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    // g_last -> e^{g_last} in place, once per chunk, by the producer that moved it
+    auto exp_gl = [&](float* gl) __attribute__((always_inline)) {
+      if (p == NP - 1) {
+#pragma unroll
+        for (int i = 0; i < (D + 63) / 64; ++i)
+          if (i * 64 + lane < D) gl[i * 64 + lane] = __expf(gl[i * 64 + lane]);
+      }
+    };
+    if (a.N > 0) issue(0, sbuf0, sGL0);
+    if (a.N > 1) touch(1);
+    for (int c = 0; c < a.N; c += 2) {
+      wait_chunk(c);
+      exp_gl(sGL0);
+      barrier();  // A(c)
+      barrier();  // B(c)
+      if (c + 1 < a.N) {
+        issue(c + 1, sbuf1, sGL1);
+        if (c + 2 < a.N) touch(c + 2);
+        wait_chunk(c + 1);
+        exp_gl(sGL1);
+        barrier();  // A(c+1)
+        barrier();  // B(c+1)
+        if (c + 2 < a.N) issue(c + 2, sbuf0, sGL0);
+        if (c + 3 < a.N) touch(c + 3);
+      }
+    }
+    return;
+  }
+
+  // ---- compute waves ----------------------------------------------------------
+  const int col = vs * 16 * NW + wv * 16 + li;
   // element offset of logical (row r, element e) in a tile whose rows hold `re` elements
   auto swz = [](int r, int e, int re) {
     constexpr int EPC = 16 / sizeof(T);           // elements per 16-byte chunk
@@ -397,60 +533,39 @@ __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
     const int j = e / EPC;
     return r * re + ((j ^ (r & m)) * EPC) + (e % EPC);
   };
-  auto issue = [&](int c, int buf) {
-    const size_t cid = (size_t)bh * a.N + c;
-    char* base = sbuf + buf * BUF;
-#pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i) {
-      const int o = (wv * PER_WAVE + i) * 1024;            // wave-uniform LDS offset
-      const int lo = o + lane * 16;                         // this lane's 16 bytes
-      const int tile = lo / WBYTES, ib = lo % WBYTES;
-      const int rowb = tile == 0 ? D * (int)sizeof(T) : BT * (int)sizeof(T);
-      const int r = ib / rowb, pch = (ib % rowb) / 16, nch = rowb / 16;
-      const int j = pch ^ (r & ((nch < 16 ? nch : 16) - 1));
-      const char* src = tile == 0
-          ? reinterpret_cast<const char*>(a.W + cid * BT * D)
-          : reinterpret_cast<const char*>(a.KgT + cid * D * BT);
-      lds_dma16(src + (size_t)r * rowb + j * 16, base + o);
-    }
-    if (wv == 0 && lane < D / 4)
-      lds_dma16(a.GL + cid * D + lane * 4, sGL + buf * D);
-  };
 
   f32x4 h[NDT];
+  if (a.h0) {
 #pragma unroll
-  for (int at = 0; at < NDT; ++at)
+    for (int at = 0; at < NDT; ++at)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      h[at][r] = a.h0 ? sanitize(a.h0[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col]) : 0.f;
-
-  f32x4 un[NB];
-  if (a.N > 0) {
-    issue(0, 0);
-    const float* up = a.UT + (size_t)bh * a.N * D * BT + (size_t)col * BT;
+      for (int r = 0; r < 4; ++r)
+        h[at][r] = sanitize(a.h0[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col]);
+  } else {
 #pragma unroll
-    for (int it = 0; it < NB; ++it) un[it] = load4f(up + it * 16 + 4 * lg);
+    for (int at = 0; at < NDT; ++at) h[at] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  for (int c = 0; c < a.N; ++c) {
-    const int buf = c & 1;
+
+  // One chunk: v_new = u - W h, h <- e^{gl} h + kg^T v_new, with chunk c in `cur`.
+  auto step = [&](int c, const char* cur, const float* eglc) __attribute__((always_inline)) {
     const size_t cid = (size_t)bh * a.N + c;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // chunk c resident for every wave; buffer buf^1 no longer read
+    __syncthreads();  // A(c)
     f32x4 vn[NB];
 #pragma unroll
-    for (int it = 0; it < NB; ++it) vn[it] = un[it];
-    if (c + 1 < a.N) {
-      issue(c + 1, buf ^ 1);
-      const float* up = a.UT + (cid + 1) * D * BT + (size_t)col * BT;
-#pragma unroll
-      for (int it = 0; it < NB; ++it) un[it] = load4f(up + it * 16 + 4 * lg);
-    }
-    const T* sW = reinterpret_cast<const T*>(sbuf + buf * BUF);
-    const T* sK = reinterpret_cast<const T*>(sbuf + buf * BUF + WBYTES);
+    for (int it = 0; it < NB; ++it) vn[it] = sU[(wv * NB + it) * 64 + lane];
+    __syncthreads();  // B(c)
+    const T* sW = reinterpret_cast<const T*>(cur);
+    const T* sK = reinterpret_cast<const T*>(cur + WBYTES);
 
     T* hT = a.HT + cid * D * D + (size_t)col * D;
+    if constexpr (F32) {
 #pragma unroll
-    for (int at = 0; at < NDT; ++at) store4(hT + at * 16 + 4 * lg, h[at]);
+      for (int at = 0; at < NDT; ++at) store4(hT + at * 16 + 4 * lg, h[at]);
+    } else {
+#pragma unroll
+      for (int p = 0; p < NDT / 2; ++p)
+        *reinterpret_cast<Op*>(hT + p * 32 + 8 * lg) = op_from_c(h[2 * p], h[2 * p + 1], (Op*)nullptr);
+    }
 
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
@@ -462,26 +577,27 @@ __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
           mma(acc, load4f(&sW[swz(r, at * 16 + 4 * lg, D)]), h[at]);
       } else {
 #pragma unroll
-        for (int p = 0; p < NDT / 2; ++p) {
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&sW[swz(r, p * 32 + 4 * lg, D)]);
-          const bf16x4 hi =
-              *reinterpret_cast<const bf16x4*>(&sW[swz(r, p * 32 + 16 + 4 * lg, D)]);
-          mma(acc, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7),
+        for (int p = 0; p < NDT / 2; ++p)
+          mma(acc, op_load<T>(&sW[swz(r, p * 32 + 8 * lg, D)]),
               op_from_c(h[2 * p], h[2 * p + 1], (Op*)nullptr));
-        }
       }
       vn[it] -= acc;
     }
     T* vT = a.VnT + cid * D * BT + (size_t)col * BT;
+    if constexpr (F32) {
 #pragma unroll
-    for (int it = 0; it < NB; ++it) store4(vT + it * 16 + 4 * lg, vn[it]);
+      for (int it = 0; it < NB; ++it) store4(vT + it * 16 + 4 * lg, vn[it]);
+    } else {
+#pragma unroll
+      for (int p = 0; p < NB / 2; ++p)
+        *reinterpret_cast<Op*>(vT + p * 32 + 8 * lg) = op_from_c(vn[2 * p], vn[2 * p + 1], (Op*)nullptr);
+    }
 
-    const float* glc = sGL + buf * D;
 #pragma unroll
     for (int at = 0; at < NDT; ++at) {
-      const f32x4 gl4 = load4f(glc + at * 16 + 4 * lg);
+      const f32x4 egl = load4f(eglc + at * 16 + 4 * lg);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) h[at][r] *= __expf(gl4[r]);
+      for (int r = 0; r < 4; ++r) h[at][r] *= egl[r];
       const int r = at * 16 + li;
       if constexpr (F32) {
 #pragma unroll
@@ -489,17 +605,18 @@ __global__ void __launch_bounds__(256) fwd_state(StateArgs<T> a) {
           mma(h[at], load4f(&sK[swz(r, it * 16 + 4 * lg, BT)]), vn[it]);
       } else {
 #pragma unroll
-        for (int p = 0; p < NB / 2; ++p) {
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&sK[swz(r, p * 32 + 4 * lg, BT)]);
-          const bf16x4 hi =
-              *reinterpret_cast<const bf16x4*>(&sK[swz(r, p * 32 + 16 + 4 * lg, BT)]);
-          mma(h[at], __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7),
+        for (int p = 0; p < NB / 2; ++p)
+          mma(h[at], op_load<T>(&sK[swz(r, p * 32 + 8 * lg, BT)]),
               op_from_c(vn[2 * p], vn[2 * p + 1], (Op*)nullptr));
-        }
       }
 #pragma unroll
       for (int r2 = 0; r2 < 4; ++r2) h[at][r2] = sanitize(h[at][r2]);
     }
+  };
+
+  for (int c = 0; c < a.N; c += 2) {
+    step(c, sbuf0, sGL0);
+    if (c + 1 < a.N) step(c + 1, sbuf1, sGL1);
   }
 #pragma unroll
   for (int at = 0; at < NDT; ++at)
@@ -549,12 +666,24 @@ __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
     Op qf[NKD], af[NKT];
     const T* qrow = a.Qg + (size_t)cid * BT * D + (size_t)t * D;
     const T* arow = a.Aqk + (size_t)cid * BT * BT + (size_t)t * BT;
+    // h^T and v_new^T are stored in chained order over d and t (kpos), so qg
+    // and Aqk are read in the matching chained pattern.  Aqk blocks right of
+    // the diagonal block are never written: masked per 16-token block.
 #pragma unroll
-    for (int kg = 0; kg < NKD; ++kg) qf[kg] = op_load<T>(qrow + kg * KS + lg * KC);
+    for (int kg = 0; kg < NKD; ++kg) qf[kg] = op_chained(qrow + kg * KS, lg);
 #pragma unroll
     for (int kg = 0; kg < NKT; ++kg) {
-      const int s0 = kg * KS + lg * KC;
-      af[kg] = (s0 <= It * 16 + 15) ? op_load<T>(arow + s0) : op_zero<T>();
+      if constexpr (sizeof(T) == 4) {
+        const int s0 = kg * KS + lg * KC;
+        af[kg] = (s0 <= It * 16 + 15) ? op_load<T>(arow + s0) : op_zero<T>();
+      } else {
+        const bf16x4 z = {(T)0.f, (T)0.f, (T)0.f, (T)0.f};
+        const bf16x4 lo = (2 * kg <= It)
+            ? *reinterpret_cast<const bf16x4*>(arow + kg * 32 + 4 * lg) : z;
+        const bf16x4 hi = (2 * kg + 1 <= It)
+            ? *reinterpret_cast<const bf16x4*>(arow + kg * 32 + 16 + 4 * lg) : z;
+        af[kg] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
     }
     const int kgmax = (It * 16 + 15) / KS;
 #pragma unroll
@@ -603,7 +732,10 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   }
   launch_mark(st);
   StateArgs<T> sa{W, UT, KgT, GL, h0, N, HT, VnT, h_final};
-  hipLaunchKernelGGL((fwd_state<T, BT, D>), dim3((size_t)B * H * (D / 64)), dim3(256), 0, st, sa);
+  constexpr int SW = 2;  // compute waves (16 value columns each) per state workgroup
+  constexpr int SP = 2;  // producer waves
+  hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3((size_t)B * H * (D / (16 * SW))),
+                     dim3(64 * (SW + SP)), 0, st, sa);
   launch_mark(st);
   if (NC > 0) {
     OutArgs<T> oa{Qg, Aqk, HT, VnT, T_len, H, N, scale, out};

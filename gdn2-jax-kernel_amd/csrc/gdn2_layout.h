@@ -12,7 +12,11 @@
 //   VnT  [cid][D][BT]   T     v_new^T                         (gdn2_fwd.py:350)
 //   A    [cid][BT][BT]  f32   (I + Akk)^{-1}, written only for the backward
 //                             (GDN2_FWD_SAVE_A)               (gdn2_fwd.py:246-260)
-// T is float for float32 inputs and bfloat16 for bfloat16 inputs.
+// T is float for float32 inputs and bfloat16 for bfloat16 inputs.  For
+// bfloat16 the last dimension of W, KgT, HT and VnT (the index the serial state
+// pass contracts over or produces) is stored in chunk order kpos<T>() of
+// gdn2_common.h: within each 32-column block, column 16*half + 4*lg + r sits at
+// position 8*lg + 4*half + r.  float32 tiles are in natural order.
 //
 // Backward workspace (all f32, chunk-major, one region per name):
 //   DAQK [BT][BT] dAqk (causal)      DVPT [D][BT] (Aqk^T do)^T    QDOT [D][D] (scale qg^T do)^T

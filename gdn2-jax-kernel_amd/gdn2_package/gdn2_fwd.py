@@ -159,16 +159,27 @@ def _residual_views(p: _Prepared, ws: torch.Tensor):
     shp = (B, H, N)
     idx = torch.arange(BT, device=p.device)
     causal = (idx[:, None] >= idx[None, :])
+    # bfloat16 W, KgT, HT, VnT keep their last dimension in chained order
+    # (gdn2_common.h kpos): undo it for the views
+    chained = p.in_dt == torch.bfloat16
+    nat = lambda x, n: x[..., _kpos_index(n, x.device)] if chained else x
     return {
-        "w_pseudo": f(views["W"].view(*shp, BT, D)),
+        "w_pseudo": f(nat(views["W"].view(*shp, BT, D), D)),
         "u": f(views["UT"].view(*shp, D, BT).transpose(-1, -2)),
-        "kg": f(views["KgT"].view(*shp, D, BT).transpose(-1, -2)),
+        "kg": f(nat(views["KgT"].view(*shp, D, BT), BT).transpose(-1, -2)),
         "qg": f(views["Qg"].view(*shp, BT, D)),
         "Aqk": torch.where(causal, f(views["Aqk"].view(*shp, BT, BT)), 0.0),
         "gc_last": f(views["GL"].view(*shp, D)),
-        "h_pre_all": f(views["HT"].view(*shp, D, D).transpose(-1, -2)),
-        "v_new_all": f(views["VnT"].view(*shp, D, BT).transpose(-1, -2)),
+        "h_pre_all": f(nat(views["HT"].view(*shp, D, D), D).transpose(-1, -2)),
+        "v_new_all": f(nat(views["VnT"].view(*shp, D, BT), BT).transpose(-1, -2)),
     }
+
+
+def _kpos_index(n: int, device) -> torch.Tensor:
+    """Stored position of each logical column in the chained order of
+    gdn2_common.h kpos: column 16*half + 4*lg + r of a 32-block at 8*lg + 4*half + r."""
+    c = torch.arange(n, device=device)
+    return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3)
 
 
 def gdn2_pallas_forward_with_residuals(q, k, v, w, b, g, scale, h0=None, debug_tag="",
