@@ -16,6 +16,14 @@ shape on this host).
 Inputs are synthetic with the BASELINE.json distributions (torch generator,
 seed 0): q,k ~ N(0,1) L2-normalised over D, v ~ N(0,1), w,b = sigmoid(N(0,1)),
 g = -softplus(N(0,1)).
+
+HBM traffic of the kernels (``roofline.traffic``) comes from two rocprofv3
+counter runs over ``--pmc-run`` (forward steps plus a plain 1 GiB copy kernel
+that calibrates the counters), reduced on any host by ``--traffic-from``:
+
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <F> -- python bench.py --pmc-run
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <W> -- python bench.py --pmc-run
+    python bench.py --traffic-from <F> <W>      # writes profiles/traffic_*.json
 """
 from __future__ import annotations
 
@@ -57,12 +65,14 @@ def kernel_table(dtype_bytes, chunk):
     chunked algorithm's MACs x2 with triangular products at half.
     """
     s, C = dtype_bytes, chunk
+    nb = C // 16
+    aqk = C * s * (nb + 1) / (2 * nb)      # Aqk: only blocks on or below the diagonal
     return {
-        "fwd_prep": {"bytes": 5 * D * s + D * 4 + 3 * D * s + C * s + D * 4 + 4 * D / C,
+        "fwd_prep": {"bytes": 5 * D * s + D * 4 + 3 * D * s + aqk + D * 4 + 4 * D / C,
                      "flops": 4 * C * D + C * C / 3},
         "fwd_state": {"bytes": 2 * D * s + D * 4 + 4 * D / C + D * D * s / C + D * s,
                       "flops": 4 * D * D},
-        "fwd_out": {"bytes": 2 * D * s + C * s + D * D * s / C + D * 4,
+        "fwd_out": {"bytes": 2 * D * s + aqk + D * D * s / C + D * 4,
                     "flops": 2 * D * D + C * D},
     }
 
@@ -120,9 +130,10 @@ def time_train(gp, xs, steps, warmup):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
-def cpu_baseline(sample_T=4096, sample_H=H):
+def cpu_baseline(min_seconds=10.0):
     """The numpy restatement of the reference's chunked forward (kernels A-D
-    with the 3-D decay tensor, float32) on a bounded sample of the workload."""
+    with the 3-D decay tensor, float32) on one batch element of the headline
+    workload (B=1, T, H, D as above), repeated until `min_seconds` have passed."""
     import numpy as np
     from oracle import gdn2_oracle as O
     try:
@@ -130,14 +141,84 @@ def cpu_baseline(sample_T=4096, sample_H=H):
         cores = max(i.get("num_threads", 1) for i in threadpool_info()) or 1
     except Exception:
         cores = os.cpu_count() or 1
-    xs = O.make_inputs(1, sample_T, sample_H, D, seed=0)
-    t0 = time.perf_counter()
-    O.chunked_fwd(*xs, D ** -0.5, BT=CHUNK, clip=True, dtype=np.float32)
-    dt = time.perf_counter() - t0
-    return {"value": sample_T / dt, "unit": "tokens/s", "cores": int(cores), "kind": "port",
-            "sample": f"forward B=1 T={sample_T} H={sample_H} D={D} BT={CHUNK} float32, numpy "
-                      f"restatement of gdn2_fwd.py kernels A-D (oracle.chunked_fwd), "
-                      f"{dt:.1f} s; tokens/s comparable to value (same H, D)"}
+    xs = O.make_inputs(1, T, H, D, seed=0)
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        O.chunked_fwd(*xs, D ** -0.5, BT=CHUNK, clip=True, dtype=np.float32)
+        runs += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            break
+    return {"value": runs * T / dt, "unit": "tokens/s", "cores": int(cores), "kind": "port",
+            "sample": f"{runs} x forward of one batch element (B=1 T={T} H={H} D={D} "
+                      f"BT={CHUNK}, float32) of the headline workload, numpy restatement of "
+                      f"gdn2_fwd.py kernels A-D (oracle.chunked_fwd), {dt:.1f} s; "
+                      f"tokens/s comparable to value (same T, H, D)"}
+
+
+COPY_BYTES = 1 << 30           # calibration copy: reads and writes this many bytes
+KERNELS = ("fwd_prep", "fwd_state", "fwd_out")
+
+
+def pmc_run(steps):
+    """Forward steps plus one plain copy kernel of COPY_BYTES, for counter runs."""
+    import torch
+    import gdn2_package as gp
+    xs = make_inputs(torch.bfloat16)
+    for _ in range(steps):
+        gp.gdn2_pallas_forward(*xs, D ** -0.5, chunk_size=CHUNK)
+    src = torch.ones(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.abs(src, out=dst)             # one elementwise kernel: reads and writes 1 GiB
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_run": steps, "copy_bytes": COPY_BYTES}), flush=True)
+
+
+def _counter_means(run_dir, counter):
+    """Per-dispatch values of `counter` in a rocprofv3 csv counter-collection
+    output directory: (mean per kernel name, value of the last dispatch)."""
+    import csv
+    files = sorted(Path(run_dir).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {run_dir}")
+    per = {}
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                key = (int(row.get("Dispatch_Id", 0)), row.get("Kernel_Name", ""))
+                per[key] = per.get(key, 0.0) + float(row["Counter_Value"])
+    by_kernel = {}
+    for (_, name), v in per.items():
+        by_kernel.setdefault(name, []).append(v)
+    last = per[max(per)]
+    return {name: sum(v) / len(v) for name, v in by_kernel.items()}, last
+
+
+def traffic_from(fetch_dir, write_dir):
+    """Copy-calibrated HBM bytes per launch of each forward kernel from the
+    FETCH_SIZE and WRITE_SIZE runs (counters in KiB per dispatch).  The
+    calibration copy is the last dispatch of a --pmc-run."""
+    fetch, f_copy = _counter_means(fetch_dir, "FETCH_SIZE")
+    write, w_copy = _counter_means(write_dir, "WRITE_SIZE")
+    f_scale = COPY_BYTES / (f_copy * 1024)
+    w_scale = COPY_BYTES / (w_copy * 1024)
+    tab = kernel_table(2, CHUNK)
+    pick = lambda t, k: next(v for n, v in t.items() if k in n)
+    out = {}
+    for k in KERNELS:
+        fb = pick(fetch, k) * 1024 * f_scale
+        wb = pick(write, k) * 1024 * w_scale
+        rec = {"kernel": k, "workload": "B8 T8192 H6 D128 bf16 chunk 128",
+               "fetch_bytes": fb, "write_bytes": wb, "bytes_per_launch": fb + wb,
+               "algorithmic_bytes": tab[k]["bytes"] * B * T * H,
+               "fetch_scale": f_scale, "write_scale": w_scale,
+               "calibration": f"copy kernel reading and writing {COPY_BYTES} bytes"}
+        (ROOT / "profiles" / f"traffic_{k}_b8t8192h6d128_bf16.json").write_text(
+            json.dumps(rec, indent=1) + "\n")
+        out[k] = rec
+    print(json.dumps(out, indent=1))
 
 
 def main():
@@ -147,11 +228,22 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true")
+    ap.add_argument("--pmc-run", action="store_true",
+                    help="forward steps plus the calibration copy, for rocprofv3 --pmc")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="reduce two rocprofv3 counter runs to profiles/traffic_*.json")
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_from(*args.traffic_from)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the op shards over (batch, head) "
               "pairs with no communication); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.pmc_run:
+        pmc_run(max(1, min(args.steps, 5)))
+        return
 
     import torch
     import gdn2_package as gp

@@ -63,3 +63,24 @@ def test_chunk_size_resolution():
     import gdn2_package as gp
     with pytest.raises(gp.GDN2ShapeError):   # fp32 with a 128-token chunk is not supported
         gp.gdn2_pallas_forward(*_inputs((1, 256, 2, 64)), 0.1, chunk_size=128)
+
+
+@pytest.mark.parametrize("n", [64, 128])
+def test_chained_column_order(n):
+    """The bfloat16 state tiles' column order (gdn2_common.h kpos): inside each
+    32-block, column 16*half + 4*lg + r is stored at 8*lg + 4*half + r.  Built
+    here by enumerating (half, lg, r) and compared with the view helper."""
+    from gdn2_package.gdn2_fwd import _kpos_index
+    expect = [0] * n
+    for blk in range(0, n, 32):
+        for half in range(2):
+            for lg in range(4):
+                for r in range(4):
+                    expect[blk + 16 * half + 4 * lg + r] = blk + 8 * lg + 4 * half + r
+    got = _kpos_index(n, "cpu").tolist()
+    assert got == expect
+    assert sorted(got) == list(range(n))
+    # a lane-group's operand k positions {4lg..4lg+3} U {16+4lg..} become one 8-wide run
+    for lg in range(4):
+        ks = [4 * lg + r for r in range(4)] + [16 + 4 * lg + r for r in range(4)]
+        assert sorted(got[k] for k in ks) == list(range(8 * lg, 8 * lg + 8))
