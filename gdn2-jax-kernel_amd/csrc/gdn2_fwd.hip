@@ -66,16 +66,21 @@ __device__ __forceinline__ float row_bcast(float x) {
              0, __builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, false));
 }
 
-// One 256-thread workgroup per chunk; wave wv owns the 16-token row blocks
-// {wv, NB-1-wv} (equal work for the triangular loops).  Per element four
+// One workgroup per chunk with prep_waves(BT) waves.  A wave owns one 16-token
+// row block (8 waves at BT = 128), or the pair {wv, NB-1-wv} when there are
+// twice as many blocks as waves (equal work for the triangular loops).  Per element four
 // exponentials are evaluated (e^{loc}, e^{T_I - loc} and the two diagonal-block
 // factors); the block-level factors e^{P_{I-1}}, e^{S_{I+1}} come from LDS.
+constexpr int prep_waves(int BT) { return BT >= 128 ? 8 : 4; }
+
 template <typename T, typename TG, int BT, int D>
-__global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
+__global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> a) {
   using Op = typename Tr<T>::Op;
   constexpr int KC = Tr<T>::KC, KS = Tr<T>::KS;
   constexpr int NB = BT / 16;             // 16-token row blocks
-  constexpr int NBW = (NB + 3) / 4;       // row blocks per wave
+  constexpr int PW = prep_waves(BT), NT = 64 * PW;   // waves, threads
+  constexpr int NBW = NB / PW;            // row blocks per wave
+  static_assert(NB % PW == 0 && (NBW == 1 || NBW == 2), "row blocks must split over waves");
   constexpr int NKD = D / KS;             // k-groups over channels
   constexpr int NKT = BT / KS;            // k-groups over tokens
   constexpr int DQ = NKD * KC;            // channels owned per lane (= D/4)
@@ -114,7 +119,7 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
       bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
     }
   }
-  for (int i = tid; i < BT * A_LD / 4; i += 256)
+  for (int i = tid; i < BT * A_LD / 4; i += NT)
     reinterpret_cast<f32x4*>(sA)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // ---- 1. in-block inclusive cumsum of g (lanes li = tokens) ----------------
@@ -129,7 +134,7 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
     }
   }
   __syncthreads();
-  for (int i = tid; i < NB * D; i += 256) {
+  for (int i = tid; i < NB * D; i += NT) {
     sETot[i] = __expf(sTot[i]);
   }
   if (tid < D) {
@@ -314,7 +319,7 @@ __global__ void __launch_bounds__(256) fwd_prep(PrepArgs<T, TG> a) {
 
   if (a.a_dbg) {
     float* dst = a.a_dbg + (size_t)cid * BT * BT;
-    for (int i = tid; i < BT * BT; i += 256) dst[i] = sA[(i / BT) * A_LD + (i % BT)];
+    for (int i = tid; i < BT * BT; i += NT) dst[i] = sA[(i / BT) * A_LD + (i % BT)];
   }
 
   // ---- 6. w_pseudo = A (b k e^gc), u = A (w v) ------------------------------
@@ -728,7 +733,8 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                        (const TG*)g, T_len, H, N, (long long)NC, scale, W, UT, KgT, Qg, Aqk, GL,
                        a_dbg ? a_dbg : ((flags & 1) ? reinterpret_cast<float*>(ws + L.A)
                                                     : nullptr)};
-    hipLaunchKernelGGL((fwd_prep<T, TG, BT, D>), dim3(NC), dim3(256), 0, st, pa);
+    hipLaunchKernelGGL((fwd_prep<T, TG, BT, D>), dim3(NC), dim3(64 * prep_waves(BT)), 0, st,
+                       pa);
   }
   launch_mark(st);
   StateArgs<T> sa{W, UT, KgT, GL, h0, N, HT, VnT, h_final};
