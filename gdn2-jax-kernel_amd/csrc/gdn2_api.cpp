@@ -144,11 +144,24 @@ int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype)
   return GDN2_OK;
 }
 
-size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {
+// Forward workspace for the segment count that `flags` selects (automatic
+// when its segment field is 0).
+static size_t fwd_ws_need(int B, int T, int H, int D, int BT, int in_dtype, int flags) {
+  const int N = BT > 0 ? T / BT : 0;
+  const int S = state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
+  return fwd_layout(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype),
+                    S > 1 ? (size_t)B * H * S : 0).total;
+}
+
+size_t gdn2_fwd_workspace_bytes_ex(int B, int T, int H, int D, int BT, int in_dtype, int flags) {
   if (gdn2_validate(B, T, H, D, BT, in_dtype, in_dtype) != GDN2_OK &&
       gdn2_validate(B, T, H, D, BT, in_dtype, GDN2_F32) != GDN2_OK)
     return 0;
-  return fwd_layout(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype)).total;
+  return fwd_ws_need(B, T, H, D, BT, in_dtype, flags);
+}
+
+size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {
+  return gdn2_fwd_workspace_bytes_ex(B, T, H, D, BT, in_dtype, 0);
 }
 
 static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
@@ -162,7 +175,7 @@ static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_d
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, out}))) return rc;
   if ((rc = check_ptrs({h_final}))) return rc;
   if ((rc = check_opt({h0, a_dbg}))) return rc;
-  const size_t need = fwd_layout(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype)).total;
+  const size_t need = fwd_ws_need(B, T, H, D, BT, in_dtype, flags);
   if (need > 0 && (rc = check_ptrs({ws}))) return rc;
   if (ws_bytes < need) return GDN2_ERR_WORKSPACE;
   return dispatch<FwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, B, T, H, q, k, v, w,

@@ -364,7 +364,11 @@ struct StateArgs {
   const T* KgT;
   const float* GL;
   const float* h0;  // nullable, (B,H,D,D)
-  int N;
+  int N;            // chunks per (b,h)
+  int S, L;         // segments per (b,h), chunks per segment (the last may be shorter)
+  int summary;      // segment-summary pass (S > 1): writes `seg`, no h^T / v_new^T
+  const float* hin; // S > 1 and !summary: segment entry states [bh][S][D][D]
+  float* seg;       // summary: [bh][S][2][D][D] = (end state, transition M_seg)
   T* HT;
   T* VnT;
   float* h_final;
@@ -380,6 +384,16 @@ struct StateArgs {
 // the traffic is split over several producers.  Two barriers per chunk: A
 // (chunk c resident, chunk c-1's buffers free) and B (u^T of chunk c copied to
 // registers, its buffer free).
+//
+// Segments (long sequences with few (b,h) pairs).  The chunk map
+// h -> M_c h + kg_c^T u_c, M_c = Diag(e^{g_last}) - kg_c^T W_c, is affine.  With
+// S > 1 segments of L chunks the scan runs in three launches: a summary pass
+// over all segments in parallel gives each segment's end state from h = 0 (h0
+// for segment 0) and, in NVS extra column slices that run the same recurrence
+// from the identity with u = 0 and no clipping, its transition M_seg; the
+// combine kernel chains the segment entry states; the final pass reruns every
+// segment from its entry state, writing h^T / v_new^T.  The combine is exact
+// while the +-1e4 clip of h stays inactive.
 //
 // W / kg^T tiles are stored unpadded with the 16-byte chunks of row r
 // XOR-permuted by (r mod 16), so the 16 rows an MFMA operand read touches land
@@ -407,22 +421,32 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
 
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // Workgroups are dealt round-robin over the 8 XCDs (XCD = id mod 8).  Place
-  // all NVS column slices of one (b,h) on the same XCD so the W / kg^T tiles
-  // they all stream are fetched into that XCD's L2 once.
-  int bh, vs;
+  // A unit is one (b,h) segment; it has NVS column slices (2 NVS in the summary
+  // pass, the second NVS carrying M).  Workgroups are dealt round-robin over the
+  // 8 XCDs (XCD = id mod 8): all slices of a unit go to one XCD so the W / kg^T
+  // tiles they all stream are fetched into that XCD's L2 once.
+  const int NSL = a.summary ? 2 * NVS : NVS;
+  int unit, vs;
   {
     const int nwg = gridDim.x, id = blockIdx.x;
     const int per_xcd = nwg / 8;
-    if (nwg % 8 == 0 && per_xcd % NVS == 0) {
+    if (nwg % 8 == 0 && per_xcd % NSL == 0) {
       const int xcd = id % 8, slot = id / 8;
-      bh = xcd * (per_xcd / NVS) + slot / NVS;
-      vs = slot % NVS;
+      unit = xcd * (per_xcd / NSL) + slot / NSL;
+      vs = slot % NSL;
     } else {
-      bh = id / NVS;
-      vs = id % NVS;
+      unit = id / NSL;
+      vs = id % NSL;
     }
   }
+  const int bh = unit / a.S, sg = unit % a.S;
+  const bool mslice = vs >= NVS;             // summary pass: columns of M_seg
+  if (mslice && sg == 0) return;             // segment 0 starts from h0: no M needed
+  if (mslice) vs -= NVS;
+  const int c0 = sg * a.L;
+  int n = a.N - c0;                          // chunks of this segment
+  n = n < a.L ? n : a.L;
+  n = n > 0 ? n : 0;
 
   if (wv >= NW) {
     // ---- producers ----------------------------------------------------------
@@ -433,7 +457,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     static_assert(PIECES % NP == 0 && (NW * NB) % NP == 0, "work must split evenly");
     const int p = wv - NW;
     auto issue = [&](int c, char* base, float* gl) __attribute__((always_inline)) {
-      const size_t cid = (size_t)bh * a.N + c;
+      const size_t cid = (size_t)bh * a.N + c0 + c;
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
       const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
 #pragma unroll
@@ -455,6 +479,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
       if (p == NP - 1 && lane < D / 4) lds_dma16(a.GL + cid * D + lane * 4, gl);
       // u^T[col][t] for compute wave w, row block it: lane (li, lg) of that
       // wave reads u^T[16 w + li][16 it + 4 lg .. +3] from sU[(w NB + it) 64 + lane]
+      if (mslice) return;  // M columns: u = 0
       const float* usrc = a.UT + cid * D * BT + (size_t)(vs * 16 * NW + li) * BT + 4 * lg;
 #pragma unroll
       for (int j = 0; j < NW * NB / NP; ++j) {
@@ -473,7 +498,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     constexpr int LTOT = 2 * LW + LU + LG;
     constexpr int NTP = ((LTOT + 63) / 64 + NP - 1) / NP;   // touch instructions per producer
     auto touch = [&](int c) __attribute__((always_inline)) {
-      const size_t cid = (size_t)bh * a.N + c;
+      const size_t cid = (size_t)bh * a.N + c0 + c;
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
       const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
       const char* usrc = reinterpret_cast<const char*>(a.UT + cid * D * BT + (size_t)vs * 16 * NW * BT);
@@ -489,9 +514,9 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
         lds_dma4(src, sJunk);
       }
     };
-    // In flight at the top of chunk c: issue(c), then touch(c+1) if c+1 < N.
+    // In flight at the top of chunk c: issue(c), then touch(c+1) if c+1 < n.
     auto wait_chunk = [&](int c) __attribute__((always_inline)) {
-      if (c + 1 < a.N) wait_vmcnt<NTP>();
+      if (c + 1 < n) wait_vmcnt<NTP>();
       else wait_vmcnt<0>();
     };
     // The producers' data ordering is the explicit vmcnt wait; a plain barrier
@@ -507,22 +532,22 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
           if (i * 64 + lane < D) gl[i * 64 + lane] = __expf(gl[i * 64 + lane]);
       }
     };
-    if (a.N > 0) issue(0, sbuf0, sGL0);
-    if (a.N > 1) touch(1);
-    for (int c = 0; c < a.N; c += 2) {
+    if (n > 0) issue(0, sbuf0, sGL0);
+    if (n > 1) touch(1);
+    for (int c = 0; c < n; c += 2) {
       wait_chunk(c);
       exp_gl(sGL0);
       barrier();  // A(c)
       barrier();  // B(c)
-      if (c + 1 < a.N) {
+      if (c + 1 < n) {
         issue(c + 1, sbuf1, sGL1);
-        if (c + 2 < a.N) touch(c + 2);
+        if (c + 2 < n) touch(c + 2);
         wait_chunk(c + 1);
         exp_gl(sGL1);
         barrier();  // A(c+1)
         barrier();  // B(c+1)
-        if (c + 2 < a.N) issue(c + 2, sbuf0, sGL0);
-        if (c + 3 < a.N) touch(c + 3);
+        if (c + 2 < n) issue(c + 2, sbuf0, sGL0);
+        if (c + 3 < n) touch(c + 3);
       }
     }
     return;
@@ -539,31 +564,44 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     return r * re + ((j ^ (r & m)) * EPC) + (e % EPC);
   };
 
+  // entry state: h0 (or 0) for a plain pass and for segment 0 of the summary
+  // pass, 0 for later segments of the summary pass, the identity for M slices,
+  // the combined entry state in the final segmented pass
   f32x4 h[NDT];
-  if (a.h0) {
+  const float* hsrc = (a.S > 1 && !a.summary) ? a.hin + ((size_t)unit) * D * D
+                    : (sg == 0 && !mslice && a.h0) ? a.h0 + (size_t)bh * D * D : nullptr;
+  if (mslice) {
+#pragma unroll
+    for (int at = 0; at < NDT; ++at)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) h[at][r] = (at * 16 + 4 * lg + r == col) ? 1.f : 0.f;
+  } else if (hsrc) {
 #pragma unroll
     for (int at = 0; at < NDT; ++at)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        h[at][r] = sanitize(a.h0[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col]);
+        h[at][r] = sanitize(hsrc[(size_t)(at * 16 + 4 * lg + r) * D + col]);
   } else {
 #pragma unroll
     for (int at = 0; at < NDT; ++at) h[at] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  const bool write_tiles = !a.summary;
 
   // One chunk: v_new = u - W h, h <- e^{gl} h + kg^T v_new, with chunk c in `cur`.
   auto step = [&](int c, const char* cur, const float* eglc) __attribute__((always_inline)) {
-    const size_t cid = (size_t)bh * a.N + c;
+    const size_t cid = (size_t)bh * a.N + c0 + c;
     __syncthreads();  // A(c)
     f32x4 vn[NB];
 #pragma unroll
-    for (int it = 0; it < NB; ++it) vn[it] = sU[(wv * NB + it) * 64 + lane];
+    for (int it = 0; it < NB; ++it)
+      vn[it] = mslice ? f32x4{0.f, 0.f, 0.f, 0.f} : sU[(wv * NB + it) * 64 + lane];
     __syncthreads();  // B(c)
     const T* sW = reinterpret_cast<const T*>(cur);
     const T* sK = reinterpret_cast<const T*>(cur + WBYTES);
 
     T* hT = a.HT + cid * D * D + (size_t)col * D;
-    if constexpr (F32) {
+    if (!write_tiles) {
+    } else if constexpr (F32) {
 #pragma unroll
       for (int at = 0; at < NDT; ++at) store4(hT + at * 16 + 4 * lg, h[at]);
     } else {
@@ -589,7 +627,8 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
       vn[it] -= acc;
     }
     T* vT = a.VnT + cid * D * BT + (size_t)col * BT;
-    if constexpr (F32) {
+    if (!write_tiles) {
+    } else if constexpr (F32) {
 #pragma unroll
       for (int it = 0; it < NB; ++it) store4(vT + it * 16 + 4 * lg, vn[it]);
     } else {
@@ -614,20 +653,87 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
           mma(h[at], op_load<T>(&sK[swz(r, p * 32 + 8 * lg, BT)]),
               op_from_c(vn[2 * p], vn[2 * p + 1], (Op*)nullptr));
       }
+      if (!mslice) {
 #pragma unroll
-      for (int r2 = 0; r2 < 4; ++r2) h[at][r2] = sanitize(h[at][r2]);
+        for (int r2 = 0; r2 < 4; ++r2) h[at][r2] = sanitize(h[at][r2]);
+      }
     }
   };
 
-  for (int c = 0; c < a.N; c += 2) {
+  for (int c = 0; c < n; c += 2) {
     step(c, sbuf0, sGL0);
-    if (c + 1 < a.N) step(c + 1, sbuf1, sGL1);
+    if (c + 1 < n) step(c + 1, sbuf1, sGL1);
   }
+  float* hout = a.summary ? a.seg + ((size_t)unit * 2 + (mslice ? 1 : 0)) * D * D
+              : (sg == a.S - 1) ? a.h_final + (size_t)bh * D * D : nullptr;
+  if (hout) {
 #pragma unroll
-  for (int at = 0; at < NDT; ++at)
+    for (int at = 0; at < NDT; ++at)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      a.h_final[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col] = h[at][r];
+      for (int r = 0; r < 4; ++r) hout[(size_t)(at * 16 + 4 * lg + r) * D + col] = h[at][r];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Segment entry states of a segmented state scan: hin_0 = h0 (or 0), hin_1 =
+// e_0 (segment 0's end state, computed from h0), hin_{s+1} = M_s hin_s + e_s
+// (e_s from h = 0), sanitized like every chunk state.  The columns of h are
+// independent: one workgroup per (b,h) and 16-column slice, serial over the
+// segments; wave w produces the row tiles w, w+4, ...  The slice of the current
+// state sits transposed in LDS as the chained operand of the next product.
+template <int D>
+__global__ void __launch_bounds__(256) seg_combine(const float* seg, const float* h0, float* hin,
+                                                   int S) {
+  constexpr int NDT = D / 16;
+  __shared__ __align__(16) float sHT[16 * (D + 4)];   // current state, [col][row]
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int bh = blockIdx.x / NDT, c0 = (blockIdx.x % NDT) * 16;
+  const size_t DD = (size_t)D * D;
+  const float* segb = seg + (size_t)bh * S * 2 * DD;   // [s][2][D][D]
+  float* hinb = hin + (size_t)bh * S * DD;             // [s][D][D]
+  // hin_0 and hin_1
+  for (int i = tid; i < D * 16; i += 256) {
+    const int r = i / 16, cc = i % 16;
+    const size_t o = (size_t)r * D + c0 + cc;
+    hinb[o] = h0 ? sanitize(h0[(size_t)bh * DD + o]) : 0.f;
+    const float e0 = segb[o];
+    hinb[DD + o] = e0;
+    sHT[cc * (D + 4) + r] = e0;
+  }
+  __syncthreads();
+  for (int s = 1; s + 1 < S; ++s) {
+    const float* M = segb + ((size_t)s * 2 + 1) * DD;
+    const float* e = segb + (size_t)s * 2 * DD;
+    f32x4 acc[(NDT + 3) / 4];
+#pragma unroll
+    for (int j = 0; j < (NDT + 3) / 4; ++j) {
+      const int at = wv + 4 * j;
+      acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (at < NDT) {
+#pragma unroll
+        for (int kt = 0; kt < NDT; ++kt)
+          mma(acc[j], load4f(M + (size_t)(at * 16 + li) * D + kt * 16 + 4 * lg),
+              load4f(&sHT[li * (D + 4) + kt * 16 + 4 * lg]));
+      }
+    }
+    __syncthreads();  // every wave has read the current state
+#pragma unroll
+    for (int j = 0; j < (NDT + 3) / 4; ++j) {
+      const int at = wv + 4 * j;
+      if (at < NDT) {
+        // acc[j] holds (M h)^T: lane (li, lg) has rows at*16 + 4lg + r of column li
+        f32x4 nh;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const size_t o = (size_t)(at * 16 + 4 * lg + r) * D + c0 + li;
+          nh[r] = sanitize(acc[j][r] + e[o]);
+          hinb[(size_t)(s + 1) * DD + o] = nh[r];
+        }
+        store4(&sHT[li * (D + 4) + at * 16 + 4 * lg], nh);
+      }
+    }
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -718,7 +824,8 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       float* a_dbg, int flags) {
   const int N = T_len / BT;
   const size_t NC = (size_t)B * H * N;
-  const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T));
+  const int S_ws = state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
+  const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), S_ws > 1 ? (size_t)B * H * S_ws : 0);
   T* W = reinterpret_cast<T*>(ws + L.W);
   float* UT = reinterpret_cast<float*>(ws + L.UT);
   T* KgT = reinterpret_cast<T*>(ws + L.KgT);
@@ -737,11 +844,28 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                        pa);
   }
   launch_mark(st);
-  StateArgs<T> sa{W, UT, KgT, GL, h0, N, HT, VnT, h_final};
   constexpr int SW = 2;  // compute waves (16 value columns each) per state workgroup
   constexpr int SP = 2;  // producer waves
-  hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3((size_t)B * H * (D / (16 * SW))),
-                     dim3(64 * (SW + SP)), 0, st, sa);
+  constexpr int NVS = D / (16 * SW);
+  const size_t BH = (size_t)B * H;
+  const int S = S_ws;
+  if (S > 1) {
+    const int Lseg = (N + S - 1) / S;
+    float* seg = reinterpret_cast<float*>(ws + L.SEG);          // [bh][S][2][D][D]
+    float* hin = seg + BH * S * 2 * (size_t)D * D;               // [bh][S][D][D]
+    StateArgs<T> sum{W, UT, KgT, GL, h0, N, S, Lseg, 1, nullptr, seg, HT, VnT, h_final};
+    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * S * 2 * NVS),
+                       dim3(64 * (SW + SP)), 0, st, sum);
+    hipLaunchKernelGGL((seg_combine<D>), dim3(BH * (D / 16)), dim3(256), 0, st, seg, h0, hin,
+                       S);
+    StateArgs<T> fin{W, UT, KgT, GL, h0, N, S, Lseg, 0, hin, nullptr, HT, VnT, h_final};
+    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * S * NVS), dim3(64 * (SW + SP)),
+                       0, st, fin);
+  } else {
+    StateArgs<T> sa{W, UT, KgT, GL, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT, h_final};
+    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * NVS), dim3(64 * (SW + SP)), 0,
+                       st, sa);
+  }
   launch_mark(st);
   if (NC > 0) {
     OutArgs<T> oa{Qg, Aqk, HT, VnT, T_len, H, N, scale, out};

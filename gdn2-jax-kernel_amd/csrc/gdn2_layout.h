@@ -30,12 +30,16 @@
 namespace gdn2 {
 
 struct FwdLayout {
-  size_t W, UT, KgT, Qg, Aqk, GL, HT, VnT, A, total;
+  size_t W, UT, KgT, Qg, Aqk, GL, HT, VnT, A, SEG, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem) {
+// SEG (only with a segmented state scan, S > 1): per (b,h) and segment the end
+// state from h = 0 and the transition M_seg ([bh][S][2][D][D] f32), then the
+// segment entry states ([bh][S][D][D] f32).  It comes last, so the offsets the
+// backward reads do not depend on S.
+inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem, size_t seg_units = 0) {
   FwdLayout L;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
@@ -48,8 +52,33 @@ inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem) {
   L.HT = take(nchunks * D * D * elem);
   L.VnT = take(nchunks * D * BT * elem);
   L.A = take(nchunks * BT * BT * 4);
+  L.SEG = take(seg_units * 3 * (size_t)D * D * 4);
   L.total = off;
   return L;
+}
+
+// Segments of the forward state scan for BH (b,h) pairs of N chunks.  Automatic
+// choice: as many as fill a 256-CU device in the final pass when the plain
+// pass's BH * D/32 workgroups cannot, each at least 16 chunks, and only when
+// that gives 4 or more (the segmented scan costs about 3/S of the serial
+// chain plus a small combine).  `forced` (1..255) overrides it.  The result is
+// adjusted so that no segment is empty.  Depends on shapes only, so the
+// workspace size is known without a device.
+inline int state_segments(long long BH, int N, int D, int forced) {
+  if (N <= 1) return 1;
+  long long s;
+  if (forced > 0) {
+    s = forced;
+  } else {
+    const long long slices = BH * (D / 32);
+    s = slices > 0 ? 256 / slices : 1;
+    if (s > N / 16) s = N / 16;
+    if (s < 4) s = 1;
+  }
+  if (s > N) s = N;
+  if (s < 1) s = 1;
+  const long long len = (N + s - 1) / s;
+  return (int)((N + len - 1) / (len > 0 ? len : 1));
 }
 
 }  // namespace gdn2

@@ -20,6 +20,11 @@ GDN2_F32 = 0
 GDN2_BF16 = 1
 FWD_SAVE_A = 1
 
+
+def FWD_SEGMENTS(n: int) -> int:
+    """gdn2_fwd flag forcing n segments of the state scan (include/gdn2.h)."""
+    return (int(n) & 0xFF) << 8
+
 OK = 0
 ERR_HEAD_DIM = -1
 ERR_SEQ_LEN = -2
@@ -39,6 +44,7 @@ SIGNATURES = {
     "gdn2_strerror": (ctypes.c_char_p, [_c_int]),
     "gdn2_validate": (_c_int, [_c_int] * 7),
     "gdn2_fwd_workspace_bytes": (_c_size, [_c_int] * 6),
+    "gdn2_fwd_workspace_bytes_ex": (_c_size, [_c_int] * 7),
     "gdn2_bwd_workspace_bytes": (_c_size, [_c_int] * 6),
     "gdn2_fwd": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7
                  + [_c_float, _vp, _vp, _vp, _c_size, _c_int]),

@@ -110,8 +110,10 @@ class _Prepared:
 
 
 def _run_forward(p: _Prepared, debug_a: bool = False, flags: int = 0):
+    """One gdn2_fwd call; `flags` as in include/gdn2.h (GDN2_FWD_SAVE_A,
+    GDN2_FWD_SEGMENTS(n)).  The debug path ignores flags."""
     L = _lib.lib()
-    nbytes = L.gdn2_fwd_workspace_bytes(*p.args[:6])
+    nbytes = L.gdn2_fwd_workspace_bytes_ex(*p.args[:6], 0 if debug_a else flags)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=p.device)
     out = torch.empty((p.B, p.T, p.H, p.D), dtype=torch.float32, device=p.device)
     h_final = torch.empty((p.B, p.H, p.D, p.D), dtype=torch.float32, device=p.device)

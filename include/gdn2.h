@@ -65,6 +65,16 @@ size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
 
 /* gdn2_fwd flags. */
 #define GDN2_FWD_SAVE_A 1  /* also keep A = (I + Akk)^{-1} in ws, needed by gdn2_bwd */
+/* Segments of the state scan (bits 8-15; 0 = automatic).  Long sequences with
+ * few (b,h) pairs split the serial chunk recurrence into S segments scanned in
+ * parallel and chained by their affine transitions (the sequence-parallel
+ * design of the reference's kernel D, gdn2_fwd.py:338-366).  n is clamped to
+ * [1, T/BT]; a forced count needs gdn2_fwd_workspace_bytes_ex's workspace. */
+#define GDN2_FWD_SEGMENTS(n) (((n) & 0xff) << 8)
+
+/* As gdn2_fwd_workspace_bytes, for the segment count `flags` selects.  No
+ * counterpart in the reference (its scan is serial); used to force a count. */
+size_t gdn2_fwd_workspace_bytes_ex(int B, int T, int H, int D, int BT, int in_dtype, int flags);
 
 /* Forward: replaces gdn2_pallas_forward (gdn2_fwd.py:400-424), kernels A-D.
  * h0 may be NULL (zero initial state, gdn2_fwd.py:403-404).  out (B,T,H,D)

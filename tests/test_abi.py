@@ -117,3 +117,30 @@ def test_launch_events_hook_is_host_only():
     # a rejected call consumes the request without touching the events
     assert _fwd(L, (1, 512, 2, 96, 64, F32, F32), [0] * 6) == _lib.ERR_HEAD_DIM
     assert L.gdn2_set_launch_events(None, 0) == 0
+
+
+def test_segment_workspace():
+    """Forward workspace with a segmented state scan: S segments add
+    B*H*S*3*D*D floats (end states, transitions, entry states) after the
+    per-chunk tensors.  The automatic choice uses S = 8 for config 5
+    (1 x 131072 x 8 heads, D = 128: 32 plain-pass workgroups) and none for the
+    headline shape."""
+    L = _lib.lib()
+    al = lambda x: (x + 255) // 256 * 256
+    plain = L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 128, BF16, _lib.FWD_SEGMENTS(1))
+    assert L.gdn2_fwd_workspace_bytes(1, 131072, 8, 128, 128, BF16) == \
+        plain + al(8 * 8 * 3 * 128 * 128 * 4)
+    assert L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 128, BF16, _lib.FWD_SEGMENTS(3)) == \
+        plain + al(8 * 3 * 3 * 128 * 128 * 4)
+    head = L.gdn2_fwd_workspace_bytes(8, 8192, 6, 128, 128, BF16)
+    assert head == L.gdn2_fwd_workspace_bytes_ex(8, 8192, 6, 128, 128, BF16, _lib.FWD_SEGMENTS(1))
+    # a count above the chunk count is clamped; uneven splits leave no empty segment
+    assert L.gdn2_fwd_workspace_bytes_ex(1, 640, 1, 64, 64, F32, _lib.FWD_SEGMENTS(200)) == \
+        L.gdn2_fwd_workspace_bytes_ex(1, 640, 1, 64, 64, F32, _lib.FWD_SEGMENTS(10))
+    base = L.gdn2_fwd_workspace_bytes_ex(1, 640, 1, 64, 64, F32, _lib.FWD_SEGMENTS(1))
+    # N = 10, asked for 4: segments of 3 -> 4 segments (3, 3, 3, 1)
+    assert L.gdn2_fwd_workspace_bytes_ex(1, 640, 1, 64, 64, F32, _lib.FWD_SEGMENTS(4)) == \
+        base + al(4 * 3 * 64 * 64 * 4)
+    # N = 10, asked for 6: segments of 2 -> 5 segments
+    assert L.gdn2_fwd_workspace_bytes_ex(1, 640, 1, 64, 64, F32, _lib.FWD_SEGMENTS(6)) == \
+        base + al(5 * 3 * 64 * 64 * 4)

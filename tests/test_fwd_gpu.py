@@ -238,3 +238,55 @@ def test_deterministic_and_noncontiguous(dev):
 def test_shape_errors_on_device(dev):
     with pytest.raises(AssertionError):
         gp().gdn2_pallas_forward(*[torch.zeros((1, 100, 2, 64), device=dev)] * 6, 0.1)
+
+
+# ----------------------------------------------------------------------------- segments
+@pytest.mark.parametrize("B,T,H,D,dtype,BT,S,h0", [
+    (1, 2048, 2, 64, torch.float32, 64, 4, False),     # N=32: 4 x 8 chunks
+    (1, 2048, 2, 64, torch.float32, 64, 3, True),      # uneven: 11 + 11 + 10
+    (2, 1280, 1, 128, torch.float32, 64, 7, True),     # N=20: 3 x 6 + 2
+    (1, 4096, 2, 128, torch.bfloat16, 128, 8, True),   # N=32: 8 x 4
+    (1, 2560, 2, 64, torch.bfloat16, 128, 5, False),   # N=20: 5 x 4
+])
+def test_segmented_scan_matches_serial_and_oracle(dev, B, T, H, D, dtype, BT, S, h0):
+    """The state scan split into S segments (summary pass, affine combine, final
+    pass) reproduces the serial pass and the recurrence."""
+    from gdn2_package import _lib
+    from gdn2_package.gdn2_fwd import _Prepared, _run_forward
+    xs = O.make_inputs(B, T, H, D, seed=T + S)
+    h0n = (0.1 * np.random.default_rng(S).standard_normal((B, H, D, D))).astype(np.float32) \
+        if h0 else None
+    xt = to_dev(xs, dev, dtype)
+    h0t = None if h0n is None else torch.tensor(h0n, device=dev)
+    p = _Prepared(*xt, D ** -0.5, h0t, BT)
+    out_s, hf_s, _, _ = _run_forward(p, flags=_lib.FWD_SEGMENTS(S))
+    out_1, hf_1, _, _ = _run_forward(p, flags=_lib.FWD_SEGMENTS(1))
+    # same arithmetic up to the order of the boundary-state products
+    ok_o, e_o = close(out_s.cpu().numpy(), out_1.cpu().numpy(), 1e-5 if dtype == torch.float32 else 2e-3)
+    ok_h, e_h = close(hf_s.cpu().numpy(), hf_1.cpu().numpy(), 1e-5 if dtype == torch.float32 else 2e-3)
+    assert ok_o and ok_h, ("vs serial", e_o, e_h)
+    ro, rh = O.recurrent_fwd(*host(xt), D ** -0.5, h0=h0n)
+    ok_o, e_o = close(out_s.cpu().numpy(), ro, TOL[dtype])
+    ok_h, e_h = close(hf_s.cpu().numpy(), rh, TOL[dtype])
+    assert ok_o and ok_h, ("vs oracle", e_o, e_h)
+
+
+def test_segmented_scan_is_automatic_for_long_few_heads(dev):
+    """One head of 128 chunks picks S = 8 by itself; it matches the forced
+    serial pass and the recurrence."""
+    from gdn2_package import _lib
+    from gdn2_package.gdn2_fwd import _Prepared, _run_forward
+    B, T, H, D = 1, 16384, 1, 128
+    L = _lib.lib()
+    assert L.gdn2_fwd_workspace_bytes(B, T, H, D, 128, _lib.GDN2_BF16) > \
+        L.gdn2_fwd_workspace_bytes_ex(B, T, H, D, 128, _lib.GDN2_BF16, _lib.FWD_SEGMENTS(1))
+    xs = O.make_inputs(B, T, H, D, seed=11, g_scale=0.1)
+    xt = to_dev(xs, dev, torch.bfloat16)
+    out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5, chunk_size=128)
+    out_1, hf_1, _, _ = _run_forward(_Prepared(*xt, D ** -0.5, None, 128),
+                                     flags=_lib.FWD_SEGMENTS(1))
+    assert (out - out_1).abs().max().item() < 2e-3 and (hf - hf_1).abs().max().item() < 2e-3
+    ro, rh = O.recurrent_fwd(*host(xt), D ** -0.5)
+    ok_o, e_o = close(out.cpu().numpy(), ro, 2e-2)
+    ok_h, e_h = close(hf.cpu().numpy(), rh, 2e-2)
+    assert ok_o and ok_h, (e_o, e_h)
