@@ -17,6 +17,8 @@ Results do not depend on the chunk size beyond rounding.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _lib
@@ -31,6 +33,31 @@ MB = 16
 CLIP = 1e4
 
 _SUPPORTED_IN = (torch.float32, torch.bfloat16)
+
+# Stage diagnostics, switched on by the environment at import as in the
+# reference (gdn2_fwd.py:36-38): with GDN2_FWD_DIAG=1 the forward keeps the
+# per-kernel outputs and reports non-finite or suspiciously large values.
+_GDN2_FWD_DIAG = os.environ.get("GDN2_FWD_DIAG", "0") == "1"
+_LARGE_THRESHOLD = 1e6
+
+
+def _stage_diag(tag: str, x: torch.Tensor) -> torch.Tensor:
+    """gdn2_fwd.py:47-76: report non-finite entries (count, largest finite
+    magnitude) or, when all are finite, a largest magnitude above 1e6.
+    Returns x unchanged."""
+    if not _GDN2_FWD_DIAG:
+        return x
+    finite = torch.isfinite(x)
+    n_bad = int((~finite).sum().item())
+    max_abs = float(torch.where(finite, x, torch.zeros_like(x)).abs().max().item()) \
+        if x.numel() else 0.0
+    if n_bad:
+        print(f"[GDN2-FWD-DIAG] non-finite at output {tag}: n_nonfinite={n_bad}  "
+              f"max_abs(finite part)={max_abs:.3e}", flush=True)
+    elif max_abs > _LARGE_THRESHOLD:
+        print(f"[GDN2-FWD-DIAG] suspiciously large value at output {tag} (still finite, "
+              f"possibly a precursor): max_abs={max_abs:.3e}", flush=True)
+    return x
 
 
 class GDN2Error(RuntimeError):
@@ -135,10 +162,17 @@ def _run_forward(p: _Prepared, debug_a: bool = False, flags: int = 0):
 def gdn2_pallas_forward(q, k, v, w, b, g, scale, h0=None, debug_tag="", chunk_size=None):
     """Forward A->B->C->D (gdn2_fwd.py:400-424) on the gfx950 library.
 
-    ``debug_tag`` is accepted for signature compatibility (the reference uses
-    it only in GDN2_FWD_DIAG prints, gdn2_fwd.py:47-76).
+    ``debug_tag`` prefixes the GDN2_FWD_DIAG stage reports (gdn2_fwd.py:47-76,
+    406-419); without GDN2_FWD_DIAG=1 it is unused.
     """
     p = _Prepared(q, k, v, w, b, g, scale, h0, chunk_size)
+    if _GDN2_FWD_DIAG:
+        out, h_final, res = _forward_with_residuals(p)
+        for name, key in (("kernel_A_Aqk", "Aqk"), ("kernel_A_Akk", "Akk"),
+                          ("kernel_B_wy_inverse_A", "A"), ("kernel_C_w_pseudo", "w_pseudo"),
+                          ("kernel_C_u", "u"), ("kernel_C_kg", "kg"), ("kernel_C_qg", "qg")):
+            _stage_diag(f"{debug_tag}:{name}", res[key])
+        return out, h_final
     out, h_final, _, _ = _run_forward(p)
     return out, h_final
 
@@ -194,6 +228,10 @@ def gdn2_pallas_forward_with_residuals(q, k, v, w, b, g, scale, h0=None, debug_t
     strict_tril(A^{-1}) for inspection.
     """
     p = _Prepared(q, k, v, w, b, g, scale, h0, chunk_size)
+    return _forward_with_residuals(p)
+
+
+def _forward_with_residuals(p: _Prepared):
     out, h_final, ws, a_out = _run_forward(p, debug_a=True)
     res = _residual_views(p, ws)
     res["A"] = a_out

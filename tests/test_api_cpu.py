@@ -84,3 +84,27 @@ def test_chained_column_order(n):
     for lg in range(4):
         ks = [4 * lg + r for r in range(4)] + [16 + 4 * lg + r for r in range(4)]
         assert sorted(got[k] for k in ks) == list(range(8 * lg, 8 * lg + 8))
+
+
+def test_stage_diag_reports(monkeypatch, capsys):
+    """GDN2_FWD_DIAG stage checks (gdn2_fwd.py:47-76): non-finite entries are
+    counted with the largest finite magnitude; finite values above 1e6 are
+    flagged; anything else, or the switch off, prints nothing.  The tensor
+    always comes back unchanged."""
+    from gdn2_package import gdn2_fwd as F
+    bad = torch.tensor([1.0, float("nan"), -3.0, float("inf")])
+    big = torch.tensor([[2e6, -1.0]])
+    ok = torch.tensor([1.0, -5e5])
+    monkeypatch.setattr(F, "_GDN2_FWD_DIAG", False)
+    assert F._stage_diag("t:off", bad) is bad
+    assert capsys.readouterr().out == ""
+    monkeypatch.setattr(F, "_GDN2_FWD_DIAG", True)
+    assert F._stage_diag("t:kernel_A_Aqk", bad) is bad
+    out = capsys.readouterr().out
+    assert "[GDN2-FWD-DIAG]" in out and "t:kernel_A_Aqk" in out
+    assert "n_nonfinite=2" in out and "3.000e+00" in out
+    F._stage_diag("t:kernel_C_u", big)
+    out = capsys.readouterr().out
+    assert "t:kernel_C_u" in out and "2.000e+06" in out and "non-finite" not in out
+    F._stage_diag("t:kernel_C_qg", ok)
+    assert capsys.readouterr().out == ""

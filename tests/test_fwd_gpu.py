@@ -290,3 +290,17 @@ def test_segmented_scan_is_automatic_for_long_few_heads(dev):
     ok_o, e_o = close(out.cpu().numpy(), ro, 2e-2)
     ok_h, e_h = close(hf.cpu().numpy(), rh, 2e-2)
     assert ok_o and ok_h, (e_o, e_h)
+
+
+def test_stage_diagnostics_path(dev, monkeypatch, capsys):
+    """With GDN2_FWD_DIAG on, the forward checks every kernel stage's output
+    (gdn2_fwd.py:406-419) and returns the same result; ordinary inputs report
+    nothing."""
+    from gdn2_package import gdn2_fwd as F
+    xs = O.make_inputs(1, 256, 2, 64, seed=3)
+    xt = to_dev(xs, dev, torch.float32)
+    o0, h0 = gp().gdn2_pallas_forward(*xt, 0.125, chunk_size=64)
+    monkeypatch.setattr(F, "_GDN2_FWD_DIAG", True)
+    o1, h1 = gp().gdn2_pallas_forward(*xt, 0.125, debug_tag="t", chunk_size=64)
+    assert torch.equal(o0, o1) and torch.equal(h0, h1)
+    assert capsys.readouterr().out == ""
