@@ -43,9 +43,8 @@ struct GemmArgs {
   GMat A, B;
   GOut C;
   int M, N, K, H, Nc;
+  int nsplit;   // workgroups per chunk, each taking N / nsplit output columns
 };
-
-constexpr int GLD = 128 + 4;
 
 __device__ __forceinline__ void load4_any(const void* p, int bf16, size_t idx, float* v) {
   if (bf16) {
@@ -57,66 +56,91 @@ __device__ __forceinline__ void load4_any(const void* p, int bf16, size_t idx, f
   }
 }
 
-// dst (pitch GLD) <- stored matrix (R x Cc): dst[r][c] = S[r][c], or dst[c][r] when
-// `transposed`.  Four rows of work are loaded before any is stored.
-__device__ __forceinline__ void stage(float* dst, const GMat& m, size_t off, int R, int Cc,
-                                      bool transposed, int tid) {
+// Staging of one operand: the stored matrix (R x Cc, R*Cc <= 128*128) as float4
+// runs, all loads issued before any LDS store (one memory round trip per chunk).
+// dst (pitch ld) <- S: dst[r][c] = S[r][c], or dst[c][r] when `transposed`.
+// (r0, c0) place the tile in the stored matrix for the masks.
+struct Staged {
+  float v[16][4];
+};
+__device__ __forceinline__ void stage_load(Staged& s, const GMat& m, size_t off, int R, int Cc,
+                                           int tid) {
   const int cq = Cc >> 2, total = R * cq;
-  for (int base = 0; base < total; base += 1024) {
-    float v[4][4];
-    int rr[4], cc[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = base + tid + 256 * u;
-      rr[u] = -1;
-      if (i < total) {
-        rr[u] = i / cq;
-        cc[u] = (i - rr[u] * cq) * 4;
-        const int sc = m.chained ? kpos<bf16_t>(cc[u]) : cc[u];
-        load4_any(m.p, m.bf16, off + (size_t)rr[u] * m.ld + sc, v[u]);
-      }
+  for (int u = 0; u < 16; ++u) {
+    const int i = tid + 256 * u;
+    if (i < total) {
+      const int r = i / cq, c = (i - r * cq) * 4;
+      const int sc = m.chained ? kpos<bf16_t>(c) : c;
+      load4_any(m.p, m.bf16, off + (size_t)r * m.ld + sc, s.v[u]);
     }
+  }
+}
+__device__ __forceinline__ void stage_store(float* dst, int ld, const Staged& s, const GMat& m,
+                                            int R, int Cc, int r0, int c0, bool transposed,
+                                            int tid) {
+  const int cq = Cc >> 2, total = R * cq;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (rr[u] < 0) continue;
-      const int r = rr[u], c = cc[u];
+  for (int u = 0; u < 16; ++u) {
+    const int i = tid + 256 * u;
+    if (i < total) {
+      const int r = i / cq, c = (i - r * cq) * 4;
+      float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        if ((m.mask == 1 && c + e > r) || (m.mask == 2 && c + e >= r)) v[u][e] = 0.f;
+        v[e] = s.v[u][e];
+        const int gr = r0 + r, gc = c0 + c + e;
+        if ((m.mask == 1 && gc > gr) || (m.mask == 2 && gc >= gr)) v[e] = 0.f;
       }
       if (!transposed) {
-        *reinterpret_cast<f32x4*>(&dst[r * GLD + c]) = f32x4{v[u][0], v[u][1], v[u][2], v[u][3]};
+        *reinterpret_cast<f32x4*>(&dst[r * ld + c]) = f32x4{v[0], v[1], v[2], v[3]};
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(c + e) * GLD + r] = v[u][e];
+        for (int e = 0; e < 4; ++e) dst[(c + e) * ld + r] = v[e];
       }
     }
   }
 }
 
+// C[m][n] = alpha * sum_k A(m,k) B(n,k) (+ C) for one chunk, fp32 MFMA.  Both
+// operands are staged as [row][k] with pitch K+4 in dynamic LDS sized to the
+// shape ((M + N/nsplit) (K+4) floats, two or more workgroups per CU for
+// every product of the backward); products with N = 128 against K = 128 are
+// split over two workgroups per chunk.
 __global__ void __launch_bounds__(256) chunk_gemm(GemmArgs a) {
-  __shared__ __align__(16) float sX[128 * GLD];  // A as [m][k]
-  __shared__ __align__(16) float sY[128 * GLD];  // B as [n][k]
+  extern __shared__ __align__(16) float smem[];
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  const int cid = blockIdx.x;
+  const int M = a.M, K = a.K, Nw = a.N / a.nsplit, ld = K + 4;
+  const int ns = blockIdx.x % a.nsplit, cid = blockIdx.x / a.nsplit, n0 = ns * Nw;
+  float* sX = smem;            // A as [m][k]
+  float* sY = smem + M * ld;   // B rows n0 .. n0 + Nw as [n][k]
   const int c = cid % a.Nc, bh = cid / a.Nc, hh = bh % a.H, bb = bh / a.H;
   const size_t offA = bb * a.A.sb + hh * a.A.sh + c * a.A.sc;
-  const size_t offB = bb * a.B.sb + hh * a.B.sh + c * a.B.sc;
+  // B stored [n][k] (trans) or [k][n]: start at row / column n0
+  const size_t offB = bb * a.B.sb + hh * a.B.sh + c * a.B.sc +
+                      (a.B.trans ? (size_t)n0 * a.B.ld : (size_t)n0);
   const size_t offC = bb * a.C.sb + hh * a.C.sh + c * a.C.sc;
-  const int M = a.M, N = a.N, K = a.K;
-  stage(sX, a.A, offA, a.A.trans ? K : M, a.A.trans ? M : K, a.A.trans != 0, tid);
-  stage(sY, a.B, offB, a.B.trans ? N : K, a.B.trans ? K : N, a.B.trans == 0, tid);
+  {
+    Staged ra, rb;
+    stage_load(ra, a.A, offA, a.A.trans ? K : M, a.A.trans ? M : K, tid);
+    stage_load(rb, a.B, offB, a.B.trans ? Nw : K, a.B.trans ? K : Nw, tid);
+    stage_store(sX, ld, ra, a.A, a.A.trans ? K : M, a.A.trans ? M : K, 0, 0, a.A.trans != 0,
+                tid);
+    stage_store(sY, ld, rb, a.B, a.B.trans ? Nw : K, a.B.trans ? K : Nw, a.B.trans ? n0 : 0,
+                a.B.trans ? 0 : n0, a.B.trans == 0, tid);
+  }
   __syncthreads();
-  const int tn = N >> 4, ntile = (M >> 4) * tn, nk = K >> 4;
+  const int tn = Nw >> 4, ntile = (M >> 4) * tn, nk = K >> 4;
   for (int t = wv; t < ntile; t += 4) {
     const int mt = t / tn, nt = t - mt * tn;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
     for (int kg = 0; kg < nk; ++kg)
-      mma(acc, load4f(&sX[(mt * 16 + li) * GLD + kg * 16 + 4 * lg]),
-          load4f(&sY[(nt * 16 + li) * GLD + kg * 16 + 4 * lg]));
+      mma(acc, load4f(&sX[(mt * 16 + li) * ld + kg * 16 + 4 * lg]),
+          load4f(&sY[(nt * 16 + li) * ld + kg * 16 + 4 * lg]));
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = mt * 16 + 4 * lg + r, n = nt * 16 + li;
+      const int m = mt * 16 + 4 * lg + r, n = n0 + nt * 16 + li;
       float val = a.C.alpha * acc[r];
       if ((a.C.mask == 1 && n > m) || (a.C.mask == 2 && n >= m)) val = 0.f;
       float* dst = a.C.p + offC + (a.C.trans ? (size_t)n * a.C.ld + m : (size_t)m * a.C.ld + n);
@@ -557,8 +581,10 @@ GOut ch_out(float* p, const Dims& d, int R, int C, float alpha = 1.f, int trans 
               alpha, accum};
 }
 void gemm(hipStream_t st, const Dims& d, GMat A, GMat B, GOut C, int M, int N, int K) {
-  GemmArgs ga{A, B, C, M, N, K, d.H, d.N};
-  hipLaunchKernelGGL(chunk_gemm, dim3((size_t)d.B * d.H * d.N), dim3(256), 0, st, ga);
+  const int nsplit = (N == 128 && K == 128) ? 2 : 1;
+  GemmArgs ga{A, B, C, M, N, K, d.H, d.N, nsplit};
+  const size_t lds = (size_t)(M + N / nsplit) * (K + 4) * sizeof(float);
+  hipLaunchKernelGGL(chunk_gemm, dim3((size_t)d.B * d.H * d.N * nsplit), dim3(256), lds, st, ga);
   launch_mark(st);
 }
 }  // namespace
