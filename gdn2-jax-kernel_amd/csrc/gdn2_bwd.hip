@@ -151,7 +151,7 @@ __global__ void __launch_bounds__(256) chunk_gemm(GemmArgs a) {
 }
 
 // ============================================================================
-// bwd_state (B1): reverse scan over chunks; workgroup = (b,h, 64 value columns).
+// bwd_state (B1): reverse scan over chunks; workgroup = (b,h, 32 value columns of dh).
 // ============================================================================
 template <typename T>
 struct BStateArgs {
@@ -167,74 +167,218 @@ struct BStateArgs {
   float* dh0;        // (B,H,D,D)
 };
 
-// dst[r][c] (pitch ld, f32) <- R x C tile of type T at src (pitch C), all loads first.
-// bfloat16 tiles (forward residuals W, kg^T) are stored in chained column order.
-template <typename T, int R, int C, int ld>
-__device__ __forceinline__ void stage_tile(float* dst, const T* src, int tid) {
-  constexpr int Q = R * C / 4, PER = Q / 256;
-  static_assert(Q % 256 == 0, "tile must split evenly over 256 threads");
-  float v[PER][4];
-#pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    const int i = tid + 256 * u;
-    load_f<4>(src + (size_t)(i / (C / 4)) * C + kpos<T>((i % (C / 4)) * 4), v[u]);
-  }
-#pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    const int i = tid + 256 * u;
-    *reinterpret_cast<f32x4*>(&dst[(i / (C / 4)) * ld + (i % (C / 4)) * 4]) =
-        f32x4{v[u][0], v[u][1], v[u][2], v[u][3]};
-  }
-}
+// One workgroup = one (b,h) and 16*NW value columns of dh: NW compute waves (16
+// columns each, dh in MFMA accumulators) and NP producer waves, scanning the
+// chunks in reverse.  Per chunk (gdn2_bwd.py:45-80):
+//   dv_new = dvp + kg dh,   dh <- e^{g_last} dh + scale qg^T do - W^T dv_new.
+// As in fwd_state, the producers stream the next chunk (W, kg^T, g_last) into the
+// other half of an LDS double buffer with global_load_lds_dwordx4 and gather the
+// workgroup's dvp and qg^T do rows into the compute lanes' order (one buffer,
+// freed by barrier B once copied to registers); the compute waves issue no
+// global loads.  Both products read their tile transposed: one 4-byte (2-byte
+// for bfloat16 residuals, chained column order) LDS read per element, which
+// the XOR swizzle of the 16-byte chunks keeps free of bank conflicts.
+template <typename T, int BT, int D, int NW, int NP>
+__global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
+  constexpr int NB = BT / 16, NDT = D / 16;
+  constexpr int NVS = D / (16 * NW);
+  constexpr int WBYTES = BT * D * (int)sizeof(T);
+  constexpr int BUF = 2 * WBYTES;
+  constexpr int PIECES = BUF / 1024;
+  static_assert(BUF % 1024 == 0, "tiles must split into 1 KB pieces");
+  __shared__ __align__(16) char sbuf0[BUF];
+  __shared__ __align__(16) char sbuf1[BUF];
+  __shared__ __align__(16) f32x4 sDV[NW * NB * 64];    // dvp^T in compute-lane order
+  __shared__ __align__(16) f32x4 sQD[NW * NDT * 64];   // (scale qg^T do)^T, same
+  __shared__ __align__(16) float sGL0[D];
+  __shared__ __align__(16) float sGL1[D];
+  __shared__ __align__(16) float sJunk[64];
 
-template <typename T, int BT, int D>
-__global__ void __launch_bounds__(256) bwd_state(BStateArgs<T> a) {
-  constexpr int NB = BT / 16, NDT = D / 16, NVS = D / 64;
-  constexpr int W_LD = D + 4, K_LD = BT + 4;
-  __shared__ __align__(16) float sW[BT * W_LD];
-  __shared__ __align__(16) float sK[D * K_LD];
-  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  const int bh = blockIdx.x / NVS, vs = blockIdx.x % NVS;
-  const int col = vs * 64 + wv * 16 + li;
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int bh, vs;
+  {
+    const int nwg = gridDim.x, id = blockIdx.x;
+    const int per_xcd = nwg / 8;
+    if (nwg % 8 == 0 && per_xcd % NVS == 0) {
+      const int xcd = id % 8, slot = id / 8;
+      bh = xcd * (per_xcd / NVS) + slot / NVS;
+      vs = slot % NVS;
+    } else {
+      bh = id / NVS;
+      vs = id % NVS;
+    }
+  }
+  const int n = a.N;
+  // step i works on chunk n-1-i
+  auto chunk_id = [&](int i) { return (size_t)bh * a.N + (a.N - 1 - i); };
+
+  if (wv >= NW) {
+    // ---- producers ----------------------------------------------------------
+    constexpr int ROWB_W = D * (int)sizeof(T), ROWB_K = BT * (int)sizeof(T);
+    constexpr int WPIECES = WBYTES / 1024;
+    constexpr int PP = PIECES / NP;
+    static_assert(PIECES % NP == 0 && (NW * NB) % NP == 0 && (NW * NDT) % NP == 0,
+                  "work must split evenly");
+    const int p = wv - NW;
+    auto issue = [&](int i, char* base, float* gl) __attribute__((always_inline)) {
+      const size_t cid = chunk_id(i);
+      const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
+      const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
+#pragma unroll
+      for (int j = 0; j < PP; ++j) {
+        const int piece = p * PP + j;
+        char* dst = base + piece * 1024;
+        if (piece < WPIECES) {
+          const int ib = piece * 1024 + lane * 16;
+          const int r = ib / ROWB_W, pch = (ib % ROWB_W) / 16;
+          constexpr int NCH = ROWB_W / 16, M = (NCH < 16 ? NCH : 16) - 1;
+          lds_dma16(wsrc + (size_t)r * ROWB_W + ((pch ^ (r & M)) * 16), dst);
+        } else {
+          const int ib = (piece - WPIECES) * 1024 + lane * 16;
+          const int r = ib / ROWB_K, pch = (ib % ROWB_K) / 16;
+          constexpr int NCH = ROWB_K / 16, M = (NCH < 16 ? NCH : 16) - 1;
+          lds_dma16(ksrc + (size_t)r * ROWB_K + ((pch ^ (r & M)) * 16), dst);
+        }
+      }
+      if (p == NP - 1 && lane < D / 4) lds_dma16(a.GL + cid * D + lane * 4, gl);
+      // dvp^T[col][t]: compute wave w, row block it -> sDV[(w NB + it) 64 + lane]
+      const float* dsrc = a.DVPT + cid * D * BT + (size_t)(vs * 16 * NW + li) * BT + 4 * lg;
+#pragma unroll
+      for (int j = 0; j < NW * NB / NP; ++j) {
+        const int q = j * NP + p, w = q / NB, it = q % NB;
+        lds_dma16(dsrc + (size_t)w * 16 * BT + it * 16, &sDV[q * 64]);
+      }
+      // (scale qg^T do)^T[col][d]: wave w, tile at -> sQD[(w NDT + at) 64 + lane]
+      const float* qsrc = a.QDOT + cid * D * D + (size_t)(vs * 16 * NW + li) * D + 4 * lg;
+#pragma unroll
+      for (int j = 0; j < NW * NDT / NP; ++j) {
+        const int q = j * NP + p, w = q / NDT, at = q % NDT;
+        lds_dma16(qsrc + (size_t)w * 16 * D + at * 16, &sQD[q * 64]);
+      }
+    };
+    constexpr int LINE = 128;
+    constexpr int LW = WBYTES / LINE;
+    constexpr int LDV = 16 * NW * (BT * 4 / LINE);
+    constexpr int LQD = 16 * NW * (D * 4 / LINE);
+    constexpr int LG = (D * 4 + LINE - 1) / LINE;
+    constexpr int LTOT = 2 * LW + LDV + LQD + LG;
+    constexpr int NTP = ((LTOT + 63) / 64 + NP - 1) / NP;
+    auto touch = [&](int i) __attribute__((always_inline)) {
+      const size_t cid = chunk_id(i);
+      const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
+      const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
+      const char* dsrc =
+          reinterpret_cast<const char*>(a.DVPT + cid * D * BT + (size_t)vs * 16 * NW * BT);
+      const char* qsrc =
+          reinterpret_cast<const char*>(a.QDOT + cid * D * D + (size_t)vs * 16 * NW * D);
+      const char* gsrc = reinterpret_cast<const char*>(a.GL + cid * D);
+#pragma unroll
+      for (int j = 0; j < NTP; ++j) {
+        int l = (j * NP + p) * 64 + lane;
+        l = l < LTOT ? l : LTOT - 1;
+        const char* src = l < LW ? wsrc + l * LINE
+                        : l < 2 * LW ? ksrc + (l - LW) * LINE
+                        : l < 2 * LW + LDV ? dsrc + (l - 2 * LW) * LINE
+                        : l < 2 * LW + LDV + LQD ? qsrc + (l - 2 * LW - LDV) * LINE
+                        : gsrc + (l - 2 * LW - LDV - LQD) * LINE;
+        lds_dma4(src, sJunk);
+      }
+    };
+    auto wait_step = [&](int i) __attribute__((always_inline)) {
+      if (i + 1 < n) wait_vmcnt<NTP>();
+      else wait_vmcnt<0>();
+    };
+    auto barrier = []() __attribute__((always_inline)) {
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    auto exp_gl = [&](float* gl) __attribute__((always_inline)) {
+      if (p == NP - 1) {
+#pragma unroll
+        for (int j = 0; j < (D + 63) / 64; ++j)
+          if (j * 64 + lane < D) gl[j * 64 + lane] = __expf(gl[j * 64 + lane]);
+      }
+    };
+    // The dvp / qdot buffer is single: the next chunk's gather goes out after B.
+    if (n > 0) issue(0, sbuf0, sGL0);
+    if (n > 1) touch(1);
+    for (int i = 0; i < n; i += 2) {
+      wait_step(i);
+      exp_gl(sGL0);
+      barrier();  // A(i)
+      barrier();  // B(i)
+      if (i + 1 < n) {
+        issue(i + 1, sbuf1, sGL1);
+        if (i + 2 < n) touch(i + 2);
+        wait_step(i + 1);
+        exp_gl(sGL1);
+        barrier();  // A(i+1)
+        barrier();  // B(i+1)
+        if (i + 2 < n) issue(i + 2, sbuf0, sGL0);
+        if (i + 3 < n) touch(i + 3);
+      }
+    }
+    return;
+  }
+
+  // ---- compute waves ----------------------------------------------------------
+  const int col = vs * 16 * NW + wv * 16 + li;
+  // element (row r, logical column c) of a swizzled tile with `re` elements per row
+  auto elem = [](const T* tile, int r, int c, int re) -> float {
+    constexpr int EPC = 16 / sizeof(T);
+    const int sc = kpos<T>(c);
+    const int nchunk = re / EPC;
+    const int m = (nchunk < 16 ? nchunk : 16) - 1;
+    const int j = sc / EPC;
+    return to_f(tile[r * re + ((j ^ (r & m)) * EPC) + (sc % EPC)]);
+  };
 
   f32x4 dh[NDT];
+  if (a.dh_final) {
 #pragma unroll
-  for (int at = 0; at < NDT; ++at)
+    for (int at = 0; at < NDT; ++at)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      dh[at][r] = a.dh_final
-                      ? sanitize(a.dh_final[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col])
-                      : 0.f;
+      for (int r = 0; r < 4; ++r)
+        dh[at][r] = sanitize(a.dh_final[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col]);
+  } else {
+#pragma unroll
+    for (int at = 0; at < NDT; ++at) dh[at] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
-  for (int c = a.N - 1; c >= 0; --c) {
-    const size_t cid = (size_t)bh * a.N + c;
-    stage_tile<T, BT, D, W_LD>(sW, a.W + cid * BT * D, tid);
-    stage_tile<T, D, BT, K_LD>(sK, a.KgT + cid * D * BT, tid);
-    __syncthreads();
+  auto step = [&](int i, const char* cur, const float* eglc) __attribute__((always_inline)) {
+    const size_t cid = chunk_id(i);
+    __syncthreads();  // A(i)
+    f32x4 dvn[NB], qd[NDT];
+#pragma unroll
+    for (int it = 0; it < NB; ++it) dvn[it] = sDV[(wv * NB + it) * 64 + lane];
+#pragma unroll
+    for (int at = 0; at < NDT; ++at) qd[at] = sQD[(wv * NDT + at) * 64 + lane];
+    __syncthreads();  // B(i)
+    const T* sW = reinterpret_cast<const T*>(cur);
+    const T* sK = reinterpret_cast<const T*>(cur + WBYTES);
+
     float* dht = a.DHT + cid * D * D + (size_t)col * D;
 #pragma unroll
     for (int at = 0; at < NDT; ++at) store4(dht + at * 16 + 4 * lg, dh[at]);
 
-    f32x4 dvn[NB];
-    const float* dvp = a.DVPT + cid * D * BT + (size_t)col * BT;
-    float* dvo = a.DVNT + cid * D * BT + (size_t)col * BT;
+    // dv_new = dvp + kg dh: X[t][d] = kg^T[d][t]
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
-      f32x4 acc = load4f(dvp + it * 16 + 4 * lg);
 #pragma unroll
       for (int at = 0; at < NDT; ++at) {
         f32x4 x;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = sK[(at * 16 + 4 * lg + e) * K_LD + it * 16 + li];
-        mma(acc, x, dh[at]);
+        for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
+        mma(dvn[it], x, dh[at]);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = sanitize(acc[r]);
-      dvn[it] = acc;
-      store4(dvo + it * 16 + 4 * lg, acc);
+      for (int r = 0; r < 4; ++r) dvn[it][r] = sanitize(dvn[it][r]);
     }
-    const float* qdo = a.QDOT + cid * D * D + (size_t)col * D;
-    const float* glc = a.GL + cid * D;
+    float* dvo = a.DVNT + cid * D * BT + (size_t)col * BT;
+#pragma unroll
+    for (int it = 0; it < NB; ++it) store4(dvo + it * 16 + 4 * lg, dvn[it]);
+
+    // dh <- e^{gl} dh + qdot - W^T dv_new: X[d][t] = W[t][d]
 #pragma unroll
     for (int at = 0; at < NDT; ++at) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -242,16 +386,18 @@ __global__ void __launch_bounds__(256) bwd_state(BStateArgs<T> a) {
       for (int it = 0; it < NB; ++it) {
         f32x4 x;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = sW[(it * 16 + 4 * lg + e) * W_LD + at * 16 + li];
+        for (int e = 0; e < 4; ++e) x[e] = elem(sW, it * 16 + 4 * lg + e, at * 16 + li, D);
         mma(acc, x, dvn[it]);
       }
-      const f32x4 q4 = load4f(qdo + at * 16 + 4 * lg);
-      const f32x4 g4 = load4f(glc + at * 16 + 4 * lg);
+      const f32x4 egl = load4f(eglc + at * 16 + 4 * lg);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        dh[at][r] = sanitize(__expf(g4[r]) * dh[at][r] + q4[r] - acc[r]);
+      for (int r = 0; r < 4; ++r) dh[at][r] = sanitize(egl[r] * dh[at][r] + qd[at][r] - acc[r]);
     }
-    __syncthreads();
+  };
+
+  for (int i = 0; i < n; i += 2) {
+    step(i, sbuf0, sGL0);
+    if (i + 1 < n) step(i + 1, sbuf1, sGL1);
   }
 #pragma unroll
   for (int at = 0; at < NDT; ++at)
@@ -630,8 +776,9 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     // B1: reverse state scan
     BStateArgs<T> sa{(const T*)fW, (const T*)fKgT, fGL, buf(B_DVPT), buf(B_QDOT), dh_final, N,
                      buf(B_DHT), buf(B_DVNT), dh0};
-    hipLaunchKernelGGL((bwd_state<T, BT, D>), dim3((size_t)B * H * (D / 64)), dim3(256), 0, st,
-                       sa);
+    constexpr int BW = 2, BP = 2;  // compute and producer waves per scan workgroup
+    hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP>), dim3((size_t)B * H * (D / (16 * BW))),
+                       dim3(64 * (BW + BP)), 0, st, sa);
     launch_mark(st);
     if (NC > 0) {
       ElemArgs<T, TG> ea{(const T*)k, (const T*)w, (const T*)v, (const T*)b, (const TG*)g,
