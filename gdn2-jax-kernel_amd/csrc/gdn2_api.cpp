@@ -24,6 +24,11 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
 
 size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t elem);
 
+template <typename T, typename TG, int D>
+hipError_t launch_decode(hipStream_t st, int B, int H, const void* q, const void* k,
+                         const void* v, const void* w, const void* b, const void* g,
+                         float scale, const float* h_in, float* h_out, float* out);
+
 static size_t elem_size(int dtype) { return dtype == GDN2_F32 ? 4 : 2; }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -90,6 +95,14 @@ struct BwdRun {
     return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
   }
 };
+
+template <typename T, typename TG, int D>
+static int run_decode(hipStream_t st, int B, int H, const void* q, const void* k, const void* v,
+                      const void* w, const void* b, const void* g, float scale,
+                      const float* h_in, float* h_out, float* out) {
+  hipError_t e = launch_decode<T, TG, D>(st, B, H, q, k, v, w, b, g, scale, h_in, h_out, out);
+  return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
 
 }  // namespace gdn2
 
@@ -228,6 +241,31 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
   return dispatch<BwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, B, T, H, q, k, v, w,
                           b, g, h0, scale, dout, dh_final, dq, dk, dv, dw, db, dg, dh0,
                           (const char*)fwd_ws, (char*)ws);
+}
+
+int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, const void* q,
+                const void* k, const void* v, const void* w, const void* b, const void* g,
+                float scale, const float* h_in, float* h_out, float* out) {
+  EventScope scope;
+  int rc = gdn2_validate(B, 0, H, D, 64, in_dtype, g_dtype);
+  if (rc) return rc;
+  if ((rc = check_ptrs({q, k, v, w, b, g, h_out, out}))) return rc;
+  if ((rc = check_opt({h_in}))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+#define GDN2_DEC(T, TG, D_) \
+  if (D == D_) return run_decode<T, TG, D_>(st, B, H, q, k, v, w, b, g, scale, h_in, h_out, out);
+  if (in_dtype == GDN2_F32) {
+    GDN2_DEC(float, float, 64)
+    GDN2_DEC(float, float, 128)
+  } else if (g_dtype == GDN2_F32) {
+    GDN2_DEC(bf16_t, float, 64)
+    GDN2_DEC(bf16_t, float, 128)
+  } else {
+    GDN2_DEC(bf16_t, bf16_t, 64)
+    GDN2_DEC(bf16_t, bf16_t, 128)
+  }
+#undef GDN2_DEC
+  return GDN2_ERR_HEAD_DIM;
 }
 
 }  // extern "C"

@@ -118,6 +118,16 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
              void* dg, float* dh0, const void* fwd_ws, size_t fwd_ws_bytes, void* ws,
              size_t ws_bytes);
 
+/* Single-token recurrent step on the (B,H,D,D) float32 state, for serving:
+ * the reference has no decode entry; this is gdn2_pallas_forward with T = 1
+ * (gdn2_fwd.py:400-424), i.e. one chunk of one token, on the state layout of
+ * h0 / h_final (gdn2_fwd.py:342).  q,k,v,w,b,g are (B,H,D) (one token of the
+ * (B,T,H,D) inputs); h_in may be NULL (zero state) and may equal h_out (update
+ * in place); out (B,H,D) float32.  Dtypes as gdn2_fwd; no chunk size applies. */
+int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, const void* q,
+                const void* k, const void* v, const void* w, const void* b, const void* g,
+                float scale, const float* h_in, float* h_out, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -144,3 +144,18 @@ def test_segment_workspace():
     # N = 10, asked for 6: segments of 2 -> 5 segments
     assert L.gdn2_fwd_workspace_bytes_ex(1, 640, 1, 64, 64, F32, _lib.FWD_SEGMENTS(6)) == \
         base + al(5 * 3 * 64 * 64 * 4)
+
+
+def test_decode_rejects_before_launch():
+    L = _lib.lib()
+    fake = [0x100000 * (i + 1) for i in range(6)]
+    call = lambda D, dt, gdt, ptrs, hin, hout, out: L.gdn2_decode(
+        None, 2, 3, D, dt, gdt, *ptrs, 0.125, hin, hout, out)
+    assert call(96, F32, F32, fake, None, 0x2000, 0x3000) == _lib.ERR_HEAD_DIM
+    assert call(64, 7, F32, fake, None, 0x2000, 0x3000) == _lib.ERR_DTYPE
+    assert call(64, F32, BF16, fake, None, 0x2000, 0x3000) == _lib.ERR_DTYPE
+    assert call(64, F32, F32, [None] + fake[1:], None, 0x2000, 0x3000) == _lib.ERR_NULL
+    assert call(64, F32, F32, fake, None, None, 0x3000) == _lib.ERR_NULL
+    assert call(64, F32, F32, fake, 0x1004, 0x2000, 0x3000) == _lib.ERR_ALIGN
+    assert L.gdn2_decode(None, 0, 3, 64, F32, F32, *fake, 0.125, None, 0x2000, 0x3000) == \
+        _lib.ERR_SHAPE
