@@ -140,6 +140,7 @@ const char* gdn2_strerror(int code) {
     case GDN2_ERR_WORKSPACE: return "workspace too small";
     case GDN2_ERR_SHAPE: return "invalid shape (B and H must be >= 1, T >= 0)";
     case GDN2_ERR_LAUNCH: return "HIP kernel launch failed";
+    case GDN2_ERR_FLAGS: return "invalid flags (GDN2_FWD_RAW_INPUTS cannot be combined with GDN2_FWD_SAVE_A)";
     default: return "unknown error";
   }
 }
@@ -185,6 +186,7 @@ static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_d
   EventScope scope;
   int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
+  if ((flags & GDN2_FWD_RAW_INPUTS) && (flags & GDN2_FWD_SAVE_A)) return GDN2_ERR_FLAGS;
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, out}))) return rc;
   if ((rc = check_ptrs({h_final}))) return rc;
   if ((rc = check_opt({h0, a_dbg}))) return rc;

@@ -37,7 +37,15 @@ struct PrepArgs {
   T* Aqk;
   float* GL;
   float* a_dbg;  // optional A = (I + Akk)^{-1} output (BT x BT fp32 per chunk)
+  int raw;       // inputs before their activations: q,k <- q,k/|.|_2, w,b <- sigmoid,
+                 // g <- -softplus(g), applied here as the values are read
 };
+
+__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
+// -softplus(x) = -(max(x,0) + log(1 + e^{-|x|}))
+__device__ __forceinline__ float neg_softplus(float x) {
+  return -(fmaxf(x, 0.f) + __logf(1.f + __expf(-fabsf(x))));
+}
 
 // Own row blocks of wave `wv` in fwd_out: {wv} and, for 8 blocks, {7 - wv} --
 // equal work for the triangular products.
@@ -123,9 +131,14 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
     reinterpret_cast<f32x4*>(sA)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // ---- 1. in-block inclusive cumsum of g (lanes li = tokens) ----------------
+  const bool raw = a.raw != 0;
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
     const int I = own_block<NB>(wv, i);
+    if (raw) {
+#pragma unroll
+      for (int x = 0; x < DQ; ++x) loc[i][x] = neg_softplus(loc[i][x]);
+    }
 #pragma unroll
     for (int x = 0; x < DQ; ++x) loc[i][x] = row_scan16(loc[i][x]);
     if (li == 15) {
@@ -157,13 +170,34 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
     T* kgT = a.KgT + (size_t)cid * D * BT;
     T* qgp = a.Qg + (size_t)cid * BT * D + (size_t)t * D;
     f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
+    // raw inputs: 1/|q_t|, 1/|k_t| over D -- the token's channels sit in the four
+    // lanes li, li+16, li+32, li+48 (F.normalize semantics: divide by max(|x|, 1e-12))
+    float iq = 1.f, ik = 1.f;
+    if (raw) {
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int j = 0; j < NKD; ++j)
+#pragma unroll
+        for (int e = 0; e < KC; ++e) {
+          const float qv = to_f(qo[i][j][e]), kv = to_f(ko[i][j][e]);
+          sq += qv * qv;
+          sk += kv * kv;
+        }
+      sq += __shfl_xor(sq, 16);
+      sq += __shfl_xor(sq, 32);
+      sk += __shfl_xor(sk, 16);
+      sk += __shfl_xor(sk, 32);
+      iq = 1.f / fmaxf(sqrtf(sq), 1e-12f);
+      ik = 1.f / fmaxf(sqrtf(sk), 1e-12f);
+    }
 #pragma unroll
     for (int j = 0; j < NKD; ++j) {
       float qg[KC], kh[KC], dq[KC], dk[KC], db[KC];
 #pragma unroll
       for (int e = 0; e < KC; ++e) {
         const int x = j * KC + e, ch = chan(x);
-        const float qv = to_f(qo[i][j][e]), kv = to_f(ko[i][j][e]), bv = to_f(bo[i][j][e]);
+        const float qv = to_f(qo[i][j][e]) * iq, kv = to_f(ko[i][j][e]) * ik;
+        const float bv = raw ? sigmoidf(to_f(bo[i][j][e])) : to_f(bo[i][j][e]);
         const float lc = loc[i][x];
         const float eloc = __expf(lc);
         const float ekh = __expf(sTot[I * D + ch] - lc);
@@ -312,8 +346,9 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
     const int t = own_block<NB>(wv, i) * 16 + li;
 #pragma unroll
     for (int x = 0; x < DQ; ++x)
-      sWVT[chan(x) * TT_LD + t] =
-          from_f<T>(to_f(wo[i][x / KC][x % KC]) * to_f(vo[i][x / KC][x % KC]));
+      sWVT[chan(x) * TT_LD + t] = from_f<T>(
+          (raw ? sigmoidf(to_f(wo[i][x / KC][x % KC])) : to_f(wo[i][x / KC][x % KC])) *
+          to_f(vo[i][x / KC][x % KC]));
   }
   __syncthreads();
 
@@ -839,7 +874,8 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     PrepArgs<T, TG> pa{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
                        (const TG*)g, T_len, H, N, (long long)NC, scale, W, UT, KgT, Qg, Aqk, GL,
                        a_dbg ? a_dbg : ((flags & 1) ? reinterpret_cast<float*>(ws + L.A)
-                                                    : nullptr)};
+                                                    : nullptr),
+                       (flags & 2) ? 1 : 0};
     hipLaunchKernelGGL((fwd_prep<T, TG, BT, D>), dim3(NC), dim3(64 * prep_waves(BT)), 0, st,
                        pa);
   }

@@ -19,6 +19,7 @@ LIB_PATH = Path(os.environ.get("GDN2_LIB", _HERE / "libgdn2_hip.so"))
 GDN2_F32 = 0
 GDN2_BF16 = 1
 FWD_SAVE_A = 1
+FWD_RAW_INPUTS = 2
 
 
 def FWD_SEGMENTS(n: int) -> int:
@@ -35,6 +36,7 @@ ERR_ALIGN = -6
 ERR_WORKSPACE = -7
 ERR_SHAPE = -8
 ERR_LAUNCH = -9
+ERR_FLAGS = -10
 
 _c_int, _c_float, _c_size, _vp = ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
 

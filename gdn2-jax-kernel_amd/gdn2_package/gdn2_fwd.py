@@ -218,6 +218,19 @@ def _kpos_index(n: int, device) -> torch.Tensor:
     return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3)
 
 
+def gdn2_pallas_forward_raw(q, k, v, w, b, g, scale, h0=None, chunk_size=None):
+    """Forward from pre-activation inputs, the caller's preparation fused into
+    the prep kernel: q,k are L2-normalised over D (divided by max(|x|_2,
+    1e-12), as torch.nn.functional.normalize), w,b pass through a sigmoid and
+    g becomes -softplus(g) -- the BASELINE input distributions' construction.
+    Equal to ``gdn2_pallas_forward`` on the activated inputs; no reference
+    counterpart (the reference takes activated inputs, gdn2_fwd.py:400).
+    Inference only (no autograd)."""
+    p = _Prepared(q, k, v, w, b, g, scale, h0, chunk_size)
+    out, h_final, _, _ = _run_forward(p, flags=_lib.FWD_RAW_INPUTS)
+    return out, h_final
+
+
 def gdn2_pallas_forward_with_residuals(q, k, v, w, b, g, scale, h0=None, debug_tag="",
                                        chunk_size=None):
     """gdn2_fwd.py:427-457: forward plus the per-chunk intermediates.

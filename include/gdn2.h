@@ -48,6 +48,7 @@ extern "C" {
 #define GDN2_ERR_WORKSPACE    -7  /* workspace smaller than *_workspace_bytes() */
 #define GDN2_ERR_SHAPE        -8  /* B<1, H<1, T<0, or sizes overflow */
 #define GDN2_ERR_LAUNCH       -9  /* HIP launch failure */
+#define GDN2_ERR_FLAGS       -10  /* invalid flag combination */
 
 /* Library version string, e.g. "0.1.0". */
 const char* gdn2_version(void);
@@ -65,6 +66,12 @@ size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
 
 /* gdn2_fwd flags. */
 #define GDN2_FWD_SAVE_A 1  /* also keep A = (I + Akk)^{-1} in ws, needed by gdn2_bwd */
+/* q,k,w,b,g are given before their activations, which the forward applies as it
+ * reads them: q,k <- q,k / max(|.|_2, 1e-12) over D, w,b <- sigmoid, g <-
+ * -softplus(g) -- the caller's preparation step of BASELINE's input
+ * distributions, fused into the forward.  Inference only: not with
+ * GDN2_FWD_SAVE_A (the backward reads the activated inputs). */
+#define GDN2_FWD_RAW_INPUTS 2
 /* Segments of the state scan (bits 8-15; 0 = automatic).  Long sequences with
  * few (b,h) pairs split the serial chunk recurrence into S segments scanned in
  * parallel and chained by their affine transitions (the sequence-parallel

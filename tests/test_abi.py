@@ -30,8 +30,8 @@ def test_version_and_strerror():
     import gdn2_package
     L = _lib.lib()
     assert L.gdn2_version().decode() == gdn2_package.__version__
-    for code in range(0, -10, -1):
-        assert L.gdn2_strerror(code)
+    for code in range(0, -11, -1):
+        assert L.gdn2_strerror(code) and L.gdn2_strerror(code) != b"unknown error"
     assert L.gdn2_strerror(-1234) == b"unknown error"
 
 
@@ -91,6 +91,9 @@ def test_fwd_rejects_before_launch():
     assert _fwd(L, good, [0x100008] + fake[1:], None, 0x1000, 0x2000, 0x3000, ws_need) \
         == _lib.ERR_ALIGN
     assert _fwd(L, good, fake, 0x1004, 0x1000, 0x2000, 0x3000, ws_need) == _lib.ERR_ALIGN
+    # raw inputs are inference-only
+    assert _fwd(L, good, fake, None, 0x1000, 0x2000, 0x3000, ws_need,
+                _lib.FWD_RAW_INPUTS | _lib.FWD_SAVE_A) == _lib.ERR_FLAGS
     # then workspace size
     assert _fwd(L, good, fake, None, 0x1000, 0x2000, 0x3000, ws_need - 1) == _lib.ERR_WORKSPACE
     assert _fwd(L, good, fake, None, 0x1000, 0x2000, None, ws_need) == _lib.ERR_NULL

@@ -304,3 +304,40 @@ def test_stage_diagnostics_path(dev, monkeypatch, capsys):
     o1, h1 = gp().gdn2_pallas_forward(*xt, 0.125, debug_tag="t", chunk_size=64)
     assert torch.equal(o0, o1) and torch.equal(h0, h1)
     assert capsys.readouterr().out == ""
+
+
+# ----------------------------------------------------------------------------- fused input prep
+@pytest.mark.parametrize("dtype,BT,D", [(torch.float32, 64, 128), (torch.bfloat16, 128, 128),
+                                        (torch.bfloat16, 64, 64)])
+def test_raw_inputs_fused_activations(dev, dtype, BT, D):
+    """gdn2_pallas_forward_raw on pre-activation inputs equals the forward on
+    the torch-activated inputs, and the recurrence on activations computed in
+    float64."""
+    B, T, H = 2, 2 * BT, 2
+    rng = np.random.default_rng(21)
+    raw = [rng.standard_normal((B, T, H, D)).astype(np.float32) for _ in range(6)]
+    raw[0][0, 3, 1] = 0.0                          # a zero query: normalised to 0, no NaN
+    rt = [torch.tensor(x, device=dev) for x in raw]
+    rt = [x.to(dtype) for x in rt[:5]] + [rt[5]]
+    out_r, h_r = gp().gdn2_pallas_forward_raw(*rt, D ** -0.5, chunk_size=BT)
+    f = torch.nn.functional
+    act = [f.normalize(rt[0].float(), dim=-1, eps=1e-12), f.normalize(rt[1].float(), dim=-1, eps=1e-12),
+           rt[2].float(), torch.sigmoid(rt[3].float()), torch.sigmoid(rt[4].float()),
+           -f.softplus(rt[5].float())]
+    out_a, h_a = gp().gdn2_pallas_forward(*[x.to(dtype) for x in act[:5]], act[5], D ** -0.5,
+                                          chunk_size=BT)
+    assert torch.isfinite(out_r).all() and torch.isfinite(h_r).all()
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    ok_o, e_o = close(out_r.cpu().numpy(), out_a.cpu().numpy(), tol)
+    ok_h, e_h = close(h_r.cpu().numpy(), h_a.cpu().numpy(), tol)
+    assert ok_o and ok_h, ("vs activated", e_o, e_h)
+    r64 = [x.double().cpu().numpy() for x in rt]
+    nq = np.linalg.norm(r64[0], axis=-1, keepdims=True)
+    nk = np.linalg.norm(r64[1], axis=-1, keepdims=True)
+    sig = lambda x: 1.0 / (1.0 + np.exp(-x))
+    ref = [r64[0] / np.maximum(nq, 1e-12), r64[1] / np.maximum(nk, 1e-12), r64[2], sig(r64[3]),
+           sig(r64[4]), -np.logaddexp(0.0, r64[5])]
+    ro, rh = O.recurrent_fwd(*ref, D ** -0.5)
+    ok_o, e_o = close(out_r.cpu().numpy(), ro, TOL[dtype])
+    ok_h, e_h = close(h_r.cpu().numpy(), rh, TOL[dtype])
+    assert ok_o and ok_h, ("vs oracle", e_o, e_h)
