@@ -13,7 +13,7 @@ template <typename T, typename TG, int BT, int D>
 hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, float* out, float* h_final, char* ws,
-                      float* a_dbg, int flags);
+                      float* a_dbg, int flags, const Varlen* vl);
 
 template <typename T, typename TG, int BT, int D>
 hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
@@ -76,9 +76,9 @@ struct FwdRun {
   static int run(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                  const void* v, const void* w, const void* b, const void* g, const float* h0,
                  float scale, float* out, float* h_final, char* ws, float* a_dbg,
-                 int flags) {
+                 int flags, const Varlen* vl) {
     hipError_t e = launch_fwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale, out,
-                                            h_final, ws, a_dbg, flags);
+                                            h_final, ws, a_dbg, flags, vl);
     return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
   }
 };
@@ -194,7 +194,8 @@ static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_d
   if (need > 0 && (rc = check_ptrs({ws}))) return rc;
   if (ws_bytes < need) return GDN2_ERR_WORKSPACE;
   return dispatch<FwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, B, T, H, q, k, v, w,
-                          b, g, h0, scale, out, h_final, (char*)ws, a_dbg, flags);
+                          b, g, h0, scale, out, h_final, (char*)ws, a_dbg, flags,
+                          (const Varlen*)nullptr);
 }
 
 int gdn2_fwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
@@ -243,6 +244,37 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
   return dispatch<BwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, B, T, H, q, k, v, w,
                           b, g, h0, scale, dout, dh_final, dq, dk, dv, dw, db, dg, dh0,
                           (const char*)fwd_ws, (char*)ws);
+}
+
+size_t gdn2_fwd_varlen_workspace_bytes(int total_chunks, int H, int D, int BT, int in_dtype) {
+  if (total_chunks < 0 || (double)total_chunks * BT > 2.0e9) return 0;
+  if (gdn2_validate(1, total_chunks * BT, H, D, BT, in_dtype, GDN2_F32) != GDN2_OK) return 0;
+  return fwd_layout((size_t)H * total_chunks, BT, D, elem_size(in_dtype)).total;
+}
+
+int gdn2_fwd_varlen(void* stream, int num_seqs, const int* cu_chunks, const int* chunk_start,
+                    int total_chunks, int T, int H, int D, int BT, int in_dtype, int g_dtype,
+                    const void* q, const void* k, const void* v, const void* w, const void* b,
+                    const void* g, const float* h0, float scale, float* out, float* h_final,
+                    void* ws, size_t ws_bytes, int flags) {
+  EventScope scope;
+  if (num_seqs < 1 || total_chunks < 0 || T < 0 || T > total_chunks * (long long)BT)
+    return GDN2_ERR_SHAPE;
+  if (T < total_chunks) return GDN2_ERR_SEQ_LEN;  // every chunk holds at least one token
+  int rc = gdn2_validate(1, 0, H, D, BT, in_dtype, g_dtype);
+  if (rc) return rc;
+  if (flags & GDN2_FWD_SAVE_A) return GDN2_ERR_FLAGS;  // forward only
+  if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, out}))) return rc;
+  if ((rc = check_ptrs({h_final, cu_chunks}))) return rc;
+  if (total_chunks > 0 && (rc = check_ptrs({chunk_start}))) return rc;
+  if ((rc = check_opt({h0}))) return rc;
+  const size_t need = gdn2_fwd_varlen_workspace_bytes(total_chunks, H, D, BT, in_dtype);
+  if (need > 0 && (rc = check_ptrs({ws}))) return rc;
+  if (ws_bytes < need) return GDN2_ERR_WORKSPACE;
+  const Varlen vl{cu_chunks, chunk_start, num_seqs, total_chunks};
+  return dispatch<FwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, 1, T, H, q, k, v, w,
+                          b, g, h0, scale, out, h_final, (char*)ws, (float*)nullptr,
+                          flags & GDN2_FWD_RAW_INPUTS, &vl);
 }
 
 int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, const void* q,

@@ -39,7 +39,26 @@ struct PrepArgs {
   float* a_dbg;  // optional A = (I + Akk)^{-1} output (BT x BT fp32 per chunk)
   int raw;       // inputs before their activations: q,k <- q,k/|.|_2, w,b <- sigmoid,
                  // g <- -softplus(g), applied here as the values are read
+  const int* cstart;  // variable-length batch: token row where chunk c starts
+                      // ([N+1], B = 1); rows past cstart[c+1] are neutral padding
 };
+
+// First token row of chunk c and its number of real tokens: from the chunk table
+// of a variable-length batch (clamped to [0, BT] and to the T rows), else
+// c*BT within batch element bb.
+struct ChunkRows {
+  size_t row0;
+  int valid;
+};
+__device__ __forceinline__ ChunkRows chunk_rows(const int* cstart, int c, int bb, int T_len,
+                                                int BT) {
+  if (!cstart) return ChunkRows{(size_t)bb * T_len + (size_t)c * BT, BT};
+  const int r0 = cstart[c];
+  int v = cstart[c + 1] - r0;
+  v = v < BT ? v : BT;
+  v = v < T_len - r0 ? v : T_len - r0;
+  return ChunkRows{(size_t)(r0 > 0 ? r0 : 0), (v > 0 && r0 >= 0) ? v : 0};
+}
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
 // -softplus(x) = -(max(x,0) + log(1 + e^{-|x|}))
@@ -109,9 +128,13 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   const int cid = blockIdx.x;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
   const size_t HD = (size_t)a.H * D;
-  const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D;
+  const ChunkRows cr = chunk_rows(a.cstart, c, bb, a.T_len, BT);
+  const size_t tok0 = cr.row0 * HD + (size_t)hh * D;
   auto rowp = [&](int t) { return tok0 + (size_t)t * HD; };
   auto chan = [&](int x) { return (x / KC) * KS + lg * KC + (x % KC); };
+  // padding rows of a short chunk read as neutral tokens (k = 0, g = 0: the
+  // state passes through unchanged)
+  auto real = [&](int i) { return own_block<NB>(wv, i) * 16 + li < cr.valid; };
 
   // all loads needed before the inverse, issued together
   float loc[NBW][DQ];
@@ -119,12 +142,21 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
     const size_t off = rowp(own_block<NB>(wv, i) * 16 + li);
+    const bool rv = real(i);
 #pragma unroll
     for (int j = 0; j < NKD; ++j) {
-      load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
-      qo[i][j] = op_load<T>(a.q + off + j * KS + lg * KC);
-      ko[i][j] = op_load<T>(a.k + off + j * KS + lg * KC);
-      bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
+      if (rv) {
+        load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
+        qo[i][j] = op_load<T>(a.q + off + j * KS + lg * KC);
+        ko[i][j] = op_load<T>(a.k + off + j * KS + lg * KC);
+        bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
+      } else {
+#pragma unroll
+        for (int e = 0; e < KC; ++e) loc[i][j * KC + e] = 0.f;
+        qo[i][j] = op_zero<T>();
+        ko[i][j] = op_zero<T>();
+        bo[i][j] = op_zero<T>();
+      }
     }
   }
   for (int i = tid; i < BT * A_LD / 4; i += NT)
@@ -136,8 +168,9 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   for (int i = 0; i < NBW; ++i) {
     const int I = own_block<NB>(wv, i);
     if (raw) {
+      const bool rv = real(i);
 #pragma unroll
-      for (int x = 0; x < DQ; ++x) loc[i][x] = neg_softplus(loc[i][x]);
+      for (int x = 0; x < DQ; ++x) loc[i][x] = rv ? neg_softplus(loc[i][x]) : 0.f;
     }
 #pragma unroll
     for (int x = 0; x < DQ; ++x) loc[i][x] = row_scan16(loc[i][x]);
@@ -272,10 +305,11 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
     const size_t off = rowp(own_block<NB>(wv, i) * 16 + li);
+    const bool rv = real(i);
 #pragma unroll
     for (int j = 0; j < NKD; ++j) {
-      wo[i][j] = op_load<T>(a.w + off + j * KS + lg * KC);
-      vo[i][j] = op_load<T>(a.v + off + j * KS + lg * KC);
+      wo[i][j] = rv ? op_load<T>(a.w + off + j * KS + lg * KC) : op_zero<T>();
+      vo[i][j] = rv ? op_load<T>(a.v + off + j * KS + lg * KC) : op_zero<T>();
     }
   }
 
@@ -407,6 +441,9 @@ struct StateArgs {
   T* HT;
   T* VnT;
   float* h_final;
+  const int* cu;    // variable-length batch (B = 1): unit (h, sequence s) scans chunks
+                    // [cu[s], cu[s+1]); h0 / h_final are [s][h][D][D]
+  int H;
 };
 
 // One workgroup = one (b,h) and 16*NW value columns: NW compute waves (16
@@ -478,9 +515,17 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
   const bool mslice = vs >= NVS;             // summary pass: columns of M_seg
   if (mslice && sg == 0) return;             // segment 0 starts from h0: no M needed
   if (mslice) vs -= NVS;
-  const int c0 = sg * a.L;
-  int n = a.N - c0;                          // chunks of this segment
-  n = n < a.L ? n : a.L;
+  int c0, n;                                 // chunks [c0, c0 + n) of this unit
+  if (a.cu) {
+    c0 = a.cu[sg];
+    c0 = c0 < 0 ? 0 : (c0 > a.N ? a.N : c0);
+    n = a.cu[sg + 1] - c0;
+    n = n < a.N - c0 ? n : a.N - c0;
+  } else {
+    c0 = sg * a.L;
+    n = a.N - c0;
+    n = n < a.L ? n : a.L;
+  }
   n = n > 0 ? n : 0;
 
   if (wv >= NW) {
@@ -603,7 +648,8 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
   // pass, 0 for later segments of the summary pass, the identity for M slices,
   // the combined entry state in the final segmented pass
   f32x4 h[NDT];
-  const float* hsrc = (a.S > 1 && !a.summary) ? a.hin + ((size_t)unit) * D * D
+  const float* hsrc = a.cu ? (a.h0 ? a.h0 + ((size_t)sg * a.H + bh) * D * D : nullptr)
+                    : (a.S > 1 && !a.summary) ? a.hin + ((size_t)unit) * D * D
                     : (sg == 0 && !mslice && a.h0) ? a.h0 + (size_t)bh * D * D : nullptr;
   if (mslice) {
 #pragma unroll
@@ -699,7 +745,8 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     step(c, sbuf0, sGL0);
     if (c + 1 < n) step(c + 1, sbuf1, sGL1);
   }
-  float* hout = a.summary ? a.seg + ((size_t)unit * 2 + (mslice ? 1 : 0)) * D * D
+  float* hout = a.cu ? a.h_final + ((size_t)sg * a.H + bh) * D * D
+              : a.summary ? a.seg + ((size_t)unit * 2 + (mslice ? 1 : 0)) * D * D
               : (sg == a.S - 1) ? a.h_final + (size_t)bh * D * D : nullptr;
   if (hout) {
 #pragma unroll
@@ -781,6 +828,7 @@ struct OutArgs {
   int T_len, H, N;
   float scale;
   float* out;
+  const int* cstart;  // variable-length batch chunk table (see PrepArgs)
 };
 
 // o = scale qg h_c + Aqk v_new per chunk (gdn2_fwd.py:349-353), computed as
@@ -804,7 +852,8 @@ __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
   __syncthreads();
 
   const size_t HD = (size_t)a.H * D;
-  float* obase = a.out + ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D;
+  const ChunkRows cr = chunk_rows(a.cstart, c, bb, a.T_len, BT);
+  float* obase = a.out + cr.row0 * HD + (size_t)hh * D;
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
     const int It = own_block<NB>(wv, i);
@@ -845,7 +894,7 @@ __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
           mma(acc, op_load<T>(&sV[(vt * 16 + li) * V_LD + kg * KS + lg * KC]), af[kg]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] = sanitize(acc[r]);
-      store4(obase + (size_t)t * HD + vt * 16 + 4 * lg, acc);
+      if (t < cr.valid) store4(obase + (size_t)t * HD + vt * 16 + 4 * lg, acc);
     }
   }
 }
@@ -856,10 +905,10 @@ template <typename T, typename TG, int BT, int D>
 hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, float* out, float* h_final, char* ws,
-                      float* a_dbg, int flags) {
-  const int N = T_len / BT;
+                      float* a_dbg, int flags, const Varlen* vl) {
+  const int N = vl ? vl->total_chunks : T_len / BT;
   const size_t NC = (size_t)B * H * N;
-  const int S_ws = state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
+  const int S_ws = vl ? 1 : state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
   const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), S_ws > 1 ? (size_t)B * H * S_ws : 0);
   T* W = reinterpret_cast<T*>(ws + L.W);
   float* UT = reinterpret_cast<float*>(ws + L.UT);
@@ -875,7 +924,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                        (const TG*)g, T_len, H, N, (long long)NC, scale, W, UT, KgT, Qg, Aqk, GL,
                        a_dbg ? a_dbg : ((flags & 1) ? reinterpret_cast<float*>(ws + L.A)
                                                     : nullptr),
-                       (flags & 2) ? 1 : 0};
+                       (flags & 2) ? 1 : 0, vl ? vl->cstart : nullptr};
     hipLaunchKernelGGL((fwd_prep<T, TG, BT, D>), dim3(NC), dim3(64 * prep_waves(BT)), 0, st,
                        pa);
   }
@@ -885,26 +934,36 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   constexpr int NVS = D / (16 * SW);
   const size_t BH = (size_t)B * H;
   const int S = S_ws;
-  if (S > 1) {
+  if (vl) {
+    // one unit per (head, sequence)
+    StateArgs<T> va{W,  UT,      KgT,     GL,     h0,           N,  vl->nseq, 0, 0, nullptr,
+                    nullptr, HT, VnT, h_final, vl->cu_chunks, H};
+    if (vl->nseq > 0)
+      hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * vl->nseq * NVS),
+                         dim3(64 * (SW + SP)), 0, st, va);
+  } else if (S > 1) {
     const int Lseg = (N + S - 1) / S;
     float* seg = reinterpret_cast<float*>(ws + L.SEG);          // [bh][S][2][D][D]
     float* hin = seg + BH * S * 2 * (size_t)D * D;               // [bh][S][D][D]
-    StateArgs<T> sum{W, UT, KgT, GL, h0, N, S, Lseg, 1, nullptr, seg, HT, VnT, h_final};
+    StateArgs<T> sum{W, UT, KgT, GL, h0, N, S, Lseg, 1, nullptr, seg, HT, VnT, h_final,
+                     nullptr, H};
     hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * S * 2 * NVS),
                        dim3(64 * (SW + SP)), 0, st, sum);
     hipLaunchKernelGGL((seg_combine<D>), dim3(BH * (D / 16)), dim3(256), 0, st, seg, h0, hin,
                        S);
-    StateArgs<T> fin{W, UT, KgT, GL, h0, N, S, Lseg, 0, hin, nullptr, HT, VnT, h_final};
+    StateArgs<T> fin{W, UT, KgT, GL, h0, N, S, Lseg, 0, hin, nullptr, HT, VnT, h_final,
+                     nullptr, H};
     hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * S * NVS), dim3(64 * (SW + SP)),
                        0, st, fin);
   } else {
-    StateArgs<T> sa{W, UT, KgT, GL, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT, h_final};
+    StateArgs<T> sa{W, UT, KgT, GL, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT, h_final,
+                    nullptr, H};
     hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * NVS), dim3(64 * (SW + SP)), 0,
                        st, sa);
   }
   launch_mark(st);
   if (NC > 0) {
-    OutArgs<T> oa{Qg, Aqk, HT, VnT, T_len, H, N, scale, out};
+    OutArgs<T> oa{Qg, Aqk, HT, VnT, T_len, H, N, scale, out, vl ? vl->cstart : nullptr};
     hipLaunchKernelGGL((fwd_out<T, BT, D>), dim3(NC), dim3(256), 0, st, oa);
   }
   launch_mark(st);
@@ -915,7 +974,8 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   template hipError_t launch_fwd<T, TG, BT, D>(hipStream_t, int, int, int, const void*,     \
                                                const void*, const void*, const void*,       \
                                                const void*, const void*, const float*,      \
-                                               float, float*, float*, char*, float*, int);
+                                               float, float*, float*, char*, float*, int,   \
+                                               const Varlen*);
 
 GDN2_INST_FWD(float, float, 64, 64)
 GDN2_INST_FWD(float, float, 64, 128)

@@ -57,6 +57,17 @@ inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem, size_t s
   return L;
 }
 
+// A variable-length batch (B = 1, sequences packed along T): sequence s owns
+// chunks [cu_chunks[s], cu_chunks[s+1]) of the packed chunk list, and chunk c
+// starts at token row cstart[c] (cstart[total_chunks] = T); a sequence's last
+// chunk may be short.  Both tables live in device memory.
+struct Varlen {
+  const int* cu_chunks;
+  const int* cstart;
+  int nseq;
+  int total_chunks;
+};
+
 // Segments of the forward state scan for BH (b,h) pairs of N chunks.  Automatic
 // choice: as many as fill a 256-CU device in the final pass when the plain
 // pass's BH * D/32 workgroups cannot, each at least 16 chunks, and only when

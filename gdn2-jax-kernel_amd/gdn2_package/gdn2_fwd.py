@@ -231,6 +231,64 @@ def gdn2_pallas_forward_raw(q, k, v, w, b, g, scale, h0=None, chunk_size=None):
     return out, h_final
 
 
+def gdn2_pallas_forward_varlen(q, k, v, w, b, g, scale, cu_seqlens, h0=None,
+                               chunk_size=None, raw=False):
+    """Forward over a variable-length batch packed along T.
+
+    q..g are (1, T, H, D) holding num_seqs sequences back to back;
+    ``cu_seqlens`` (num_seqs + 1 integers, 0 first, T last, non-decreasing)
+    marks their boundaries.  Each sequence is chunked on its own (any length:
+    a short last chunk is padded inside the kernels with neutral tokens) and
+    scanned from ``h0[s]`` ((num_seqs, H, D, D) float32, default zeros) to
+    ``h_final[s]``.  Returns ``out`` (1, T, H, D) float32 and ``h_final``.
+    The same as running ``gdn2_pallas_forward`` per sequence.  ``raw=True``
+    fuses the input activations (``gdn2_pallas_forward_raw``).  No reference
+    counterpart (the reference needs equal lengths with T % BT == 0,
+    gdn2_fwd.py:145-146); forward only."""
+    if q.dim() != 4 or q.shape[0] != 1:
+        raise GDN2ShapeError(f"gdn2 varlen: expected packed (1,T,H,D) inputs, got {tuple(q.shape)}")
+    _, T, H, D = q.shape
+    cu_host = torch.as_tensor(cu_seqlens).detach().to("cpu", torch.int64).reshape(-1)
+    if cu_host.numel() < 2 or int(cu_host[0]) != 0 or int(cu_host[-1]) != T or \
+            bool((cu_host[1:] < cu_host[:-1]).any()):
+        raise GDN2ShapeError("gdn2 varlen: cu_seqlens must start at 0, end at T and not decrease")
+    S = cu_host.numel() - 1
+    # reuse the (B,T,H,D) checks with T padded to a whole chunk
+    p_chk = _Prepared(*(x[:, :0] for x in (q, k, v, w, b, g)), scale, None, chunk_size)
+    BT = p_chk.BT
+    dev = q.device
+    if h0 is not None and tuple(h0.shape) != (S, H, D, D):
+        raise GDN2ShapeError(f"gdn2 varlen: h0 must be (num_seqs,H,D,D); got {tuple(h0.shape)}")
+    lens = cu_host[1:] - cu_host[:-1]
+    nch = (lens + BT - 1) // BT
+    cu_chunks = torch.zeros(S + 1, dtype=torch.int64)
+    cu_chunks[1:] = torch.cumsum(nch, 0)
+    total = int(cu_chunks[-1])
+    seq_of = torch.repeat_interleave(torch.arange(S), nch)
+    cstart = torch.empty(total + 1, dtype=torch.int64)
+    cstart[:total] = cu_host[seq_of] + (torch.arange(total) - cu_chunks[seq_of]) * BT
+    cstart[total] = T
+    cu_d = cu_chunks.to(torch.int32).to(dev)
+    cs_d = cstart.to(torch.int32).to(dev)
+    in_dt, g_dt = p_chk.in_dt, p_chk.g_dt
+    xs = [x.to(in_dt).contiguous() for x in (q, k, v, w, b)] + [g.to(g_dt).contiguous()]
+    h0c = None if h0 is None else h0.to(device=dev, dtype=torch.float32).contiguous()
+    L = _lib.lib()
+    nbytes = L.gdn2_fwd_varlen_workspace_bytes(total, H, D, BT, _dtype_code(in_dt))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    out = torch.empty((1, T, H, D), dtype=torch.float32, device=dev)
+    h_final = torch.empty((S, H, D, D), dtype=torch.float32, device=dev)
+    rc = L.gdn2_fwd_varlen(torch.cuda.current_stream(dev).cuda_stream, S, cu_d.data_ptr(),
+                           cs_d.data_ptr(), total, T, H, D, BT, _dtype_code(in_dt),
+                           _dtype_code(g_dt), *(x.data_ptr() for x in xs),
+                           None if h0c is None else h0c.data_ptr(), float(scale),
+                           out.data_ptr(), h_final.data_ptr(), ws.data_ptr(), nbytes,
+                           _lib.FWD_RAW_INPUTS if raw else 0)
+    if rc:
+        _raise(rc, f"gdn2_fwd_varlen (T,H,D)=({T},{H},{D}), {S} sequences")
+    return out, h_final
+
+
 def gdn2_pallas_forward_with_residuals(q, k, v, w, b, g, scale, h0=None, debug_tag="",
                                        chunk_size=None):
     """gdn2_fwd.py:427-457: forward plus the per-chunk intermediates.

@@ -125,6 +125,24 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
              void* dg, float* dh0, const void* fwd_ws, size_t fwd_ws_bytes, void* ws,
              size_t ws_bytes);
 
+/* Variable-length batch.  No reference counterpart: the reference takes
+ * equal-length sequences with T % BT == 0 (gdn2_fwd.py:145-146).  num_seqs
+ * sequences are packed along T in (1,T,H,D) inputs; each is chunked on its
+ * own -- its last chunk may be short and is padded inside the kernels with
+ * neutral tokens -- and scanned from its own h0[s] ((num_seqs,H,D,D), may be
+ * NULL) to h_final[s] ((num_seqs,H,D,D)).  Device tables (int32):
+ * cu_chunks[num_seqs+1], sequence s owning chunks [cu_chunks[s],
+ * cu_chunks[s+1]) of the packed chunk list; chunk_start[total_chunks+1], the
+ * first token row of each chunk, chunk_start[total_chunks] = T.  Table values
+ * are clamped in the kernels (no access outside the buffers).  Forward only:
+ * flags 0 or GDN2_FWD_RAW_INPUTS. */
+size_t gdn2_fwd_varlen_workspace_bytes(int total_chunks, int H, int D, int BT, int in_dtype);
+int gdn2_fwd_varlen(void* stream, int num_seqs, const int* cu_chunks, const int* chunk_start,
+                    int total_chunks, int T, int H, int D, int BT, int in_dtype, int g_dtype,
+                    const void* q, const void* k, const void* v, const void* w, const void* b,
+                    const void* g, const float* h0, float scale, float* out, float* h_final,
+                    void* ws, size_t ws_bytes, int flags);
+
 /* Single-token recurrent step on the (B,H,D,D) float32 state, for serving:
  * the reference has no decode entry; this is gdn2_pallas_forward with T = 1
  * (gdn2_fwd.py:400-424), i.e. one chunk of one token, on the state layout of

@@ -162,3 +162,19 @@ def test_decode_rejects_before_launch():
     assert call(64, F32, F32, fake, 0x1004, 0x2000, 0x3000) == _lib.ERR_ALIGN
     assert L.gdn2_decode(None, 0, 3, 64, F32, F32, *fake, 0.125, None, 0x2000, 0x3000) == \
         _lib.ERR_SHAPE
+
+
+def test_varlen_rejects_before_launch():
+    L = _lib.lib()
+    fake = [0x100000 * (i + 1) for i in range(6)]
+    call = lambda nseq, total, T, flags=0, cu=0x7000, cs=0x8000, hf=0x2000: L.gdn2_fwd_varlen(
+        None, nseq, cu, cs, total, T, 2, 64, 64, F32, F32, *fake, None, 0.125, 0x1000, hf,
+        0x3000, 1 << 30, flags)
+    assert call(0, 1, 10) == _lib.ERR_SHAPE                 # no sequences
+    assert call(2, 2, 200) == _lib.ERR_SHAPE                # more tokens than chunks can hold
+    assert call(2, 3, 2) == _lib.ERR_SEQ_LEN                # a chunk without tokens
+    assert call(2, 2, 100, _lib.FWD_SAVE_A) == _lib.ERR_FLAGS
+    assert call(2, 2, 100, cu=None) == _lib.ERR_NULL
+    assert call(2, 2, 100, hf=None) == _lib.ERR_NULL
+    assert L.gdn2_fwd_varlen_workspace_bytes(5, 2, 64, 64, F32) == \
+        L.gdn2_fwd_workspace_bytes(1, 5 * 64, 2, 64, 64, F32)
