@@ -57,7 +57,8 @@ __device__ __forceinline__ ChunkRows chunk_rows(const int* cstart, int c, int bb
   int v = cstart[c + 1] - r0;
   v = v < BT ? v : BT;
   v = v < T_len - r0 ? v : T_len - r0;
-  return ChunkRows{(size_t)(r0 > 0 ? r0 : 0), (v > 0 && r0 >= 0) ? v : 0};
+  if (v <= 0 || r0 < 0) return ChunkRows{0, 0};  // no real rows: point at row 0
+  return ChunkRows{(size_t)r0, v};
 }
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
@@ -132,31 +133,29 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   const size_t tok0 = cr.row0 * HD + (size_t)hh * D;
   auto rowp = [&](int t) { return tok0 + (size_t)t * HD; };
   auto chan = [&](int x) { return (x / KC) * KS + lg * KC + (x % KC); };
-  // padding rows of a short chunk read as neutral tokens (k = 0, g = 0: the
-  // state passes through unchanged)
+  // Padding rows of a short chunk act as neutral tokens (k = 0, g = 0: the state
+  // passes through unchanged).  They load a real row of the chunk (no branch
+  // around the loads) and are zeroed once the values are first needed, only in
+  // chunks that have padding.
+  const bool padded = cr.valid < BT;
   auto real = [&](int i) { return own_block<NB>(wv, i) * 16 + li < cr.valid; };
+  auto load_row = [&](int i) {
+    const int t = own_block<NB>(wv, i) * 16 + li, last = cr.valid > 0 ? cr.valid - 1 : 0;
+    return rowp(t < last ? t : last);
+  };
 
   // all loads needed before the inverse, issued together
   float loc[NBW][DQ];
   Op qo[NBW][NKD], ko[NBW][NKD], bo[NBW][NKD];
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
-    const size_t off = rowp(own_block<NB>(wv, i) * 16 + li);
-    const bool rv = real(i);
+    const size_t off = load_row(i);
 #pragma unroll
     for (int j = 0; j < NKD; ++j) {
-      if (rv) {
-        load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
-        qo[i][j] = op_load<T>(a.q + off + j * KS + lg * KC);
-        ko[i][j] = op_load<T>(a.k + off + j * KS + lg * KC);
-        bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
-      } else {
-#pragma unroll
-        for (int e = 0; e < KC; ++e) loc[i][j * KC + e] = 0.f;
-        qo[i][j] = op_zero<T>();
-        ko[i][j] = op_zero<T>();
-        bo[i][j] = op_zero<T>();
-      }
+      load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
+      qo[i][j] = op_load<T>(a.q + off + j * KS + lg * KC);
+      ko[i][j] = op_load<T>(a.k + off + j * KS + lg * KC);
+      bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
     }
   }
   for (int i = tid; i < BT * A_LD / 4; i += NT)
@@ -164,6 +163,21 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
 
   // ---- 1. in-block inclusive cumsum of g (lanes li = tokens) ----------------
   const bool raw = a.raw != 0;
+  if (padded) {
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      if (!real(i)) {
+#pragma unroll
+        for (int x = 0; x < DQ; ++x) loc[i][x] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NKD; ++j) {
+          qo[i][j] = op_zero<T>();
+          ko[i][j] = op_zero<T>();
+          bo[i][j] = op_zero<T>();
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
     const int I = own_block<NB>(wv, i);
@@ -203,9 +217,9 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
     T* kgT = a.KgT + (size_t)cid * D * BT;
     T* qgp = a.Qg + (size_t)cid * BT * D + (size_t)t * D;
     f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
-    // raw inputs: 1/|q_t|, 1/|k_t| over D -- the token's channels sit in the four
-    // lanes li, li+16, li+32, li+48 (F.normalize semantics: divide by max(|x|, 1e-12))
-    float iq = 1.f, ik = 1.f;
+    // raw inputs: q,k <- q,k / max(|.|_2, 1e-12) over D (F.normalize) and
+    // b <- sigmoid(b), in place in the loaded registers; a token's channels sit
+    // in the four lanes li, li+16, li+32, li+48
     if (raw) {
       float sq = 0.f, sk = 0.f;
 #pragma unroll
@@ -220,8 +234,15 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
       sq += __shfl_xor(sq, 32);
       sk += __shfl_xor(sk, 16);
       sk += __shfl_xor(sk, 32);
-      iq = 1.f / fmaxf(sqrtf(sq), 1e-12f);
-      ik = 1.f / fmaxf(sqrtf(sk), 1e-12f);
+      const float iq = 1.f / fmaxf(sqrtf(sq), 1e-12f), ik = 1.f / fmaxf(sqrtf(sk), 1e-12f);
+#pragma unroll
+      for (int j = 0; j < NKD; ++j)
+#pragma unroll
+        for (int e = 0; e < KC; ++e) {
+          qo[i][j][e] = from_f<T>(to_f(qo[i][j][e]) * iq);
+          ko[i][j][e] = from_f<T>(to_f(ko[i][j][e]) * ik);
+          bo[i][j][e] = from_f<T>(sigmoidf(to_f(bo[i][j][e])));
+        }
     }
 #pragma unroll
     for (int j = 0; j < NKD; ++j) {
@@ -229,8 +250,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
 #pragma unroll
       for (int e = 0; e < KC; ++e) {
         const int x = j * KC + e, ch = chan(x);
-        const float qv = to_f(qo[i][j][e]) * iq, kv = to_f(ko[i][j][e]) * ik;
-        const float bv = raw ? sigmoidf(to_f(bo[i][j][e])) : to_f(bo[i][j][e]);
+        const float qv = to_f(qo[i][j][e]), kv = to_f(ko[i][j][e]), bv = to_f(bo[i][j][e]);
         const float lc = loc[i][x];
         const float eloc = __expf(lc);
         const float ekh = __expf(sTot[I * D + ch] - lc);
@@ -304,12 +324,11 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   Op wo[NBW][NKD], vo[NBW][NKD];
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
-    const size_t off = rowp(own_block<NB>(wv, i) * 16 + li);
-    const bool rv = real(i);
+    const size_t off = load_row(i);
 #pragma unroll
     for (int j = 0; j < NKD; ++j) {
-      wo[i][j] = rv ? op_load<T>(a.w + off + j * KS + lg * KC) : op_zero<T>();
-      vo[i][j] = rv ? op_load<T>(a.v + off + j * KS + lg * KC) : op_zero<T>();
+      wo[i][j] = op_load<T>(a.w + off + j * KS + lg * KC);
+      vo[i][j] = op_load<T>(a.v + off + j * KS + lg * KC);
     }
   }
 
@@ -374,15 +393,30 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
     }
   }
   // ---- 5. (w v)^T into LDS (khat's region, free since step 3) ---------------
+  if (padded) {
+#pragma unroll
+    for (int i = 0; i < NBW; ++i)
+      if (!real(i)) {
+#pragma unroll
+        for (int j = 0; j < NKD; ++j) vo[i][j] = op_zero<T>();
+      }
+  }
+  if (raw) {  // w <- sigmoid(w)
+#pragma unroll
+    for (int i = 0; i < NBW; ++i)
+#pragma unroll
+      for (int j = 0; j < NKD; ++j)
+#pragma unroll
+        for (int e = 0; e < KC; ++e) wo[i][j][e] = from_f<T>(sigmoidf(to_f(wo[i][j][e])));
+  }
   T* sWVT = sR0;
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
     const int t = own_block<NB>(wv, i) * 16 + li;
 #pragma unroll
     for (int x = 0; x < DQ; ++x)
-      sWVT[chan(x) * TT_LD + t] = from_f<T>(
-          (raw ? sigmoidf(to_f(wo[i][x / KC][x % KC])) : to_f(wo[i][x / KC][x % KC])) *
-          to_f(vo[i][x / KC][x % KC]));
+      sWVT[chan(x) * TT_LD + t] =
+          from_f<T>(to_f(wo[i][x / KC][x % KC]) * to_f(vo[i][x / KC][x % KC]));
   }
   __syncthreads();
 
