@@ -130,6 +130,98 @@ def time_train(gp, xs, steps, warmup):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
+def _time(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+def _event_ms(fn, nmarks):
+    """Run fn once with HIP events recorded at the library's launch marks
+    (gdn2_set_launch_events) and return the nmarks-1 intervals in ms."""
+    import ctypes
+    import torch
+    from gdn2_package import _lib
+    L = _lib.lib()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(nmarks)]
+    for e in evs:
+        e.record()
+    arr = (ctypes.c_void_p * nmarks)(*[ctypes.c_void_p(int(e.cuda_event)) for e in evs])
+    torch.cuda.synchronize()
+    L.gdn2_set_launch_events(arr, nmarks)
+    fn()
+    torch.cuda.synchronize()
+    return [evs[i].elapsed_time(evs[i + 1]) for i in range(nmarks - 1)]
+
+
+def extras(gp, steps=10, warmup=3):
+    """The paths beyond the headline, each timed on the GPU in the same run:
+    configs[4] (1 x 131072 x 8 heads, segmented state scan), the forward with
+    the input activations fused (vs torch activations + forward), a
+    variable-length batch with the headline's token count, and the decode step
+    (state read + written per token)."""
+    import torch
+    f = torch.nn.functional
+    res = {}
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    # configs[4]
+    B5, T5, H5 = 1, 131072, 8
+    r = lambda shape: torch.randn(shape, generator=gen, device="cuda")
+    q, k, v, w, b, g = (r((B5, T5, H5, D)) for _ in range(6))
+    q, k = f.normalize(q, dim=-1), f.normalize(k, dim=-1)
+    w, b, g = torch.sigmoid(w), torch.sigmoid(b), -f.softplus(g) * 0.1
+    xs = [x.to(torch.bfloat16) for x in (q, k, v, w, b)] + [g]
+    ms = _time(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5), steps, warmup)
+    kms = _event_ms(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5), 4)
+    res["config5_fwd"] = {"shape": "B1 T131072 H8 D128 bf16, chunk 128 (state scan in 8 "
+                                   "segments)", "ms": ms, "tokens_per_s": B5 * T5 / (ms * 1e-3),
+                          "kernels_ms": dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms))}
+    del q, k, v, w, b, g, xs
+    # fused input preparation at the headline shape
+    raw = [r((B, T, H, D)).to(torch.bfloat16) for _ in range(5)] + [r((B, T, H, D))]
+    ms_raw = _time(lambda: gp.gdn2_pallas_forward_raw(*raw, D ** -0.5), steps, warmup)
+
+    def torch_prep_then_fwd():
+        a = [f.normalize(raw[0].float(), dim=-1).to(torch.bfloat16),
+             f.normalize(raw[1].float(), dim=-1).to(torch.bfloat16), raw[2],
+             torch.sigmoid(raw[3]), torch.sigmoid(raw[4]), -f.softplus(raw[5])]
+        return gp.gdn2_pallas_forward(*a, D ** -0.5)
+    ms_sep = _time(torch_prep_then_fwd, steps, warmup)
+    res["fused_input_prep"] = {"shape": "B8 T8192 H6 D128 bf16", "fused_ms": ms_raw,
+                               "torch_activations_plus_forward_ms": ms_sep}
+    # variable length: the headline's 65536 tokens as 16 sequences of uneven length
+    lens = torch.randint(1, 2 * (B * T) // 16, (16,), generator=torch.Generator().manual_seed(1))
+    lens = (lens.float() * (B * T) / lens.sum()).long().clamp(min=1)
+    lens[-1] += B * T - lens.sum()
+    cu = torch.cat([torch.zeros(1, dtype=torch.long), lens.cumsum(0)])
+    packed = [x.reshape(1, B * T, H, D) for x in raw]
+    ms_v = _time(lambda: gp.gdn2_pallas_forward_varlen(*packed, D ** -0.5, cu, raw=True),
+                 steps, warmup)
+    kms = _event_ms(lambda: gp.gdn2_pallas_forward_varlen(*packed, D ** -0.5, cu, raw=True), 4)
+    res["varlen_fwd"] = {"shape": f"1 x {B * T} tokens in 16 sequences ({int(lens.min())}.."
+                                  f"{int(lens.max())} tokens), H6 D128 bf16, fused activations",
+                         "ms": ms_v, "tokens_per_s": B * T / (ms_v * 1e-3),
+                         "kernels_ms": dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms)),
+                         "note": "ms includes building the chunk tables on the host"}
+    del raw, packed
+    # decode: one token for B*H = 48 states of 128 x 128 fp32
+    tok = [r((B, 1, H, D)).to(torch.bfloat16) for _ in range(5)] + [-f.softplus(r((B, 1, H, D)))]
+    state = torch.zeros((B, H, D, D), device="cuda")
+    ms_d = _time(lambda: gp.gdn2_decode_step(*tok, D ** -0.5, state=state, inplace=True),
+                 100, 10)
+    res["decode_step"] = {"shape": "B8 H6 D128, one token", "call_us": ms_d * 1e3,
+                          "note": "per call, Python wrapper and launch included (host-bound); "
+                                  "the kernel (decode_step, 6.3 MB of fp32 state read and "
+                                  "written) is timed by rocprofv3 in profiles/"}
+    return res
+
+
 def cpu_baseline(min_seconds=10.0):
     """The numpy restatement of the reference's chunked forward (kernels A-D
     with the 3-D decay tensor, float32) on one batch element of the headline
@@ -228,6 +320,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip configs[4], fused input prep, varlen and decode timings")
     ap.add_argument("--pmc-run", action="store_true",
                     help="forward steps plus the calibration copy, for rocprofv3 --pmc")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -299,6 +393,8 @@ def main():
         "roofline": roof,
         "train": train,
     }
+    if not args.no_extras:
+        line["extras"] = extras(gp)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

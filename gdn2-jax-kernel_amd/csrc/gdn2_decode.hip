@@ -72,9 +72,11 @@ template <typename T, typename TG, int D>
 hipError_t launch_decode(hipStream_t st, int B, int H, const void* q, const void* k,
                          const void* v, const void* w, const void* b, const void* g,
                          float scale, const float* h_in, float* h_out, float* out) {
+  launch_mark(st);
   hipLaunchKernelGGL((decode_step<T, TG, D>), dim3((size_t)B * H), dim3(256), 0, st,
                      (const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
                      (const TG*)g, scale, h_in, h_out, out);
+  launch_mark(st);
   return hipGetLastError();
 }
 

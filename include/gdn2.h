@@ -148,7 +148,8 @@ int gdn2_fwd_varlen(void* stream, int num_seqs, const int* cu_chunks, const int*
  * (gdn2_fwd.py:400-424), i.e. one chunk of one token, on the state layout of
  * h0 / h_final (gdn2_fwd.py:342).  q,k,v,w,b,g are (B,H,D) (one token of the
  * (B,T,H,D) inputs); h_in may be NULL (zero state) and may equal h_out (update
- * in place); out (B,H,D) float32.  Dtypes as gdn2_fwd; no chunk size applies. */
+ * in place); out (B,H,D) float32.  Dtypes as gdn2_fwd; no chunk size applies.
+ * One kernel (see gdn2_set_launch_events). */
 int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, const void* q,
                 const void* k, const void* v, const void* w, const void* b, const void* g,
                 float scale, const float* h_in, float* h_out, float* out);
