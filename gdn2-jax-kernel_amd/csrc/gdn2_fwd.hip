@@ -881,8 +881,58 @@ __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int cid = blockIdx.x;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
-  g2s<T, 256>(sH, H_LD, a.HT + (size_t)cid * D * D, D, D, D, tid);
-  g2s<T, 256>(sV, V_LD, a.VnT + (size_t)cid * D * BT, BT, D, BT, tid);
+
+  // All global loads are issued before the first LDS store: the qg / Aqk
+  // operand rows of both own row blocks, then the h^T and v_new^T tiles.
+  // h^T and v_new^T are stored in chained order over d and t (kpos), so qg and
+  // Aqk are read in the matching chained pattern.  Aqk blocks right of the
+  // diagonal block are never written: masked per 16-token block.
+  Op qf[NBW][NKD], af[NBW][NKT];
+#pragma unroll
+  for (int i = 0; i < NBW; ++i) {
+    const int It = own_block<NB>(wv, i);
+    const int t = It * 16 + li;
+    const T* qrow = a.Qg + (size_t)cid * BT * D + (size_t)t * D;
+    const T* arow = a.Aqk + (size_t)cid * BT * BT + (size_t)t * BT;
+#pragma unroll
+    for (int kg = 0; kg < NKD; ++kg) qf[i][kg] = op_chained(qrow + kg * KS, lg);
+#pragma unroll
+    for (int kg = 0; kg < NKT; ++kg) {
+      if constexpr (sizeof(T) == 4) {
+        const int s0 = kg * KS + lg * KC;
+        af[i][kg] = (s0 <= It * 16 + 15) ? op_load<T>(arow + s0) : op_zero<T>();
+      } else {
+        const bf16x4 z = {(T)0.f, (T)0.f, (T)0.f, (T)0.f};
+        const bf16x4 lo = (2 * kg <= It)
+            ? *reinterpret_cast<const bf16x4*>(arow + kg * 32 + 4 * lg) : z;
+        const bf16x4 hi = (2 * kg + 1 <= It)
+            ? *reinterpret_cast<const bf16x4*>(arow + kg * 32 + 16 + 4 * lg) : z;
+        af[i][kg] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    }
+  }
+  {
+    constexpr int EPV = 16 / sizeof(T);                  // elements per 16-byte piece
+    constexpr int NH = D * D / EPV / 256, NV = D * BT / EPV / 256;
+    static_assert(D * D % (EPV * 256) == 0 && D * BT % (EPV * 256) == 0, "tiles split evenly");
+    uint4 rh[NH], rv[NV];
+    const uint4* gh = reinterpret_cast<const uint4*>(a.HT + (size_t)cid * D * D);
+    const uint4* gv = reinterpret_cast<const uint4*>(a.VnT + (size_t)cid * D * BT);
+#pragma unroll
+    for (int u = 0; u < NH; ++u) rh[u] = gh[tid + 256 * u];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) rv[u] = gv[tid + 256 * u];
+#pragma unroll
+    for (int u = 0; u < NH; ++u) {
+      const int i = tid + 256 * u, r = i / (D / EPV), cc = (i % (D / EPV)) * EPV;
+      *reinterpret_cast<uint4*>(&sH[r * H_LD + cc]) = rh[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int i = tid + 256 * u, r = i / (BT / EPV), cc = (i % (BT / EPV)) * EPV;
+      *reinterpret_cast<uint4*>(&sV[r * V_LD + cc]) = rv[u];
+    }
+  }
   __syncthreads();
 
   const size_t HD = (size_t)a.H * D;
@@ -892,40 +942,18 @@ __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
   for (int i = 0; i < NBW; ++i) {
     const int It = own_block<NB>(wv, i);
     const int t = It * 16 + li;
-    Op qf[NKD], af[NKT];
-    const T* qrow = a.Qg + (size_t)cid * BT * D + (size_t)t * D;
-    const T* arow = a.Aqk + (size_t)cid * BT * BT + (size_t)t * BT;
-    // h^T and v_new^T are stored in chained order over d and t (kpos), so qg
-    // and Aqk are read in the matching chained pattern.  Aqk blocks right of
-    // the diagonal block are never written: masked per 16-token block.
-#pragma unroll
-    for (int kg = 0; kg < NKD; ++kg) qf[kg] = op_chained(qrow + kg * KS, lg);
-#pragma unroll
-    for (int kg = 0; kg < NKT; ++kg) {
-      if constexpr (sizeof(T) == 4) {
-        const int s0 = kg * KS + lg * KC;
-        af[kg] = (s0 <= It * 16 + 15) ? op_load<T>(arow + s0) : op_zero<T>();
-      } else {
-        const bf16x4 z = {(T)0.f, (T)0.f, (T)0.f, (T)0.f};
-        const bf16x4 lo = (2 * kg <= It)
-            ? *reinterpret_cast<const bf16x4*>(arow + kg * 32 + 4 * lg) : z;
-        const bf16x4 hi = (2 * kg + 1 <= It)
-            ? *reinterpret_cast<const bf16x4*>(arow + kg * 32 + 16 + 4 * lg) : z;
-        af[kg] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
-    }
     const int kgmax = (It * 16 + 15) / KS;
 #pragma unroll
     for (int vt = 0; vt < NDT; ++vt) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kg = 0; kg < NKD; ++kg)
-        mma(acc, op_load<T>(&sH[(vt * 16 + li) * H_LD + kg * KS + lg * KC]), qf[kg]);
+        mma(acc, op_load<T>(&sH[(vt * 16 + li) * H_LD + kg * KS + lg * KC]), qf[i][kg]);
       acc *= a.scale;
 #pragma unroll
       for (int kg = 0; kg < NKT; ++kg)
         if (kg <= kgmax)
-          mma(acc, op_load<T>(&sV[(vt * 16 + li) * V_LD + kg * KS + lg * KC]), af[kg]);
+          mma(acc, op_load<T>(&sV[(vt * 16 + li) * V_LD + kg * KS + lg * KC]), af[i][kg]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] = sanitize(acc[r]);
       if (t < cr.valid) store4(obase + (size_t)t * HD + vt * 16 + 4 * lg, acc);
