@@ -46,7 +46,25 @@ static int check_opt(std::initializer_list<const void*> ps) {
   return GDN2_OK;
 }
 
-static size_t nchunks(int B, int T, int H, int BT) { return (size_t)B * H * (size_t)(T / BT); }
+// Chunks per sequence, a short last chunk included.
+static int chunks_per_seq(int T, int BT) { return BT > 0 ? (T + BT - 1) / BT : 0; }
+static size_t nchunks(int B, int T, int H, int BT) {
+  return (size_t)B * H * (size_t)chunks_per_seq(T, BT);
+}
+
+// gdn2_validate, with T % BT != 0 accepted when flags has GDN2_FWD_PARTIAL_CHUNK.
+static int validate_fwd(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
+                        int flags) {
+  if ((flags & GDN2_FWD_PARTIAL_CHUNK) && T > 0 && BT > 0 && T % BT != 0) {
+    const int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
+    if (rc != GDN2_ERR_SEQ_LEN) return rc;
+    // the same checks on the rounded-up length (the size limit included)
+    return (long long)chunks_per_seq(T, BT) * BT > 0x7fffffffLL
+               ? GDN2_ERR_SHAPE
+               : gdn2_validate(B, chunks_per_seq(T, BT) * BT, H, D, BT, in_dtype, g_dtype);
+  }
+  return gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
+}
 
 // Dispatch on (in dtype, g dtype, BT, D).
 template <template <typename, typename, int, int> class F, typename... A>
@@ -161,15 +179,15 @@ int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype)
 // Forward workspace for the segment count that `flags` selects (automatic
 // when its segment field is 0).
 static size_t fwd_ws_need(int B, int T, int H, int D, int BT, int in_dtype, int flags) {
-  const int N = BT > 0 ? T / BT : 0;
+  const int N = chunks_per_seq(T, BT);
   const int S = state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
   return fwd_layout(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype),
                     S > 1 ? (size_t)B * H * S : 0).total;
 }
 
 size_t gdn2_fwd_workspace_bytes_ex(int B, int T, int H, int D, int BT, int in_dtype, int flags) {
-  if (gdn2_validate(B, T, H, D, BT, in_dtype, in_dtype) != GDN2_OK &&
-      gdn2_validate(B, T, H, D, BT, in_dtype, GDN2_F32) != GDN2_OK)
+  if (validate_fwd(B, T, H, D, BT, in_dtype, in_dtype, flags) != GDN2_OK &&
+      validate_fwd(B, T, H, D, BT, in_dtype, GDN2_F32, flags) != GDN2_OK)
     return 0;
   return fwd_ws_need(B, T, H, D, BT, in_dtype, flags);
 }
@@ -184,7 +202,7 @@ static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_d
                       float* h_final, void* ws, size_t ws_bytes, float* a_dbg,
                       int flags) {
   EventScope scope;
-  int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
+  int rc = validate_fwd(B, T, H, D, BT, in_dtype, g_dtype, flags);
   if (rc) return rc;
   if ((flags & GDN2_FWD_RAW_INPUTS) && (flags & GDN2_FWD_SAVE_A)) return GDN2_ERR_FLAGS;
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, out}))) return rc;
@@ -212,7 +230,7 @@ int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtyp
                    float* h_final, void* ws, size_t ws_bytes, float* a_out) {
   if (!a_out && T > 0) return GDN2_ERR_NULL;
   return fwd_common(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale,
-                    out, h_final, ws, ws_bytes, a_out, 0);
+                    out, h_final, ws, ws_bytes, a_out, GDN2_FWD_PARTIAL_CHUNK);
 }
 
 size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {

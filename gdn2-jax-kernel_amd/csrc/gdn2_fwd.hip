@@ -45,14 +45,17 @@ struct PrepArgs {
 
 // First token row of chunk c and its number of real tokens: from the chunk table
 // of a variable-length batch (clamped to [0, BT] and to the T rows), else
-// c*BT within batch element bb.
+// c*BT within batch element bb, with min(BT, T_len - c*BT) real tokens.
 struct ChunkRows {
   size_t row0;
   int valid;
 };
 __device__ __forceinline__ ChunkRows chunk_rows(const int* cstart, int c, int bb, int T_len,
                                                 int BT) {
-  if (!cstart) return ChunkRows{(size_t)bb * T_len + (size_t)c * BT, BT};
+  if (!cstart) {  // equal sequences of T_len tokens; the last chunk may be short
+    const int rest = T_len - c * BT;
+    return ChunkRows{(size_t)bb * T_len + (size_t)c * BT, rest < BT ? rest : BT};
+  }
   const int r0 = cstart[c];
   int v = cstart[c + 1] - r0;
   v = v < BT ? v : BT;
@@ -968,7 +971,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, float* out, float* h_final, char* ws,
                       float* a_dbg, int flags, const Varlen* vl) {
-  const int N = vl ? vl->total_chunks : T_len / BT;
+  const int N = vl ? vl->total_chunks : (T_len + BT - 1) / BT;
   const size_t NC = (size_t)B * H * N;
   const int S_ws = vl ? 1 : state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
   const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), S_ws > 1 ? (size_t)B * H * S_ws : 0);

@@ -20,6 +20,7 @@ GDN2_F32 = 0
 GDN2_BF16 = 1
 FWD_SAVE_A = 1
 FWD_RAW_INPUTS = 2
+FWD_PARTIAL_CHUNK = 4
 
 
 def FWD_SEGMENTS(n: int) -> int:

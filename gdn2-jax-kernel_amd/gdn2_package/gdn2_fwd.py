@@ -111,7 +111,12 @@ class _Prepared:
         self.BT = chunk_size_for(in_dt, chunk_size)
         self.args = (self.B, self.T, self.H, self.D, self.BT, _dtype_code(in_dt),
                      _dtype_code(g_dt))
-        rc = _lib.lib().gdn2_validate(*self.args)
+        # T % BT != 0: the last chunk is short (GDN2_FWD_PARTIAL_CHUNK); the
+        # reference asserts instead (gdn2_fwd.py:146)
+        self.N = -(-self.T // self.BT) if self.BT > 0 else 0
+        self.partial = self.BT > 0 and self.T % self.BT != 0
+        rc = _lib.lib().gdn2_validate(self.B, self.N * self.BT if self.partial else self.T,
+                                      *self.args[2:])
         if rc:
             _raise(rc, f"gdn2 (B,T,H,D)={tuple(q.shape)}, BT={self.BT}")
         if h0 is not None and tuple(h0.shape) != (self.B, self.H, self.D, self.D):
@@ -140,7 +145,10 @@ def _run_forward(p: _Prepared, debug_a: bool = False, flags: int = 0):
     """One gdn2_fwd call; `flags` as in include/gdn2.h (GDN2_FWD_SAVE_A,
     GDN2_FWD_SEGMENTS(n)).  The debug path ignores flags."""
     L = _lib.lib()
-    nbytes = L.gdn2_fwd_workspace_bytes_ex(*p.args[:6], 0 if debug_a else flags)
+    if p.partial:
+        flags |= _lib.FWD_PARTIAL_CHUNK
+    nbytes = L.gdn2_fwd_workspace_bytes_ex(*p.args[:6], _lib.FWD_PARTIAL_CHUNK if debug_a
+                                           else flags)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=p.device)
     out = torch.empty((p.B, p.T, p.H, p.D), dtype=torch.float32, device=p.device)
     h_final = torch.empty((p.B, p.H, p.D, p.D), dtype=torch.float32, device=p.device)
@@ -149,8 +157,8 @@ def _run_forward(p: _Prepared, debug_a: bool = False, flags: int = 0):
               ws.data_ptr(), nbytes)
     a_out = None
     if debug_a:
-        N = p.T // p.BT
-        a_out = torch.empty((p.B, p.H, N, p.BT, p.BT), dtype=torch.float32, device=p.device)
+        a_out = torch.empty((p.B, p.H, p.N, p.BT, p.BT), dtype=torch.float32,
+                            device=p.device)
         rc = L.gdn2_fwd_debug(*common, a_out.data_ptr())
     else:
         rc = L.gdn2_fwd(*common, flags)
@@ -161,6 +169,10 @@ def _run_forward(p: _Prepared, debug_a: bool = False, flags: int = 0):
 
 def gdn2_pallas_forward(q, k, v, w, b, g, scale, h0=None, debug_tag="", chunk_size=None):
     """Forward A->B->C->D (gdn2_fwd.py:400-424) on the gfx950 library.
+
+    T need not be a multiple of the chunk size: the last chunk of each sequence
+    is then short, padded inside the kernels with neutral tokens (the reference
+    asserts T % BT == 0, gdn2_fwd.py:146).
 
     ``debug_tag`` prefixes the GDN2_FWD_DIAG stage reports (gdn2_fwd.py:47-76,
     406-419); without GDN2_FWD_DIAG=1 it is unused.
@@ -179,8 +191,7 @@ def gdn2_pallas_forward(q, k, v, w, b, g, scale, h0=None, debug_tag="", chunk_si
 
 def _residual_views(p: _Prepared, ws: torch.Tensor):
     """Workspace tensors as (B,H,N,...) views in the reference's layouts."""
-    B, H, D, BT = p.B, p.H, p.D, p.BT
-    N = p.T // BT
+    B, H, D, BT, N = p.B, p.H, p.D, p.BT, p.N
     es = 4 if p.in_dt == torch.float32 else 2
     NC = B * H * N
     sizes = [("W", NC * BT * D * es), ("UT", NC * D * BT * 4), ("KgT", NC * D * BT * es),

@@ -78,8 +78,20 @@ class _GDN2Core(torch.autograd.Function):
 
 def gdn2_pallas_forward_trainable(q, k, v, w, b, g, scale, h0=None, chunk_size=None,
                                   recompute=False):
-    """gdn2_pipeline.py:143-159.  h0 defaults to a zero float32 state."""
+    """gdn2_pipeline.py:143-159.  h0 defaults to a zero float32 state.
+
+    T % chunk != 0 (the reference asserts, gdn2_fwd.py:146): the inputs are
+    padded with zero tokens up to whole chunks.  A zero token is neutral (k = 0
+    adds nothing to the state, g = 0 does not decay it, q = 0 reads nothing), so
+    out[:, :T], h_final and every gradient of the real tokens are unchanged;
+    the pad costs one copy of the inputs."""
+    B, T, H, D = q.shape
     if h0 is None:
-        B, T, H, D = q.shape
         h0 = torch.zeros((B, H, D, D), dtype=torch.float32, device=q.device)
+    bt = TRAIN_CHUNK if chunk_size is None else int(chunk_size)
+    pad = (-T) % bt if bt > 0 else 0
+    if pad:
+        xs = [torch.nn.functional.pad(x, (0, 0, 0, 0, 0, pad)) for x in (q, k, v, w, b, g)]
+        out, h_final = _GDN2Core.apply(*xs, h0, scale, chunk_size, recompute)
+        return out[:, :T], h_final
     return _GDN2Core.apply(q, k, v, w, b, g, h0, scale, chunk_size, recompute)

@@ -78,6 +78,14 @@ size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
  * design of the reference's kernel D, gdn2_fwd.py:338-366).  n is clamped to
  * [1, T/BT]; a forced count needs gdn2_fwd_workspace_bytes_ex's workspace. */
 #define GDN2_FWD_SEGMENTS(n) (((n) & 0xff) << 8)
+/* Accept T % BT != 0: the last chunk of each sequence holds T % BT tokens and
+ * is padded inside the kernels with neutral tokens (k = q = 0, g = 0; the state
+ * passes through them unchanged), so out and h_final equal the forward over the
+ * T real tokens.  Without this flag T % BT != 0 is GDN2_ERR_SEQ_LEN, as the
+ * reference asserts (gdn2_fwd.py:146).  gdn2_fwd_workspace_bytes_ex with the
+ * same flag sizes the workspace.  Not for gdn2_bwd (its inputs are whole
+ * chunks: a caller pads with zero tokens, which leaves every result unchanged). */
+#define GDN2_FWD_PARTIAL_CHUNK 4
 
 /* As gdn2_fwd_workspace_bytes, for the segment count `flags` selects.  No
  * counterpart in the reference (its scan is serial); used to force a count. */

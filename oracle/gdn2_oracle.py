@@ -49,7 +49,7 @@ DECAY_CLIP = 20.0
 MB = 16
 
 __all__ = [
-    "CLIP", "sanitize", "make_inputs", "recurrent_fwd", "chunk_scores", "wy_solve",
+    "CLIP", "sanitize", "make_inputs", "recurrent_fwd", "recurrent_grads", "chunk_scores", "wy_solve",
     "recompute_wy", "inter_chunk_combine", "chunked_fwd", "chunked_bwd",
     "assoc_scan_fwd", "to_chunks", "from_chunks",
 ]
@@ -108,6 +108,35 @@ def recurrent_fwd(q, k, v, w, b, g, scale, h0=None):
         S = S + np.einsum("bhd,bhe->bhde", k[:, t], delta)
         out[:, t] = scale * np.einsum("bhd,bhde->bhe", q[:, t], S)
     return out, S
+
+
+def recurrent_grads(q, k, v, w, b, g, scale, do, dh_final=None, h0=None):
+    """Gradients (dq,dk,dv,dw,db,dg,dh0) of ``recurrent_fwd`` for the loss
+    sum(out * do) + sum(h_final * dh_final), by torch.autograd in float64 on the
+    CPU.  Valid for any T (chunk sizes play no part), which ``chunked_bwd``'s
+    16-token sub-blocks do not allow; no clipping (the reference's clip is
+    inactive at test magnitudes)."""
+    import torch
+    xs = [torch.tensor(np.asarray(x, dtype=np.float64), requires_grad=True)
+          for x in (q, k, v, w, b, g)]
+    B, T, H, D = xs[0].shape
+    Dv = xs[2].shape[-1]
+    S0 = torch.zeros((B, H, D, Dv), dtype=torch.float64) if h0 is None else \
+        torch.tensor(np.asarray(h0, dtype=np.float64))
+    S0.requires_grad_(True)
+    qt, kt, vt, wt, bt, gt = xs
+    S, outs = S0, []
+    for t in range(T):
+        S = torch.exp(gt[:, t])[..., None] * S
+        pred = torch.einsum("bhd,bhde->bhe", bt[:, t] * kt[:, t], S)
+        S = S + torch.einsum("bhd,bhe->bhde", kt[:, t], wt[:, t] * vt[:, t] - pred)
+        outs.append(scale * torch.einsum("bhd,bhde->bhe", qt[:, t], S))
+    out = torch.stack(outs, 1) if T else torch.zeros((B, 0, H, Dv), dtype=torch.float64)
+    loss = (out * torch.tensor(np.asarray(do, dtype=np.float64))).sum()
+    if dh_final is not None:
+        loss = loss + (S * torch.tensor(np.asarray(dh_final, dtype=np.float64))).sum()
+    loss.backward()
+    return tuple(x.grad.numpy() for x in xs) + (S0.grad.numpy(),)
 
 
 # ----------------------------------------------------------------------------

@@ -94,6 +94,15 @@ def test_fwd_rejects_before_launch():
     # raw inputs are inference-only
     assert _fwd(L, good, fake, None, 0x1000, 0x2000, 0x3000, ws_need,
                 _lib.FWD_RAW_INPUTS | _lib.FWD_SAVE_A) == _lib.ERR_FLAGS
+    # a short last chunk only with GDN2_FWD_PARTIAL_CHUNK; sized as the rounded-up T
+    part = (1, 500, 2, 64, 64, F32, F32)
+    ws_part = L.gdn2_fwd_workspace_bytes_ex(*part[:6], _lib.FWD_PARTIAL_CHUNK)
+    assert L.gdn2_fwd_workspace_bytes(*part[:6]) == 0
+    assert ws_part == L.gdn2_fwd_workspace_bytes(1, 512, 2, 64, 64, F32)
+    assert _fwd(L, part, fake, None, 0x1000, 0x2000, 0x3000, ws_part - 1,
+                _lib.FWD_PARTIAL_CHUNK) == _lib.ERR_WORKSPACE
+    assert _fwd(L, (1, 500, 2, 96, 64, F32, F32), fake, None, 0x1000, 0x2000, 0x3000,
+                ws_part, _lib.FWD_PARTIAL_CHUNK) == _lib.ERR_HEAD_DIM
     # then workspace size
     assert _fwd(L, good, fake, None, 0x1000, 0x2000, 0x3000, ws_need - 1) == _lib.ERR_WORKSPACE
     assert _fwd(L, good, fake, None, 0x1000, 0x2000, None, ws_need) == _lib.ERR_NULL

@@ -26,7 +26,7 @@ def _inputs(shape, dtype=torch.float32):
     return [torch.zeros(shape, dtype=dtype) for _ in range(6)]
 
 
-@pytest.mark.parametrize("shape", [(1, 512, 2, 96), (1, 500, 2, 64)])
+@pytest.mark.parametrize("shape", [(1, 512, 2, 96), (1, 512, 2, 32)])
 def test_shape_errors_are_assertion_errors(shape):
     import gdn2_package as gp
     with pytest.raises(AssertionError):
@@ -41,6 +41,15 @@ def test_mismatched_input_shapes_rejected():
     xs[3] = torch.zeros((1, 128, 2, 32))
     with pytest.raises(gp.GDN2ShapeError):
         gp.gdn2_pallas_forward(*xs, 0.1)
+
+
+def test_partial_last_chunk_passes_validation():
+    """T % BT != 0 is accepted (short last chunk); the reference asserts
+    (gdn2_fwd.py:146).  On host tensors the device check is what refuses."""
+    import gdn2_package as gp
+    with pytest.raises(gp.GDN2Error) as e:
+        gp.gdn2_pallas_forward(*_inputs((1, 500, 2, 64)), 0.1)
+    assert not isinstance(e.value, gp.GDN2ShapeError)
 
 
 def test_no_cpu_fallback():

@@ -78,6 +78,22 @@ def test_bwd_matches_oracle_fp32(dev, B, T, H, D, h0, dh, gs):
     check(grads, ref, 1e-4)
 
 
+@pytest.mark.parametrize("T,h0", [(200, True), (37, False)])
+def test_bwd_partial_last_chunk(dev, T, h0):
+    """T % 64 != 0 in the trainable path (zero tokens pad the inputs to whole
+    chunks): gradients of the real tokens against the oracle's."""
+    B, H, D = 1, 2, 64
+    xs = O.make_inputs(B, T, H, D, seed=T + 3)
+    rng = np.random.default_rng(12)
+    h0n = (0.2 * rng.standard_normal((B, H, D, D))).astype(np.float32) if h0 else None
+    do = rng.standard_normal((B, T, H, D)).astype(np.float32)
+    dhn = rng.standard_normal((B, H, D, D)).astype(np.float32)
+    (out, _), grads, _ = run_grads(xs, D ** -0.5, do, dhn, h0=h0n, dev=dev)
+    assert out.shape == (B, T, H, D)
+    ref = O.recurrent_grads(*xs, D ** -0.5, do, dhn, h0=h0n)
+    check(grads, ref, 1e-4)
+
+
 def test_bwd_bf16_inputs(dev):
     xs = O.make_inputs(1, 256, 2, 128, seed=21)
     rng = np.random.default_rng(3)

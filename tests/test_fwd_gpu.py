@@ -237,7 +237,43 @@ def test_deterministic_and_noncontiguous(dev):
 
 def test_shape_errors_on_device(dev):
     with pytest.raises(AssertionError):
-        gp().gdn2_pallas_forward(*[torch.zeros((1, 100, 2, 64), device=dev)] * 6, 0.1)
+        gp().gdn2_pallas_forward(*[torch.zeros((1, 128, 2, 96), device=dev)] * 6, 0.1)
+
+
+# ----------------------------------------------------------------------------- T % BT tails
+@pytest.mark.parametrize("B,T,H,D,dtype,BT,h0", [
+    (2, 500, 2, 64, torch.float32, 64, True),      # 7 full chunks + 52 tokens
+    (1, 1, 2, 128, torch.float32, 64, True),       # one token: T < BT
+    (2, 200, 3, 128, torch.bfloat16, 128, False),  # 1 full + 72
+    (1, 129, 2, 64, torch.bfloat16, 128, True),    # one token in the last chunk
+    (1, 77, 2, 128, torch.bfloat16, 64, False),
+])
+def test_partial_last_chunk_matches_oracle(dev, B, T, H, D, dtype, BT, h0):
+    """T % BT != 0 (the reference asserts, gdn2_fwd.py:146): the token recurrence
+    over the real T tokens is the oracle."""
+    xs = O.make_inputs(B, T, H, D, seed=T + 7 * D + H)
+    h0n = (0.1 * np.random.default_rng(6).standard_normal((B, H, D, D))).astype(np.float32) \
+        if h0 else None
+    xt = to_dev(xs, dev, dtype)
+    h0t = None if h0n is None else torch.tensor(h0n, device=dev)
+    out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5, h0=h0t, chunk_size=BT)
+    assert out.shape == (B, T, H, D)
+    ro, rh = O.recurrent_fwd(*host(xt), D ** -0.5, h0=h0n)
+    ok_o, e_o = close(out.cpu().numpy(), ro, TOL[dtype])
+    ok_h, e_h = close(hf.cpu().numpy(), rh, TOL[dtype])
+    assert ok_o and ok_h, (e_o, e_h)
+
+
+def test_partial_last_chunk_equals_zero_padded_inputs(dev):
+    """A short last chunk acts as zero-padded tokens: the forward on inputs padded
+    with zero rows up to whole chunks gives the same out rows and h_final."""
+    B, T, H, D, BT = 2, 300, 2, 128, 128
+    xt = to_dev(O.make_inputs(B, T, H, D, seed=31), dev, torch.bfloat16)
+    o1, h1 = gp().gdn2_pallas_forward(*xt, 0.1, chunk_size=BT)
+    pad = [torch.nn.functional.pad(x, (0, 0, 0, 0, 0, 384 - T)) for x in xt]
+    o2, h2 = gp().gdn2_pallas_forward(*pad, 0.1, chunk_size=BT)
+    assert torch.allclose(o1, o2[:, :T], rtol=1e-5, atol=1e-6)
+    assert torch.allclose(h1, h2, rtol=1e-5, atol=1e-6)
 
 
 # ----------------------------------------------------------------------------- segments

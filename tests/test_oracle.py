@@ -235,6 +235,39 @@ def test_backward_matches_autograd(BT):
         assert maxerr(gv, ref) < 1e-10 * max(1.0, np.abs(ref).max()), name
 
 
+def test_recurrent_grads_match_chunked_bwd_and_finite_differences():
+    """recurrent_grads (autograd of the token recurrence, any T) against
+    chunked_bwd at a whole number of chunks and against a central finite
+    difference in one coordinate of each input."""
+    q, k, v, w, b, g = inputs(B=1, T=64, H=2, D=8, seed=4)
+    rng = np.random.default_rng(9)
+    h0 = rng.standard_normal((1, 2, 8, 8)) * 0.3
+    do = rng.standard_normal(q.shape)
+    dh = rng.standard_normal(h0.shape)
+    got = O.recurrent_grads(q, k, v, w, b, g, 0.35, do, dh, h0=h0)
+    ref = O.chunked_bwd(q, k, v, w, b, g, 0.35, do, dh, h0=h0, BT=32, clip=False)
+    for gv, rv in zip(got, ref):
+        assert maxerr(gv, rv) < 1e-10 * max(1.0, np.abs(rv).max())
+    q2, k2, v2, w2, b2, g2 = inputs(B=1, T=37, H=1, D=4, seed=2)
+    h02 = rng.standard_normal((1, 1, 4, 4)) * 0.3
+    do2 = rng.standard_normal(q2.shape)
+    dh2 = rng.standard_normal(h02.shape)
+    got2 = O.recurrent_grads(q2, k2, v2, w2, b2, g2, 0.35, do2, dh2, h0=h02)
+    xs2 = [q2, k2, v2, w2, b2, g2, h02]
+    def loss2(ys):
+        o, h = O.recurrent_fwd(*ys[:6], 0.35, h0=ys[6])
+        return float((o * do2).sum() + (h * dh2).sum())
+    for i, gv in enumerate(got2):
+        idx = (0, 36, 0, 3) if i < 6 else (0, 0, 2, 1)
+        eps = 1e-6
+        up = [x.copy() for x in xs2]
+        dn = [x.copy() for x in xs2]
+        up[i][idx] += eps
+        dn[i][idx] -= eps
+        fd = (loss2(up) - loss2(dn)) / (2 * eps)
+        assert abs(gv[idx] - fd) < 1e-6 * max(1.0, abs(fd)), (i, gv[idx], fd)
+
+
 def test_backward_finite_differences():
     q, k, v, w, b, g = inputs(B=1, T=32, H=1, D=4, seed=8)
     rng = np.random.default_rng(7)
