@@ -74,16 +74,19 @@ static int dispatch(int in_dtype, int g_dtype, int BT, int D, A... args) {
   if (in_dtype == GDN2_F32 && g_dtype == GDN2_F32) {
     GDN2_CASE(float, float, 64, 64)
     GDN2_CASE(float, float, 64, 128)
+    GDN2_CASE(float, float, 64, 256)
   } else if (in_dtype == GDN2_BF16 && g_dtype == GDN2_F32) {
     GDN2_CASE(bf16_t, float, 64, 64)
     GDN2_CASE(bf16_t, float, 64, 128)
     GDN2_CASE(bf16_t, float, 128, 64)
     GDN2_CASE(bf16_t, float, 128, 128)
+    GDN2_CASE(bf16_t, float, 64, 256)
   } else if (in_dtype == GDN2_BF16 && g_dtype == GDN2_BF16) {
     GDN2_CASE(bf16_t, bf16_t, 64, 64)
     GDN2_CASE(bf16_t, bf16_t, 64, 128)
     GDN2_CASE(bf16_t, bf16_t, 128, 64)
     GDN2_CASE(bf16_t, bf16_t, 128, 128)
+    GDN2_CASE(bf16_t, bf16_t, 64, 256)
   }
 #undef GDN2_CASE
   return GDN2_ERR_CHUNK;
@@ -108,9 +111,14 @@ struct BwdRun {
                  float scale, const float* dout, const float* dh_final, void* dq, void* dk,
                  void* dv, void* dw, void* db, void* dg, float* dh0, const char* fws,
                  char* ws) {
-    hipError_t e = launch_bwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale, dout,
-                                            dh_final, dq, dk, dv, dw, db, dg, dh0, fws, ws);
-    return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+    if constexpr (D > 128) {
+      return GDN2_ERR_HEAD_DIM;  // the backward kernels are built for D <= 128
+    } else {
+      hipError_t e = launch_bwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale,
+                                              dout, dh_final, dq, dk, dv, dw, db, dg, dh0, fws,
+                                              ws);
+      return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+    }
   }
 };
 
@@ -149,9 +157,11 @@ int gdn2_set_launch_events(void* const* events, int n) {
 const char* gdn2_strerror(int code) {
   switch (code) {
     case GDN2_OK: return "ok";
-    case GDN2_ERR_HEAD_DIM: return "head dim D must be 64 or 128";
+    case GDN2_ERR_HEAD_DIM:
+      return "head dim D must be 64, 128 or 256 (256: forward and decode only)";
     case GDN2_ERR_SEQ_LEN: return "sequence length T must be divisible by the chunk size BT";
-    case GDN2_ERR_CHUNK: return "chunk size BT must be 64 or 128 (128 needs bfloat16 inputs)";
+    case GDN2_ERR_CHUNK:
+      return "chunk size BT must be 64 or 128 (128 needs bfloat16 inputs and D <= 128)";
     case GDN2_ERR_DTYPE: return "unsupported dtype (inputs: float32 or bfloat16; g: float32, or bfloat16 with bfloat16 inputs)";
     case GDN2_ERR_NULL: return "required pointer is NULL";
     case GDN2_ERR_ALIGN: return "pointer is not 16-byte aligned";
@@ -168,9 +178,9 @@ int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype)
   if (in_dtype != GDN2_F32 && in_dtype != GDN2_BF16) return GDN2_ERR_DTYPE;
   if (g_dtype != GDN2_F32 && g_dtype != GDN2_BF16) return GDN2_ERR_DTYPE;
   if (in_dtype == GDN2_F32 && g_dtype != GDN2_F32) return GDN2_ERR_DTYPE;
-  if (D != 64 && D != 128) return GDN2_ERR_HEAD_DIM;
+  if (D != 64 && D != 128 && D != 256) return GDN2_ERR_HEAD_DIM;
   if (BT != 64 && BT != 128) return GDN2_ERR_CHUNK;
-  if (BT == 128 && in_dtype == GDN2_F32) return GDN2_ERR_CHUNK;
+  if (BT == 128 && (in_dtype == GDN2_F32 || D == 256)) return GDN2_ERR_CHUNK;
   if (T % BT != 0) return GDN2_ERR_SEQ_LEN;
   if ((double)B * T * H * D > 9.0e15) return GDN2_ERR_SHAPE;
   return GDN2_OK;
@@ -234,6 +244,7 @@ int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtyp
 }
 
 size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {
+  if (D > 128) return 0;  // forward only at D = 256
   if (gdn2_validate(B, T, H, D, BT, in_dtype, in_dtype) != GDN2_OK &&
       gdn2_validate(B, T, H, D, BT, in_dtype, GDN2_F32) != GDN2_OK)
     return 0;
@@ -249,6 +260,7 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
   EventScope scope;
   int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
+  if (D > 128) return GDN2_ERR_HEAD_DIM;  // forward only at D = 256
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, dout, dq, dk, dv, dw, db, dg}))) return rc;
   if ((rc = check_ptrs({dh0}))) return rc;
   if ((rc = check_opt({h0, dh_final}))) return rc;
@@ -309,12 +321,15 @@ int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, co
   if (in_dtype == GDN2_F32) {
     GDN2_DEC(float, float, 64)
     GDN2_DEC(float, float, 128)
+    GDN2_DEC(float, float, 256)
   } else if (g_dtype == GDN2_F32) {
     GDN2_DEC(bf16_t, float, 64)
     GDN2_DEC(bf16_t, float, 128)
+    GDN2_DEC(bf16_t, float, 256)
   } else {
     GDN2_DEC(bf16_t, bf16_t, 64)
     GDN2_DEC(bf16_t, bf16_t, 128)
+    GDN2_DEC(bf16_t, bf16_t, 256)
   }
 #undef GDN2_DEC
   return GDN2_ERR_HEAD_DIM;

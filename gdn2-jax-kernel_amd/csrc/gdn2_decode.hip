@@ -6,31 +6,38 @@
 // are sanitized like every chunk state and output, gdn2_fwd.py:355-356).  The
 // state layout is h0 / h_final's: S[b][h][dk][dv] (gdn2_fwd.py:342).
 //
-// One 256-thread workgroup per (b,h): thread (column e, row group rg) keeps
+// One 256-thread workgroup per (b,h) and slice of CS state columns (all D
+// columns up to D = 128, 64 at D = 256): thread (column e, row group rg) keeps
 // D / RG state rows of column e in registers.  Both column reductions (pred
-// and o) are summed over the row groups in LDS.  The state is read and written
-// once (memory-bound); h_out may alias h_in.
+// and o) run over the rows, so the columns split freely; they are summed over
+// the row groups in LDS.  The state is read and written once (memory-bound);
+// h_out may alias h_in.
 #include "gdn2_common.h"
 
 namespace gdn2 {
+
+template <int D>
+constexpr int decode_cols() { return D <= 128 ? D : 64; }
 
 template <typename T, typename TG, int D>
 __global__ void __launch_bounds__(256) decode_step(const T* q, const T* k, const T* v,
                                                    const T* w, const T* b, const TG* g,
                                                    float scale, const float* h_in,
                                                    float* h_out, float* out) {
-  constexpr int RG = 256 / D, RPT = D / RG;   // row groups, rows per thread
+  constexpr int CS = decode_cols<D>(), NSL = D / CS;
+  constexpr int RG = 256 / CS, RPT = D / RG;   // row groups, rows per thread
   __shared__ float sQ[D], sK[D], sBK[D], sEG[D];
-  __shared__ float sRed[RG][D];
-  const int tid = threadIdx.x, e = tid % D, rg = tid / D;
-  const size_t bh = blockIdx.x;
+  __shared__ float sRed[RG][CS];
+  const int tid = threadIdx.x, e = tid % CS, rg = tid / CS;
+  const size_t bh = blockIdx.x / NSL;
+  const int col = (blockIdx.x % NSL) * CS + e;
   const size_t vo = bh * D;                  // token vectors are (B,H,D) contiguous
-  if (tid < D) {
-    const float kv = to_f(k[vo + tid]);
-    sQ[tid] = to_f(q[vo + tid]);
-    sK[tid] = kv;
-    sBK[tid] = to_f(b[vo + tid]) * kv;
-    sEG[tid] = __expf(to_f(g[vo + tid]));
+  for (int i = tid; i < D; i += 256) {
+    const float kv = to_f(k[vo + i]);
+    sQ[i] = to_f(q[vo + i]);
+    sK[i] = kv;
+    sBK[i] = to_f(b[vo + i]) * kv;
+    sEG[i] = __expf(to_f(g[vo + i]));
   }
   __syncthreads();
   const float* src = h_in ? h_in + bh * D * D : nullptr;
@@ -39,7 +46,7 @@ __global__ void __launch_bounds__(256) decode_step(const T* q, const T* k, const
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
     const int d = rg * RPT + i;
-    s[i] = (src ? sanitize(src[(size_t)d * D + e]) : 0.f) * sEG[d];
+    s[i] = (src ? sanitize(src[(size_t)d * D + col]) : 0.f) * sEG[d];
     pred += sBK[d] * s[i];
   }
   sRed[rg][e] = pred;
@@ -47,7 +54,7 @@ __global__ void __launch_bounds__(256) decode_step(const T* q, const T* k, const
   pred = 0.f;
 #pragma unroll
   for (int r = 0; r < RG; ++r) pred += sRed[r][e];
-  const float delta = to_f(w[vo + e]) * to_f(v[vo + e]) - pred;
+  const float delta = to_f(w[vo + col]) * to_f(v[vo + col]) - pred;
   __syncthreads();  // every thread has read sRed
   float o = 0.f;
   float* dst = h_out + bh * D * D;
@@ -55,7 +62,7 @@ __global__ void __launch_bounds__(256) decode_step(const T* q, const T* k, const
   for (int i = 0; i < RPT; ++i) {
     const int d = rg * RPT + i;
     const float nv = sanitize(s[i] + sK[d] * delta);
-    dst[(size_t)d * D + e] = nv;
+    dst[(size_t)d * D + col] = nv;
     o += sQ[d] * nv;
   }
   sRed[rg][e] = o;
@@ -64,7 +71,7 @@ __global__ void __launch_bounds__(256) decode_step(const T* q, const T* k, const
     o = 0.f;
 #pragma unroll
     for (int r = 0; r < RG; ++r) o += sRed[r][e];
-    out[vo + e] = sanitize(scale * o);
+    out[vo + col] = sanitize(scale * o);
   }
 }
 
@@ -73,7 +80,8 @@ hipError_t launch_decode(hipStream_t st, int B, int H, const void* q, const void
                          const void* v, const void* w, const void* b, const void* g,
                          float scale, const float* h_in, float* h_out, float* out) {
   launch_mark(st);
-  hipLaunchKernelGGL((decode_step<T, TG, D>), dim3((size_t)B * H), dim3(256), 0, st,
+  hipLaunchKernelGGL((decode_step<T, TG, D>), dim3((size_t)B * H * (D / decode_cols<D>())),
+                     dim3(256), 0, st,
                      (const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
                      (const TG*)g, scale, h_in, h_out, out);
   launch_mark(st);
@@ -91,5 +99,8 @@ GDN2_INST_DEC(bf16_t, float, 64)
 GDN2_INST_DEC(bf16_t, float, 128)
 GDN2_INST_DEC(bf16_t, bf16_t, 64)
 GDN2_INST_DEC(bf16_t, bf16_t, 128)
+GDN2_INST_DEC(float, float, 256)
+GDN2_INST_DEC(bf16_t, float, 256)
+GDN2_INST_DEC(bf16_t, bf16_t, 256)
 
 }  // namespace gdn2

@@ -102,6 +102,13 @@ __device__ __forceinline__ float row_bcast(float x) {
 // twice as many blocks as waves (equal work for the triangular loops).  Per element four
 // exponentials are evaluated (e^{loc}, e^{T_I - loc} and the two diagonal-block
 // factors); the block-level factors e^{P_{I-1}}, e^{S_{I+1}} come from LDS.
+//
+// Channels are processed in panels of up to 128 (D = 256: two panels).  The
+// cumsum, decay factors, q_g / kg^T / (b k e^gc)^T and khat are per channel, so
+// steps 1-3 run once per panel; the score blocks Aqk, Akk are sums over
+// channels, accumulated over the panels in float32 LDS (sA, sQA) and stored
+// after the last one.  u = A (w v) is computed per panel of (w v)^T.  With one
+// panel (D <= 128) every score block is stored as soon as it is computed.
 constexpr int prep_waves(int BT) { return BT >= 128 ? 8 : 4; }
 
 template <typename T, typename TG, int BT, int D>
@@ -112,21 +119,25 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   constexpr int PW = prep_waves(BT), NT = 64 * PW;   // waves, threads
   constexpr int NBW = NB / PW;            // row blocks per wave
   static_assert(NB % PW == 0 && (NBW == 1 || NBW == 2), "row blocks must split over waves");
-  constexpr int NKD = D / KS;             // k-groups over channels
+  constexpr int DP = D < 128 ? D : 128;   // channels per panel
+  constexpr int NPN = D / DP;             // panels
+  static_assert(D % DP == 0 && DP <= NT, "panels must tile D");
+  constexpr int NKD = DP / KS;            // k-groups over a panel's channels
   constexpr int NKT = BT / KS;            // k-groups over tokens
-  constexpr int DQ = NKD * KC;            // channels owned per lane (= D/4)
+  constexpr int DQ = NKD * KC;            // channels of a panel owned per lane (= DP/4)
   constexpr int PADT = 16 / sizeof(T);
-  constexpr int KH_LD = D + PADT;         // khat [t][d]
+  constexpr int KH_LD = DP + PADT;        // khat [t][d], one panel
   constexpr int TT_LD = BT + PADT;        // [d][t] tiles
   constexpr int A_LD = BT + 4;            // A [t][s] fp32
-  constexpr int R0 = (BT * KH_LD > D * TT_LD) ? BT * KH_LD : D * TT_LD;
+  constexpr int R0 = (BT * KH_LD > DP * TT_LD) ? BT * KH_LD : DP * TT_LD;
 
-  __shared__ __align__(16) T sR0[R0];         // khat [t][d]; later (w v)^T [d][t]
+  __shared__ __align__(16) T sR0[R0];         // khat [t][d]; later (w v)^T [d][t], one panel
   __shared__ __align__(16) T sKbdT[D * TT_LD];  // (b k e^gc)^T [d][t]
   __shared__ __align__(16) float sA[BT * A_LD];
-  __shared__ __align__(16) float sTot[NB * D];  // T_m: per-block sums of g
-  __shared__ __align__(16) float sETot[NB * D]; // e^{T_m}
-  __shared__ __align__(16) float sF[2][NB * D]; // e^{P_{I-1}}, e^{S_{I+1}} per (block, channel)
+  __shared__ __align__(16) float sQA[NPN > 1 ? BT * A_LD : 4];  // Aqk partial sums
+  __shared__ __align__(16) float sTot[NB * DP];  // T_m: per-block sums of g
+  __shared__ __align__(16) float sETot[NB * DP]; // e^{T_m}
+  __shared__ __align__(16) float sF[2][NB * DP]; // e^{P_{I-1}}, e^{S_{I+1}} per (block, channel)
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int cid = blockIdx.x;
@@ -146,194 +157,269 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
     const int t = own_block<NB>(wv, i) * 16 + li, last = cr.valid > 0 ? cr.valid - 1 : 0;
     return rowp(t < last ? t : last);
   };
+  const bool raw = a.raw != 0;
+  T* kgT = a.KgT + (size_t)cid * D * BT;
+  T* aqk = a.Aqk + (size_t)cid * BT * BT;
 
-  // all loads needed before the inverse, issued together
-  float loc[NBW][DQ];
-  Op qo[NBW][NKD], ko[NBW][NKD], bo[NBW][NKD];
+  // raw inputs with several panels: 1 / max(|q|_2, 1e-12) and the same for k over
+  // all D channels, before the panel loop
+  float iqn[NBW], ikn[NBW];
+  if constexpr (NPN > 1) {
+    if (raw) {
 #pragma unroll
-  for (int i = 0; i < NBW; ++i) {
-    const size_t off = load_row(i);
+      for (int i = 0; i < NBW; ++i) {
+        const size_t off = load_row(i);
+        float sq = 0.f, sk = 0.f;
 #pragma unroll
-    for (int j = 0; j < NKD; ++j) {
-      load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
-      qo[i][j] = op_load<T>(a.q + off + j * KS + lg * KC);
-      ko[i][j] = op_load<T>(a.k + off + j * KS + lg * KC);
-      bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
+        for (int pn = 0; pn < NPN; ++pn)
+#pragma unroll
+          for (int j = 0; j < NKD; ++j) {
+            const Op qv = op_load<T>(a.q + off + pn * DP + j * KS + lg * KC);
+            const Op kv = op_load<T>(a.k + off + pn * DP + j * KS + lg * KC);
+#pragma unroll
+            for (int e = 0; e < KC; ++e) {
+              sq += to_f(qv[e]) * to_f(qv[e]);
+              sk += to_f(kv[e]) * to_f(kv[e]);
+            }
+          }
+        sq += __shfl_xor(sq, 16);
+        sq += __shfl_xor(sq, 32);
+        sk += __shfl_xor(sk, 16);
+        sk += __shfl_xor(sk, 32);
+        iqn[i] = 1.f / fmaxf(sqrtf(sq), 1e-12f);
+        ikn[i] = 1.f / fmaxf(sqrtf(sk), 1e-12f);
+      }
     }
   }
-  for (int i = tid; i < BT * A_LD / 4; i += NT)
-    reinterpret_cast<f32x4*>(sA)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- 1. in-block inclusive cumsum of g (lanes li = tokens) ----------------
-  const bool raw = a.raw != 0;
-  if (padded) {
+#pragma unroll
+  for (int pn = 0; pn < NPN; ++pn) {
+    const int d0 = pn * DP;               // first channel of the panel
+    constexpr bool one = NPN == 1;
+    const bool last_pn = pn == NPN - 1;
+    if (pn > 0) __syncthreads();          // the previous panel's LDS reads are done
+
+    // all loads needed before the inverse, issued together
+    float loc[NBW][DQ];
+    Op qo[NBW][NKD], ko[NBW][NKD], bo[NBW][NKD];
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
-      if (!real(i)) {
-#pragma unroll
-        for (int x = 0; x < DQ; ++x) loc[i][x] = 0.f;
-#pragma unroll
-        for (int j = 0; j < NKD; ++j) {
-          qo[i][j] = op_zero<T>();
-          ko[i][j] = op_zero<T>();
-          bo[i][j] = op_zero<T>();
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < NBW; ++i) {
-    const int I = own_block<NB>(wv, i);
-    if (raw) {
-      const bool rv = real(i);
-#pragma unroll
-      for (int x = 0; x < DQ; ++x) loc[i][x] = rv ? neg_softplus(loc[i][x]) : 0.f;
-    }
-#pragma unroll
-    for (int x = 0; x < DQ; ++x) loc[i][x] = row_scan16(loc[i][x]);
-    if (li == 15) {
-#pragma unroll
-      for (int x = 0; x < DQ; ++x) sTot[I * D + chan(x)] = loc[i][x];
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < NB * D; i += NT) {
-    sETot[i] = __expf(sTot[i]);
-  }
-  if (tid < D) {
-    float run = 0.f;
-#pragma unroll
-    for (int m = 0; m < NB; ++m) { sF[0][m * D + tid] = __expf(run); run += sTot[m * D + tid]; }
-    a.GL[(size_t)cid * D + tid] = run;
-    run = 0.f;
-#pragma unroll
-    for (int m = NB - 1; m >= 0; --m) { sF[1][m * D + tid] = __expf(run); run += sTot[m * D + tid]; }
-  }
-  __syncthreads();
-
-  // ---- 2. per-token factors: qg, kbd, kg, khat; diagonal score blocks -------
-  float aq[NBW][DQ], ak[NBW][DQ];
-#pragma unroll
-  for (int i = 0; i < NBW; ++i) {
-    const int I = own_block<NB>(wv, i);
-    const int t = I * 16 + li;
-    T* kgT = a.KgT + (size_t)cid * D * BT;
-    T* qgp = a.Qg + (size_t)cid * BT * D + (size_t)t * D;
-    f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
-    // raw inputs: q,k <- q,k / max(|.|_2, 1e-12) over D (F.normalize) and
-    // b <- sigmoid(b), in place in the loaded registers; a token's channels sit
-    // in the four lanes li, li+16, li+32, li+48
-    if (raw) {
-      float sq = 0.f, sk = 0.f;
-#pragma unroll
-      for (int j = 0; j < NKD; ++j)
-#pragma unroll
-        for (int e = 0; e < KC; ++e) {
-          const float qv = to_f(qo[i][j][e]), kv = to_f(ko[i][j][e]);
-          sq += qv * qv;
-          sk += kv * kv;
-        }
-      sq += __shfl_xor(sq, 16);
-      sq += __shfl_xor(sq, 32);
-      sk += __shfl_xor(sk, 16);
-      sk += __shfl_xor(sk, 32);
-      const float iq = 1.f / fmaxf(sqrtf(sq), 1e-12f), ik = 1.f / fmaxf(sqrtf(sk), 1e-12f);
-#pragma unroll
-      for (int j = 0; j < NKD; ++j)
-#pragma unroll
-        for (int e = 0; e < KC; ++e) {
-          qo[i][j][e] = from_f<T>(to_f(qo[i][j][e]) * iq);
-          ko[i][j][e] = from_f<T>(to_f(ko[i][j][e]) * ik);
-          bo[i][j][e] = from_f<T>(sigmoidf(to_f(bo[i][j][e])));
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < NKD; ++j) {
-      float qg[KC], kh[KC], dq[KC], dk[KC], db[KC];
-#pragma unroll
-      for (int e = 0; e < KC; ++e) {
-        const int x = j * KC + e, ch = chan(x);
-        const float qv = to_f(qo[i][j][e]), kv = to_f(ko[i][j][e]), bv = to_f(bo[i][j][e]);
-        const float lc = loc[i][x];
-        const float eloc = __expf(lc);
-        const float ekh = __expf(sTot[I * D + ch] - lc);
-        const float egc = eloc * sF[0][I * D + ch];
-        const float bk = bv * kv;
-        qg[e] = qv * egc;
-        sKbdT[ch * TT_LD + t] = from_f<T>(bk * egc);
-        kgT[(size_t)ch * BT + kpos<T>(t)] = from_f<T>(kv * ekh * sF[1][I * D + ch]);
-        kh[e] = kv * ekh;
-        aq[i][x] = qv * eloc;
-        ak[i][x] = bk * eloc;
-        // the diagonal-block factors keep their own exponentials: e^{loc} or
-        // e^{T_I-loc} may underflow where e^{loc-loc_m} e^{loc_m-loc'} does not
-        const float lm = row_bcast<7>(lc);
-        const float edq = __expf(lc - lm), edk = __expf(lm - lc);
-        dq[e] = qv * edq;
-        db[e] = bk * edq;
-        dk[e] = kv * edk;
-      }
-      *reinterpret_cast<Op*>(qgp + j * KS + lg * KC) = op_from<T>(qg);
-      *reinterpret_cast<Op*>(&sR0[t * KH_LD + j * KS + lg * KC]) = op_from<T>(kh);
-      // diagonal block, factorised around its 8th token: X = k rows (j),
-      // Y = q / bk rows (i) -> lane holds [i=li][j=4lg+r]
-      const Op xo = op_from<T>(dk);
-      mma(accq, xo, op_from<T>(dq));
-      mma(acck, xo, op_from<T>(db));
-    }
-    f32x4 sq, sk;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int jj = 4 * lg + r;
-      sq[r] = (jj <= li) ? a.scale * accq[r] : 0.f;
-      sk[r] = (jj < li) ? acck[r] : 0.f;
-    }
-    store4(a.Aqk + (size_t)cid * BT * BT + (size_t)t * BT + I * 16 + 4 * lg, sq);
-    store4(&sA[t * A_LD + I * 16 + 4 * lg], sk);
-  }
-  __syncthreads();
-
-  // ---- 3. off-diagonal score blocks (I > J) on MFMA --------------------------
-#pragma unroll
-  for (int i = 0; i < NBW; ++i) {
-    const int I = own_block<NB>(wv, i);
-    const int t = I * 16 + li;
-    float F[DQ];
-#pragma unroll
-    for (int x = 0; x < DQ; ++x) F[x] = 1.f;
-    for (int J = I - 1; J >= 0; --J) {
-      f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
+      const size_t off = load_row(i) + d0;
 #pragma unroll
       for (int j = 0; j < NKD; ++j) {
-        float yq[KC], yk[KC];
+        load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
+        qo[i][j] = op_load<T>(a.q + off + j * KS + lg * KC);
+        ko[i][j] = op_load<T>(a.k + off + j * KS + lg * KC);
+        bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
+      }
+    }
+    if (pn == 0) {
+      for (int i = tid; i < BT * A_LD / 4; i += NT)
+        reinterpret_cast<f32x4*>(sA)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // ---- 1. in-block inclusive cumsum of g (lanes li = tokens) --------------
+    if (padded) {
+#pragma unroll
+      for (int i = 0; i < NBW; ++i) {
+        if (!real(i)) {
+#pragma unroll
+          for (int x = 0; x < DQ; ++x) loc[i][x] = 0.f;
+#pragma unroll
+          for (int j = 0; j < NKD; ++j) {
+            qo[i][j] = op_zero<T>();
+            ko[i][j] = op_zero<T>();
+            bo[i][j] = op_zero<T>();
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int I = own_block<NB>(wv, i);
+      if (raw) {
+        const bool rv = real(i);
+#pragma unroll
+        for (int x = 0; x < DQ; ++x) loc[i][x] = rv ? neg_softplus(loc[i][x]) : 0.f;
+      }
+#pragma unroll
+      for (int x = 0; x < DQ; ++x) loc[i][x] = row_scan16(loc[i][x]);
+      if (li == 15) {
+#pragma unroll
+        for (int x = 0; x < DQ; ++x) sTot[I * DP + chan(x)] = loc[i][x];
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < NB * DP; i += NT) {
+      sETot[i] = __expf(sTot[i]);
+    }
+    if (tid < DP) {
+      float run = 0.f;
+#pragma unroll
+      for (int m = 0; m < NB; ++m) { sF[0][m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
+      a.GL[(size_t)cid * D + d0 + tid] = run;
+      run = 0.f;
+#pragma unroll
+      for (int m = NB - 1; m >= 0; --m) { sF[1][m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
+    }
+    __syncthreads();
+
+    // ---- 2. per-token factors: qg, kbd, kg, khat; diagonal score blocks -----
+    float aq[NBW][DQ], ak[NBW][DQ];
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int I = own_block<NB>(wv, i);
+      const int t = I * 16 + li;
+      T* qgp = a.Qg + (size_t)cid * BT * D + (size_t)t * D + d0;
+      f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
+      // raw inputs: q,k <- q,k / max(|.|_2, 1e-12) over D (F.normalize) and
+      // b <- sigmoid(b), in place in the loaded registers; a token's channels sit
+      // in the four lanes li, li+16, li+32, li+48
+      if (raw) {
+        float iq, ik;
+        if constexpr (one) {
+          float sq = 0.f, sk = 0.f;
+#pragma unroll
+          for (int j = 0; j < NKD; ++j)
+#pragma unroll
+            for (int e = 0; e < KC; ++e) {
+              const float qv = to_f(qo[i][j][e]), kv = to_f(ko[i][j][e]);
+              sq += qv * qv;
+              sk += kv * kv;
+            }
+          sq += __shfl_xor(sq, 16);
+          sq += __shfl_xor(sq, 32);
+          sk += __shfl_xor(sk, 16);
+          sk += __shfl_xor(sk, 32);
+          iq = 1.f / fmaxf(sqrtf(sq), 1e-12f);
+          ik = 1.f / fmaxf(sqrtf(sk), 1e-12f);
+        } else {
+          iq = iqn[i];
+          ik = ikn[i];
+        }
+#pragma unroll
+        for (int j = 0; j < NKD; ++j)
+#pragma unroll
+          for (int e = 0; e < KC; ++e) {
+            qo[i][j][e] = from_f<T>(to_f(qo[i][j][e]) * iq);
+            ko[i][j][e] = from_f<T>(to_f(ko[i][j][e]) * ik);
+            bo[i][j][e] = from_f<T>(sigmoidf(to_f(bo[i][j][e])));
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < NKD; ++j) {
+        float qg[KC], kh[KC], dq[KC], dk[KC], db[KC];
 #pragma unroll
         for (int e = 0; e < KC; ++e) {
-          yq[e] = aq[i][j * KC + e] * F[j * KC + e];
-          yk[e] = ak[i][j * KC + e] * F[j * KC + e];
+          const int x = j * KC + e, ch = chan(x);
+          const float qv = to_f(qo[i][j][e]), kv = to_f(ko[i][j][e]), bv = to_f(bo[i][j][e]);
+          const float lc = loc[i][x];
+          const float eloc = __expf(lc);
+          const float ekh = __expf(sTot[I * DP + ch] - lc);
+          const float egc = eloc * sF[0][I * DP + ch];
+          const float bk = bv * kv;
+          qg[e] = qv * egc;
+          sKbdT[(d0 + ch) * TT_LD + t] = from_f<T>(bk * egc);
+          kgT[(size_t)(d0 + ch) * BT + kpos<T>(t)] = from_f<T>(kv * ekh * sF[1][I * DP + ch]);
+          kh[e] = kv * ekh;
+          aq[i][x] = qv * eloc;
+          ak[i][x] = bk * eloc;
+          // the diagonal-block factors keep their own exponentials: e^{loc} or
+          // e^{T_I-loc} may underflow where e^{loc-loc_m} e^{loc_m-loc'} does not
+          const float lm = row_bcast<7>(lc);
+          const float edq = __expf(lc - lm), edk = __expf(lm - lc);
+          dq[e] = qv * edq;
+          db[e] = bk * edq;
+          dk[e] = kv * edk;
         }
-        const Op xo = op_load<T>(&sR0[(J * 16 + li) * KH_LD + j * KS + lg * KC]);
-        mma(accq, xo, op_from<T>(yq));
-        mma(acck, xo, op_from<T>(yk));
+        *reinterpret_cast<Op*>(qgp + j * KS + lg * KC) = op_from<T>(qg);
+        *reinterpret_cast<Op*>(&sR0[t * KH_LD + j * KS + lg * KC]) = op_from<T>(kh);
+        // diagonal block, factorised around its 8th token: X = k rows (j),
+        // Y = q / bk rows (i) -> lane holds [i=li][j=4lg+r]
+        const Op xo = op_from<T>(dk);
+        mma(accq, xo, op_from<T>(dq));
+        mma(acck, xo, op_from<T>(db));
       }
-      store4(a.Aqk + (size_t)cid * BT * BT + (size_t)t * BT + J * 16 + 4 * lg, accq * a.scale);
-      store4(&sA[t * A_LD + J * 16 + 4 * lg], acck);
+      f32x4 sq, sk;
 #pragma unroll
-      for (int x = 0; x < DQ; ++x) F[x] *= sETot[J * D + chan(x)];
+      for (int r = 0; r < 4; ++r) {
+        const int jj = 4 * lg + r;
+        sq[r] = (jj <= li) ? a.scale * accq[r] : 0.f;
+        sk[r] = (jj < li) ? acck[r] : 0.f;
+      }
+      const int e0 = t * A_LD + I * 16 + 4 * lg;
+      if constexpr (one) {
+        store4(aqk + (size_t)t * BT + I * 16 + 4 * lg, sq);
+        store4(&sA[e0], sk);
+      } else {
+        if (pn > 0) {
+          sq += load4f(&sQA[e0]);
+          sk += load4f(&sA[e0]);
+        }
+        if (last_pn) store4(aqk + (size_t)t * BT + I * 16 + 4 * lg, sq);
+        else store4(&sQA[e0], sq);
+        store4(&sA[e0], sk);
+      }
+    }
+    __syncthreads();
+
+    // ---- 3. off-diagonal score blocks (I > J) on MFMA ------------------------
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int I = own_block<NB>(wv, i);
+      const int t = I * 16 + li;
+      float F[DQ];
+#pragma unroll
+      for (int x = 0; x < DQ; ++x) F[x] = 1.f;
+      for (int J = I - 1; J >= 0; --J) {
+        f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NKD; ++j) {
+          float yq[KC], yk[KC];
+#pragma unroll
+          for (int e = 0; e < KC; ++e) {
+            yq[e] = aq[i][j * KC + e] * F[j * KC + e];
+            yk[e] = ak[i][j * KC + e] * F[j * KC + e];
+          }
+          const Op xo = op_load<T>(&sR0[(J * 16 + li) * KH_LD + j * KS + lg * KC]);
+          mma(accq, xo, op_from<T>(yq));
+          mma(acck, xo, op_from<T>(yk));
+        }
+        const int e0 = t * A_LD + J * 16 + 4 * lg;
+        if constexpr (one) {
+          store4(aqk + (size_t)t * BT + J * 16 + 4 * lg, accq * a.scale);
+          store4(&sA[e0], acck);
+        } else {
+          f32x4 sq = accq * a.scale;
+          if (pn > 0) {
+            sq += load4f(&sQA[e0]);
+            acck += load4f(&sA[e0]);
+          }
+          if (last_pn) store4(aqk + (size_t)t * BT + J * 16 + 4 * lg, sq);
+          else store4(&sQA[e0], sq);
+          store4(&sA[e0], acck);
+        }
+#pragma unroll
+        for (int x = 0; x < DQ; ++x) F[x] *= sETot[J * DP + chan(x)];
+      }
     }
   }
   __syncthreads();
 
-  // w, v: in flight during the inverse
+  // w, v of the first panel: in flight during the inverse
   Op wo[NBW][NKD], vo[NBW][NKD];
+  auto load_wv = [&](int d0) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < NBW; ++i) {
-    const size_t off = load_row(i);
+    for (int i = 0; i < NBW; ++i) {
+      const size_t off = load_row(i) + d0;
 #pragma unroll
-    for (int j = 0; j < NKD; ++j) {
-      wo[i][j] = op_load<T>(a.w + off + j * KS + lg * KC);
-      vo[i][j] = op_load<T>(a.v + off + j * KS + lg * KC);
+      for (int j = 0; j < NKD; ++j) {
+        wo[i][j] = op_load<T>(a.w + off + j * KS + lg * KC);
+        vo[i][j] = op_load<T>(a.v + off + j * KS + lg * KC);
+      }
     }
-  }
+  };
+  load_wv(0);
 
   // ---- 4. A = (I + Akk)^{-1}: diagonal blocks by substitution ---------------
   if (lg < NBW) {
@@ -395,69 +481,79 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
       }
     }
   }
-  // ---- 5. (w v)^T into LDS (khat's region, free since step 3) ---------------
-  if (padded) {
-#pragma unroll
-    for (int i = 0; i < NBW; ++i)
-      if (!real(i)) {
-#pragma unroll
-        for (int j = 0; j < NKD; ++j) vo[i][j] = op_zero<T>();
-      }
-  }
-  if (raw) {  // w <- sigmoid(w)
-#pragma unroll
-    for (int i = 0; i < NBW; ++i)
-#pragma unroll
-      for (int j = 0; j < NKD; ++j)
-#pragma unroll
-        for (int e = 0; e < KC; ++e) wo[i][j][e] = from_f<T>(sigmoidf(to_f(wo[i][j][e])));
-  }
+
   T* sWVT = sR0;
 #pragma unroll
-  for (int i = 0; i < NBW; ++i) {
-    const int t = own_block<NB>(wv, i) * 16 + li;
-#pragma unroll
-    for (int x = 0; x < DQ; ++x)
-      sWVT[chan(x) * TT_LD + t] =
-          from_f<T>(to_f(wo[i][x / KC][x % KC]) * to_f(vo[i][x / KC][x % KC]));
-  }
-  __syncthreads();
-
-  if (a.a_dbg) {
-    float* dst = a.a_dbg + (size_t)cid * BT * BT;
-    for (int i = tid; i < BT * BT; i += NT) dst[i] = sA[(i / BT) * A_LD + (i % BT)];
-  }
-
-  // ---- 6. w_pseudo = A (b k e^gc), u = A (w v) ------------------------------
-#pragma unroll
-  for (int i = 0; i < NBW; ++i) {
-    const int I = own_block<NB>(wv, i);
-    const int kgmax = (I * 16 + 15) / KS;
-    Op af[NKT];
-#pragma unroll
-    for (int kg = 0; kg < NKT; ++kg) {
-      float tmp[KC];
-#pragma unroll
-      for (int e = 0; e < KC; e += 4) {
-        const f32x4 v4 = load4f(&sA[(I * 16 + li) * A_LD + kg * KS + lg * KC + e]);
-        tmp[e] = v4[0]; tmp[e + 1] = v4[1]; tmp[e + 2] = v4[2]; tmp[e + 3] = v4[3];
-      }
-      af[kg] = op_from<T>(tmp);
+  for (int pn = 0; pn < NPN; ++pn) {
+    const int d0 = pn * DP;
+    if (pn > 0) {
+      load_wv(d0);
+      __syncthreads();  // the previous panel's (w v)^T reads are done
     }
-    T* Wc = a.W + (size_t)cid * BT * D;
-    float* Uc = a.UT + (size_t)cid * D * BT;
+    // ---- 5. (w v)^T of the panel into LDS (khat's region, free since step 3) --
+    if (padded) {
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-      f32x4 accw = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < NBW; ++i)
+        if (!real(i)) {
+#pragma unroll
+          for (int j = 0; j < NKD; ++j) vo[i][j] = op_zero<T>();
+        }
+    }
+    if (raw) {  // w <- sigmoid(w)
+#pragma unroll
+      for (int i = 0; i < NBW; ++i)
+#pragma unroll
+        for (int j = 0; j < NKD; ++j)
+#pragma unroll
+          for (int e = 0; e < KC; ++e) wo[i][j][e] = from_f<T>(sigmoidf(to_f(wo[i][j][e])));
+    }
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int t = own_block<NB>(wv, i) * 16 + li;
+#pragma unroll
+      for (int x = 0; x < DQ; ++x)
+        sWVT[chan(x) * TT_LD + t] =
+            from_f<T>(to_f(wo[i][x / KC][x % KC]) * to_f(vo[i][x / KC][x % KC]));
+    }
+    __syncthreads();
+
+    if (pn == 0 && a.a_dbg) {
+      float* dst = a.a_dbg + (size_t)cid * BT * BT;
+      for (int i = tid; i < BT * BT; i += NT) dst[i] = sA[(i / BT) * A_LD + (i % BT)];
+    }
+
+    // ---- 6. w_pseudo = A (b k e^gc), u = A (w v), the panel's columns ---------
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int I = own_block<NB>(wv, i);
+      const int kgmax = (I * 16 + 15) / KS;
+      Op af[NKT];
 #pragma unroll
       for (int kg = 0; kg < NKT; ++kg) {
-        if (kg <= kgmax) {
-          mma(accw, op_load<T>(&sKbdT[(dt * 16 + li) * TT_LD + kg * KS + lg * KC]), af[kg]);
-          mma(accu, af[kg], op_load<T>(&sWVT[(dt * 16 + li) * TT_LD + kg * KS + lg * KC]));
+        float tmp[KC];
+#pragma unroll
+        for (int e = 0; e < KC; e += 4) {
+          const f32x4 v4 = load4f(&sA[(I * 16 + li) * A_LD + kg * KS + lg * KC + e]);
+          tmp[e] = v4[0]; tmp[e + 1] = v4[1]; tmp[e + 2] = v4[2]; tmp[e + 3] = v4[3];
         }
+        af[kg] = op_from<T>(tmp);
       }
-      store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dt * 16 + 4 * lg), accw);
-      store4(Uc + (size_t)(dt * 16 + li) * BT + I * 16 + 4 * lg, accu);
+      T* Wc = a.W + (size_t)cid * BT * D;
+      float* Uc = a.UT + (size_t)cid * D * BT;
+#pragma unroll
+      for (int dt = 0; dt < DP / 16; ++dt) {
+        const int dg = d0 + dt * 16;      // first channel of the tile
+        f32x4 accw = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kg = 0; kg < NKT; ++kg) {
+          if (kg <= kgmax) {
+            mma(accw, op_load<T>(&sKbdT[(dg + li) * TT_LD + kg * KS + lg * KC]), af[kg]);
+            mma(accu, af[kg], op_load<T>(&sWVT[(dt * 16 + li) * TT_LD + kg * KS + lg * KC]));
+          }
+        }
+        store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dg + 4 * lg), accw);
+        store4(Uc + (size_t)(dg + li) * BT + I * 16 + 4 * lg, accu);
+      }
     }
   }
 }
@@ -511,6 +607,14 @@ struct StateArgs {
 // halves of the W / kg^T double buffer are separate __shared__ arrays selected
 // at compile time (the chunk loop is unrolled by two), so the compiler can see
 // that reads of one half never alias the DMA into the other.
+//
+// Where two buffers do not fit in LDS (float32 at D = 256: 128 KB per chunk)
+// the kernel runs single-buffered: a third barrier E per chunk marks the end of
+// the compute waves' reads, after which the producers move the next chunk, by
+// then in L2 through the touch issued one chunk ahead.
+template <typename T, int BT, int D>
+constexpr int state_bufs() { return 4 * BT * D * (int)sizeof(T) <= 132 * 1024 ? 2 : 1; }
+
 template <typename T, int BT, int D, int NW, int NP>
 __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
   using Op = typename Tr<T>::Op;
@@ -520,12 +624,13 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
   constexpr int WBYTES = BT * D * (int)sizeof(T);   // one tile (W or kg^T)
   constexpr int BUF = 2 * WBYTES;                    // W + kg^T
   constexpr int PIECES = BUF / 1024;                 // 1 KB DMA instructions per chunk
+  constexpr int NBUF = state_bufs<T, BT, D>();
   static_assert(BUF % 1024 == 0, "tiles must split into 1 KB pieces");
   __shared__ __align__(16) char sbuf0[BUF];
-  __shared__ __align__(16) char sbuf1[BUF];
+  __shared__ __align__(16) char sbuf1[NBUF == 2 ? BUF : 16];
   __shared__ __align__(16) f32x4 sU[NW * NB * 64];   // u^T in compute-lane order
   __shared__ __align__(16) float sGL0[D];
-  __shared__ __align__(16) float sGL1[D];
+  __shared__ __align__(16) float sGL1[NBUF == 2 ? D : 4];
   __shared__ __align__(16) float sJunk[64];        // target of the L2 touches
 
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
@@ -651,6 +756,20 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     };
     if (n > 0) issue(0, sbuf0, sGL0);
     if (n > 1) touch(1);
+    if constexpr (NBUF == 1) {
+      for (int c = 0; c < n; ++c) {
+        wait_chunk(c);
+        exp_gl(sGL0);
+        barrier();  // A(c)
+        barrier();  // B(c)
+        barrier();  // E(c): chunk c's tiles are no longer read
+        if (c + 1 < n) {
+          issue(c + 1, sbuf0, sGL0);
+          if (c + 2 < n) touch(c + 2);
+        }
+      }
+      return;
+    }
     for (int c = 0; c < n; c += 2) {
       wait_chunk(c);
       exp_gl(sGL0);
@@ -778,9 +897,16 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     }
   };
 
-  for (int c = 0; c < n; c += 2) {
-    step(c, sbuf0, sGL0);
-    if (c + 1 < n) step(c + 1, sbuf1, sGL1);
+  if constexpr (NBUF == 1) {
+    for (int c = 0; c < n; ++c) {
+      step(c, sbuf0, sGL0);
+      __syncthreads();  // E(c)
+    }
+  } else {
+    for (int c = 0; c < n; c += 2) {
+      step(c, sbuf0, sGL0);
+      if (c + 1 < n) step(c + 1, sbuf1, sGL1);
+    }
   }
   float* hout = a.cu ? a.h_final + ((size_t)sg * a.H + bh) * D * D
               : a.summary ? a.seg + ((size_t)unit * 2 + (mslice ? 1 : 0)) * D * D
@@ -869,20 +995,27 @@ struct OutArgs {
 };
 
 // o = scale qg h_c + Aqk v_new per chunk (gdn2_fwd.py:349-353), computed as
-// o^T tiles so each lane stores 4 consecutive floats of an output row.
+// o^T tiles so each lane stores 4 consecutive floats of an output row.  One
+// workgroup per chunk and slice of out_cols() value columns (all D columns up
+// to D = 128; at D = 256 the h^T slice would not fit LDS whole).
+template <typename T, int D>
+constexpr int out_cols() { return D <= 128 ? D : (sizeof(T) == 4 ? 64 : 128); }
+
 template <typename T, int BT, int D>
 __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
   using Op = typename Tr<T>::Op;
   constexpr int KC = Tr<T>::KC, KS = Tr<T>::KS;
-  constexpr int NB = BT / 16, NBW = (NB + 3) / 4, NDT = D / 16;
+  constexpr int DVS = out_cols<T, D>();   // value columns per workgroup
+  constexpr int NSL = D / DVS;
+  constexpr int NB = BT / 16, NBW = (NB + 3) / 4, NDT = DVS / 16;
   constexpr int NKD = D / KS, NKT = BT / KS;
   constexpr int PADT = 16 / sizeof(T);
   constexpr int H_LD = D + PADT, V_LD = BT + PADT;
-  __shared__ __align__(16) T sH[D * H_LD];
-  __shared__ __align__(16) T sV[D * V_LD];
+  __shared__ __align__(16) T sH[DVS * H_LD];
+  __shared__ __align__(16) T sV[DVS * V_LD];
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  const int cid = blockIdx.x;
+  const int cid = blockIdx.x / NSL, sl = blockIdx.x % NSL;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
 
   // All global loads are issued before the first LDS store: the qg / Aqk
@@ -916,11 +1049,13 @@ __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
   }
   {
     constexpr int EPV = 16 / sizeof(T);                  // elements per 16-byte piece
-    constexpr int NH = D * D / EPV / 256, NV = D * BT / EPV / 256;
-    static_assert(D * D % (EPV * 256) == 0 && D * BT % (EPV * 256) == 0, "tiles split evenly");
+    constexpr int NH = DVS * D / EPV / 256, NV = DVS * BT / EPV / 256;
+    static_assert(DVS * D % (EPV * 256) == 0 && DVS * BT % (EPV * 256) == 0,
+                  "tiles split evenly");
     uint4 rh[NH], rv[NV];
-    const uint4* gh = reinterpret_cast<const uint4*>(a.HT + (size_t)cid * D * D);
-    const uint4* gv = reinterpret_cast<const uint4*>(a.VnT + (size_t)cid * D * BT);
+    // rows [sl DVS, (sl+1) DVS) of h^T [col][d] and v_new^T [col][t]
+    const uint4* gh = reinterpret_cast<const uint4*>(a.HT + ((size_t)cid * D + sl * DVS) * D);
+    const uint4* gv = reinterpret_cast<const uint4*>(a.VnT + ((size_t)cid * D + sl * DVS) * BT);
 #pragma unroll
     for (int u = 0; u < NH; ++u) rh[u] = gh[tid + 256 * u];
 #pragma unroll
@@ -940,7 +1075,7 @@ __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
 
   const size_t HD = (size_t)a.H * D;
   const ChunkRows cr = chunk_rows(a.cstart, c, bb, a.T_len, BT);
-  float* obase = a.out + cr.row0 * HD + (size_t)hh * D;
+  float* obase = a.out + cr.row0 * HD + (size_t)hh * D + sl * DVS;
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
     const int It = own_block<NB>(wv, i);
@@ -1029,7 +1164,8 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   launch_mark(st);
   if (NC > 0) {
     OutArgs<T> oa{Qg, Aqk, HT, VnT, T_len, H, N, scale, out, vl ? vl->cstart : nullptr};
-    hipLaunchKernelGGL((fwd_out<T, BT, D>), dim3(NC), dim3(256), 0, st, oa);
+    hipLaunchKernelGGL((fwd_out<T, BT, D>), dim3(NC * (D / out_cols<T, D>())), dim3(256), 0,
+                       st, oa);
   }
   launch_mark(st);
   return hipGetLastError();
@@ -1052,5 +1188,8 @@ GDN2_INST_FWD(bf16_t, bf16_t, 64, 64)
 GDN2_INST_FWD(bf16_t, bf16_t, 64, 128)
 GDN2_INST_FWD(bf16_t, bf16_t, 128, 64)
 GDN2_INST_FWD(bf16_t, bf16_t, 128, 128)
+GDN2_INST_FWD(float, float, 64, 256)
+GDN2_INST_FWD(bf16_t, float, 64, 256)
+GDN2_INST_FWD(bf16_t, bf16_t, 64, 256)
 
 }  // namespace gdn2

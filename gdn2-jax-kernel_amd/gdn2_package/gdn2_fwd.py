@@ -80,10 +80,12 @@ def _dtype_code(dt):
     return _lib.GDN2_F32 if dt == torch.float32 else _lib.GDN2_BF16
 
 
-def chunk_size_for(dtype, chunk_size=None) -> int:
+def chunk_size_for(dtype, chunk_size=None, D=128) -> int:
+    """Chunk size: explicit, else the module-level BT override, else 128 for
+    bfloat16 inputs with D <= 128 and 64 otherwise (float32, and D = 256)."""
     bt = chunk_size if chunk_size is not None else BT
     if bt is None:
-        return 128 if dtype == torch.bfloat16 else 64
+        return 128 if dtype == torch.bfloat16 and D <= 128 else 64
     return int(bt)
 
 
@@ -108,7 +110,7 @@ class _Prepared:
         if in_dt == torch.bfloat16 and g.dtype == torch.bfloat16:
             g_dt = torch.bfloat16
         self.B, self.T, self.H, self.D = q.shape
-        self.BT = chunk_size_for(in_dt, chunk_size)
+        self.BT = chunk_size_for(in_dt, chunk_size, self.D)
         self.args = (self.B, self.T, self.H, self.D, self.BT, _dtype_code(in_dt),
                      _dtype_code(g_dt))
         # T % BT != 0: the last chunk is short (GDN2_FWD_PARTIAL_CHUNK); the

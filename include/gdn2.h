@@ -39,9 +39,10 @@ extern "C" {
 
 /* Error codes. */
 #define GDN2_OK                0
-#define GDN2_ERR_HEAD_DIM     -1  /* D not in {64,128}; ref asserts D==128, gdn2_fwd.py:145 */
+#define GDN2_ERR_HEAD_DIM     -1  /* D not in {64,128,256} (256: forward and decode only);
+                                     ref asserts D==128, gdn2_fwd.py:145, gdn2_bwd.py:348 */
 #define GDN2_ERR_SEQ_LEN      -2  /* T % BT != 0; ref asserts, gdn2_fwd.py:146 */
-#define GDN2_ERR_CHUNK        -3  /* BT not in {64,128}, or BT=128 with float32 inputs */
+#define GDN2_ERR_CHUNK        -3  /* BT not in {64,128}, or BT=128 with float32 inputs or D=256 */
 #define GDN2_ERR_DTYPE        -4  /* unknown dtype code */
 #define GDN2_ERR_NULL         -5  /* required pointer is NULL */
 #define GDN2_ERR_ALIGN        -6  /* pointer not 16-byte aligned */

@@ -44,6 +44,10 @@ F32, BF16 = _lib.GDN2_F32, _lib.GDN2_BF16
     ((8, 8192, 6, 128, 128, BF16, BF16), _lib.OK),
     ((1, 0, 2, 64, 64, F32, F32), _lib.OK),                 # empty sequence
     ((1, 512, 2, 96, 64, F32, F32), _lib.ERR_HEAD_DIM),     # ref: D==128 assert, gdn2_fwd.py:145
+    ((1, 512, 2, 256, 64, F32, F32), _lib.OK),              # D = 256 (forward), chunk 64
+    ((1, 512, 2, 256, 64, BF16, BF16), _lib.OK),
+    ((1, 512, 2, 256, 128, BF16, F32), _lib.ERR_CHUNK),     # D = 256 needs BT = 64
+    ((1, 512, 2, 512, 64, F32, F32), _lib.ERR_HEAD_DIM),
     ((1, 500, 2, 64, 64, F32, F32), _lib.ERR_SEQ_LEN),      # ref: L%BT assert, gdn2_fwd.py:146
     ((1, 512, 2, 64, 256, BF16, F32), _lib.ERR_CHUNK),
     ((1, 512, 2, 64, 128, F32, F32), _lib.ERR_CHUNK),       # fp32 needs BT=64
@@ -118,6 +122,9 @@ def test_bwd_rejects_before_launch():
     call = lambda d, dout, fwsb: L.gdn2_bwd(None, *d, *fake, None, 0.125, dout, None, *grads,
                                             0x5000, 0x6000, fwsb, 0x7000, bws)
     assert call((1, 512, 2, 96, 64, F32, F32), 0x4000, fws) == _lib.ERR_HEAD_DIM
+    # D = 256 is forward-only: the backward refuses it before touching anything
+    assert L.gdn2_bwd_workspace_bytes(1, 512, 2, 256, 64, F32) == 0
+    assert call((1, 512, 2, 256, 64, F32, F32), 0x4000, 1 << 30) == _lib.ERR_HEAD_DIM
     assert call(dims, None, fws) == _lib.ERR_NULL
     assert call(dims, 0x4000, fws - 1) == _lib.ERR_WORKSPACE
 

@@ -52,6 +52,13 @@ def test_partial_last_chunk_passes_validation():
     assert not isinstance(e.value, gp.GDN2ShapeError)
 
 
+def test_trainable_d256_is_refused():
+    """D = 256 runs forward only; the trainable path refuses it with the shape
+    error (its backward kernels are built for D <= 128)."""
+    from gdn2_package import _lib
+    assert _lib.lib().gdn2_bwd_workspace_bytes(1, 128, 2, 256, 64, _lib.GDN2_F32) == 0
+
+
 def test_no_cpu_fallback():
     """Host tensors are refused: the only compute path is the gfx950 library."""
     import gdn2_package as gp
@@ -63,6 +70,7 @@ def test_chunk_size_resolution():
     from gdn2_package import gdn2_fwd
     assert gdn2_fwd.chunk_size_for(torch.bfloat16) == 128
     assert gdn2_fwd.chunk_size_for(torch.float32) == 64
+    assert gdn2_fwd.chunk_size_for(torch.bfloat16, D=256) == 64
     old = gdn2_fwd.BT
     try:
         gdn2_fwd.BT = 64              # README.md:87-92 style override, read at call time

@@ -157,3 +157,13 @@ def test_grad_of_h0_only_when_given(dev):
     do = np.ones(xs[0].shape, dtype=np.float32)
     _, grads, _ = run_grads(xs, 0.125, do, dev=dev)
     assert grads[6] is None
+
+
+def test_trainable_d256_raises_shape_error(dev):
+    """D = 256 is forward-only: the backward raises the shape error (the
+    reference asserts D == 128 in both directions, gdn2_fwd.py:145,
+    gdn2_bwd.py:348)."""
+    xs = [torch.randn((1, 64, 1, 256), device=dev, requires_grad=True) for _ in range(6)]
+    out, hf = gp().gdn2_pallas_forward_trainable(*xs, 0.0625)
+    with pytest.raises(gp().GDN2ShapeError):
+        out.sum().backward()

@@ -28,7 +28,8 @@ def dev_inputs(xs, dev, dtype):
 
 
 @pytest.mark.parametrize("D,dtype,with_state", [(128, torch.float32, True), (64, torch.float32, False),
-                                                (128, torch.bfloat16, True), (64, torch.bfloat16, True)])
+                                                (128, torch.bfloat16, True), (64, torch.bfloat16, True),
+                                                (256, torch.float32, True), (256, torch.bfloat16, False)])
 def test_one_token_matches_recurrence(dev, D, dtype, with_state):
     import gdn2_package as gp
     B, H = 2, 3
@@ -48,7 +49,7 @@ def test_one_token_matches_recurrence(dev, D, dtype, with_state):
 
 
 @pytest.mark.parametrize("dtype,BT,D", [(torch.float32, 64, 128), (torch.bfloat16, 128, 128),
-                                        (torch.bfloat16, 64, 64)])
+                                        (torch.bfloat16, 64, 64), (torch.bfloat16, 64, 256)])
 def test_prefix_then_decode_equals_forward(dev, dtype, BT, D):
     """forward(prefix) -> decode 24 tokens == forward(prefix + 24 tokens)."""
     import gdn2_package as gp

@@ -64,6 +64,8 @@ def test_config1_golden_fixture(dev):
     (2, 384, 2, 64, torch.bfloat16, 128, False),
     (1, 512, 3, 128, torch.bfloat16, 128, True),
     (1, 256, 2, 128, torch.bfloat16, 64, False),
+    (1, 256, 2, 256, torch.float32, 64, True),      # D = 256: two channel panels,
+    (2, 192, 2, 256, torch.bfloat16, 64, True),     # sliced state and output kernels
 ])
 def test_forward_matches_oracle(dev, B, T, H, D, dtype, BT, h0):
     xs = O.make_inputs(B, T, H, D, seed=B * 1000 + T + H)
@@ -136,7 +138,8 @@ def test_config5_long_context_bf16(dev):
 
 
 # ----------------------------------------------------------------------------- intermediates
-@pytest.mark.parametrize("dtype,BT,D", [(torch.float32, 64, 64), (torch.bfloat16, 128, 128)])
+@pytest.mark.parametrize("dtype,BT,D", [(torch.float32, 64, 64), (torch.bfloat16, 128, 128),
+                                        (torch.float32, 64, 256), (torch.bfloat16, 64, 256)])
 def test_intermediates_match_reference_kernels(dev, dtype, BT, D):
     """Per-kernel outputs (A, Aqk, w_pseudo, u, kg, qg, gc_last, h_pre, v_new) of
     gdn2_pallas_forward_with_residuals vs the oracle's restatement of kernels A-D."""
@@ -247,6 +250,8 @@ def test_shape_errors_on_device(dev):
     (2, 200, 3, 128, torch.bfloat16, 128, False),  # 1 full + 72
     (1, 129, 2, 64, torch.bfloat16, 128, True),    # one token in the last chunk
     (1, 77, 2, 128, torch.bfloat16, 64, False),
+    (1, 150, 2, 256, torch.bfloat16, 64, True),
+    (1, 100, 1, 256, torch.float32, 64, False),
 ])
 def test_partial_last_chunk_matches_oracle(dev, B, T, H, D, dtype, BT, h0):
     """T % BT != 0 (the reference asserts, gdn2_fwd.py:146): the token recurrence
@@ -283,6 +288,8 @@ def test_partial_last_chunk_equals_zero_padded_inputs(dev):
     (2, 1280, 1, 128, torch.float32, 64, 7, True),     # N=20: 3 x 6 + 2
     (1, 4096, 2, 128, torch.bfloat16, 128, 8, True),   # N=32: 8 x 4
     (1, 2560, 2, 64, torch.bfloat16, 128, 5, False),   # N=20: 5 x 4
+    (1, 1024, 1, 256, torch.float32, 64, 4, True),     # D = 256, single-buffered scan
+    (1, 1024, 2, 256, torch.bfloat16, 64, 3, False),   # N=16: 6 + 6 + 4
 ])
 def test_segmented_scan_matches_serial_and_oracle(dev, B, T, H, D, dtype, BT, S, h0):
     """The state scan split into S segments (summary pass, affine combine, final
@@ -344,7 +351,8 @@ def test_stage_diagnostics_path(dev, monkeypatch, capsys):
 
 # ----------------------------------------------------------------------------- fused input prep
 @pytest.mark.parametrize("dtype,BT,D", [(torch.float32, 64, 128), (torch.bfloat16, 128, 128),
-                                        (torch.bfloat16, 64, 64)])
+                                        (torch.bfloat16, 64, 64), (torch.float32, 64, 256),
+                                        (torch.bfloat16, 64, 256)])
 def test_raw_inputs_fused_activations(dev, dtype, BT, D):
     """gdn2_pallas_forward_raw on pre-activation inputs equals the forward on
     the torch-activated inputs, and the recurrence on activations computed in

@@ -23,6 +23,8 @@ def close(got, ref, tol):
     (torch.float32, 64, 64, [130, 0, 64, 17, 200]),          # tails, empty, exact, short
     (torch.bfloat16, 128, 128, [300, 128, 5, 257]),
     (torch.bfloat16, 64, 128, [1, 63, 65, 190]),
+    (torch.bfloat16, 64, 256, [70, 1, 128]),
+    (torch.float32, 64, 256, [100, 64]),
 ])
 def test_varlen_matches_per_sequence_recurrence(dev, dtype, BT, D, lens):
     import gdn2_package as gp
