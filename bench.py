@@ -164,8 +164,8 @@ def extras(gp, steps=10, warmup=3):
     """The paths beyond the headline, each timed on the GPU in the same run:
     configs[4] (1 x 131072 x 8 heads, segmented state scan), the forward with
     the input activations fused (vs torch activations + forward), a
-    variable-length batch with the headline's token count, and the decode step
-    (state read + written per token)."""
+    variable-length batch with the headline's token count, D = 256, a partial
+    last chunk, and the decode step (state read + written per token)."""
     import torch
     f = torch.nn.functional
     res = {}
@@ -210,6 +210,25 @@ def extras(gp, steps=10, warmup=3):
                          "kernels_ms": dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms)),
                          "note": "ms includes building the chunk tables on the host"}
     del raw, packed
+    def dist(shape):   # the headline's input distributions at another shape
+        q, k, v, w, b_, g = (r(shape) for _ in range(6))
+        return [x.to(torch.bfloat16) for x in (f.normalize(q, dim=-1), f.normalize(k, dim=-1), v,
+                                               torch.sigmoid(w), torch.sigmoid(b_))] + \
+            [-f.softplus(g)]
+    # D = 256 (chunk 64): the headline's B, T and element count with H = 3
+    x256 = dist((B, T, 3, 256))
+    ms = _time(lambda: gp.gdn2_pallas_forward(*x256, 256 ** -0.5), steps, warmup)
+    kms = _event_ms(lambda: gp.gdn2_pallas_forward(*x256, 256 ** -0.5), 4)
+    res["d256_fwd"] = {"shape": "B8 T8192 H3 D256 bf16, chunk 64", "ms": ms,
+                       "tokens_per_s": B * T / (ms * 1e-3),
+                       "kernels_ms": dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms))}
+    del x256
+    # T % BT != 0: 8100 tokens per sequence, the last chunk of each 36 tokens short
+    xp = dist((B, 8100, H, D))
+    ms = _time(lambda: gp.gdn2_pallas_forward(*xp, D ** -0.5), steps, warmup)
+    res["partial_chunk_fwd"] = {"shape": "B8 T8100 H6 D128 bf16, chunk 128 (last chunk 36 "
+                                         "tokens)", "ms": ms, "tokens_per_s": B * 8100 / (ms * 1e-3)}
+    del xp
     # decode: one token for B*H = 48 states of 128 x 128 fp32
     tok = [r((B, 1, H, D)).to(torch.bfloat16) for _ in range(5)] + [-f.softplus(r((B, 1, H, D)))]
     state = torch.zeros((B, H, D, D), device="cuda")
