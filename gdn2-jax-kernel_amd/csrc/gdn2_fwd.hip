@@ -847,21 +847,42 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
         *reinterpret_cast<Op*>(hT + p * 32 + 8 * lg) = op_from_c(h[2 * p], h[2 * p + 1], (Op*)nullptr);
     }
 
+    // v_new -= W h.  The NB row blocks are independent accumulators: the k-step
+    // loop is outermost, so consecutive MFMAs never wait on each other, and the
+    // next k-step's W operands are read while this one's MFMAs run.
+    {
+      constexpr int NKD = F32 ? NDT : NDT / 2;   // k-steps over d
+      Op hb[NKD];
 #pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const int r = it * 16 + li;
-      if constexpr (F32) {
-#pragma unroll
-        for (int at = 0; at < NDT; ++at)
-          mma(acc, load4f(&sW[swz(r, at * 16 + 4 * lg, D)]), h[at]);
-      } else {
-#pragma unroll
-        for (int p = 0; p < NDT / 2; ++p)
-          mma(acc, op_load<T>(&sW[swz(r, p * 32 + 8 * lg, D)]),
-              op_from_c(h[2 * p], h[2 * p + 1], (Op*)nullptr));
+      for (int kk = 0; kk < NKD; ++kk) {
+        if constexpr (F32) hb[kk] = h[kk];
+        else hb[kk] = op_from_c(h[2 * kk], h[2 * kk + 1], (Op*)nullptr);
       }
-      vn[it] -= acc;
+      auto wop = [&](int it, int kk) __attribute__((always_inline)) {
+        const int r = it * 16 + li;
+        if constexpr (F32) return load4f(&sW[swz(r, kk * 16 + 4 * lg, D)]);
+        else return op_load<T>(&sW[swz(r, kk * 32 + 8 * lg, D)]);
+      };
+      f32x4 acc[NB];
+      Op wc[NB], wn[NB];
+#pragma unroll
+      for (int it = 0; it < NB; ++it) {
+        acc[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+        wc[it] = wop(it, 0);
+      }
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk) {
+        if (kk + 1 < NKD) {
+#pragma unroll
+          for (int it = 0; it < NB; ++it) wn[it] = wop(it, kk + 1);
+        }
+#pragma unroll
+        for (int it = 0; it < NB; ++it) mma(acc[it], wc[it], hb[kk]);
+#pragma unroll
+        for (int it = 0; it < NB; ++it) wc[it] = wn[it];
+      }
+#pragma unroll
+      for (int it = 0; it < NB; ++it) vn[it] -= acc[it];
     }
     T* vT = a.VnT + cid * D * BT + (size_t)col * BT;
     if (!write_tiles) {
@@ -874,25 +895,52 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
         *reinterpret_cast<Op*>(vT + p * 32 + 8 * lg) = op_from_c(vn[2 * p], vn[2 * p + 1], (Op*)nullptr);
     }
 
+    // h <- e^{g_last} h + kg^T v_new: the NDT row tiles of h are independent
+    // accumulators, the k-step over tokens outermost (as above); the next
+    // k-step's kg^T operands are read ahead while NDT <= 8 (registers).
+    {
+      constexpr int NKT = F32 ? NB : NB / 2;     // k-steps over t
+      constexpr bool AHEAD = NDT <= 8;
 #pragma unroll
-    for (int at = 0; at < NDT; ++at) {
-      const f32x4 egl = load4f(eglc + at * 16 + 4 * lg);
+      for (int at = 0; at < NDT; ++at) {
+        const f32x4 egl = load4f(eglc + at * 16 + 4 * lg);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) h[at][r] *= egl[r];
-      const int r = at * 16 + li;
-      if constexpr (F32) {
+        for (int r = 0; r < 4; ++r) h[at][r] *= egl[r];
+      }
+      auto kop = [&](int at, int kk) __attribute__((always_inline)) {
+        const int r = at * 16 + li;
+        if constexpr (F32) return load4f(&sK[swz(r, kk * 16 + 4 * lg, BT)]);
+        else return op_load<T>(&sK[swz(r, kk * 32 + 8 * lg, BT)]);
+      };
+      Op kc[NDT], kn[AHEAD ? NDT : 1];
+      if constexpr (AHEAD) {
 #pragma unroll
-        for (int it = 0; it < NB; ++it)
-          mma(h[at], load4f(&sK[swz(r, it * 16 + 4 * lg, BT)]), vn[it]);
-      } else {
+        for (int at = 0; at < NDT; ++at) kc[at] = kop(at, 0);
+      }
 #pragma unroll
-        for (int p = 0; p < NB / 2; ++p)
-          mma(h[at], op_load<T>(&sK[swz(r, p * 32 + 8 * lg, BT)]),
-              op_from_c(vn[2 * p], vn[2 * p + 1], (Op*)nullptr));
+      for (int kk = 0; kk < NKT; ++kk) {
+        Op vb;
+        if constexpr (F32) vb = vn[kk];
+        else vb = op_from_c(vn[2 * kk], vn[2 * kk + 1], (Op*)nullptr);
+        if constexpr (AHEAD) {
+          if (kk + 1 < NKT) {
+#pragma unroll
+            for (int at = 0; at < NDT; ++at) kn[at] = kop(at, kk + 1);
+          }
+#pragma unroll
+          for (int at = 0; at < NDT; ++at) mma(h[at], kc[at], vb);
+#pragma unroll
+          for (int at = 0; at < NDT; ++at) kc[at] = kn[at];
+        } else {
+#pragma unroll
+          for (int at = 0; at < NDT; ++at) mma(h[at], kop(at, kk), vb);
+        }
       }
       if (!mslice) {
 #pragma unroll
-        for (int r2 = 0; r2 < 4; ++r2) h[at][r2] = sanitize(h[at][r2]);
+        for (int at = 0; at < NDT; ++at)
+#pragma unroll
+          for (int r2 = 0; r2 < 4; ++r2) h[at][r2] = sanitize(h[at][r2]);
       }
     }
   };
