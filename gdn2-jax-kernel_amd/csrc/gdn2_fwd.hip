@@ -135,9 +135,15 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   __shared__ __align__(16) T sKbdT[D * TT_LD];  // (b k e^gc)^T [d][t]
   __shared__ __align__(16) float sA[BT * A_LD];
   __shared__ __align__(16) float sQA[NPN > 1 ? BT * A_LD : 4];  // Aqk partial sums
-  __shared__ __align__(16) float sTot[NB * DP];  // T_m: per-block sums of g
-  __shared__ __align__(16) float sETot[NB * DP]; // e^{T_m}
-  __shared__ __align__(16) float sF[2][NB * DP]; // e^{P_{I-1}}, e^{S_{I+1}} per (block, channel)
+  // per-(block, channel) decay factors of steps 1-3, then (free after step 3)
+  // the parked T = L_BA X_AA blocks of the inverse's doubling steps
+  constexpr int PARK = 16 * 20;   // one parked 16 x 16 block, rows padded to 20 floats
+  constexpr int SMALL = (4 * NB * DP > NB * NB / 4 * PARK) ? 4 * NB * DP : NB * NB / 4 * PARK;
+  __shared__ __align__(16) float sSmall[SMALL];
+  float* const sTot = sSmall;                  // T_m: per-block sums of g
+  float* const sETot = sSmall + NB * DP;       // e^{T_m}
+  float* const sF0 = sSmall + 2 * NB * DP;     // e^{P_{I-1}}
+  float* const sF1 = sSmall + 3 * NB * DP;     // e^{S_{I+1}}
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int cid = blockIdx.x;
@@ -256,11 +262,11 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
     if (tid < DP) {
       float run = 0.f;
 #pragma unroll
-      for (int m = 0; m < NB; ++m) { sF[0][m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
+      for (int m = 0; m < NB; ++m) { sF0[m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
       a.GL[(size_t)cid * D + d0 + tid] = run;
       run = 0.f;
 #pragma unroll
-      for (int m = NB - 1; m >= 0; --m) { sF[1][m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
+      for (int m = NB - 1; m >= 0; --m) { sF1[m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
     }
     __syncthreads();
 
@@ -316,11 +322,11 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
           const float lc = loc[i][x];
           const float eloc = __expf(lc);
           const float ekh = __expf(sTot[I * DP + ch] - lc);
-          const float egc = eloc * sF[0][I * DP + ch];
+          const float egc = eloc * sF0[I * DP + ch];
           const float bk = bv * kv;
           qg[e] = qv * egc;
           sKbdT[(d0 + ch) * TT_LD + t] = from_f<T>(bk * egc);
-          kgT[(size_t)(d0 + ch) * BT + kpos<T>(t)] = from_f<T>(kv * ekh * sF[1][I * DP + ch]);
+          kgT[(size_t)(d0 + ch) * BT + kpos<T>(t)] = from_f<T>(kv * ekh * sF1[I * DP + ch]);
           kh[e] = kv * ekh;
           aq[i][x] = qv * eloc;
           ak[i][x] = bk * eloc;
@@ -439,49 +445,83 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   }
   __syncthreads();
 
-  // ---- 4b. off-diagonal blocks, one column chain per (wave, column) ---------
-  //   X_IJ = -X_II * sum_{K=J}^{I-1} L_IK X_KJ, X_KJ kept in C layout.
-  f32x4 X[NBW][NB];
+  // ---- 4b. off-diagonal blocks by recursive doubling ------------------------
+  // For h = 1, 2, 4, ... 16-row blocks and each group [A0, A0 + 2h) with
+  // B0 = A0 + h: X_BA = -X_BB (L_BA X_AA), X_AA and X_BB being inverses from
+  // the previous h.  All groups and blocks of one h run in parallel over the
+  // waves (at h = NB/2 two blocks per wave, paired for equal work); T = L_BA X_AA
+  // is parked in sSmall between its two barriers.  L_BA is read before the
+  // barrier after which X_BA overwrites it.
+  {
+    auto rowop = [&](int R, int C) __attribute__((always_inline)) {
+      return load4f(&sA[(R * 16 + li) * A_LD + C * 16 + 4 * lg]);
+    };
+    auto colop = [&](const float* base, int ld) __attribute__((always_inline)) {
+      f32x4 y;
 #pragma unroll
-  for (int i = 0; i < NBW; ++i) {
-    const int J = own_block<NB>(wv, i);
+      for (int r = 0; r < 4; ++r) y[r] = base[(4 * lg + r) * ld + li];
+      return y;
+    };
+    auto Xc = [&](int R, int C) __attribute__((always_inline)) {
+      return colop(&sA[(R * 16) * A_LD + C * 16], A_LD);
+    };
+    auto put = [&](float* base, int ld, f32x4 v) __attribute__((always_inline)) {
 #pragma unroll
-    for (int I = 0; I < NB; ++I) {
-      X[i][I] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (I > J) {
-        f32x4 S = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int K = 0; K < NB; ++K) {
-          if (K >= J && K < I) {
-            f32x4 y;
-            if (K == J) {
-#pragma unroll
-              for (int r = 0; r < 4; ++r) y[r] = sA[(J * 16 + 4 * lg + r) * A_LD + J * 16 + li];
-            } else {
-              y = X[i][K];
-            }
-            mma(S, load4f(&sA[(I * 16 + li) * A_LD + K * 16 + 4 * lg]), y);
-          }
-        }
-        f32x4 R = {0.f, 0.f, 0.f, 0.f};
-        mma(R, load4f(&sA[(I * 16 + li) * A_LD + I * 16 + 4 * lg]), S);
-        X[i][I] = -R;
-      }
+      for (int r = 0; r < 4; ++r) base[(4 * lg + r) * ld + li] = v[r];
+    };
+    // h = 1: T is one block, kept in registers
+    if (wv < NB / 2) {
+      const int A0 = 2 * wv, B0 = A0 + 1;
+      f32x4 t = {0.f, 0.f, 0.f, 0.f}, x = {0.f, 0.f, 0.f, 0.f};
+      mma(t, rowop(B0, A0), Xc(A0, A0));
+      mma(x, rowop(B0, B0), t);
+      put(&sA[(B0 * 16) * A_LD + A0 * 16], A_LD, -x);
     }
-  }
-  __syncthreads();
+    __syncthreads();
+    auto level = [&](auto hc) __attribute__((always_inline)) {
+      constexpr int h = decltype(hc)::value;
+      constexpr int NOUT = NB * h / 2;          // blocks X_BA of this h, all groups
+      static_assert(NOUT <= PW || (NOUT == 2 * PW && h % 2 == 0), "blocks must split over waves");
+      auto tblock = [&](int g, int i, int j) __attribute__((always_inline)) {
+        const int A0 = g * 2 * h, B0 = A0 + h;
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < NBW; ++i) {
-    const int J = own_block<NB>(wv, i);
+        for (int k = 0; k < h; ++k)
+          if (k >= j) mma(t, rowop(B0 + i, A0 + k), Xc(A0 + k, A0 + j));
+        put(&sSmall[((g * h + i) * h + j) * PARK], 20, t);
+      };
+      auto xblock = [&](int g, int i, int j) __attribute__((always_inline)) {
+        const int A0 = g * 2 * h, B0 = A0 + h;
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int I = 0; I < NB; ++I) {
-      if (I > J) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sA[(I * 16 + 4 * lg + r) * A_LD + J * 16 + li] = X[i][I][r];
+        for (int k = 0; k < h; ++k)
+          if (k <= i) mma(x, rowop(B0 + i, B0 + k), colop(&sSmall[((g * h + k) * h + j) * PARK], 20));
+        put(&sA[((B0 + i) * 16) * A_LD + (A0 + j) * 16], A_LD, -x);
+      };
+      if constexpr (NOUT <= PW) {
+        const int g = wv / (h * h), i = (wv / h) % h, j = wv % h;
+        if (wv < NOUT) tblock(g, i, j);
+        __syncthreads();
+        if (wv < NOUT) xblock(g, i, j);
+        __syncthreads();
+      } else {
+        // one group (h = NB/2), two blocks per wave: T_ij costs h - j products,
+        // so a wave takes T_{i,q} and T_{i,h-1-q}; X_ij costs i + 1, so it takes
+        // X_{q,j} and X_{h-1-q,j} (i1 = its T row and X column)
+        static_assert(h * (h / 2) == PW, "pairs must cover the blocks once");
+        const int i1 = wv / (h / 2), q = wv % (h / 2);
+        tblock(0, i1, q);
+        tblock(0, i1, h - 1 - q);
+        __syncthreads();
+        xblock(0, q, i1);
+        xblock(0, h - 1 - q, i1);
+        __syncthreads();
       }
-    }
+    };
+    if constexpr (NB >= 4) level(std::integral_constant<int, 2>{});
+    if constexpr (NB >= 8) level(std::integral_constant<int, 4>{});
+    static_assert(NB <= 8, "doubling steps up to h = 4");
   }
-
   T* sWVT = sR0;
 #pragma unroll
   for (int pn = 0; pn < NPN; ++pn) {
