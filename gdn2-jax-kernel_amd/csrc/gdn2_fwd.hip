@@ -412,7 +412,9 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   }
   __syncthreads();
 
-  // w, v of the first panel: in flight during the inverse
+
+  // w, v of the first panel: in flight during the inverse (issued earlier they
+  // slow the load-bound first phase or hold registers through steps 2-3)
   Op wo[NBW][NKD], vo[NBW][NKD];
   auto load_wv = [&](int d0) __attribute__((always_inline)) {
 #pragma unroll
@@ -427,21 +429,39 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   };
   load_wv(0);
 
-  // ---- 4. A = (I + Akk)^{-1}: diagonal blocks by substitution ---------------
-  if (lg < NBW) {
-    const int I = own_block<NB>(wv, lg);
-    const int j = li;
-    const float* blk = &sA[(I * 16) * A_LD + I * 16];
-    float x[16];
+  // ---- 4. A = (I + Akk)^{-1}: diagonal blocks ---------------------------------
+  // The diagonal block L of Akk is strictly lower 16 x 16, so L^16 = 0 and
+  // (I + L)^{-1} = (I - L)(I + L^2)(I + L^4)(I + L^8): ten 16 x 16 products in
+  // four dependent rounds, on MFMA in registers.  For C-layout tiles
+  // mma(acc, C(P), C(Q)) accumulates P^T Q (a C tile read as the row operand is
+  // the transposed matrix), so each factor is carried with its transpose.
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float s = (r == j) ? 1.f : 0.f;
+  for (int i = 0; i < NBW; ++i) {
+    const int I = own_block<NB>(wv, i);
+    float* blk = &sA[(I * 16) * A_LD + I * 16];
+    f32x4 L, E;
 #pragma unroll
-      for (int kk = 0; kk < r; ++kk) s -= blk[r * A_LD + kk] * x[kk];
-      x[r] = s;
+    for (int r = 0; r < 4; ++r) {
+      L[r] = blk[(4 * lg + r) * A_LD + li];
+      E[r] = (4 * lg + r == li) ? 1.f : 0.f;
     }
+    const f32x4 Lt = load4f(&blk[li * A_LD + 4 * lg]);   // C(L^T)
+    auto mul = [](f32x4 a, f32x4 b) __attribute__((always_inline)) {
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+      mma(c, a, b);
+      return c;
+    };
+    const f32x4 P2 = mul(Lt, L), P2t = mul(L, Lt);          // L^2, (L^2)^T
+    const f32x4 M1 = mul(E - Lt, E + P2);                    // (I - L)(I + L^2)
+    const f32x4 M1t = mul(E + P2, E - Lt);
+    const f32x4 P4 = mul(P2t, P2), P4t = mul(P2, P2t);      // L^4, (L^4)^T
+    const f32x4 M2 = mul(M1t, E + P4);                       // M1 (I + L^4)
+    const f32x4 M2t = mul(E + P4, M1t);
+    const f32x4 P8 = mul(P4t, P4);                           // L^8
+    const f32x4 M = mul(M2t, E + P8);                        // M2 (I + L^8)
+    (void)M2;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sA[(I * 16 + r) * A_LD + I * 16 + j] = x[r];
+    for (int r = 0; r < 4; ++r) blk[(4 * lg + r) * A_LD + li] = M[r];
   }
   __syncthreads();
 
