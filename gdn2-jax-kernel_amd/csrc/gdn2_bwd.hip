@@ -406,29 +406,272 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
 }
 
 // ============================================================================
-// bwd_elem: b k e^gc and w v per token (chunk-major [t][d]); one thread per channel.
+// bwd_wy (B3, fused): per chunk the products of gdn2_bwd.py:126-210 and the
+// element-wise b k e^{gc}, w v, with dW, dA and dA A^T kept on chip:
+//   dqg  = scale do h^T              dW    = -dv_new h^T
+//   dkg  = v_new dh'^T               dA    = (dW (b k e^gc)^T + dv_new (w v)^T) . strict
+//   d(bke^gc) = A^T dW               d(wv) = A^T dv_new
+//   dAkk = -(A^T (dA A^T)) . strict
+// Stored operands per chunk: do in (B,T,H,D) rows; h^T, dh'^T as [e][d]; v_new^T,
+// dv_new^T as [e][t]; A as [t][s].  One workgroup per chunk; wave w owns the
+// 16-token row block w of every product (up to 2 x 8 independent 16 x 16
+// accumulators).  Shared operands sit in LDS:
+//   R1: h^T, then dh'^T, then (b k e^gc | w v) as [s][d], then dv_new^T
+//   R2: dW [t][d]     R4: dA [t][s], then dA A^T     R5: A [t][s]
+// A stored matrix read with its row index as the MFMA k index is read per lane
+// as four scalars (colop); one read with k contiguous is one 16-byte load (rowop).
 // ============================================================================
 template <typename T, typename TG>
-struct ElemArgs {
+struct WyArgs {
   const T *k, *w, *v, *b;
   const TG* g;
-  int T_len, H, N, BT, D;
-  float *KBD, *WVM;
+  const float* dout;
+  const T* HT;        // forward residual h^T [cid][D][D] (bfloat16: chained columns)
+  const T* VnT;       // forward residual v_new^T [cid][D][BT] (bfloat16: chained columns)
+  const float* A;     // forward residual A [cid][BT][BT]
+  const float* DHT;   // dh'^T [cid][D][D]
+  const float* DVNT;  // dv_new^T [cid][D][BT]
+  int T_len, H, N;
+  float scale;
+  float *DQG, *DKG, *DKBD, *DWV, *DAKK;  // [cid][BT][D] x 4, [cid][BT][BT]
 };
 
-template <typename T, typename TG>
-__global__ void bwd_elem(ElemArgs<T, TG> a) {
-  const int d = threadIdx.x, cid = blockIdx.x;
+template <typename T, typename TG, int D>
+__global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
+  constexpr int BT = 64, NB = BT / 16, NDT = D / 16, NKT = BT / 16;
+  constexpr int LD1 = D + 4, LDV = BT + 4, LD2 = D + 4, LD4 = BT + 4;
+  constexpr int R1 = (D * LD1 > 2 * BT * LD1) ? D * LD1 : 2 * BT * LD1;
+  constexpr int BF = sizeof(T) == 2;
+  __shared__ __align__(16) float sR1[R1];
+  __shared__ __align__(16) float sR2[BT * LD2];
+  __shared__ __align__(16) float sR4[BT * LD4];
+  __shared__ __align__(16) float sR5[BT * LD4];
+  __shared__ __align__(16) float sTot[NB * D];
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int cid = blockIdx.x;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
-  const size_t HD = (size_t)a.H * a.D;
-  const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * a.BT) * HD + (size_t)hh * a.D + d;
-  float gc = 0.f;
-  for (int t = 0; t < a.BT; ++t) {
-    const size_t o = tok0 + (size_t)t * HD;
-    gc += to_f(a.g[o]);
-    const size_t od = ((size_t)cid * a.BT + t) * a.D + d;
-    a.KBD[od] = to_f(a.b[o]) * to_f(a.k[o]) * __expf(gc);
-    a.WVM[od] = to_f(a.w[o]) * to_f(a.v[o]);
+  const size_t HD = (size_t)a.H * D;
+  const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D;
+  const int t = wv * 16 + li;   // this lane's row for row operands of the own block
+
+  auto rowop = [&](const float* base, int ld, int r0, int k0) __attribute__((always_inline)) {
+    return load4f(&base[(r0 + li) * ld + k0 + 4 * lg]);
+  };
+  auto colop = [&](const float* base, int ld, int k0, int c0) __attribute__((always_inline)) {
+    f32x4 y;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = base[(k0 + 4 * lg + r) * ld + c0 + li];
+    return y;
+  };
+  // C-layout element (r) of the own block's tile at column tile nt: row, column
+  auto orow = [&](int r) { return wv * 16 + 4 * lg + r; };
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+
+  // ---- 1. dqg = scale do h^T, dW = -dv_new h^T --------------------------------
+  Staged st;
+  const GMat mH{a.HT, BF, 0, 0, 0, D, 0, 0, BF};
+  stage_load(st, mH, (size_t)cid * D * D, D, D, tid);
+  f32x4 xdo[NDT], xdv[NDT];
+#pragma unroll
+  for (int kg = 0; kg < NDT; ++kg) {
+    xdo[kg] = load4f(a.dout + tok0 + (size_t)t * HD + kg * 16 + 4 * lg);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      xdv[kg][r] = a.DVNT[((size_t)cid * D + kg * 16 + 4 * lg + r) * BT + t];
+  }
+  stage_store(sR1, LD1, st, mH, D, D, 0, 0, false, tid);
+  __syncthreads();
+  {
+    f32x4 aq[NDT], aw[NDT];
+#pragma unroll
+    for (int nt = 0; nt < NDT; ++nt) aq[nt] = aw[nt] = z4;
+#pragma unroll
+    for (int kg = 0; kg < NDT; ++kg)
+#pragma unroll
+      for (int nt = 0; nt < NDT; ++nt) {
+        const f32x4 y = colop(sR1, LD1, kg * 16, nt * 16);    // h[d][e] as (n = d, k = e)
+        mma(aq[nt], xdo[kg], y);
+        mma(aw[nt], xdv[kg], y);
+      }
+    float* dqg = a.DQG + (size_t)cid * BT * D;
+#pragma unroll
+    for (int nt = 0; nt < NDT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dqg[orow(r) * D + nt * 16 + li] = a.scale * aq[nt][r];
+        sR2[orow(r) * LD2 + nt * 16 + li] = -aw[nt][r];
+      }
+  }
+  __syncthreads();   // every wave is done with h^T
+
+  // ---- 2. dkg = v_new dh'^T ------------------------------------------------------
+  const GMat mDH{a.DHT, 0, 0, 0, 0, D, 0, 0, 0};
+  const GMat mA{a.A, 0, 0, 0, 0, BT, 0, 0, 0};
+  Staged sa;
+  stage_load(st, mDH, (size_t)cid * D * D, D, D, tid);
+  stage_load(sa, mA, (size_t)cid * BT * BT, BT, BT, tid);
+  {
+    f32x4 xvn[NDT];
+    const int tp = BF ? kpos<bf16_t>(t) : t;   // stored column of token t
+#pragma unroll
+    for (int kg = 0; kg < NDT; ++kg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        xvn[kg][r] = to_f(a.VnT[((size_t)cid * D + kg * 16 + 4 * lg + r) * BT + tp]);
+    stage_store(sR1, LD1, st, mDH, D, D, 0, 0, false, tid);
+    stage_store(sR5, LD4, sa, mA, BT, BT, 0, 0, false, tid);
+    __syncthreads();
+    f32x4 ak[NDT];
+#pragma unroll
+    for (int nt = 0; nt < NDT; ++nt) ak[nt] = z4;
+#pragma unroll
+    for (int kg = 0; kg < NDT; ++kg)
+#pragma unroll
+      for (int nt = 0; nt < NDT; ++nt) mma(ak[nt], xvn[kg], colop(sR1, LD1, kg * 16, nt * 16));
+    float* dkg = a.DKG + (size_t)cid * BT * D;
+#pragma unroll
+    for (int nt = 0; nt < NDT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dkg[orow(r) * D + nt * 16 + li] = ak[nt][r];
+  }
+
+  // ---- 3. b k e^{gc} and w v into R1 (rows s of the own block) ------------------
+  // lane (li, lg): token s = t, channels 16 j + 4 lg + e; gc = in-block cumsum over
+  // the 16 lanes li (DPP) + the sums of the earlier blocks (sTot)
+  constexpr int NJ = D / 16;
+  float loc[NJ][4], bk[NJ][4];
+  {
+    const size_t row = tok0 + (size_t)t * HD;
+    float gv[NJ][4], bv[NJ][4], kv[NJ][4], wvv[NJ][4], vv[NJ][4];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const size_t o = row + j * 16 + 4 * lg;
+      load_f<4>(a.g + o, gv[j]);
+      load_f<4>(a.b + o, bv[j]);
+      load_f<4>(a.k + o, kv[j]);
+      load_f<4>(a.w + o, wvv[j]);
+      load_f<4>(a.v + o, vv[j]);
+    }
+    __syncthreads();   // every wave is done with dh'^T
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      f32x4 wvo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        loc[j][e] = row_scan16(gv[j][e]);
+        bk[j][e] = bv[j][e] * kv[j][e];
+        wvo[e] = wvv[j][e] * vv[j][e];
+      }
+      *reinterpret_cast<f32x4*>(&sR1[(BT + t) * LD1 + j * 16 + 4 * lg]) = wvo;
+      if (li == 15) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sTot[wv * D + j * 16 + 4 * lg + e] = loc[j][e];
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    f32x4 kb;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float gc = loc[j][e];
+      for (int m = 0; m < wv; ++m) gc += sTot[m * D + j * 16 + 4 * lg + e];
+      kb[e] = bk[j][e] * __expf(gc);
+    }
+    *reinterpret_cast<f32x4*>(&sR1[t * LD1 + j * 16 + 4 * lg]) = kb;
+  }
+  __syncthreads();
+
+  // ---- 4. dA = (dW (b k e^gc)^T + dv_new (w v)^T) . strict ----------------------
+  {
+    f32x4 ada[NKT];
+#pragma unroll
+    for (int st2 = 0; st2 < NKT; ++st2) ada[st2] = z4;
+#pragma unroll
+    for (int kg = 0; kg < NDT; ++kg) {
+      const f32x4 x1 = rowop(sR2, LD2, wv * 16, kg * 16);   // dW rows, k = d
+#pragma unroll
+      for (int st2 = 0; st2 < NKT; ++st2) {
+        mma(ada[st2], x1, rowop(sR1, LD1, st2 * 16, kg * 16));           // (b k e^gc)[s][d]
+        mma(ada[st2], xdv[kg], rowop(sR1, LD1, BT + st2 * 16, kg * 16));  // (w v)[s][e]
+      }
+    }
+#pragma unroll
+    for (int st2 = 0; st2 < NKT; ++st2)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int s2 = st2 * 16 + li;
+        sR4[orow(r) * LD4 + s2] = s2 < orow(r) ? ada[st2][r] : 0.f;
+      }
+  }
+  __syncthreads();   // dA complete; (b k e^gc | w v) no longer read
+
+  // ---- 5. d(bke^gc) = A^T dW, d(wv) = A^T dv_new, TMP = dA A^T -------------------
+  const GMat mDV{a.DVNT, 0, 0, 0, 0, BT, 0, 0, 0};
+  stage_load(st, mDV, (size_t)cid * D * BT, D, BT, tid);
+  stage_store(sR1, LDV, st, mDV, D, BT, 0, 0, false, tid);
+  __syncthreads();
+  {
+    f32x4 akb[NDT], awv[NDT];
+#pragma unroll
+    for (int nt = 0; nt < NDT; ++nt) akb[nt] = awv[nt] = z4;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+      const f32x4 x = colop(sR5, LD4, kt * 16, wv * 16);   // A^T rows m, k = t
+#pragma unroll
+      for (int nt = 0; nt < NDT; ++nt) {
+        mma(akb[nt], x, colop(sR2, LD2, kt * 16, nt * 16));   // dW[t][d] as (n = d, k = t)
+        mma(awv[nt], x, rowop(sR1, LDV, nt * 16, kt * 16));   // dv_new^T[e][t]
+      }
+    }
+    float* dkbd = a.DKBD + (size_t)cid * BT * D;
+    float* dwv = a.DWV + (size_t)cid * BT * D;
+#pragma unroll
+    for (int nt = 0; nt < NDT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dkbd[orow(r) * D + nt * 16 + li] = akb[nt][r];
+        dwv[orow(r) * D + nt * 16 + li] = awv[nt][r];
+      }
+  }
+  {
+    f32x4 atm[NKT];
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt) atm[nt] = z4;
+#pragma unroll
+    for (int ks = 0; ks < NKT; ++ks) {
+      const f32x4 x = rowop(sR4, LD4, wv * 16, ks * 16);    // dA rows t, k = s
+#pragma unroll
+      for (int nt = 0; nt < NKT; ++nt) mma(atm[nt], x, rowop(sR5, LD4, nt * 16, ks * 16));  // A[n][s]
+    }
+    // the own rows of dA are read only by this wave: overwrite them with dA A^T
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sR4[orow(r) * LD4 + nt * 16 + li] = atm[nt][r];
+  }
+  __syncthreads();
+
+  // ---- 6. dAkk = -(A^T (dA A^T)) . strict -----------------------------------------
+  {
+    f32x4 aak[NKT];
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt) aak[nt] = z4;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+      const f32x4 x = colop(sR5, LD4, kt * 16, wv * 16);    // A^T rows m, k
+#pragma unroll
+      for (int nt = 0; nt < NKT; ++nt) mma(aak[nt], x, colop(sR4, LD4, kt * 16, nt * 16));
+    }
+    float* dakk = a.DAKK + (size_t)cid * BT * BT;
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n2 = nt * 16 + li;
+        dakk[orow(r) * BT + n2] = n2 < orow(r) ? -aak[nt][r] : 0.f;
+      }
   }
 }
 
@@ -781,29 +1024,14 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                        dim3(64 * (BW + BP)), 0, st, sa);
     launch_mark(st);
     if (NC > 0) {
-      ElemArgs<T, TG> ea{(const T*)k, (const T*)w, (const T*)v, (const T*)b, (const TG*)g,
-                         T_len, H, N, BT, D, buf(B_KBD), buf(B_WVM)};
-      hipLaunchKernelGGL((bwd_elem<T, TG>), dim3(NC), dim3(D), 0, st, ea);
+      // B3, one fused kernel
+      WyArgs<T, TG> wa{(const T*)k,  (const T*)w,     (const T*)v,  (const T*)b, (const TG*)g,
+                       dout,         (const T*)fHT,   (const T*)fVnT,
+                       reinterpret_cast<const float*>(fA), buf(B_DHT), buf(B_DVNT),
+                       T_len, H, N, scale, buf(B_DQG), buf(B_DKG), buf(B_DKBD), buf(B_DWV),
+                       buf(B_DAKK)};
+      hipLaunchKernelGGL((bwd_wy<T, TG, D>), dim3(NC), dim3(256), 0, st, wa);
       launch_mark(st);
-      // B3 products
-      gemm(st, dm, tok_mat(dout, 0, dm), res_mat(fHT, tb, dm, D, D),
-           ch_out(buf(B_DQG), dm, BT, D, scale), BT, D, D);
-      gemm(st, dm, ch_mat(buf(B_DVNT), 0, dm, D, BT, 1), res_mat(fHT, tb, dm, D, D),
-           ch_out(buf(B_DW), dm, BT, D, -1.f), BT, D, D);
-      gemm(st, dm, res_mat(fVnT, tb, dm, D, BT, 1), ch_mat(buf(B_DHT), 0, dm, D, D),
-           ch_out(buf(B_DKG), dm, BT, D), BT, D, D);
-      gemm(st, dm, ch_mat(buf(B_DW), 0, dm, BT, D), ch_mat(buf(B_KBD), 0, dm, BT, D, 1),
-           ch_out(buf(B_DA), dm, BT, BT, 1.f, 0, 2), BT, BT, D);
-      gemm(st, dm, ch_mat(buf(B_DVNT), 0, dm, D, BT, 1), ch_mat(buf(B_WVM), 0, dm, BT, D, 1),
-           ch_out(buf(B_DA), dm, BT, BT, 1.f, 0, 2, 1), BT, BT, D);
-      gemm(st, dm, ch_mat(fA, 0, dm, BT, BT, 1), ch_mat(buf(B_DW), 0, dm, BT, D),
-           ch_out(buf(B_DKBD), dm, BT, D), BT, D, BT);
-      gemm(st, dm, ch_mat(fA, 0, dm, BT, BT, 1), ch_mat(buf(B_DVNT), 0, dm, D, BT, 1),
-           ch_out(buf(B_DWV), dm, BT, D), BT, D, BT);
-      gemm(st, dm, ch_mat(buf(B_DA), 0, dm, BT, BT), ch_mat(fA, 0, dm, BT, BT, 1),
-           ch_out(buf(B_TMP), dm, BT, BT), BT, BT, BT);
-      gemm(st, dm, ch_mat(fA, 0, dm, BT, BT, 1), ch_mat(buf(B_TMP), 0, dm, BT, BT),
-           ch_out(buf(B_DAKK), dm, BT, BT, -1.f, 0, 2), BT, BT, BT);
       // B4
       GramArgs<T, TG> gr{(const T*)q, (const T*)k, (const T*)b, (const TG*)g, buf(B_DAQK),
                          buf(B_DAKK), T_len, H, N, scale, buf(B_RQ), buf(B_RBK), buf(B_RK),

@@ -191,6 +191,26 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Row-wise (16-lane) DPP helpers: inclusive prefix sum over lanes li = 0..15
+// (row_shr 1,2,4,8 with out-of-row sources reading 0) and broadcast of lane n
+// of each row (row_newbcast).
+template <int CTRL>
+__device__ __forceinline__ float row_shr_add(float x) {
+  return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                 0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float row_scan16(float x) {
+  x = row_shr_add<0x111>(x);
+  x = row_shr_add<0x112>(x);
+  x = row_shr_add<0x114>(x);
+  return row_shr_add<0x118>(x);
+}
+template <int N>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+             0, __builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, false));
+}
+
 // Copy `rows` rows of `cols` elements (row pitch `gpitch` in global, `lpitch`
 // in LDS) with 16-byte transactions spread over the workgroup.
 template <typename T, int NT>

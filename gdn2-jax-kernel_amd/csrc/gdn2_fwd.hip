@@ -77,25 +77,6 @@ __device__ __forceinline__ int own_block(int wv, int i) {
   return i == 0 ? wv : NB - 1 - wv;
 }
 
-// Row-wise (16-lane) DPP helpers: inclusive prefix sum over lanes li = 0..15
-// (row_shr 1,2,4,8 with out-of-row sources reading 0) and broadcast of lane n
-// of each row (row_newbcast).
-template <int CTRL>
-__device__ __forceinline__ float row_shr_add(float x) {
-  return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                 0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float row_scan16(float x) {
-  x = row_shr_add<0x111>(x);
-  x = row_shr_add<0x112>(x);
-  x = row_shr_add<0x114>(x);
-  return row_shr_add<0x118>(x);
-}
-template <int N>
-__device__ __forceinline__ float row_bcast(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-             0, __builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, false));
-}
 
 // One workgroup per chunk with prep_waves(BT) waves.  A wave owns one 16-token
 // row block (8 waves at BT = 128), or the pair {wv, NB-1-wv} when there are

@@ -97,8 +97,8 @@ inline int state_segments(long long BH, int N, int D, int forced) {
 namespace gdn2 {
 
 enum BwdBuf {
-  B_DAQK, B_DVPT, B_QDOT, B_DHT, B_DVNT, B_KBD, B_WVM, B_DQG, B_DW, B_DKG, B_DKBD, B_DWV,
-  B_DA, B_TMP, B_DAKK, B_RQ, B_RBK, B_RK, B_DQD, B_DKD, B_DBKD, B_COUNT
+  B_DAQK, B_DVPT, B_QDOT, B_DHT, B_DVNT, B_DQG, B_DKG, B_DKBD, B_DWV, B_DAKK,
+  B_RQ, B_RBK, B_RK, B_DQD, B_DKD, B_DBKD, B_COUNT
 };
 
 struct BwdLayout {
@@ -110,8 +110,8 @@ struct BwdLayout {
 inline BwdLayout bwd_layout(size_t nchunks, int BT, int D) {
   BwdLayout L;
   const size_t tt = (size_t)BT * BT, td = (size_t)BT * D, dd = (size_t)D * D;
-  const size_t per[B_COUNT] = {tt, td, dd, dd, td, td, td, td, td, td, td,
-                               td, tt, tt, tt, td, td, td, td, td, td};
+  const size_t per[B_COUNT] = {tt, td, dd, dd, td, td, td, td, td, tt,
+                               td, td, td, td, td, td};
   size_t off = 0;
   for (int i = 0; i < B_COUNT; ++i) {
     L.off[i] = off;
