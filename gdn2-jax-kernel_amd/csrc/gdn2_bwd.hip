@@ -434,6 +434,7 @@ struct WyArgs {
   int T_len, H, N;
   float scale;
   float *DQG, *DKG, *DKBD, *DWV, *DAKK;  // [cid][BT][D] x 4, [cid][BT][BT]
+  float* SDH;         // [cid][D]: sum_e dh'[d][e] h[d][e] (the g_last term of dgc)
 };
 
 template <typename T, typename TG, int D>
@@ -447,12 +448,14 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
   __shared__ __align__(16) float sR4[BT * LD4];
   __shared__ __align__(16) float sR5[BT * LD4];
   __shared__ __align__(16) float sTot[NB * D];
+  __shared__ __align__(16) float sSdh[D];
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int cid = blockIdx.x;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
   const size_t HD = (size_t)a.H * D;
   const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D;
   const int t = wv * 16 + li;   // this lane's row for row operands of the own block
+  if (tid < D) sSdh[tid] = 0.f;
 
   auto rowop = [&](const float* base, int ld, int r0, int k0) __attribute__((always_inline)) {
     return load4f(&base[(r0 + li) * ld + k0 + 4 * lg]);
@@ -518,9 +521,29 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         xvn[kg][r] = to_f(a.VnT[((size_t)cid * D + kg * 16 + 4 * lg + r) * BT + tp]);
+    // sum_e dh'[d][e] h[d][e]: each thread multiplies the dh'^T runs it staged
+    // with the h^T runs still at the same places in R1 (the thread's column
+    // group is fixed: index tid + 256 u keeps tid mod D/4), then one LDS add per
+    // column
+    {
+      float part[4] = {0.f, 0.f, 0.f, 0.f};
+      constexpr int CQ = D / 4;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int i = tid + 256 * u;
+        if (i < D * CQ) {
+          const f32x4 hv = load4f(&sR1[(i / CQ) * LD1 + (i % CQ) * 4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) part[e] += st.v[u][e] * hv[e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) atomicAdd(&sSdh[(tid % CQ) * 4 + e], part[e]);
+    }
     stage_store(sR1, LD1, st, mDH, D, D, 0, 0, false, tid);
     stage_store(sR5, LD4, sa, mA, BT, BT, 0, 0, false, tid);
     __syncthreads();
+    if (tid < D) a.SDH[(size_t)cid * D + tid] = sSdh[tid];
     f32x4 ak[NDT];
 #pragma unroll
     for (int nt = 0; nt < NDT; ++nt) ak[nt] = z4;
@@ -865,8 +888,7 @@ template <typename T, typename TG>
 struct CombArgs {
   const T *q, *k, *v, *w, *b;
   const TG* g;
-  const T* HT;   // fwd ws [cid][D][D]
-  const float *DHT, *DQG, *DKG, *DKBD, *DWV, *RQ, *RBK, *RK, *DQD, *DKD, *DBKD;
+  const float *SDH, *DQG, *DKG, *DKBD, *DWV, *RQ, *RBK, *RK, *DQD, *DKD, *DBKD;
   int T_len, H, N;
   float scale;
   T *dq, *dk, *dv, *dw, *db;
@@ -894,13 +916,8 @@ __global__ void __launch_bounds__(128) bwd_combine(CombArgs<T, TG> a) {
     if (t % 16 == 15) tot[t / 16] = lrun;
   }
   const float gl = run;
-  // exp(gl) * sum_dv dh'[d][dv] h[d][dv]  (gdn2_bwd.py:196-197)
-  float sdh = 0.f;
-  {
-    const T* ht = a.HT + (size_t)cid * D * D + kpos<T>(d);
-    const float* dht = a.DHT + (size_t)cid * D * D + d;
-    for (int dv = 0; dv < D; ++dv) sdh += dht[(size_t)dv * D] * to_f(ht[(size_t)dv * D]);
-  }
+  // exp(gl) * sum_dv dh'[d][dv] h[d][dv]  (gdn2_bwd.py:196-197), the sum from bwd_wy
+  const float sdh = a.SDH[(size_t)cid * D + d];
   float dgc[BT];
   float skg = 0.f;
 #pragma unroll
@@ -910,8 +927,8 @@ __global__ void __launch_bounds__(128) bwd_combine(CombArgs<T, TG> a) {
     const float qv = to_f(a.q[o]), kv = to_f(a.k[o]), vv = to_f(a.v[o]), wv = to_f(a.w[o]),
                 bv = to_f(a.b[o]);
     const float eg = __expf(gcv[t]), ekg = __expf(gl - gcv[t]);
-    const float el = __expf(lcv[t]), ek = __expf(tot[t / 16] - lcv[t]);
     const float dqg = a.DQG[w_], dkg = a.DKG[w_], dkbd = a.DKBD[w_], dwv = a.DWV[w_];
+    const float el = __expf(lcv[t]), ek = __expf(tot[t / 16] - lcv[t]);
     const float gq = a.scale * el * a.RQ[w_] + a.DQD[w_];
     const float gbk = el * a.RBK[w_] + a.DBKD[w_];
     const float gk = ek * a.RK[w_] + a.DKD[w_];
@@ -1029,7 +1046,7 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                        dout,         (const T*)fHT,   (const T*)fVnT,
                        reinterpret_cast<const float*>(fA), buf(B_DHT), buf(B_DVNT),
                        T_len, H, N, scale, buf(B_DQG), buf(B_DKG), buf(B_DKBD), buf(B_DWV),
-                       buf(B_DAKK)};
+                       buf(B_DAKK), buf(B_SDH)};
       hipLaunchKernelGGL((bwd_wy<T, TG, D>), dim3(NC), dim3(256), 0, st, wa);
       launch_mark(st);
       // B4
@@ -1040,9 +1057,10 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
       launch_mark(st);
       // B3 tail + B5
       CombArgs<T, TG> ca{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
-                         (const TG*)g, (const T*)fHT, buf(B_DHT), buf(B_DQG), buf(B_DKG),
-                         buf(B_DKBD), buf(B_DWV), buf(B_RQ), buf(B_RBK), buf(B_RK), buf(B_DQD),
-                         buf(B_DKD), buf(B_DBKD), T_len, H, N, scale, (T*)dq, (T*)dk, (T*)dv,
+                         (const TG*)g, buf(B_SDH), buf(B_DQG), buf(B_DKG),
+                         buf(B_DKBD), buf(B_DWV), buf(B_RQ), buf(B_RBK), buf(B_RK),
+                         buf(B_DQD), buf(B_DKD), buf(B_DBKD), T_len, H, N, scale, (T*)dq,
+                         (T*)dk, (T*)dv,
                          (T*)dw, (T*)db, (TG*)dg};
       hipLaunchKernelGGL((bwd_combine<T, TG, D>), dim3(NC), dim3(128), 0, st, ca);
       launch_mark(st);
