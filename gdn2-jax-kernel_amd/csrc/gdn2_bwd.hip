@@ -4,12 +4,12 @@
 //
 // Per chunk c with state h = h_c entering it, dh' = dh_{c+1} leaving it
 // (kg = k e^{gl-gc}, qg = q e^{gc}, W = A (b k e^{gc}), u = A (w v)):
-//   B2   dAqk = (do v_new^T) . causal              Aqk^T do, scale qg^T do   (chunk_gemm)
+//   B2   dAqk = (do v_new^T) . causal              Aqk^T do, scale qg^T do   (bwd_b2)
 //   B1   dv_new = Aqk^T do + kg dh'                                          (bwd_state,
 //        dh = e^{gl} dh' + scale qg^T do - W^T dv_new                         serial)
 //   B3   dqg = scale do h^T, dW = -dv_new h^T, dkg = v_new dh'^T,
 //        dA = dW (b k e^gc)^T + dv_new (w v)^T, d(bke^gc) = A^T dW, d(wv) = A^T dv_new,
-//        dAkk = -(A^T dA A^T) . strict                                        (chunk_gemm)
+//        dAkk = -(A^T dA A^T) . strict                                        (bwd_wy)
 //   B4   gradients of Aqk/Akk wrt q, k, b k, gc                              (gram_bwd)
 //   B5   chain rule through the exponentials + reverse cumsum of dgc          (bwd_combine)
 
@@ -19,33 +19,16 @@
 namespace gdn2 {
 
 // ============================================================================
-// chunk_gemm: per chunk, C = alpha * op(A) op(B) (+ C), M,N,K <= 128, K % 16 == 0.
+// Operand staging: a stored per-chunk matrix into LDS as float32, all loads
+// issued before any LDS store (one memory round trip per operand).
 // ============================================================================
 struct GMat {
   const void* p;
   int bf16;                 // element type in memory
-  long long sb, sh, sc;     // element offset per batch, head, chunk index
   int ld;                   // row pitch of the stored matrix
-  int trans;                // logical (r, k) stored at [k*ld + r] (1) or [r*ld + k] (0)
   int mask;                 // on stored (row, col): 1 keep col <= row, 2 keep col < row
   int chained;              // bfloat16 columns stored in chained order (kpos)
 };
-struct GOut {
-  float* p;
-  long long sb, sh, sc;
-  int ld;
-  int trans;                // C[m][n] stored at [n*ld + m] (1) or [m*ld + n] (0)
-  int mask;                 // on (m, n): 1 keep n <= m, 2 keep n < m
-  float alpha;
-  int accum;
-};
-struct GemmArgs {
-  GMat A, B;
-  GOut C;
-  int M, N, K, H, Nc;
-  int nsplit;   // workgroups per chunk, each taking N / nsplit output columns
-};
-
 __device__ __forceinline__ void load4_any(const void* p, int bf16, size_t idx, float* v) {
   if (bf16) {
     const bf16x4 t = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const bf16_t*>(p) + idx);
@@ -98,54 +81,6 @@ __device__ __forceinline__ void stage_store(float* dst, int ld, const Staged& s,
 #pragma unroll
         for (int e = 0; e < 4; ++e) dst[(c + e) * ld + r] = v[e];
       }
-    }
-  }
-}
-
-// C[m][n] = alpha * sum_k A(m,k) B(n,k) (+ C) for one chunk, fp32 MFMA.  Both
-// operands are staged as [row][k] with pitch K+4 in dynamic LDS sized to the
-// shape ((M + N/nsplit) (K+4) floats, two or more workgroups per CU for
-// every product of the backward); products with N = 128 against K = 128 are
-// split over two workgroups per chunk.
-__global__ void __launch_bounds__(256) chunk_gemm(GemmArgs a) {
-  extern __shared__ __align__(16) float smem[];
-  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  const int M = a.M, K = a.K, Nw = a.N / a.nsplit, ld = K + 4;
-  const int ns = blockIdx.x % a.nsplit, cid = blockIdx.x / a.nsplit, n0 = ns * Nw;
-  float* sX = smem;            // A as [m][k]
-  float* sY = smem + M * ld;   // B rows n0 .. n0 + Nw as [n][k]
-  const int c = cid % a.Nc, bh = cid / a.Nc, hh = bh % a.H, bb = bh / a.H;
-  const size_t offA = bb * a.A.sb + hh * a.A.sh + c * a.A.sc;
-  // B stored [n][k] (trans) or [k][n]: start at row / column n0
-  const size_t offB = bb * a.B.sb + hh * a.B.sh + c * a.B.sc +
-                      (a.B.trans ? (size_t)n0 * a.B.ld : (size_t)n0);
-  const size_t offC = bb * a.C.sb + hh * a.C.sh + c * a.C.sc;
-  {
-    Staged ra, rb;
-    stage_load(ra, a.A, offA, a.A.trans ? K : M, a.A.trans ? M : K, tid);
-    stage_load(rb, a.B, offB, a.B.trans ? Nw : K, a.B.trans ? K : Nw, tid);
-    stage_store(sX, ld, ra, a.A, a.A.trans ? K : M, a.A.trans ? M : K, 0, 0, a.A.trans != 0,
-                tid);
-    stage_store(sY, ld, rb, a.B, a.B.trans ? Nw : K, a.B.trans ? K : Nw, a.B.trans ? n0 : 0,
-                a.B.trans ? 0 : n0, a.B.trans == 0, tid);
-  }
-  __syncthreads();
-  const int tn = Nw >> 4, ntile = (M >> 4) * tn, nk = K >> 4;
-  for (int t = wv; t < ntile; t += 4) {
-    const int mt = t / tn, nt = t - mt * tn;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int kg = 0; kg < nk; ++kg)
-      mma(acc, load4f(&sX[(mt * 16 + li) * ld + kg * 16 + 4 * lg]),
-          load4f(&sY[(nt * 16 + li) * ld + kg * 16 + 4 * lg]));
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = mt * 16 + 4 * lg + r, n = n0 + nt * 16 + li;
-      float val = a.C.alpha * acc[r];
-      if ((a.C.mask == 1 && n > m) || (a.C.mask == 2 && n >= m)) val = 0.f;
-      float* dst = a.C.p + offC + (a.C.trans ? (size_t)n * a.C.ld + m : (size_t)m * a.C.ld + n);
-      if (a.C.accum) val += *dst;
-      *dst = val;
     }
   }
 }
@@ -406,6 +341,129 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
 }
 
 // ============================================================================
+// bwd_b2 (B2, fused): per chunk (gdn2_bwd.py:84-122 and the qg^T do term of B1)
+//   dAqk = (do v_new^T) . causal        [t][s]
+//   dvp^T = (Aqk^T do)^T                [e][s]   (the causal Aqk)
+//   qdot = scale do^T qg                [e][d]   ((scale qg^T do)^T)
+// with do, v_new^T, Aqk and qg staged once in LDS as float32.  Wave w owns the
+// 16-row block w of dAqk and of Aqk^T do, and row blocks 2w, 2w+1 (over e) of
+// qdot (D = 128; one block per wave at D = 64).
+// ============================================================================
+template <typename T>
+struct B2Args {
+  const float* dout;
+  const T* VnT;       // forward residual v_new^T [cid][D][BT] (bfloat16: chained columns)
+  const T* Aqk;       // forward residual Aqk [cid][BT][BT] (entries right of the diagonal
+                      // block are not written: masked here)
+  const T* Qg;        // forward residual qg [cid][BT][D]
+  int T_len, H, N;
+  float scale;
+  float *DAQK, *DVPT, *QDOT;
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) bwd_b2(B2Args<T> a) {
+  constexpr int BT = 64, NDT = D / 16, NKT = BT / 16;
+  constexpr int LDO = D + 4, LDV = BT + 4, LDA = BT + 4, LDQ = D + 4;
+  constexpr int BF = sizeof(T) == 2;
+  constexpr int QB = NDT / 4;               // qdot row blocks per wave
+  __shared__ __align__(16) float sDo[BT * LDO];
+  __shared__ __align__(16) float sV[D * LDV];
+  __shared__ __align__(16) float sA[BT * LDA];
+  __shared__ __align__(16) float sQ[BT * LDQ];
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int cid = blockIdx.x;
+  const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
+  const size_t HD = (size_t)a.H * D;
+  const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D;
+  auto rowop = [&](const float* base, int ld, int r0, int k0) __attribute__((always_inline)) {
+    return load4f(&base[(r0 + li) * ld + k0 + 4 * lg]);
+  };
+  auto colop = [&](const float* base, int ld, int k0, int c0) __attribute__((always_inline)) {
+    f32x4 y;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = base[(k0 + 4 * lg + r) * ld + c0 + li];
+    return y;
+  };
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  {
+    // do rows are (B,T,H,D) token rows: pitch H*D
+    const GMat mDo{a.dout, 0, (int)HD, 0, 0};
+    const GMat mV{a.VnT, BF, BT, 0, BF};
+    const GMat mQ{a.Qg, BF, D, 0, 0};
+    // Aqk: blocks right of the diagonal block are unwritten; causal mask on load
+    const GMat mA{a.Aqk, BF, BT, 1, 0};
+    Staged s1, s2;
+    stage_load(s1, mDo, tok0, BT, D, tid);
+    stage_load(s2, mV, (size_t)cid * D * BT, D, BT, tid);
+    stage_store(sDo, LDO, s1, mDo, BT, D, 0, 0, false, tid);
+    stage_store(sV, LDV, s2, mV, D, BT, 0, 0, false, tid);
+    stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
+    stage_load(s2, mA, (size_t)cid * BT * BT, BT, BT, tid);
+    stage_store(sQ, LDQ, s1, mQ, BT, D, 0, 0, false, tid);
+    stage_store(sA, LDA, s2, mA, BT, BT, 0, 0, false, tid);
+  }
+  __syncthreads();
+  // dAqk[t][s] = sum_e do[t][e] v_new[s][e], s <= t
+  {
+    f32x4 acc[NKT];
+#pragma unroll
+    for (int st = 0; st < NKT; ++st) acc[st] = z4;
+#pragma unroll
+    for (int kg = 0; kg < NDT; ++kg) {
+      const f32x4 x = rowop(sDo, LDO, wv * 16, kg * 16);
+#pragma unroll
+      for (int st = 0; st < NKT; ++st) mma(acc[st], x, colop(sV, LDV, kg * 16, st * 16));
+    }
+    float* o = a.DAQK + (size_t)cid * BT * BT;
+#pragma unroll
+    for (int st = 0; st < NKT; ++st)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = wv * 16 + 4 * lg + r, s2 = st * 16 + li;
+        o[row * BT + s2] = s2 <= row ? acc[st][r] : 0.f;
+      }
+  }
+  // dvp^T[e][s] = sum_t Aqk[t][s] do[t][e]: rows s of the own block, stored as [e][s]
+  {
+    f32x4 acc[NDT];
+#pragma unroll
+    for (int nt = 0; nt < NDT; ++nt) acc[nt] = z4;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+      const f32x4 x = colop(sA, LDA, kt * 16, wv * 16);      // Aqk^T rows s, k = t
+#pragma unroll
+      for (int nt = 0; nt < NDT; ++nt) mma(acc[nt], x, colop(sDo, LDO, kt * 16, nt * 16));
+    }
+    float* o = a.DVPT + (size_t)cid * D * BT;
+#pragma unroll
+    for (int nt = 0; nt < NDT; ++nt)
+      store4(o + (size_t)(nt * 16 + li) * BT + wv * 16 + 4 * lg, acc[nt]);
+  }
+  // qdot[e][d] = scale sum_t do[t][e] qg[t][d]
+  {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int eb = wv * QB + qb;
+      f32x4 acc[NDT];
+#pragma unroll
+      for (int nt = 0; nt < NDT; ++nt) acc[nt] = z4;
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) {
+        const f32x4 x = colop(sDo, LDO, kt * 16, eb * 16);   // do^T rows e, k = t
+#pragma unroll
+        for (int nt = 0; nt < NDT; ++nt) mma(acc[nt], x, colop(sQ, LDQ, kt * 16, nt * 16));
+      }
+      float* o = a.QDOT + (size_t)cid * D * D;
+#pragma unroll
+      for (int nt = 0; nt < NDT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[(eb * 16 + 4 * lg + r) * D + nt * 16 + li] = a.scale * acc[nt][r];
+    }
+  }
+}
+
+// ============================================================================
 // bwd_wy (B3, fused): per chunk the products of gdn2_bwd.py:126-210 and the
 // element-wise b k e^{gc}, w v, with dW, dA and dA A^T kept on chip:
 //   dqg  = scale do h^T              dW    = -dv_new h^T
@@ -472,7 +530,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 
   // ---- 1. dqg = scale do h^T, dW = -dv_new h^T --------------------------------
   Staged st;
-  const GMat mH{a.HT, BF, 0, 0, 0, D, 0, 0, BF};
+  const GMat mH{a.HT, BF, D, 0, BF};
   stage_load(st, mH, (size_t)cid * D * D, D, D, tid);
   f32x4 xdo[NDT], xdv[NDT];
 #pragma unroll
@@ -508,8 +566,8 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
   __syncthreads();   // every wave is done with h^T
 
   // ---- 2. dkg = v_new dh'^T ------------------------------------------------------
-  const GMat mDH{a.DHT, 0, 0, 0, 0, D, 0, 0, 0};
-  const GMat mA{a.A, 0, 0, 0, 0, BT, 0, 0, 0};
+  const GMat mDH{a.DHT, 0, D, 0, 0};
+  const GMat mA{a.A, 0, BT, 0, 0};
   Staged sa;
   stage_load(st, mDH, (size_t)cid * D * D, D, D, tid);
   stage_load(sa, mA, (size_t)cid * BT * BT, BT, BT, tid);
@@ -631,7 +689,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
   __syncthreads();   // dA complete; (b k e^gc | w v) no longer read
 
   // ---- 5. d(bke^gc) = A^T dW, d(wv) = A^T dv_new, TMP = dA A^T -------------------
-  const GMat mDV{a.DVNT, 0, 0, 0, 0, BT, 0, 0, 0};
+  const GMat mDV{a.DVNT, 0, BT, 0, 0};
   stage_load(st, mDV, (size_t)cid * D * BT, D, BT, tid);
   stage_store(sR1, LDV, st, mDV, D, BT, 0, 0, false, tid);
   __syncthreads();
@@ -960,40 +1018,6 @@ size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t) {
   return BT == 64 ? bwd_layout(nchunks, BT, D).total : 0;
 }
 
-namespace {
-struct Dims {
-  int B, T, H, D, BT, N;
-};
-// (B,T,H,D) token layout
-GMat tok_mat(const void* p, int bf16, const Dims& d, int trans = 0, int mask = 0) {
-  return GMat{p, bf16, (long long)d.T * d.H * d.D, (long long)d.D,
-              (long long)d.BT * d.H * d.D, d.H * d.D, trans, mask};
-}
-// chunk-major [cid][R][C]
-GMat ch_mat(const void* p, int bf16, const Dims& d, int R, int C, int trans = 0, int mask = 0) {
-  const long long tile = (long long)R * C;
-  return GMat{p, bf16, (long long)d.H * d.N * tile, (long long)d.N * tile, tile, C, trans, mask};
-}
-// A forward residual tile (h^T, v_new^T): bfloat16 ones are in chained column order.
-GMat res_mat(const void* p, int bf16, const Dims& d, int R, int C, int trans = 0) {
-  GMat m = ch_mat(p, bf16, d, R, C, trans);
-  m.chained = bf16;
-  return m;
-}
-GOut ch_out(float* p, const Dims& d, int R, int C, float alpha = 1.f, int trans = 0,
-            int mask = 0, int accum = 0) {
-  const long long tile = (long long)R * C;
-  return GOut{p, (long long)d.H * d.N * tile, (long long)d.N * tile, tile, C, trans, mask,
-              alpha, accum};
-}
-void gemm(hipStream_t st, const Dims& d, GMat A, GMat B, GOut C, int M, int N, int K) {
-  const int nsplit = (N == 128 && K == 128) ? 2 : 1;
-  GemmArgs ga{A, B, C, M, N, K, d.H, d.N, nsplit};
-  const size_t lds = (size_t)(M + N / nsplit) * (K + 4) * sizeof(float);
-  hipLaunchKernelGGL(chunk_gemm, dim3((size_t)d.B * d.H * d.N * nsplit), dim3(256), lds, st, ga);
-  launch_mark(st);
-}
-}  // namespace
 
 template <typename T, typename TG, int BT, int D>
 hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
@@ -1007,8 +1031,6 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     (void)h0;
     const int N = T_len / BT;
     const size_t NC = (size_t)B * H * N;
-    const Dims dm{B, T_len, H, D, BT, N};
-    const int tb = sizeof(T) == 2;
     const FwdLayout F = fwd_layout(NC, BT, D, sizeof(T));
     const BwdLayout L = bwd_layout(NC, BT, D);
     auto buf = [&](BwdBuf i) { return reinterpret_cast<float*>(ws + L.off[i]); };
@@ -1026,12 +1048,10 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     }
     // B2: dAqk, Aqk^T do, scale qg^T do
     if (NC > 0) {
-      gemm(st, dm, tok_mat(dout, 0, dm), res_mat(fVnT, tb, dm, D, BT),
-           ch_out(buf(B_DAQK), dm, BT, BT, 1.f, 0, 1), BT, BT, D);
-      gemm(st, dm, ch_mat(fAqk, tb, dm, BT, BT, 1, 1), tok_mat(dout, 0, dm),
-           ch_out(buf(B_DVPT), dm, D, BT, 1.f, 1), BT, D, BT);
-      gemm(st, dm, tok_mat(dout, 0, dm, 1), ch_mat(fQg, tb, dm, BT, D),
-           ch_out(buf(B_QDOT), dm, D, D, scale), D, D, BT);
+      B2Args<T> ba{dout, (const T*)fVnT, (const T*)fAqk, (const T*)fQg, T_len, H, N, scale,
+                   buf(B_DAQK), buf(B_DVPT), buf(B_QDOT)};
+      hipLaunchKernelGGL((bwd_b2<T, D>), dim3(NC), dim3(256), 0, st, ba);
+      launch_mark(st);
     }
     // B1: reverse state scan
     BStateArgs<T> sa{(const T*)fW, (const T*)fKgT, fGL, buf(B_DVPT), buf(B_QDOT), dh_final, N,
