@@ -292,6 +292,9 @@ def _counter_means(run_dir, counter):
     files = sorted(Path(run_dir).rglob("*counter_collection.csv"))
     if not files:
         raise SystemExit(f"no *counter_collection.csv under {run_dir}")
+    if len(files) > 1:   # dispatch ids restart per run: two runs would be summed
+        raise SystemExit(f"{len(files)} counter files under {run_dir}: give each run "
+                         f"its own output directory")
     per = {}
     for f in files:
         with open(f, newline="") as fh:

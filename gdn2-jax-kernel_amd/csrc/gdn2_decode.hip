@@ -6,18 +6,18 @@
 // are sanitized like every chunk state and output, gdn2_fwd.py:355-356).  The
 // state layout is h0 / h_final's: S[b][h][dk][dv] (gdn2_fwd.py:342).
 //
-// One 256-thread workgroup per (b,h) and slice of CS state columns (all D
-// columns up to D = 128, 64 at D = 256): thread (column e, row group rg) keeps
-// D / RG state rows of column e in registers.  Both column reductions (pred
-// and o) run over the rows, so the columns split freely; they are summed over
-// the row groups in LDS.  The state is read and written once (memory-bound);
-// h_out may alias h_in.
+// One 256-thread workgroup per (b,h) and slice of 32 state columns (B H D / 32
+// workgroups: enough to spread one decode step over the chip): thread (column
+// e, row group rg) keeps D / 8 state rows of column e in registers.  Both
+// column reductions (pred and o) run over the rows, so the columns split
+// freely; they are summed over the 8 row groups in LDS.  The state is read and
+// written once (memory-bound); h_out may alias h_in.
 #include "gdn2_common.h"
 
 namespace gdn2 {
 
 template <int D>
-constexpr int decode_cols() { return D <= 128 ? D : 64; }
+constexpr int decode_cols() { return 32; }
 
 template <typename T, typename TG, int D>
 __global__ void __launch_bounds__(256) decode_step(const T* q, const T* k, const T* v,
