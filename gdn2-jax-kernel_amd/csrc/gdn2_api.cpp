@@ -20,7 +20,7 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, const float* dout, const float* dh_final,
                       void* dq, void* dk, void* dv, void* dw, void* db, void* dg, float* dh0,
-                      const char* fws, char* ws);
+                      const char* fws, char* ws, const int* cu_chunks, int nseq);
 
 size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t elem);
 
@@ -110,13 +110,13 @@ struct BwdRun {
                  const void* v, const void* w, const void* b, const void* g, const float* h0,
                  float scale, const float* dout, const float* dh_final, void* dq, void* dk,
                  void* dv, void* dw, void* db, void* dg, float* dh0, const char* fws,
-                 char* ws) {
+                 char* ws, const int* cu_chunks, int nseq) {
     if constexpr (D > 128) {
       return GDN2_ERR_HEAD_DIM;  // the backward kernels are built for D <= 128
     } else {
       hipError_t e = launch_bwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale,
                                               dout, dh_final, dq, dk, dv, dw, db, dg, dh0, fws,
-                                              ws);
+                                              ws, cu_chunks, nseq);
       return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
     }
   }
@@ -273,7 +273,40 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
   if (fwd_ws_bytes < fneed || ws_bytes < bneed) return GDN2_ERR_WORKSPACE;
   return dispatch<BwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, B, T, H, q, k, v, w,
                           b, g, h0, scale, dout, dh_final, dq, dk, dv, dw, db, dg, dh0,
-                          (const char*)fwd_ws, (char*)ws);
+                          (const char*)fwd_ws, (char*)ws, (const int*)nullptr, 0);
+}
+
+size_t gdn2_bwd_varlen_workspace_bytes(int total_chunks, int H, int D, int BT, int in_dtype) {
+  if (total_chunks < 0 || (double)total_chunks * BT > 2.0e9) return 0;
+  return gdn2_bwd_workspace_bytes(1, total_chunks * BT, H, D, BT, in_dtype);
+}
+
+int gdn2_bwd_varlen(void* stream, int num_seqs, const int* cu_chunks, int total_chunks, int H,
+                    int D, int BT, int in_dtype, int g_dtype, const void* q, const void* k,
+                    const void* v, const void* w, const void* b, const void* g, const float* h0,
+                    float scale, const float* dout, const float* dh_final, void* dq, void* dk,
+                    void* dv, void* dw, void* db, void* dg, float* dh0, const void* fwd_ws,
+                    size_t fwd_ws_bytes, void* ws, size_t ws_bytes) {
+  EventScope scope;
+  if (num_seqs < 1 || total_chunks < 0 || (double)total_chunks * BT > 2.0e9)
+    return GDN2_ERR_SHAPE;
+  const int T = total_chunks * BT;
+  int rc = gdn2_validate(1, T, H, D, BT, in_dtype, g_dtype);
+  if (rc) return rc;
+  if (D > 128) return GDN2_ERR_HEAD_DIM;
+  if (BT != 64) return GDN2_ERR_CHUNK;
+  if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, dout, dq, dk, dv, dw, db, dg}))) return rc;
+  if ((rc = check_ptrs({dh0, cu_chunks}))) return rc;
+  if ((rc = check_opt({h0, dh_final}))) return rc;
+  const size_t nc = nchunks(1, T, H, BT);
+  const size_t fneed = fwd_layout(nc, BT, D, elem_size(in_dtype)).total;
+  const size_t bneed = bwd_ws_bytes(nc, BT, D, elem_size(in_dtype));
+  if (fneed > 0 && (rc = check_ptrs({fwd_ws}))) return rc;
+  if (bneed > 0 && (rc = check_ptrs({ws}))) return rc;
+  if (fwd_ws_bytes < fneed || ws_bytes < bneed) return GDN2_ERR_WORKSPACE;
+  return dispatch<BwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, 1, T, H, q, k, v, w,
+                          b, g, h0, scale, dout, dh_final, dq, dk, dv, dw, db, dg, dh0,
+                          (const char*)fwd_ws, (char*)ws, cu_chunks, num_seqs);
 }
 
 size_t gdn2_fwd_varlen_workspace_bytes(int total_chunks, int H, int D, int BT, int in_dtype) {
@@ -293,7 +326,7 @@ int gdn2_fwd_varlen(void* stream, int num_seqs, const int* cu_chunks, const int*
   if (T < total_chunks) return GDN2_ERR_SEQ_LEN;  // every chunk holds at least one token
   int rc = gdn2_validate(1, 0, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
-  if (flags & GDN2_FWD_SAVE_A) return GDN2_ERR_FLAGS;  // forward only
+  if ((flags & GDN2_FWD_SAVE_A) && (flags & GDN2_FWD_RAW_INPUTS)) return GDN2_ERR_FLAGS;
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, out}))) return rc;
   if ((rc = check_ptrs({h_final, cu_chunks}))) return rc;
   if (total_chunks > 0 && (rc = check_ptrs({chunk_start}))) return rc;
@@ -304,7 +337,7 @@ int gdn2_fwd_varlen(void* stream, int num_seqs, const int* cu_chunks, const int*
   const Varlen vl{cu_chunks, chunk_start, num_seqs, total_chunks};
   return dispatch<FwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, 1, T, H, q, k, v, w,
                           b, g, h0, scale, out, h_final, (char*)ws, (float*)nullptr,
-                          flags & GDN2_FWD_RAW_INPUTS, &vl);
+                          flags & (GDN2_FWD_RAW_INPUTS | GDN2_FWD_SAVE_A), &vl);
 }
 
 int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, const void* q,

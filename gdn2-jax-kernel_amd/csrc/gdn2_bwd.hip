@@ -100,6 +100,9 @@ struct BStateArgs {
   float* DHT;        // [cid][D][D]   dh_{c+1}^T
   float* DVNT;       // [cid][D][BT]  dv_new^T
   float* dh0;        // (B,H,D,D)
+  const int* cu;     // variable-length batch (B = 1): unit (h, sequence s) scans chunks
+                     // [cu[s], cu[s+1]) in reverse; dh_final / dh0 are [s][h][D][D]
+  int S, H;          // sequences and heads of a variable-length batch
 };
 
 // One workgroup = one (b,h) and 16*NW value columns of dh: NW compute waves (16
@@ -131,22 +134,34 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
 
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  int bh, vs;
+  int unit, vs;
   {
     const int nwg = gridDim.x, id = blockIdx.x;
     const int per_xcd = nwg / 8;
     if (nwg % 8 == 0 && per_xcd % NVS == 0) {
       const int xcd = id % 8, slot = id / 8;
-      bh = xcd * (per_xcd / NVS) + slot / NVS;
+      unit = xcd * (per_xcd / NVS) + slot / NVS;
       vs = slot % NVS;
     } else {
-      bh = id / NVS;
+      unit = id / NVS;
       vs = id % NVS;
     }
   }
-  const int n = a.N;
-  // step i works on chunk n-1-i
-  auto chunk_id = [&](int i) { return (size_t)bh * a.N + (a.N - 1 - i); };
+  // a unit is one (b,h), or one (head, sequence) of a variable-length batch
+  int bh = unit, c0 = 0, n = a.N;
+  size_t st_idx = (size_t)unit;          // index of this unit's dh_final / dh0
+  if (a.cu) {
+    const int sg = unit % a.S;
+    bh = unit / a.S;
+    c0 = a.cu[sg];
+    c0 = c0 < 0 ? 0 : (c0 > a.N ? a.N : c0);
+    n = a.cu[sg + 1] - c0;
+    n = n < a.N - c0 ? n : a.N - c0;
+    n = n > 0 ? n : 0;
+    st_idx = (size_t)sg * a.H + bh;
+  }
+  // step i works on chunk c0 + n-1-i
+  auto chunk_id = [&](int i) { return (size_t)bh * a.N + c0 + (n - 1 - i); };
 
   if (wv >= NW) {
     // ---- producers ----------------------------------------------------------
@@ -274,7 +289,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
     for (int at = 0; at < NDT; ++at)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        dh[at][r] = sanitize(a.dh_final[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col]);
+        dh[at][r] = sanitize(a.dh_final[(st_idx * D + at * 16 + 4 * lg + r) * D + col]);
   } else {
 #pragma unroll
     for (int at = 0; at < NDT; ++at) dh[at] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -337,7 +352,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
 #pragma unroll
   for (int at = 0; at < NDT; ++at)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) a.dh0[((size_t)bh * D + at * 16 + 4 * lg + r) * D + col] = dh[at][r];
+    for (int r = 0; r < 4; ++r) a.dh0[(st_idx * D + at * 16 + 4 * lg + r) * D + col] = dh[at][r];
 }
 
 // ============================================================================
@@ -1024,7 +1039,7 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, const float* dout, const float* dh_final,
                       void* dq, void* dk, void* dv, void* dw, void* db, void* dg, float* dh0,
-                      const char* fws, char* ws) {
+                      const char* fws, char* ws, const int* cu_chunks, int nseq) {
   if constexpr (BT != 64) {
     return hipErrorNotSupported;
   } else {
@@ -1054,10 +1069,12 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
       launch_mark(st);
     }
     // B1: reverse state scan
+    // variable-length batch (B = 1): one scan unit per (head, sequence)
     BStateArgs<T> sa{(const T*)fW, (const T*)fKgT, fGL, buf(B_DVPT), buf(B_QDOT), dh_final, N,
-                     buf(B_DHT), buf(B_DVNT), dh0};
+                     buf(B_DHT), buf(B_DVNT), dh0, cu_chunks, cu_chunks ? nseq : 1, H};
     constexpr int BW = 2, BP = 2;  // compute and producer waves per scan workgroup
-    hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP>), dim3((size_t)B * H * (D / (16 * BW))),
+    const size_t units = cu_chunks ? (size_t)H * nseq : (size_t)B * H;
+    hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP>), dim3(units * (D / (16 * BW))),
                        dim3(64 * (BW + BP)), 0, st, sa);
     launch_mark(st);
     if (NC > 0) {
@@ -1093,7 +1110,7 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   template hipError_t launch_bwd<T, TG, BT, D>(                                            \
       hipStream_t, int, int, int, const void*, const void*, const void*, const void*,      \
       const void*, const void*, const float*, float, const float*, const float*, void*,    \
-      void*, void*, void*, void*, void*, float*, const char*, char*);
+      void*, void*, void*, void*, void*, float*, const char*, char*, const int*, int);
 GDN2_INST_BWD(float, float, 64, 64)
 GDN2_INST_BWD(float, float, 64, 128)
 GDN2_INST_BWD(bf16_t, float, 64, 64)

@@ -60,6 +60,9 @@ SIGNATURES = {
     "gdn2_fwd_varlen_workspace_bytes": (_c_size, [_c_int] * 5),
     "gdn2_fwd_varlen": (_c_int, [_vp, _c_int, _vp, _vp] + [_c_int] * 7 + [_vp] * 7
                         + [_c_float, _vp, _vp, _vp, _c_size, _c_int]),
+    "gdn2_bwd_varlen_workspace_bytes": (_c_size, [_c_int] * 5),
+    "gdn2_bwd_varlen": (_c_int, [_vp, _c_int, _vp] + [_c_int] * 6 + [_vp] * 7
+                        + [_c_float, _vp, _vp] + [_vp] * 7 + [_vp, _c_size, _vp, _c_size]),
 }
 
 

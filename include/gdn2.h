@@ -143,14 +143,30 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
  * cu_chunks[num_seqs+1], sequence s owning chunks [cu_chunks[s],
  * cu_chunks[s+1]) of the packed chunk list; chunk_start[total_chunks+1], the
  * first token row of each chunk, chunk_start[total_chunks] = T.  Table values
- * are clamped in the kernels (no access outside the buffers).  Forward only:
- * flags 0 or GDN2_FWD_RAW_INPUTS. */
+ * are clamped in the kernels (no access outside the buffers).  flags: 0,
+ * GDN2_FWD_RAW_INPUTS, or GDN2_FWD_SAVE_A when gdn2_bwd_varlen will consume ws. */
 size_t gdn2_fwd_varlen_workspace_bytes(int total_chunks, int H, int D, int BT, int in_dtype);
 int gdn2_fwd_varlen(void* stream, int num_seqs, const int* cu_chunks, const int* chunk_start,
                     int total_chunks, int T, int H, int D, int BT, int in_dtype, int g_dtype,
                     const void* q, const void* k, const void* v, const void* w, const void* b,
                     const void* g, const float* h0, float scale, float* out, float* h_final,
                     void* ws, size_t ws_bytes, int flags);
+
+/* Backward of a variable-length batch.  No reference counterpart (see
+ * gdn2_fwd_varlen).  Every sequence must occupy whole chunks: the packed
+ * inputs are (1, total_chunks*BT, H, D), sequence s owning chunks
+ * [cu_chunks[s], cu_chunks[s+1]); a caller pads each sequence with zero tokens
+ * (neutral: its results and gradients are unchanged).  fwd_ws holds the
+ * residuals of gdn2_fwd_varlen with GDN2_FWD_SAVE_A on the same inputs, with
+ * chunk_start[c] = c*BT.  dh_final and dh0 are (num_seqs,H,D,D) float32
+ * (dh_final may be NULL); gradients as gdn2_bwd.  BT must be 64. */
+size_t gdn2_bwd_varlen_workspace_bytes(int total_chunks, int H, int D, int BT, int in_dtype);
+int gdn2_bwd_varlen(void* stream, int num_seqs, const int* cu_chunks, int total_chunks, int H,
+                    int D, int BT, int in_dtype, int g_dtype, const void* q, const void* k,
+                    const void* v, const void* w, const void* b, const void* g, const float* h0,
+                    float scale, const float* dout, const float* dh_final, void* dq, void* dk,
+                    void* dv, void* dw, void* db, void* dg, float* dh0, const void* fwd_ws,
+                    size_t fwd_ws_bytes, void* ws, size_t ws_bytes);
 
 /* Single-token recurrent step on the (B,H,D,D) float32 state, for serving:
  * the reference has no decode entry; this is gdn2_pallas_forward with T = 1

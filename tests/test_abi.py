@@ -189,8 +189,29 @@ def test_varlen_rejects_before_launch():
     assert call(0, 1, 10) == _lib.ERR_SHAPE                 # no sequences
     assert call(2, 2, 200) == _lib.ERR_SHAPE                # more tokens than chunks can hold
     assert call(2, 3, 2) == _lib.ERR_SEQ_LEN                # a chunk without tokens
-    assert call(2, 2, 100, _lib.FWD_SAVE_A) == _lib.ERR_FLAGS
+    assert call(2, 2, 100, _lib.FWD_SAVE_A | _lib.FWD_RAW_INPUTS) == _lib.ERR_FLAGS
     assert call(2, 2, 100, cu=None) == _lib.ERR_NULL
     assert call(2, 2, 100, hf=None) == _lib.ERR_NULL
     assert L.gdn2_fwd_varlen_workspace_bytes(5, 2, 64, 64, F32) == \
         L.gdn2_fwd_workspace_bytes(1, 5 * 64, 2, 64, 64, F32)
+
+
+def test_bwd_varlen_rejects_before_launch():
+    L = _lib.lib()
+    fake = [0x100000 * (i + 1) for i in range(6)]
+    grads = [0x900000 * (i + 1) for i in range(6)]
+    need_f = L.gdn2_fwd_varlen_workspace_bytes(4, 2, 64, 64, F32)
+    need_b = L.gdn2_bwd_varlen_workspace_bytes(4, 2, 64, 64, F32)
+    assert need_b == L.gdn2_bwd_workspace_bytes(1, 4 * 64, 2, 64, 64, F32) > 0
+    call = lambda nseq, total, D=64, BT=64, cu=0x7000, fws=need_f, bws=need_b, dh0=0x6000: \
+        L.gdn2_bwd_varlen(None, nseq, cu, total, 2, D, BT, F32, F32, *fake, None, 0.125, 0x4000,
+                          None, *grads, dh0, 0x5000, fws, 0x7100, bws)
+    assert call(0, 4) == _lib.ERR_SHAPE                     # no sequences
+    assert call(2, -1) == _lib.ERR_SHAPE
+    assert call(2, 4, D=96) == _lib.ERR_HEAD_DIM
+    assert call(2, 4, D=256) == _lib.ERR_HEAD_DIM           # forward only at D = 256
+    assert call(2, 4, BT=128) == _lib.ERR_CHUNK             # float32 needs chunk 64
+    assert call(2, 4, cu=None) == _lib.ERR_NULL
+    assert call(2, 4, dh0=None) == _lib.ERR_NULL
+    assert call(2, 4, fws=need_f - 1) == _lib.ERR_WORKSPACE
+    assert call(2, 4, bws=need_b - 1) == _lib.ERR_WORKSPACE

@@ -97,3 +97,49 @@ def test_varlen_bad_tables_stay_in_bounds(dev):
                            hf.data_ptr(), ws.data_ptr(), nb, 0)
     torch.cuda.synchronize()
     assert rc == 0 and torch.isfinite(out).all() and torch.isfinite(hf).all()
+
+
+# ----------------------------------------------------------------------------- training
+@pytest.mark.parametrize("dtype,D,lens,h0", [
+    (torch.float32, 64, [70, 1, 128, 33], True),   # tails, one token, whole chunks
+    (torch.float32, 128, [200, 64], False),
+    (torch.bfloat16, 64, [100, 29], True),
+])
+def test_varlen_trainable_matches_per_sequence_oracle(dev, dtype, D, lens, h0):
+    """gdn2_pallas_forward_varlen_trainable: out, h_final and every gradient
+    (q..g, h0) of each sequence against the float64 recurrence and its autograd
+    over that sequence alone (oracle.recurrent_grads).  bfloat16 inputs keep
+    bfloat16 forward residuals (h, v_new, W) and return bfloat16 gradients: with
+    a unit-scale dh_final the largest dk errors reach the 2e-2 bound in the plain
+    path too, so that case uses dh_final at scale 0.1."""
+    import gdn2_package as gp
+    H, T, S = 2, sum(lens), len(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    xs = O.make_inputs(1, T, H, D, seed=T + D)
+    xt = [torch.tensor(np.asarray(x), device=dev).to(dtype if i < 5 else torch.float32)
+          .requires_grad_(True) for i, x in enumerate(xs)]
+    rng = np.random.default_rng(S + D)
+    h0n = (0.2 * rng.standard_normal((S, H, D, D))).astype(np.float32) if h0 else None
+    h0t = None if h0n is None else torch.tensor(h0n, device=dev, requires_grad=True)
+    do = rng.standard_normal((1, T, H, D)).astype(np.float32)
+    dh = ((0.1 if dtype == torch.bfloat16 else 1.0)
+          * rng.standard_normal((S, H, D, D))).astype(np.float32)
+    out, hf = gp.gdn2_pallas_forward_varlen_trainable(*xt, D ** -0.5, cu, h0=h0t)
+    assert out.shape == (1, T, H, D) and hf.shape == (S, H, D, D)
+    ((out * torch.tensor(do, device=dev)).sum() + (hf * torch.tensor(dh, device=dev)).sum()).backward()
+    xin = [x.detach().float().cpu().numpy() for x in xt]
+    tol = TOL[dtype]
+    for s in range(S):
+        a, e = int(cu[s]), int(cu[s + 1])
+        seg = [x[:, a:e] for x in xin]
+        hs = None if h0n is None else h0n[s:s + 1]
+        ro, rh = O.recurrent_fwd(*seg, D ** -0.5, h0=hs)
+        assert close(out.detach()[:, a:e].cpu().numpy(), ro, tol)[0], ("out", s)
+        assert close(hf.detach()[s:s + 1].cpu().numpy(), rh, tol)[0], ("h_final", s)
+        ref = O.recurrent_grads(*seg, D ** -0.5, do[:, a:e], dh[s:s + 1], h0=hs)
+        for name, x, r in zip("qkvwbg", xt, ref[:6]):
+            ok, err = close(x.grad[:, a:e].float().cpu().numpy(), r, tol)
+            assert ok, (name, s, err)
+        if h0t is not None:
+            ok, err = close(h0t.grad[s:s + 1].cpu().numpy(), ref[6], tol)
+            assert ok, ("h0", s, err)
