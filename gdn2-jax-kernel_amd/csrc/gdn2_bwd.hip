@@ -528,6 +528,8 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
   const size_t HD = (size_t)a.H * D;
   const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D;
   const int t = wv * 16 + li;   // this lane's row for row operands of the own block
+  // Barriers order LDS data only (lds_barrier): no wave reads global memory
+  // another wave of this workgroup wrote.
   if (tid < D) sSdh[tid] = 0.f;
 
   auto rowop = [&](const float* base, int ld, int r0, int k0) __attribute__((always_inline)) {
@@ -556,7 +558,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
       xdv[kg][r] = a.DVNT[((size_t)cid * D + kg * 16 + 4 * lg + r) * BT + t];
   }
   stage_store(sR1, LD1, st, mH, D, D, 0, 0, false, tid);
-  __syncthreads();
+  lds_barrier();
   {
     f32x4 aq[NDT], aw[NDT];
 #pragma unroll
@@ -578,7 +580,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
         sR2[orow(r) * LD2 + nt * 16 + li] = -aw[nt][r];
       }
   }
-  __syncthreads();   // every wave is done with h^T
+  lds_barrier();   // every wave is done with h^T
 
   // ---- 2. dkg = v_new dh'^T ------------------------------------------------------
   const GMat mDH{a.DHT, 0, D, 0, 0};
@@ -615,7 +617,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
     }
     stage_store(sR1, LD1, st, mDH, D, D, 0, 0, false, tid);
     stage_store(sR5, LD4, sa, mA, BT, BT, 0, 0, false, tid);
-    __syncthreads();
+    lds_barrier();
     if (tid < D) a.SDH[(size_t)cid * D + tid] = sSdh[tid];
     f32x4 ak[NDT];
 #pragma unroll
@@ -648,7 +650,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
       load_f<4>(a.w + o, wvv[j]);
       load_f<4>(a.v + o, vv[j]);
     }
-    __syncthreads();   // every wave is done with dh'^T
+    lds_barrier();   // every wave is done with dh'^T
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       f32x4 wvo;
@@ -665,19 +667,28 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
+  // gc = loc + sums of the earlier blocks: independent 16-byte LDS reads per
+  // (block, channel group), all issued before the exponentials
+#pragma unroll
+  for (int m = 0; m < NB - 1; ++m) {
+    if (m < wv) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const f32x4 tv = load4f(&sTot[m * D + j * 16 + 4 * lg]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) loc[j][e] += tv[e];
+      }
+    }
+  }
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     f32x4 kb;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float gc = loc[j][e];
-      for (int m = 0; m < wv; ++m) gc += sTot[m * D + j * 16 + 4 * lg + e];
-      kb[e] = bk[j][e] * __expf(gc);
-    }
+    for (int e = 0; e < 4; ++e) kb[e] = bk[j][e] * __expf(loc[j][e]);
     *reinterpret_cast<f32x4*>(&sR1[t * LD1 + j * 16 + 4 * lg]) = kb;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 4. dA = (dW (b k e^gc)^T + dv_new (w v)^T) . strict ----------------------
   {
@@ -701,13 +712,13 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
         sR4[orow(r) * LD4 + s2] = s2 < orow(r) ? ada[st2][r] : 0.f;
       }
   }
-  __syncthreads();   // dA complete; (b k e^gc | w v) no longer read
+  lds_barrier();   // dA complete; (b k e^gc | w v) no longer read
 
   // ---- 5. d(bke^gc) = A^T dW, d(wv) = A^T dv_new, TMP = dA A^T -------------------
   const GMat mDV{a.DVNT, 0, BT, 0, 0};
   stage_load(st, mDV, (size_t)cid * D * BT, D, BT, tid);
   stage_store(sR1, LDV, st, mDV, D, BT, 0, 0, false, tid);
-  __syncthreads();
+  lds_barrier();
   {
     f32x4 akb[NDT], awv[NDT];
 #pragma unroll
@@ -747,7 +758,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) sR4[orow(r) * LD4 + nt * 16 + li] = atm[nt][r];
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 6. dAkk = -(A^T (dA A^T)) . strict -----------------------------------------
   {

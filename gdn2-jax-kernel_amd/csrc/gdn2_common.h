@@ -211,6 +211,14 @@ __device__ __forceinline__ float row_bcast(float x) {
              0, __builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, false));
 }
 
+// Workgroup barrier for LDS data only: the wave's own LDS operations complete,
+// then s_barrier.  Unlike __syncthreads() it does not drain vector memory
+// operations, so global loads stay in flight and global stores (never read back
+// by another wave of the workgroup where this is used) are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Copy `rows` rows of `cols` elements (row pitch `gpitch` in global, `lpitch`
 // in LDS) with 16-byte transactions spread over the workgroup.
 template <typename T, int NT>
