@@ -793,8 +793,8 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 //   RK [j]  = sum_I F_IJ (scale dAqk_IJ^T AQ_I + dAkk_IJ^T ABK_I),  dk_g = e^{T_J-loc_j} RK
 // with loc = in-block cumsum of g, T_J = block sum, F_IJ = exp(sum of T over blocks
 // strictly between J and I), Khat = k e^{T-loc}, AQ = q e^{loc}, ABK = b k e^{loc}.
-// Diagonal blocks are summed exactly per channel (exp of each in-block
-// difference) into DQD, DKD, DBKD.  Wave w owns row block w (BT = 64).
+// Diagonal blocks are summed per channel, factorised around the block's 8th
+// token as in the forward, into DQD, DKD, DBKD.  Wave w owns row block w (BT = 64).
 // ============================================================================
 template <typename T, typename TG>
 struct GramArgs {
@@ -844,15 +844,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) load_f<4>(a.g + rowo + j * 16 + lg * 4, &loc[j * 4]);
 #pragma unroll
-  for (int x = 0; x < DQ; ++x) {
-    float s = loc[x];
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      const float y = __shfl_up(s, o, 16);
-      if (li >= o) s += y;
-    }
-    loc[x] = s;
-  }
+  for (int x = 0; x < DQ; ++x) loc[x] = row_scan16(loc[x]);
   if (li == 15) {
 #pragma unroll
     for (int x = 0; x < DQ; ++x) sTot[I * D + chan(x)] = loc[x];
@@ -926,34 +918,50 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
     }
   }
 
-  // ---- diagonal block, exact per channel --------------------------------------
+  // ---- diagonal block, per channel -------------------------------------------
+  // e^{lc_i - lc_j} = e^{lc_i - lm} e^{lm - lc_j} around the block's 8th token
+  // (as the forward's diagonal blocks): 32 exponentials per channel and block
   for (int d = lane; d < D; d += 64) {
-    float qv[16], kv[16], bk[16], lc[16], dq[16], dk[16], db[16];
+    float qe[16], ke[16], be[16], el[16], er[16], dq[16], dk[16], db[16];
     float run = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const size_t o = tok0 + (size_t)(I * 16 + i) * HD + d;
-      qv[i] = to_f(a.q[o]);
-      kv[i] = to_f(a.k[o]);
-      bk[i] = to_f(a.b[o]) * kv[i];
+      qe[i] = to_f(a.q[o]);
+      ke[i] = to_f(a.k[o]);
+      be[i] = to_f(a.b[o]) * ke[i];
       run += to_f(a.g[o]);
-      lc[i] = run;
+      el[i] = run;
       dq[i] = dk[i] = db[i] = 0.f;
+    }
+    const float lm = el[7];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      er[i] = __expf(lm - el[i]);
+      el[i] = __expf(el[i] - lm);
+      qe[i] *= a.scale * el[i];   // scale q_i e^{lc_i - lm}
+      be[i] *= el[i];             // (b k)_i e^{lc_i - lm}
+      ke[i] *= er[i];             // k_j e^{lm - lc_j}
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
 #pragma unroll
       for (int j = 0; j <= i; ++j) {
-        const float E = __expf(lc[i] - lc[j]);
-        const float gq = sDQK[(I * 16 + i) * LD2 + I * 16 + j] * E * a.scale;
-        dq[i] += gq * kv[j];
-        dk[j] += gq * qv[i];
+        const float aq = sDQK[(I * 16 + i) * LD2 + I * 16 + j];
+        dq[i] += aq * ke[j];
+        dk[j] += aq * qe[i];
         if (j < i) {
-          const float gk = sDKK[(I * 16 + i) * LD2 + I * 16 + j] * E;
-          dk[j] += gk * bk[i];
-          db[i] += gk * kv[j];
+          const float ak = sDKK[(I * 16 + i) * LD2 + I * 16 + j];
+          dk[j] += ak * be[i];
+          db[i] += ak * ke[j];
         }
       }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      dq[i] *= a.scale * el[i];
+      db[i] *= el[i];
+      dk[i] *= er[i];
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
