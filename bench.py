@@ -130,6 +130,105 @@ def time_train(gp, xs, steps, warmup):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
+# Algorithmic MFMA flops per chunk of the float32 training kernels (chunk 64,
+# D = 128; masked triangular products counted in full, as the kernels run them):
+#   bwd_b2:    dAqk, Aqk^T do (2 BT BT D each), qg^T do (2 D D BT)
+#   bwd_state: kg dh and W^T dv_new per chunk (2 BT D D each)
+#   bwd_wy:    three (BT, D, D), two (BT, BT, D), two (BT, D, BT), two (BT, BT, BT)
+TRAIN_CHUNK = 64
+_C = TRAIN_CHUNK
+TRAIN_FLOPS = {
+    "bwd_b2": 2 * 2 * _C * _C * D + 2 * D * D * _C,
+    "bwd_state": 2 * 2 * _C * D * D,
+    "bwd_wy": 3 * 2 * _C * D * D + 2 * 2 * _C * _C * D + 2 * 2 * _C * D * _C + 2 * 2 * _C ** 3,
+}
+FP32_MFMA_PEAK = 157.3   # TFLOP/s, MI355X dense float32 matrix
+
+
+def train_kernels(gp, xs):
+    """Per-kernel times (HIP events at the library's launch marks) of one
+    float32 training step: the forward with residuals, then the backward."""
+    import ctypes
+    import torch
+    from gdn2_package import _lib
+    from gdn2_package.gdn2_fwd import _Prepared, _run_forward
+    from gdn2_package.gdn2_pipeline import _run_backward
+    L = _lib.lib()
+    p = _Prepared(*xs, D ** -0.5, None, TRAIN_CHUNK)
+    dout = torch.randn((B, T, H, D), device="cuda")
+    res = {}
+    for names, run in ((("fwd_prep", "fwd_state", "fwd_out"),
+                        lambda: _run_forward(p, flags=_lib.FWD_SAVE_A)),
+                       (("bwd_b2", "bwd_state", "bwd_wy", "gram_bwd", "bwd_combine"), None)):
+        n = len(names) + 1
+        for _ in range(2):            # second pass timed
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+            for e in evs:
+                e.record()
+            arr = (ctypes.c_void_p * n)(*[ctypes.c_void_p(int(e.cuda_event)) for e in evs])
+            torch.cuda.synchronize()
+            if run is not None:
+                L.gdn2_set_launch_events(arr, n)
+                _, _, ws, _ = run()
+            else:
+                L.gdn2_set_launch_events(arr, n)
+                _run_backward(p, ws, dout, None)
+            torch.cuda.synchronize()
+        res.update({nm: evs[i].elapsed_time(evs[i + 1]) for i, nm in enumerate(names)})
+    nc = B * H * (T // TRAIN_CHUNK)
+    mfma = {k: {"tflops": f * nc / (res[k] * 1e-3) / 1e12,
+                "frac_of_fp32_peak": f * nc / (res[k] * 1e-3) / 1e12 / FP32_MFMA_PEAK}
+            for k, f in TRAIN_FLOPS.items()}
+    return res, mfma
+
+
+def pmc_train_run():
+    """One float32 training step and one headline forward, for MFMA counters."""
+    import torch
+    import gdn2_package as gp
+    xs = make_inputs(torch.float32)
+    train_kernels(gp, xs)
+    del xs
+    xb = make_inputs(torch.bfloat16)
+    gp.gdn2_pallas_forward(*xb, D ** -0.5, chunk_size=CHUNK)
+    torch.cuda.synchronize()
+
+
+def mfma_from(run_dir):
+    """Per-kernel MFMA flops (SQ_INSTS_VALU_MFMA_MOPS_* x 512) and utilisation
+    (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs)) of a --pmc-train-run
+    counter run; durations from the same run's dispatch timestamps."""
+    import csv
+    files = sorted(Path(run_dir).rglob("*counter_collection.csv"))
+    if len(files) != 1:
+        raise SystemExit(f"expected one counter file under {run_dir}, found {len(files)}")
+    per = {}
+    with open(files[0], newline="") as fh:
+        for row in csv.DictReader(fh):
+            key = (int(row["Dispatch_Id"]), row["Kernel_Name"])
+            d = per.setdefault(key, {"ns": int(row["End_Timestamp"]) - int(row["Start_Timestamp"])})
+            d[row["Counter_Name"]] = d.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    # GRBM_GUI_ACTIVE arrives summed over the 8 XCDs: per-XCD active cycles are
+    # a eighth of it (rocprof's MfmaUtil takes the maximum over instances)
+    simds, xcds = 256 * 4, 8
+    out = {}
+    for (_, name), d in sorted(per.items()):
+        if "gdn2" not in name:
+            continue
+        short = next((k for k in ("fwd_prep", "fwd_state", "fwd_out", "bwd_b2", "bwd_state",
+                                  "bwd_wy", "gram_bwd", "bwd_combine") if k in name), name)
+        dt = "bf16" if ("DF16b" in name or "__bf16" in name or "bool" in name) else "fp32"
+        flops = 512 * (d.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0) + d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0))
+        peak = FP32_MFMA_PEAK if dt == "fp32" else 2516.6
+        out[f"{short} ({dt})"] = {
+            "mfma_flops": flops, "ns": d["ns"],
+            "tflops": flops / d["ns"] / 1e3, "frac_of_peak": flops / d["ns"] / 1e3 / peak,
+            "mfma_busy": d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0)
+            / max(1.0, d.get("GRBM_GUI_ACTIVE", 0) / xcds * simds)}
+    print(json.dumps(out, indent=1))
+    return out
+
+
 def _time(fn, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -348,7 +447,17 @@ def main():
                     help="forward steps plus the calibration copy, for rocprofv3 --pmc")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="reduce two rocprofv3 counter runs to profiles/traffic_*.json")
+    ap.add_argument("--pmc-train-run", action="store_true",
+                    help="one float32 training step and one headline forward, for MFMA counters")
+    ap.add_argument("--mfma-from", metavar="DIR",
+                    help="reduce a --pmc-train-run MFMA counter run (per-kernel flops, utilisation)")
     args = ap.parse_args()
+    if args.mfma_from:
+        mfma_from(args.mfma_from)
+        return
+    if args.pmc_train_run:
+        pmc_train_run()
+        return
     if args.traffic_from:
         traffic_from(*args.traffic_from)
         return
@@ -397,8 +506,10 @@ def main():
         try:
             xs32 = make_inputs(torch.float32)
             tms = time_train(gp, xs32, max(1, args.steps // 4), max(1, args.warmup // 2))
+            kms, mfma = train_kernels(gp, xs32)
             train = {"config": "B8 T8192 H6 D128 float32, forward + backward (trainable)",
-                     "ms_per_step": tms, "tokens_per_s": tokens / (tms * 1e-3)}
+                     "ms_per_step": tms, "tokens_per_s": tokens / (tms * 1e-3),
+                     "kernels_ms": kms, "mfma": mfma}
             del xs32
         except Exception as e:  # backward entry point not available in this build
             train = {"error": f"{type(e).__name__}: {e}"[:200]}
