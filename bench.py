@@ -68,9 +68,9 @@ def kernel_table(dtype_bytes, chunk):
     nb = C // 16
     aqk = C * s * (nb + 1) / (2 * nb)      # Aqk: only blocks on or below the diagonal
     return {
-        "fwd_prep": {"bytes": 5 * D * s + D * 4 + 3 * D * s + aqk + D * 4 + 4 * D / C,
+        "fwd_prep": {"bytes": 5 * D * s + D * 4 + 4 * D * s + aqk + 4 * D / C,
                      "flops": 4 * C * D + C * C / 3},
-        "fwd_state": {"bytes": 2 * D * s + D * 4 + 4 * D / C + D * D * s / C + D * s,
+        "fwd_state": {"bytes": 3 * D * s + 4 * D / C + D * D * s / C + D * s,
                       "flops": 4 * D * D},
         "fwd_out": {"bytes": 2 * D * s + aqk + D * D * s / C + D * 4,
                     "flops": 2 * D * D + C * D},

@@ -31,7 +31,7 @@ struct PrepArgs {
   long long NC;   // number of chunks, B*H*N
   float scale;
   T* W;
-  float* UT;
+  T* UT;
   T* KgT;
   T* Qg;
   T* Aqk;
@@ -580,7 +580,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
         af[kg] = op_from<T>(tmp);
       }
       T* Wc = a.W + (size_t)cid * BT * D;
-      float* Uc = a.UT + (size_t)cid * D * BT;
+      T* Uc = a.UT + (size_t)cid * D * BT;
 #pragma unroll
       for (int dt = 0; dt < DP / 16; ++dt) {
         const int dg = d0 + dt * 16;      // first channel of the tile
@@ -593,7 +593,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
           }
         }
         store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dg + 4 * lg), accw);
-        store4(Uc + (size_t)(dg + li) * BT + I * 16 + 4 * lg, accu);
+        store4(Uc + (size_t)(dg + li) * BT + kpos<T>(I * 16 + 4 * lg), accu);
       }
     }
   }
@@ -603,7 +603,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
 template <typename T>
 struct StateArgs {
   const T* W;
-  const float* UT;
+  const T* UT;
   const T* KgT;
   const float* GL;
   const float* h0;  // nullable, (B,H,D,D)
@@ -669,7 +669,10 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
   static_assert(BUF % 1024 == 0, "tiles must split into 1 KB pieces");
   __shared__ __align__(16) char sbuf0[BUF];
   __shared__ __align__(16) char sbuf1[NBUF == 2 ? BUF : 16];
-  __shared__ __align__(16) f32x4 sU[NW * NB * 64];   // u^T in compute-lane order
+  // u^T in compute-lane order: 16 bytes per lane and row block (float32) or
+  // row-block pair (bfloat16, chained order)
+  constexpr int UB = F32 ? NB : NB / 2;              // u^T pieces per compute wave
+  __shared__ __align__(16) uint4 sU[NW * UB * 64];
   __shared__ __align__(16) float sGL0[D];
   __shared__ __align__(16) float sGL1[NBUF == 2 ? D : 4];
   __shared__ __align__(16) float sJunk[64];        // target of the L2 touches
@@ -717,7 +720,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     constexpr int ROWB_W = D * (int)sizeof(T), ROWB_K = BT * (int)sizeof(T);
     constexpr int WPIECES = WBYTES / 1024;
     constexpr int PP = PIECES / NP;
-    static_assert(PIECES % NP == 0 && (NW * NB) % NP == 0, "work must split evenly");
+    static_assert(PIECES % NP == 0 && (NW * UB) % NP == 0, "work must split evenly");
     const int p = wv - NW;
     auto issue = [&](int c, char* base, float* gl) __attribute__((always_inline)) {
       const size_t cid = (size_t)bh * a.N + c0 + c;
@@ -740,14 +743,16 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
         }
       }
       if (p == NP - 1 && lane < D / 4) lds_dma16(a.GL + cid * D + lane * 4, gl);
-      // u^T[col][t] for compute wave w, row block it: lane (li, lg) of that
-      // wave reads u^T[16 w + li][16 it + 4 lg .. +3] from sU[(w NB + it) 64 + lane]
+      // u^T[col][t] for compute wave w, piece q: lane (li, lg) of that wave gets
+      // the 16 bytes at u^T[16 w + li][16 q + 4 lg] (float32: row block q) or
+      // [32 q + 8 lg] (bfloat16: row blocks 2q, 2q+1, chained), at sU[(w UB + q) 64 + lane]
       if (mslice) return;  // M columns: u = 0
-      const float* usrc = a.UT + cid * D * BT + (size_t)(vs * 16 * NW + li) * BT + 4 * lg;
+      constexpr int EPP = 16 / sizeof(T);              // elements per piece per lane
+      const T* usrc = a.UT + cid * D * BT + (size_t)(vs * 16 * NW + li) * BT + EPP * lg;
 #pragma unroll
-      for (int j = 0; j < NW * NB / NP; ++j) {
-        const int q = j * NP + p, w = q / NB, it = q % NB;
-        lds_dma16(usrc + (size_t)w * 16 * BT + it * 16, &sU[q * 64]);
+      for (int j = 0; j < NW * UB / NP; ++j) {
+        const int q = j * NP + p, w = q / UB, it = q % UB;
+        lds_dma16(usrc + (size_t)w * 16 * BT + it * 4 * EPP, &sU[q * 64]);
       }
     };
     // L2 touch of chunk c: one 4-byte DMA into a junk slot per 128-byte line of
@@ -755,7 +760,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     // chunk ahead of the DMA, it turns the DMA's HBM latency into L2 latency.
     constexpr int LINE = 128;
     constexpr int LW = WBYTES / LINE;                       // lines per W / kg^T tile
-    constexpr int LUR = BT * 4 / LINE;                      // lines per u^T row
+    constexpr int LUR = BT * (int)sizeof(T) / LINE;         // lines per u^T row
     constexpr int LU = 16 * NW * LUR;                       // this workgroup's u^T rows
     constexpr int LG = (D * 4 + LINE - 1) / LINE;           // g_last
     constexpr int LTOT = 2 * LW + LU + LG;
@@ -764,7 +769,8 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
       const size_t cid = (size_t)bh * a.N + c0 + c;
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
       const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
-      const char* usrc = reinterpret_cast<const char*>(a.UT + cid * D * BT + (size_t)vs * 16 * NW * BT);
+      const char* usrc =
+          reinterpret_cast<const char*>(a.UT + cid * D * BT + (size_t)vs * 16 * NW * BT);
       const char* gsrc = reinterpret_cast<const char*>(a.GL + cid * D);
 #pragma unroll
       for (int j = 0; j < NTP; ++j) {
@@ -871,8 +877,19 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     __syncthreads();  // A(c)
     f32x4 vn[NB];
 #pragma unroll
-    for (int it = 0; it < NB; ++it)
-      vn[it] = mslice ? f32x4{0.f, 0.f, 0.f, 0.f} : sU[(wv * NB + it) * 64 + lane];
+    for (int q = 0; q < UB; ++q) {
+      const uint4 pc = sU[(wv * UB + q) * 64 + lane];
+      if constexpr (F32) {
+        vn[q] = mslice ? f32x4{0.f, 0.f, 0.f, 0.f} : __builtin_bit_cast(f32x4, pc);
+      } else {
+        const bf16x8 e = __builtin_bit_cast(bf16x8, pc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          vn[2 * q][r] = mslice ? 0.f : (float)e[r];
+          vn[2 * q + 1][r] = mslice ? 0.f : (float)e[4 + r];
+        }
+      }
+    }
     __syncthreads();  // B(c)
     const T* sW = reinterpret_cast<const T*>(cur);
     const T* sK = reinterpret_cast<const T*>(cur + WBYTES);
@@ -1200,7 +1217,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   const int S_ws = vl ? 1 : state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
   const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), S_ws > 1 ? (size_t)B * H * S_ws : 0);
   T* W = reinterpret_cast<T*>(ws + L.W);
-  float* UT = reinterpret_cast<float*>(ws + L.UT);
+  T* UT = reinterpret_cast<T*>(ws + L.UT);
   T* KgT = reinterpret_cast<T*>(ws + L.KgT);
   T* Qg = reinterpret_cast<T*>(ws + L.Qg);
   T* Aqk = reinterpret_cast<T*>(ws + L.Aqk);

@@ -3,7 +3,7 @@
 // Every per-chunk tensor is stored chunk-major: chunk id cid = (b*H + h)*N + c,
 // then the tile.  Tiles are laid out so that each consumer reads 16-byte rows:
 //   W    [cid][BT][D]   T     w_pseudo = A (b k e^gc)        (gdn2_fwd.py:278-279)
-//   UT   [cid][D][BT]   f32   u^T, u = A (w v)               (gdn2_fwd.py:280)
+//   UT   [cid][D][BT]   T     u^T, u = A (w v)               (gdn2_fwd.py:280)
 //   KgT  [cid][D][BT]   T     kg^T, kg = k e^(gc_last - gc)  (gdn2_fwd.py:285)
 //   Qg   [cid][BT][D]   T     qg = q e^gc                    (gdn2_fwd.py:286)
 //   Aqk  [cid][BT][BT]  T     intra-chunk scores, lower blocks only (gdn2_fwd.py:127)
@@ -13,16 +13,17 @@
 //   A    [cid][BT][BT]  f32   (I + Akk)^{-1}, written only for the backward
 //                             (GDN2_FWD_SAVE_A)               (gdn2_fwd.py:246-260)
 // T is float for float32 inputs and bfloat16 for bfloat16 inputs.  For
-// bfloat16 the last dimension of W, KgT, HT and VnT (the index the serial state
+// bfloat16 the last dimension of W, UT, KgT, HT and VnT (the index the serial state
 // pass contracts over or produces) is stored in chunk order kpos<T>() of
 // gdn2_common.h: within each 32-column block, column 16*half + 4*lg + r sits at
 // position 8*lg + 4*half + r.  float32 tiles are in natural order.
 //
 // Backward workspace (all f32, chunk-major, one region per name):
 //   DAQK [BT][BT] dAqk (causal)      DVPT [D][BT] (Aqk^T do)^T    QDOT [D][D] (scale qg^T do)^T
-//   DHT  [D][D]  dh_{c+1}^T           DVNT [D][BT] dv_new^T        KBD, WVM [BT][D] b k e^gc, w v
-//   DQG, DW, DKG, DKBD, DWV [BT][D]   DA, TMP, DAKK [BT][BT]
+//   DHT  [D][D]  dh_{c+1}^T           DVNT [D][BT] dv_new^T
+//   DQG, DKG, DKBD, DWV [BT][D]       DAKK [BT][BT]
 //   RQ, RBK, RK [BT][D] off-diagonal score-gradient sums, DQD, DKD, DBKD [BT][D] diagonal ones
+//   SDH  [D]      sum_e dh_{c+1}[d][e] h_c[d][e]
 #pragma once
 
 #include <stddef.h>
@@ -44,7 +45,7 @@ inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem, size_t s
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
   L.W = take(nchunks * BT * D * elem);
-  L.UT = take(nchunks * D * BT * 4);
+  L.UT = take(nchunks * D * BT * elem);
   L.KgT = take(nchunks * D * BT * elem);
   L.Qg = take(nchunks * BT * D * elem);
   L.Aqk = take(nchunks * BT * BT * elem);

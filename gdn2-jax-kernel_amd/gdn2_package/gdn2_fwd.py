@@ -196,25 +196,25 @@ def _residual_views(p: _Prepared, ws: torch.Tensor):
     B, H, D, BT, N = p.B, p.H, p.D, p.BT, p.N
     es = 4 if p.in_dt == torch.float32 else 2
     NC = B * H * N
-    sizes = [("W", NC * BT * D * es), ("UT", NC * D * BT * 4), ("KgT", NC * D * BT * es),
+    sizes = [("W", NC * BT * D * es), ("UT", NC * D * BT * es), ("KgT", NC * D * BT * es),
              ("Qg", NC * BT * D * es), ("Aqk", NC * BT * BT * es), ("GL", NC * D * 4),
              ("HT", NC * D * D * es), ("VnT", NC * D * BT * es)]
     off, views = 0, {}
     for name, nb in sizes:
-        dt = torch.float32 if name in ("UT", "GL") else p.in_dt
+        dt = torch.float32 if name == "GL" else p.in_dt
         views[name] = ws[off:off + nb].view(dt)
         off = (off + nb + 255) // 256 * 256
     f = lambda x: x.float()
     shp = (B, H, N)
     idx = torch.arange(BT, device=p.device)
     causal = (idx[:, None] >= idx[None, :])
-    # bfloat16 W, KgT, HT, VnT keep their last dimension in chained order
+    # bfloat16 W, UT, KgT, HT, VnT keep their last dimension in chained order
     # (gdn2_common.h kpos): undo it for the views
     chained = p.in_dt == torch.bfloat16
     nat = lambda x, n: x[..., _kpos_index(n, x.device)] if chained else x
     return {
         "w_pseudo": f(nat(views["W"].view(*shp, BT, D), D)),
-        "u": f(views["UT"].view(*shp, D, BT).transpose(-1, -2)),
+        "u": f(nat(views["UT"].view(*shp, D, BT), BT).transpose(-1, -2)),
         "kg": f(nat(views["KgT"].view(*shp, D, BT), BT).transpose(-1, -2)),
         "qg": f(views["Qg"].view(*shp, BT, D)),
         "Aqk": torch.where(causal, f(views["Aqk"].view(*shp, BT, BT)), 0.0),
