@@ -159,7 +159,7 @@ def train_kernels(gp, xs):
     res = {}
     for names, run in ((("fwd_prep", "fwd_state", "fwd_out"),
                         lambda: _run_forward(p, flags=_lib.FWD_SAVE_A)),
-                       (("bwd_b2", "bwd_state", "bwd_wy", "gram_bwd", "bwd_combine"), None)):
+                       (("bwd_b2", "bwd_state", "bwd_wy", "gram_bwd"), None)):
         n = len(names) + 1
         for _ in range(2):            # second pass timed
             evs = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
@@ -216,7 +216,7 @@ def mfma_from(run_dir):
         if "gdn2" not in name:
             continue
         short = next((k for k in ("fwd_prep", "fwd_state", "fwd_out", "bwd_b2", "bwd_state",
-                                  "bwd_wy", "gram_bwd", "bwd_combine") if k in name), name)
+                                  "bwd_wy", "gram_bwd") if k in name), name)
         dt = "bf16" if ("DF16b" in name or "__bf16" in name or "bool" in name) else "fp32"
         flops = 512 * (d.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0) + d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0))
         peak = FP32_MFMA_PEAK if dt == "fp32" else 2516.6

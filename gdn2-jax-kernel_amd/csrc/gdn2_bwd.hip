@@ -10,8 +10,8 @@
 //   B3   dqg = scale do h^T, dW = -dv_new h^T, dkg = v_new dh'^T,
 //        dA = dW (b k e^gc)^T + dv_new (w v)^T, d(bke^gc) = A^T dW, d(wv) = A^T dv_new,
 //        dAkk = -(A^T dA A^T) . strict                                        (bwd_wy)
-//   B4   gradients of Aqk/Akk wrt q, k, b k, gc                              (gram_bwd)
-//   B5   chain rule through the exponentials + reverse cumsum of dgc          (bwd_combine)
+//   B4   gradients of Aqk/Akk wrt q, k, b k, gc, then the chain rule through
+//        the exponentials (B3 tail) and the reverse cumsum of dgc (B5)       (gram_bwd)
 
 #include "gdn2_common.h"
 #include "gdn2_layout.h"
@@ -783,46 +783,74 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 }
 
 // ============================================================================
-// gram_bwd (B4): gradients of the intra-chunk scores
+// gram_bwd (B4, with the B3 elementwise tail and B5): gradients of the
+// intra-chunk scores
 //   Aqk[i,j] = scale sum_d q_i k_j e^{gc_i-gc_j} (j<=i),  Akk[i,j] = sum_d (bk)_i k_j e^{..} (j<i)
-// Off-diagonal 16-row block pairs (I > J) use the forward's factorisation around
-// P_J (gc at the end of block J): the MFMA sums below are written without their
-// row factors, which bwd_combine applies:
+// and from them the input gradients.  Off-diagonal 16-row block pairs (I > J) use
+// the forward's factorisation around P_J (gc at the end of block J); the MFMA sums
+// are formed without their row factors:
 //   RQ [i]  = sum_J F_IJ (dAqk_IJ  Khat_J),   dq_g  = scale e^{loc_i} RQ
 //   RBK[i]  = sum_J F_IJ (dAkk_IJ  Khat_J),   dbk_g = e^{loc_i} RBK
 //   RK [j]  = sum_I F_IJ (scale dAqk_IJ^T AQ_I + dAkk_IJ^T ABK_I),  dk_g = e^{T_J-loc_j} RK
 // with loc = in-block cumsum of g, T_J = block sum, F_IJ = exp(sum of T over blocks
 // strictly between J and I), Khat = k e^{T-loc}, AQ = q e^{loc}, ABK = b k e^{loc}.
-// Diagonal blocks are summed per channel, factorised around the block's 8th
-// token as in the forward, into DQD, DKD, DBKD.  Wave w owns row block w (BT = 64).
+// Every wave does three block pairs per 16-channel slice, so a barrier after each
+// slice frees that slice of AQ / ABK / Khat and RQ / RBK / RK take its place in LDS.
+// Diagonal blocks are summed per channel (one lane per channel), factorised around
+// the block's 8th token as in the forward.  The same lane then applies the chain
+// rule through the exponentials of qg, kg and b k e^gc (gdn2_bwd.py:186-210; dqg,
+// dkg, d(b k e^gc), d(w v) and sum_e dh' h come from bwd_wy) and the reverse cumsum
+// of dgc (gdn2_bwd.py:32-41): suffix sums inside the block, block totals across the
+// waves through LDS.  Wave w owns row block w (BT = 64).
 // ============================================================================
 template <typename T, typename TG>
 struct GramArgs {
-  const T *q, *k, *b;
+  const T *q, *k, *v, *w, *b;
   const TG* g;
-  const float *DAQK, *DAKK;
+  const float *DAQK, *DAKK, *SDH, *DQG, *DKG, *DKBD, *DWV;
   int T_len, H, N;
   float scale;
-  float *RQ, *RBK, *RK, *DQD, *DKD, *DBKD;
+  T *dq, *dk, *dv, *dw, *db;
+  TG* dg;
 };
+
+// Channels are independent in all of this, so a workgroup takes one chunk and
+// one panel of GP = 32 channels (62 KB of LDS: two workgroups per CU, one
+// streaming while the other computes).  The panels of a chunk run on one XCD,
+// sharing the chunk's dAqk / dAkk tiles in its L2.
+constexpr int gram_panel() { return 32; }
 
 template <typename T, typename TG, int D>
 __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
-  constexpr int BT = 64, NB = 4, NDT = D / 16, DQ = D / 4;
-  constexpr int LD1 = D + 4, LD2 = BT + 4;
-  __shared__ __align__(16) float sAQ[BT * LD1];
-  __shared__ __align__(16) float sABK[BT * LD1];
-  __shared__ __align__(16) float sKH[BT * LD1];
+  constexpr int BT = 64, NB = 4, GP = gram_panel(), NPN = D / GP, NDT = GP / 16, DQ = GP / 4;
+  constexpr int LD1 = GP + 4, LD2 = BT + 4;
+  static_assert(D % GP == 0, "panels must tile D");
+  __shared__ __align__(16) float sAQ[BT * LD1];    // q e^loc, then RQ, then gq, then dgc sums
+  __shared__ __align__(16) float sABK[BT * LD1];   // b k e^loc, then RBK, then gbk
+  __shared__ __align__(16) float sKH[BT * LD1];    // k e^{T-loc}, then RK, then gk
   __shared__ __align__(16) float sDQK[BT * LD2];
   __shared__ __align__(16) float sDKK[BT * LD2];
-  __shared__ __align__(16) float sTot[NB * D];
-  __shared__ __align__(16) float sETot[NB * D];
+  __shared__ __align__(16) float sTot[NB * GP];
+  __shared__ __align__(16) float sETot[NB * GP];   // e^{T_m}, then per-block sums of dgc
+  __shared__ __align__(16) float sSkg[NB * GP];    // per-block sums of dkg kg
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  const int cid = blockIdx.x;
+  int cid, pn;
+  {
+    const int id = blockIdx.x, nwg = gridDim.x;
+    if (nwg % (8 * NPN) == 0) {   // block id mod 8 = XCD: a chunk's panels on one XCD
+      const int xcd = id % 8, slot = id / 8;
+      pn = slot % NPN;
+      cid = (slot / NPN) * 8 + xcd;
+    } else {
+      cid = id / NPN;
+      pn = id % NPN;
+    }
+  }
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
   const size_t HD = (size_t)a.H * D;
-  const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D;
+  const int ch0 = pn * GP;   // first channel of the panel
+  const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D + ch0;
   auto chan = [&](int x) { return (x / 4) * 16 + lg * 4 + (x % 4); };
   const int I = wv;
 
@@ -840,21 +868,21 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   // in-block cumsum of g for own rows (lane li = token)
   const int t = I * 16 + li;
   const size_t rowo = tok0 + (size_t)t * HD;
-  float loc[DQ];
-#pragma unroll
-  for (int j = 0; j < D / 16; ++j) load_f<4>(a.g + rowo + j * 16 + lg * 4, &loc[j * 4]);
-#pragma unroll
-  for (int x = 0; x < DQ; ++x) loc[x] = row_scan16(loc[x]);
-  if (li == 15) {
-#pragma unroll
-    for (int x = 0; x < DQ; ++x) sTot[I * D + chan(x)] = loc[x];
-  }
-  __syncthreads();
-  for (int i = tid; i < NB * D; i += 256) sETot[i] = __expf(sTot[i]);
   {
+    float loc[DQ];
+#pragma unroll
+    for (int j = 0; j < NDT; ++j) load_f<4>(a.g + rowo + j * 16 + lg * 4, &loc[j * 4]);
+#pragma unroll
+    for (int x = 0; x < DQ; ++x) loc[x] = row_scan16(loc[x]);
+    if (li == 15) {
+#pragma unroll
+      for (int x = 0; x < DQ; ++x) sTot[I * GP + chan(x)] = loc[x];
+    }
+    __syncthreads();
+    for (int i = tid; i < NB * GP; i += 256) sETot[i] = __expf(sTot[i]);
     float qv[DQ], kv[DQ], bv[DQ];
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
+    for (int j = 0; j < NDT; ++j) {
       load_f<4>(a.q + rowo + j * 16 + lg * 4, &qv[j * 4]);
       load_f<4>(a.k + rowo + j * 16 + lg * 4, &kv[j * 4]);
       load_f<4>(a.b + rowo + j * 16 + lg * 4, &bv[j * 4]);
@@ -865,15 +893,12 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
       const float el = __expf(loc[x]);
       sAQ[t * LD1 + ch] = qv[x] * el;
       sABK[t * LD1 + ch] = bv[x] * kv[x] * el;
-      sKH[t * LD1 + ch] = kv[x] * __expf(sTot[I * D + ch] - loc[x]);
+      sKH[t * LD1 + ch] = kv[x] * __expf(sTot[I * GP + ch] - loc[x]);
     }
   }
   __syncthreads();
 
   // ---- off-diagonal pairs on MFMA --------------------------------------------
-  float* rq = a.RQ + (size_t)cid * BT * D;
-  float* rbk = a.RBK + (size_t)cid * BT * D;
-  float* rk = a.RK + (size_t)cid * BT * D;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) {
     const int dcol = dt * 16 + li;
@@ -888,7 +913,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
       mma(tk, load4f(&sDKK[(I * 16 + li) * LD2 + J * 16 + 4 * lg]), y);
 #pragma unroll
       for (int r = 0; r < 4; ++r) { aq[r] += F * tq[r]; ab[r] += F * tk[r]; }
-      F *= sETot[J * D + dcol];
+      F *= sETot[J * GP + dcol];
     }
     // rows of block I (as the column block) against I' > I
     f32x4 akk = {0.f, 0.f, 0.f, 0.f};
@@ -907,22 +932,27 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
       mma(t2, xk, yk);
 #pragma unroll
       for (int r = 0; r < 4; ++r) akk[r] += F * (a.scale * t1[r] + t2[r]);
-      F *= sETot[Ip * D + dcol];
+      F *= sETot[Ip * GP + dcol];
     }
+    lds_barrier();  // every wave is done with channel slice dt of sAQ, sABK, sKH, sETot
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const size_t o = (size_t)(I * 16 + 4 * lg + r) * D + dcol;
-      rq[o] = aq[r];
-      rbk[o] = ab[r];
-      rk[o] = akk[r];
+      const int o = (I * 16 + 4 * lg + r) * LD1 + dcol;
+      sAQ[o] = aq[r];
+      sABK[o] = ab[r];
+      sKH[o] = akk[r];
     }
   }
 
-  // ---- diagonal block, per channel -------------------------------------------
-  // e^{lc_i - lc_j} = e^{lc_i - lm} e^{lm - lc_j} around the block's 8th token
-  // (as the forward's diagonal blocks): 32 exponentials per channel and block
-  for (int d = lane; d < D; d += 64) {
-    float qe[16], ke[16], be[16], el[16], er[16], dq[16], dk[16], db[16];
+  // ---- diagonal block, one lane per channel ------------------------------------
+  // Wave I reads back only its own rows of RQ / RBK / RK (written by its own
+  // lanes above).
+  if (lane < GP) {
+    const int d = lane;
+    const float totI = sTot[I * GP + d];
+    // e^{lc_i - lc_j} = e^{lc_i - lm} e^{lm - lc_j} around the block's 8th token
+    // (as the forward's diagonal blocks): 32 exponentials per channel and block
+    float qe[16], ke[16], be[16], fl[16], fr[16], lc[16], dq[16], dk[16], db[16];
     float run = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -931,117 +961,124 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
       ke[i] = to_f(a.k[o]);
       be[i] = to_f(a.b[o]) * ke[i];
       run += to_f(a.g[o]);
-      el[i] = run;
+      lc[i] = run;
       dq[i] = dk[i] = db[i] = 0.f;
     }
-    const float lm = el[7];
+    const float lm = lc[7];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      er[i] = __expf(lm - el[i]);
-      el[i] = __expf(el[i] - lm);
-      qe[i] *= a.scale * el[i];   // scale q_i e^{lc_i - lm}
-      be[i] *= el[i];             // (b k)_i e^{lc_i - lm}
-      ke[i] *= er[i];             // k_j e^{lm - lc_j}
+      fr[i] = __expf(lm - lc[i]);
+      fl[i] = __expf(lc[i] - lm);
+      qe[i] *= a.scale * fl[i];   // scale q_i e^{lc_i - lm}
+      be[i] *= fl[i];             // (b k)_i e^{lc_i - lm}
+      ke[i] *= fr[i];             // k_j e^{lm - lc_j}
     }
+    const int dblk = I * 16 * LD2 + I * 16;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
 #pragma unroll
       for (int j = 0; j <= i; ++j) {
-        const float aq = sDQK[(I * 16 + i) * LD2 + I * 16 + j];
+        const float aq = sDQK[dblk + i * LD2 + j];
         dq[i] += aq * ke[j];
         dk[j] += aq * qe[i];
         if (j < i) {
-          const float ak = sDKK[(I * 16 + i) * LD2 + I * 16 + j];
+          const float ak = sDKK[dblk + i * LD2 + j];
           dk[j] += ak * be[i];
           db[i] += ak * ke[j];
         }
       }
     }
+    // score gradients wrt q, b k, k: off-diagonal sums with their row factors plus
+    // the diagonal block, in place of RQ, RBK, RK
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      dq[i] *= a.scale * el[i];
-      db[i] *= el[i];
-      dk[i] *= er[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const size_t o = ((size_t)cid * BT + I * 16 + i) * D + d;
-      a.DQD[o] = dq[i];
-      a.DKD[o] = dk[i];
-      a.DBKD[o] = db[i];
+      const int so = (I * 16 + i) * LD1 + d;
+      const float el = __expf(lc[i]), ek = __expf(totI - lc[i]);
+      sAQ[so] = a.scale * (el * sAQ[so] + dq[i] * fl[i]);
+      sABK[so] = el * sABK[so] + db[i] * fl[i];
+      sKH[so] = ek * sKH[so] + dk[i] * fr[i];
     }
   }
-}
 
-// ============================================================================
-// bwd_combine (B3 elementwise tail + B5): one thread per channel.
-// ============================================================================
-template <typename T, typename TG>
-struct CombArgs {
-  const T *q, *k, *v, *w, *b;
-  const TG* g;
-  const float *SDH, *DQG, *DKG, *DKBD, *DWV, *RQ, *RBK, *RK, *DQD, *DKD, *DBKD;
-  int T_len, H, N;
-  float scale;
-  T *dq, *dk, *dv, *dw, *db;
-  TG* dg;
-};
-
-template <typename T, typename TG, int D>
-__global__ void __launch_bounds__(128) bwd_combine(CombArgs<T, TG> a) {
-  constexpr int BT = 64;
-  const int d = threadIdx.x, cid = blockIdx.x;
-  if (d >= D) return;
-  const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
-  const size_t HD = (size_t)a.H * D;
-  const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D + d;
-  // gc (running) and loc (in 16-token blocks) for this channel
-  float gcv[BT], lcv[BT], tot[BT / 16];
-  float run = 0.f, lrun = 0.f;
+  // ---- chain rule, lane = token t of block I, channels chan(x) -----------------
+  // (gdn2_bwd.py:186-210; dqg, dkg, dkbd, dwv come from bwd_wy).  Wave I reads the
+  // score gradients of its own rows, written by its own lanes above.  dgc is summed
+  // from each token to the block end by a row scan; the block totals cross the
+  // waves through LDS.
+  const size_t wrow_t = ((size_t)cid * BT + t) * D + ch0;
 #pragma unroll
-  for (int t = 0; t < BT; ++t) {
-    const float gv = to_f(a.g[tok0 + (size_t)t * HD]);
-    run += gv;
-    lrun = (t % 16 == 0) ? gv : lrun + gv;
-    gcv[t] = run;
-    lcv[t] = lrun;
-    if (t % 16 == 15) tot[t / 16] = lrun;
+  for (int j = 0; j < NDT; ++j) {
+    const int c0 = j * 16 + lg * 4;
+    const f32x4 qv = load4f(a.q + rowo + c0), kv = load4f(a.k + rowo + c0),
+                vv = load4f(a.v + rowo + c0), wvv = load4f(a.w + rowo + c0),
+                bv = load4f(a.b + rowo + c0);
+    const f32x4 dqg = load4f(a.DQG + wrow_t + c0), dkg = load4f(a.DKG + wrow_t + c0),
+                dkbd = load4f(a.DKBD + wrow_t + c0), dwv = load4f(a.DWV + wrow_t + c0);
+    const f32x4 gq = load4f(&sAQ[t * LD1 + c0]), gbk = load4f(&sABK[t * LD1 + c0]),
+                gk = load4f(&sKH[t * LD1 + c0]);
+    f32x4 lc = load4f(a.g + rowo + c0);   // in-block cumsum again, as at the start
+#pragma unroll
+    for (int e = 0; e < 4; ++e) lc[e] = row_scan16(lc[e]);
+    f32x4 pre = {0.f, 0.f, 0.f, 0.f}, gl = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+      const f32x4 tm = load4f(&sTot[m * GP + c0]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gl[e] += tm[e];
+        pre[e] += m < I ? tm[e] : 0.f;
+      }
+    }
+    f32x4 odq, odk, odb, odw, odv, suf;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float gc = pre[e] + lc[e];
+      const float eg = __expf(gc), ekg = __expf(gl[e] - gc);
+      const float kgv = kv[e] * ekg;
+      odq[e] = sanitize(dqg[e] * eg + gq[e]);
+      odk[e] = sanitize(dkbd[e] * bv[e] * eg + dkg[e] * ekg + gk[e] + gbk[e] * bv[e]);
+      odb[e] = sanitize(dkbd[e] * kv[e] * eg + gbk[e] * kv[e]);
+      odw[e] = sanitize(dwv[e] * vv[e]);
+      odv[e] = sanitize(dwv[e] * wvv[e]);
+      const float dgc = dkbd[e] * bv[e] * kv[e] * eg + dqg[e] * qv[e] * eg - dkg[e] * kgv +
+                        qv[e] * gq[e] + bv[e] * kv[e] * gbk[e] - kv[e] * gk[e];
+      suf[e] = row_suffix16(dgc);
+      const float skg = row_suffix16(dkg[e] * kgv);   // lane 0: the block's sum
+      if (li == 0) {
+        sETot[I * GP + c0 + e] = suf[e];
+        sSkg[I * GP + c0 + e] = skg;
+      }
+    }
+    store4(&sAQ[t * LD1 + c0], suf);   // in place of gq, read by this lane only
+    store4(a.dq + rowo + c0, odq);
+    store4(a.dk + rowo + c0, odk);
+    store4(a.db + rowo + c0, odb);
+    store4(a.dw + rowo + c0, odw);
+    store4(a.dv + rowo + c0, odv);
   }
-  const float gl = run;
-  // exp(gl) * sum_dv dh'[d][dv] h[d][dv]  (gdn2_bwd.py:196-197), the sum from bwd_wy
-  const float sdh = a.SDH[(size_t)cid * D + d];
-  float dgc[BT];
-  float skg = 0.f;
+  lds_barrier();
+  // dg[t] = sum_{s >= t} dgc[s] + sum_t dkg kg + e^{gl} sum_e dh' h  (the last two
+  // enter at the chunk's last token, gdn2_bwd.py:196-199)
 #pragma unroll
-  for (int t = 0; t < BT; ++t) {
-    const size_t o = tok0 + (size_t)t * HD;
-    const size_t w_ = ((size_t)cid * BT + t) * D + d;
-    const float qv = to_f(a.q[o]), kv = to_f(a.k[o]), vv = to_f(a.v[o]), wv = to_f(a.w[o]),
-                bv = to_f(a.b[o]);
-    const float eg = __expf(gcv[t]), ekg = __expf(gl - gcv[t]);
-    const float dqg = a.DQG[w_], dkg = a.DKG[w_], dkbd = a.DKBD[w_], dwv = a.DWV[w_];
-    const float el = __expf(lcv[t]), ek = __expf(tot[t / 16] - lcv[t]);
-    const float gq = a.scale * el * a.RQ[w_] + a.DQD[w_];
-    const float gbk = el * a.RBK[w_] + a.DBKD[w_];
-    const float gk = ek * a.RK[w_] + a.DKD[w_];
-    const float kgv = kv * ekg;
-    const float dqv = dqg * eg + gq;
-    const float dkv = dkbd * bv * eg + dkg * ekg + gk + gbk * bv;
-    const float dbv = dkbd * kv * eg + gbk * kv;
-    a.dq[o] = from_f<T>(sanitize(dqv));
-    a.dk[o] = from_f<T>(sanitize(dkv));
-    a.db[o] = from_f<T>(sanitize(dbv));
-    a.dw[o] = from_f<T>(sanitize(dwv * vv));
-    a.dv[o] = from_f<T>(sanitize(dwv * wv));
-    dgc[t] = dkbd * bv * kv * eg + dqg * qv * eg - dkg * kgv + qv * gq + bv * kv * gbk - kv * gk;
-    skg += dkg * kgv;
-  }
-  dgc[BT - 1] += skg + __expf(gl) * sdh;
-  float acc = 0.f;
+  for (int j = 0; j < NDT; ++j) {
+    const int c0 = j * 16 + lg * 4;
+    const f32x4 sdh = load4f(a.SDH + (size_t)cid * D + ch0 + c0);
+    f32x4 gl = {0.f, 0.f, 0.f, 0.f}, tail = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int t = BT - 1; t >= 0; --t) {
-    acc += dgc[t];
-    a.dg[tok0 + (size_t)t * HD] = from_f<TG>(sanitize(acc));
+    for (int m = 0; m < NB; ++m) {
+      const f32x4 tm = load4f(&sTot[m * GP + c0]), sk = load4f(&sSkg[m * GP + c0]),
+                  bt = load4f(&sETot[m * GP + c0]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gl[e] += tm[e];
+        tail[e] += sk[e] + (m > I ? bt[e] : 0.f);
+      }
+    }
+    const f32x4 suf = load4f(&sAQ[t * LD1 + c0]);
+    f32x4 odg;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) odg[e] = sanitize(suf[e] + tail[e] + __expf(gl[e]) * sdh[e]);
+    store4(a.dg + rowo + c0, odg);
   }
 }
 
@@ -1105,20 +1142,15 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                        buf(B_DAKK), buf(B_SDH)};
       hipLaunchKernelGGL((bwd_wy<T, TG, D>), dim3(NC), dim3(256), 0, st, wa);
       launch_mark(st);
-      // B4
-      GramArgs<T, TG> gr{(const T*)q, (const T*)k, (const T*)b, (const TG*)g, buf(B_DAQK),
-                         buf(B_DAKK), T_len, H, N, scale, buf(B_RQ), buf(B_RBK), buf(B_RK),
-                         buf(B_DQD), buf(B_DKD), buf(B_DBKD)};
-      hipLaunchKernelGGL((gram_bwd<T, TG, D>), dim3(NC), dim3(256), 0, st, gr);
-      launch_mark(st);
-      // B3 tail + B5
-      CombArgs<T, TG> ca{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
-                         (const TG*)g, buf(B_SDH), buf(B_DQG), buf(B_DKG),
-                         buf(B_DKBD), buf(B_DWV), buf(B_RQ), buf(B_RBK), buf(B_RK),
-                         buf(B_DQD), buf(B_DKD), buf(B_DBKD), T_len, H, N, scale, (T*)dq,
-                         (T*)dk, (T*)dv,
-                         (T*)dw, (T*)db, (TG*)dg};
-      hipLaunchKernelGGL((bwd_combine<T, TG, D>), dim3(NC), dim3(128), 0, st, ca);
+      // B4 + B3 elementwise tail + B5
+      GramArgs<T, TG> gr{(const T*)q,  (const T*)k,  (const T*)v,  (const T*)w,
+                         (const T*)b,  (const TG*)g, buf(B_DAQK),  buf(B_DAKK),
+                         buf(B_SDH),   buf(B_DQG),   buf(B_DKG),   buf(B_DKBD),
+                         buf(B_DWV),   T_len,        H,            N,
+                         scale,        (T*)dq,       (T*)dk,       (T*)dv,
+                         (T*)dw,       (T*)db,       (TG*)dg};
+      hipLaunchKernelGGL((gram_bwd<T, TG, D>), dim3(NC * (D / gram_panel())), dim3(256), 0,
+                         st, gr);
       launch_mark(st);
     }
     return hipGetLastError();

@@ -205,6 +205,14 @@ __device__ __forceinline__ float row_scan16(float x) {
   x = row_shr_add<0x114>(x);
   return row_shr_add<0x118>(x);
 }
+// inclusive suffix sum over the 16 lanes of a row: lane i gets lanes i..15
+// (row_shl steps; lanes shifted in from beyond the row read 0)
+__device__ __forceinline__ float row_suffix16(float x) {
+  x = row_shr_add<0x101>(x);
+  x = row_shr_add<0x102>(x);
+  x = row_shr_add<0x104>(x);
+  return row_shr_add<0x108>(x);
+}
 template <int N>
 __device__ __forceinline__ float row_bcast(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(

@@ -126,7 +126,7 @@ size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
  * first).  BT must be 64.  dh_final and h0 may be NULL (zero).  dq,dk,dv,dw,db
  * are in_dtype, dg is g_dtype, dh0 is float32 (B,H,D,D); all gradients are
  * sanitized as gdn2_pipeline.py:129-135.  Computes in float32 throughout.
- * Launches 5 kernels (see gdn2_set_launch_events). */
+ * Launches 4 kernels (see gdn2_set_launch_events). */
 int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
              const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, const float* h0, float scale, const float* dout,
