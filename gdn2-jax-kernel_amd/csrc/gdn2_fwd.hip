@@ -653,11 +653,20 @@ struct StateArgs {
 // the kernel runs single-buffered: a third barrier E per chunk marks the end of
 // the compute waves' reads, after which the producers move the next chunk, by
 // then in L2 through the touch issued one chunk ahead.
+//
+// K-split (KS = 2, float32): on float32 MFMA the two chained products of a
+// chunk are the step's critical path (256 16x16x4 instructions per compute wave
+// at BT = 64, D = 128).  Each 16-column slice then has two compute waves, each
+// holding half of h's rows: both form their half of W h, exchange it through
+// LDS (barrier X, after B), form the same v_new = u - (W h)_lo - (W h)_hi and
+// update their own rows of h -- half the MFMA chain per wave.
 template <typename T, int BT, int D>
 constexpr int state_bufs() { return 4 * BT * D * (int)sizeof(T) <= 132 * 1024 ? 2 : 1; }
+template <typename T, int D>
+constexpr int state_ksplit() { return (sizeof(T) == 4 && D <= 128) ? 2 : 1; }
 
-template <typename T, int BT, int D, int NW, int NP>
-__global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
+template <typename T, int BT, int D, int NW, int NP, int KS>
+__global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a) {
   using Op = typename Tr<T>::Op;
   constexpr int NB = BT / 16, NDT = D / 16;
   constexpr int NVS = D / (16 * NW);
@@ -666,13 +675,17 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
   constexpr int BUF = 2 * WBYTES;                    // W + kg^T
   constexpr int PIECES = BUF / 1024;                 // 1 KB DMA instructions per chunk
   constexpr int NBUF = state_bufs<T, BT, D>();
+  constexpr int NCW = NW * KS;                       // compute waves
+  constexpr int NDH = NDT / KS;                      // row tiles of h per compute wave
   static_assert(BUF % 1024 == 0, "tiles must split into 1 KB pieces");
+  static_assert(KS == 1 || (F32 && NDT % KS == 0 && NB % KS == 0), "K-split: float32 only");
   __shared__ __align__(16) char sbuf0[BUF];
   __shared__ __align__(16) char sbuf1[NBUF == 2 ? BUF : 16];
   // u^T in compute-lane order: 16 bytes per lane and row block (float32) or
   // row-block pair (bfloat16, chained order)
   constexpr int UB = F32 ? NB : NB / 2;              // u^T pieces per compute wave
   __shared__ __align__(16) uint4 sU[NW * UB * 64];
+  __shared__ __align__(16) f32x4 sX[KS > 1 ? NCW * NB * 64 : 1];   // K-split partials of W h
   __shared__ __align__(16) float sGL0[D];
   __shared__ __align__(16) float sGL1[NBUF == 2 ? D : 4];
   __shared__ __align__(16) float sJunk[64];        // target of the L2 touches
@@ -714,14 +727,14 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
   }
   n = n > 0 ? n : 0;
 
-  if (wv >= NW) {
+  if (wv >= NCW) {
     // ---- producers ----------------------------------------------------------
     // producer p moves W / kg^T pieces [p PP, (p+1) PP) and u^T blocks q = p mod NP
     constexpr int ROWB_W = D * (int)sizeof(T), ROWB_K = BT * (int)sizeof(T);
     constexpr int WPIECES = WBYTES / 1024;
     constexpr int PP = PIECES / NP;
     static_assert(PIECES % NP == 0 && (NW * UB) % NP == 0, "work must split evenly");
-    const int p = wv - NW;
+    const int p = wv - NCW;
     auto issue = [&](int c, char* base, float* gl) __attribute__((always_inline)) {
       const size_t cid = (size_t)bh * a.N + c0 + c;
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
@@ -809,6 +822,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
         exp_gl(sGL0);
         barrier();  // A(c)
         barrier();  // B(c)
+        if constexpr (KS > 1) barrier();  // X(c)
         barrier();  // E(c): chunk c's tiles are no longer read
         if (c + 1 < n) {
           issue(c + 1, sbuf0, sGL0);
@@ -825,19 +839,24 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
       if (c + 1 < n) {
         issue(c + 1, sbuf1, sGL1);
         if (c + 2 < n) touch(c + 2);
+        if constexpr (KS > 1) barrier();  // X(c)
         wait_chunk(c + 1);
         exp_gl(sGL1);
         barrier();  // A(c+1)
         barrier();  // B(c+1)
         if (c + 2 < n) issue(c + 2, sbuf0, sGL0);
         if (c + 3 < n) touch(c + 3);
+        if constexpr (KS > 1) barrier();  // X(c+1)
+      } else {
+        if constexpr (KS > 1) barrier();  // X(c)
       }
     }
     return;
   }
 
   // ---- compute waves ----------------------------------------------------------
-  const int col = vs * 16 * NW + wv * 16 + li;
+  const int wcol = wv % NW, ks = wv / NW;          // column slice, k-half (K-split)
+  const int col = vs * 16 * NW + wcol * 16 + li;
   // element offset of logical (row r, element e) in a tile whose rows hold `re` elements
   auto swz = [](int r, int e, int re) {
     constexpr int EPC = 16 / sizeof(T);           // elements per 16-byte chunk
@@ -850,24 +869,25 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
   // entry state: h0 (or 0) for a plain pass and for segment 0 of the summary
   // pass, 0 for later segments of the summary pass, the identity for M slices,
   // the combined entry state in the final segmented pass
-  f32x4 h[NDT];
+  f32x4 h[NDH];   // row tiles at = ks NDH + i of this slice's h
   const float* hsrc = a.cu ? (a.h0 ? a.h0 + ((size_t)sg * a.H + bh) * D * D : nullptr)
                     : (a.S > 1 && !a.summary) ? a.hin + ((size_t)unit) * D * D
                     : (sg == 0 && !mslice && a.h0) ? a.h0 + (size_t)bh * D * D : nullptr;
   if (mslice) {
 #pragma unroll
-    for (int at = 0; at < NDT; ++at)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) h[at][r] = (at * 16 + 4 * lg + r == col) ? 1.f : 0.f;
-  } else if (hsrc) {
-#pragma unroll
-    for (int at = 0; at < NDT; ++at)
+    for (int i = 0; i < NDH; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        h[at][r] = sanitize(hsrc[(size_t)(at * 16 + 4 * lg + r) * D + col]);
+        h[i][r] = ((ks * NDH + i) * 16 + 4 * lg + r == col) ? 1.f : 0.f;
+  } else if (hsrc) {
+#pragma unroll
+    for (int i = 0; i < NDH; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        h[i][r] = sanitize(hsrc[(size_t)((ks * NDH + i) * 16 + 4 * lg + r) * D + col]);
   } else {
 #pragma unroll
-    for (int at = 0; at < NDT; ++at) h[at] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < NDH; ++i) h[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const bool write_tiles = !a.summary;
 
@@ -878,7 +898,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     f32x4 vn[NB];
 #pragma unroll
     for (int q = 0; q < UB; ++q) {
-      const uint4 pc = sU[(wv * UB + q) * 64 + lane];
+      const uint4 pc = sU[(wcol * UB + q) * 64 + lane];
       if constexpr (F32) {
         vn[q] = mslice ? f32x4{0.f, 0.f, 0.f, 0.f} : __builtin_bit_cast(f32x4, pc);
       } else {
@@ -898,7 +918,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     if (!write_tiles) {
     } else if constexpr (F32) {
 #pragma unroll
-      for (int at = 0; at < NDT; ++at) store4(hT + at * 16 + 4 * lg, h[at]);
+      for (int i = 0; i < NDH; ++i) store4(hT + (ks * NDH + i) * 16 + 4 * lg, h[i]);
     } else {
 #pragma unroll
       for (int p = 0; p < NDT / 2; ++p)
@@ -909,7 +929,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
     // loop is outermost, so consecutive MFMAs never wait on each other, and the
     // next k-step's W operands are read while this one's MFMAs run.
     {
-      constexpr int NKD = F32 ? NDT : NDT / 2;   // k-steps over d
+      constexpr int NKD = F32 ? NDH : NDT / 2;   // k-steps over this wave's d
       Op hb[NKD];
 #pragma unroll
       for (int kk = 0; kk < NKD; ++kk) {
@@ -918,7 +938,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
       }
       auto wop = [&](int it, int kk) __attribute__((always_inline)) {
         const int r = it * 16 + li;
-        if constexpr (F32) return load4f(&sW[swz(r, kk * 16 + 4 * lg, D)]);
+        if constexpr (F32) return load4f(&sW[swz(r, (ks * NDH + kk) * 16 + 4 * lg, D)]);
         else return op_load<T>(&sW[swz(r, kk * 32 + 8 * lg, D)]);
       };
       f32x4 acc[NB];
@@ -939,14 +959,28 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
 #pragma unroll
         for (int it = 0; it < NB; ++it) wc[it] = wn[it];
       }
+      if constexpr (KS > 1) {
+        // exchange the halves; both waves form v_new in the same order
 #pragma unroll
-      for (int it = 0; it < NB; ++it) vn[it] -= acc[it];
+        for (int it = 0; it < NB; ++it) sX[(wv * NB + it) * 64 + lane] = acc[it];
+        lds_barrier();  // X(c)
+        const int pw = (1 - ks) * NW + wcol;
+#pragma unroll
+        for (int it = 0; it < NB; ++it) {
+          const f32x4 o = sX[(pw * NB + it) * 64 + lane];
+          vn[it] -= ks == 0 ? acc[it] + o : o + acc[it];
+        }
+      } else {
+#pragma unroll
+        for (int it = 0; it < NB; ++it) vn[it] -= acc[it];
+      }
     }
     T* vT = a.VnT + cid * D * BT + (size_t)col * BT;
     if (!write_tiles) {
     } else if constexpr (F32) {
 #pragma unroll
-      for (int it = 0; it < NB; ++it) store4(vT + it * 16 + 4 * lg, vn[it]);
+      for (int it = ks * (NB / KS); it < (ks + 1) * (NB / KS); ++it)
+        store4(vT + it * 16 + 4 * lg, vn[it]);
     } else {
 #pragma unroll
       for (int p = 0; p < NB / 2; ++p)
@@ -960,20 +994,20 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
       constexpr int NKT = F32 ? NB : NB / 2;     // k-steps over t
       constexpr bool AHEAD = NDT <= 8;
 #pragma unroll
-      for (int at = 0; at < NDT; ++at) {
-        const f32x4 egl = load4f(eglc + at * 16 + 4 * lg);
+      for (int i = 0; i < NDH; ++i) {
+        const f32x4 egl = load4f(eglc + (ks * NDH + i) * 16 + 4 * lg);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) h[at][r] *= egl[r];
+        for (int r = 0; r < 4; ++r) h[i][r] *= egl[r];
       }
-      auto kop = [&](int at, int kk) __attribute__((always_inline)) {
-        const int r = at * 16 + li;
+      auto kop = [&](int i, int kk) __attribute__((always_inline)) {
+        const int r = (ks * NDH + i) * 16 + li;
         if constexpr (F32) return load4f(&sK[swz(r, kk * 16 + 4 * lg, BT)]);
         else return op_load<T>(&sK[swz(r, kk * 32 + 8 * lg, BT)]);
       };
-      Op kc[NDT], kn[AHEAD ? NDT : 1];
+      Op kc[NDH], kn[AHEAD ? NDH : 1];
       if constexpr (AHEAD) {
 #pragma unroll
-        for (int at = 0; at < NDT; ++at) kc[at] = kop(at, 0);
+        for (int at = 0; at < NDH; ++at) kc[at] = kop(at, 0);
       }
 #pragma unroll
       for (int kk = 0; kk < NKT; ++kk) {
@@ -983,20 +1017,20 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
         if constexpr (AHEAD) {
           if (kk + 1 < NKT) {
 #pragma unroll
-            for (int at = 0; at < NDT; ++at) kn[at] = kop(at, kk + 1);
+            for (int at = 0; at < NDH; ++at) kn[at] = kop(at, kk + 1);
           }
 #pragma unroll
-          for (int at = 0; at < NDT; ++at) mma(h[at], kc[at], vb);
+          for (int at = 0; at < NDH; ++at) mma(h[at], kc[at], vb);
 #pragma unroll
-          for (int at = 0; at < NDT; ++at) kc[at] = kn[at];
+          for (int at = 0; at < NDH; ++at) kc[at] = kn[at];
         } else {
 #pragma unroll
-          for (int at = 0; at < NDT; ++at) mma(h[at], kop(at, kk), vb);
+          for (int at = 0; at < NDH; ++at) mma(h[at], kop(at, kk), vb);
         }
       }
       if (!mslice) {
 #pragma unroll
-        for (int at = 0; at < NDT; ++at)
+        for (int at = 0; at < NDH; ++at)
 #pragma unroll
           for (int r2 = 0; r2 < 4; ++r2) h[at][r2] = sanitize(h[at][r2]);
       }
@@ -1019,9 +1053,10 @@ __global__ void __launch_bounds__(64 * (NW + NP)) fwd_state(StateArgs<T> a) {
               : (sg == a.S - 1) ? a.h_final + (size_t)bh * D * D : nullptr;
   if (hout) {
 #pragma unroll
-    for (int at = 0; at < NDT; ++at)
+    for (int i = 0; i < NDH; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) hout[(size_t)(at * 16 + 4 * lg + r) * D + col] = h[at][r];
+      for (int r = 0; r < 4; ++r)
+        hout[(size_t)((ks * NDH + i) * 16 + 4 * lg + r) * D + col] = h[i][r];
   }
 }
 
@@ -1237,6 +1272,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   launch_mark(st);
   constexpr int SW = 2;  // compute waves (16 value columns each) per state workgroup
   constexpr int SP = 2;  // producer waves
+  constexpr int SK = state_ksplit<T, D>();   // compute waves per column slice
   constexpr int NVS = D / (16 * SW);
   const size_t BH = (size_t)B * H;
   const int S = S_ws;
@@ -1245,26 +1281,26 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     StateArgs<T> va{W,  UT,      KgT,     GL,     h0,           N,  vl->nseq, 0, 0, nullptr,
                     nullptr, HT, VnT, h_final, vl->cu_chunks, H};
     if (vl->nseq > 0)
-      hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * vl->nseq * NVS),
-                         dim3(64 * (SW + SP)), 0, st, va);
+      hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * vl->nseq * NVS),
+                         dim3(64 * (SW * SK + SP)), 0, st, va);
   } else if (S > 1) {
     const int Lseg = (N + S - 1) / S;
     float* seg = reinterpret_cast<float*>(ws + L.SEG);          // [bh][S][2][D][D]
     float* hin = seg + BH * S * 2 * (size_t)D * D;               // [bh][S][D][D]
     StateArgs<T> sum{W, UT, KgT, GL, h0, N, S, Lseg, 1, nullptr, seg, HT, VnT, h_final,
                      nullptr, H};
-    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * S * 2 * NVS),
-                       dim3(64 * (SW + SP)), 0, st, sum);
+    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * S * 2 * NVS),
+                       dim3(64 * (SW * SK + SP)), 0, st, sum);
     hipLaunchKernelGGL((seg_combine<D>), dim3(BH * (D / 16)), dim3(256), 0, st, seg, h0, hin,
                        S);
     StateArgs<T> fin{W, UT, KgT, GL, h0, N, S, Lseg, 0, hin, nullptr, HT, VnT, h_final,
                      nullptr, H};
-    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * S * NVS), dim3(64 * (SW + SP)),
+    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * S * NVS), dim3(64 * (SW * SK + SP)),
                        0, st, fin);
   } else {
     StateArgs<T> sa{W, UT, KgT, GL, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT, h_final,
                     nullptr, H};
-    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP>), dim3(BH * NVS), dim3(64 * (SW + SP)), 0,
+    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * NVS), dim3(64 * (SW * SK + SP)), 0,
                        st, sa);
   }
   launch_mark(st);
