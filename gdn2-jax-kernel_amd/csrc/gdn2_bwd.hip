@@ -116,9 +116,22 @@ struct BStateArgs {
 // global loads.  Both products read their tile transposed: one 4-byte (2-byte
 // for bfloat16 residuals, chained column order) LDS read per element, which
 // the XOR swizzle of the 16-byte chunks keeps free of bank conflicts.
-template <typename T, int BT, int D, int NW, int NP>
-__global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
+//
+// K-split (KS = 2, float32 residuals), as in fwd_state: two compute waves per
+// 16-column slice, each holding half of dh's rows; the halves of kg dh are
+// exchanged through LDS (barrier X, after B).  The exchange buffer takes the
+// place of the qdot gather: each compute wave then loads its own 16-byte qdot
+// pieces (four per step) straight from global memory one step ahead, hitting
+// L2 behind the producers' touch.
+template <typename T, int D>
+constexpr int bstate_ksplit() { return (sizeof(T) == 4 && D <= 128) ? 2 : 1; }
+
+template <typename T, int BT, int D, int NW, int NP, int KS>
+__global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a) {
   constexpr int NB = BT / 16, NDT = D / 16;
+  constexpr int NCW = NW * KS, NDH = NDT / KS;
+  static_assert(KS == 1 || (sizeof(T) == 4 && NDT % KS == 0 && NB % KS == 0),
+                "K-split: float32 only");
   constexpr int NVS = D / (16 * NW);
   constexpr int WBYTES = BT * D * (int)sizeof(T);
   constexpr int BUF = 2 * WBYTES;
@@ -127,7 +140,8 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
   __shared__ __align__(16) char sbuf0[BUF];
   __shared__ __align__(16) char sbuf1[BUF];
   __shared__ __align__(16) f32x4 sDV[NW * NB * 64];    // dvp^T in compute-lane order
-  __shared__ __align__(16) f32x4 sQD[NW * NDT * 64];   // (scale qg^T do)^T, same
+  __shared__ __align__(16) f32x4 sQD[KS == 1 ? NW * NDT * 64 : 1];   // (scale qg^T do)^T, same
+  __shared__ __align__(16) f32x4 sX[KS > 1 ? NCW * NB * 64 : 1];     // K-split partials of kg dh
   __shared__ __align__(16) float sGL0[D];
   __shared__ __align__(16) float sGL1[D];
   __shared__ __align__(16) float sJunk[64];
@@ -163,14 +177,14 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
   // step i works on chunk c0 + n-1-i
   auto chunk_id = [&](int i) { return (size_t)bh * a.N + c0 + (n - 1 - i); };
 
-  if (wv >= NW) {
+  if (wv >= NCW) {
     // ---- producers ----------------------------------------------------------
     constexpr int ROWB_W = D * (int)sizeof(T), ROWB_K = BT * (int)sizeof(T);
     constexpr int WPIECES = WBYTES / 1024;
     constexpr int PP = PIECES / NP;
     static_assert(PIECES % NP == 0 && (NW * NB) % NP == 0 && (NW * NDT) % NP == 0,
                   "work must split evenly");
-    const int p = wv - NW;
+    const int p = wv - NCW;
     auto issue = [&](int i, char* base, float* gl) __attribute__((always_inline)) {
       const size_t cid = chunk_id(i);
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
@@ -200,11 +214,13 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
         lds_dma16(dsrc + (size_t)w * 16 * BT + it * 16, &sDV[q * 64]);
       }
       // (scale qg^T do)^T[col][d]: wave w, tile at -> sQD[(w NDT + at) 64 + lane]
-      const float* qsrc = a.QDOT + cid * D * D + (size_t)(vs * 16 * NW + li) * D + 4 * lg;
+      if constexpr (KS == 1) {
+        const float* qsrc = a.QDOT + cid * D * D + (size_t)(vs * 16 * NW + li) * D + 4 * lg;
 #pragma unroll
-      for (int j = 0; j < NW * NDT / NP; ++j) {
-        const int q = j * NP + p, w = q / NDT, at = q % NDT;
-        lds_dma16(qsrc + (size_t)w * 16 * D + at * 16, &sQD[q * 64]);
+        for (int j = 0; j < NW * NDT / NP; ++j) {
+          const int q = j * NP + p, w = q / NDT, at = q % NDT;
+          lds_dma16(qsrc + (size_t)w * 16 * D + at * 16, &sQD[q * 64]);
+        }
       }
     };
     constexpr int LINE = 128;
@@ -260,19 +276,24 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
       if (i + 1 < n) {
         issue(i + 1, sbuf1, sGL1);
         if (i + 2 < n) touch(i + 2);
+        if constexpr (KS > 1) barrier();  // X(i)
         wait_step(i + 1);
         exp_gl(sGL1);
         barrier();  // A(i+1)
         barrier();  // B(i+1)
         if (i + 2 < n) issue(i + 2, sbuf0, sGL0);
         if (i + 3 < n) touch(i + 3);
+        if constexpr (KS > 1) barrier();  // X(i+1)
+      } else {
+        if constexpr (KS > 1) barrier();  // X(i)
       }
     }
     return;
   }
 
   // ---- compute waves ----------------------------------------------------------
-  const int col = vs * 16 * NW + wv * 16 + li;
+  const int wcol = wv % NW, ks = wv / NW;   // column slice, k-half (K-split)
+  const int col = vs * 16 * NW + wcol * 16 + li;
   // element (row r, logical column c) of a swizzled tile with `re` elements per row
   auto elem = [](const T* tile, int r, int c, int re) -> float {
     constexpr int EPC = 16 / sizeof(T);
@@ -283,54 +304,105 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
     return to_f(tile[r * re + ((j ^ (r & m)) * EPC) + (sc % EPC)]);
   };
 
-  f32x4 dh[NDT];
+  f32x4 dh[NDH];   // row tiles at = ks NDH + j of this slice's dh
   if (a.dh_final) {
 #pragma unroll
-    for (int at = 0; at < NDT; ++at)
+    for (int j = 0; j < NDH; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        dh[at][r] = sanitize(a.dh_final[(st_idx * D + at * 16 + 4 * lg + r) * D + col]);
+        dh[j][r] = sanitize(
+            a.dh_final[(st_idx * D + (ks * NDH + j) * 16 + 4 * lg + r) * D + col]);
   } else {
 #pragma unroll
-    for (int at = 0; at < NDT; ++at) dh[at] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NDH; ++j) dh[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // K-split: this wave's qdot pieces, loaded one step ahead
+  f32x4 qnext[KS > 1 ? NDH : 1];
+  auto load_qd = [&](int i) __attribute__((always_inline)) {
+    const float* qsrc = a.QDOT + chunk_id(i) * D * D + (size_t)col * D + 4 * lg;
+#pragma unroll
+    for (int j = 0; j < NDH; ++j) qnext[j] = load4f(qsrc + (ks * NDH + j) * 16);
+  };
+  if constexpr (KS > 1) {
+    if (n > 0) load_qd(0);
   }
 
   auto step = [&](int i, const char* cur, const float* eglc) __attribute__((always_inline)) {
     const size_t cid = chunk_id(i);
-    __syncthreads();  // A(i)
-    f32x4 dvn[NB], qd[NDT];
+    // K-split: LDS-only barriers, so the qdot loads of the next step stay in
+    // flight (the producers order their DMA with their own vmcnt waits)
+    if constexpr (KS > 1) lds_barrier(); else __syncthreads();  // A(i)
+    f32x4 dvn[NB], qd[NDH];
 #pragma unroll
-    for (int it = 0; it < NB; ++it) dvn[it] = sDV[(wv * NB + it) * 64 + lane];
+    for (int it = 0; it < NB; ++it) dvn[it] = sDV[(wcol * NB + it) * 64 + lane];
+    if constexpr (KS > 1) {
 #pragma unroll
-    for (int at = 0; at < NDT; ++at) qd[at] = sQD[(wv * NDT + at) * 64 + lane];
-    __syncthreads();  // B(i)
+      for (int j = 0; j < NDH; ++j) qd[j] = qnext[j];
+      if (i + 1 < n) load_qd(i + 1);
+    } else {
+#pragma unroll
+      for (int at = 0; at < NDT; ++at) qd[at] = sQD[(wv * NDT + at) * 64 + lane];
+    }
+    if constexpr (KS > 1) lds_barrier(); else __syncthreads();  // B(i)
     const T* sW = reinterpret_cast<const T*>(cur);
     const T* sK = reinterpret_cast<const T*>(cur + WBYTES);
 
     float* dht = a.DHT + cid * D * D + (size_t)col * D;
 #pragma unroll
-    for (int at = 0; at < NDT; ++at) store4(dht + at * 16 + 4 * lg, dh[at]);
+    for (int j = 0; j < NDH; ++j) store4(dht + (ks * NDH + j) * 16 + 4 * lg, dh[j]);
 
     // dv_new = dvp + kg dh: X[t][d] = kg^T[d][t]
+    if constexpr (KS > 1) {
+      // this wave's half of kg dh; the NB row blocks are independent accumulators
+      f32x4 part[NB];
 #pragma unroll
-    for (int it = 0; it < NB; ++it) {
+      for (int it = 0; it < NB; ++it) part[it] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int at = 0; at < NDT; ++at) {
-        f32x4 x;
+      for (int j = 0; j < NDH; ++j) {
+        const int at = ks * NDH + j;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
-        mma(dvn[it], x, dh[at]);
+        for (int it = 0; it < NB; ++it) {
+          f32x4 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
+          mma(part[it], x, dh[j]);
+        }
       }
+      // exchange the halves; both waves form dv_new in the same order
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dvn[it][r] = sanitize(dvn[it][r]);
+      for (int it = 0; it < NB; ++it) sX[(wv * NB + it) * 64 + lane] = part[it];
+      lds_barrier();  // X(i)
+      const int pw = (1 - ks) * NW + wcol;
+#pragma unroll
+      for (int it = 0; it < NB; ++it) {
+        const f32x4 o = sX[(pw * NB + it) * 64 + lane];
+        const f32x4 sum = ks == 0 ? part[it] + o : o + part[it];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dvn[it][r] = sanitize(dvn[it][r] + sum[r]);
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < NB; ++it) {
+#pragma unroll
+        for (int at = 0; at < NDT; ++at) {
+          f32x4 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
+          mma(dvn[it], x, dh[at]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dvn[it][r] = sanitize(dvn[it][r]);
+      }
     }
     float* dvo = a.DVNT + cid * D * BT + (size_t)col * BT;
 #pragma unroll
-    for (int it = 0; it < NB; ++it) store4(dvo + it * 16 + 4 * lg, dvn[it]);
+    for (int it = ks * (NB / KS); it < (ks + 1) * (NB / KS); ++it)
+      store4(dvo + it * 16 + 4 * lg, dvn[it]);
 
     // dh <- e^{gl} dh + qdot - W^T dv_new: X[d][t] = W[t][d]
 #pragma unroll
-    for (int at = 0; at < NDT; ++at) {
+    for (int j = 0; j < NDH; ++j) {
+      const int at = ks * NDH + j;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int it = 0; it < NB; ++it) {
@@ -341,7 +413,7 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
       }
       const f32x4 egl = load4f(eglc + at * 16 + 4 * lg);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dh[at][r] = sanitize(egl[r] * dh[at][r] + qd[at][r] - acc[r]);
+      for (int r = 0; r < 4; ++r) dh[j][r] = sanitize(egl[r] * dh[j][r] + qd[j][r] - acc[r]);
     }
   };
 
@@ -350,9 +422,10 @@ __global__ void __launch_bounds__(64 * (NW + NP)) bwd_state(BStateArgs<T> a) {
     if (i + 1 < n) step(i + 1, sbuf1, sGL1);
   }
 #pragma unroll
-  for (int at = 0; at < NDT; ++at)
+  for (int j = 0; j < NDH; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) a.dh0[(st_idx * D + at * 16 + 4 * lg + r) * D + col] = dh[at][r];
+    for (int r = 0; r < 4; ++r)
+      a.dh0[(st_idx * D + (ks * NDH + j) * 16 + 4 * lg + r) * D + col] = dh[j][r];
 }
 
 // ============================================================================
@@ -1128,10 +1201,11 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     // variable-length batch (B = 1): one scan unit per (head, sequence)
     BStateArgs<T> sa{(const T*)fW, (const T*)fKgT, fGL, buf(B_DVPT), buf(B_QDOT), dh_final, N,
                      buf(B_DHT), buf(B_DVNT), dh0, cu_chunks, cu_chunks ? nseq : 1, H};
-    constexpr int BW = 2, BP = 2;  // compute and producer waves per scan workgroup
+    constexpr int BW = 2, BP = 2;  // column slices and producer waves per scan workgroup
+    constexpr int BK = bstate_ksplit<T, D>();   // compute waves per column slice
     const size_t units = cu_chunks ? (size_t)H * nseq : (size_t)B * H;
-    hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP>), dim3(units * (D / (16 * BW))),
-                       dim3(64 * (BW + BP)), 0, st, sa);
+    hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP, BK>), dim3(units * (D / (16 * BW))),
+                       dim3(64 * (BW * BK + BP)), 0, st, sa);
     launch_mark(st);
     if (NC > 0) {
       // B3, one fused kernel
