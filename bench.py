@@ -117,8 +117,9 @@ def time_train(gp, xs, steps, warmup):
     dout = torch.randn((B, T, H, D), generator=gen, device="cuda")
 
     def step():
+        # gradients returned as jax.grad returns them (no accumulation into .grad)
         out, hf = gp.gdn2_pallas_forward_trainable(*xs, scale)
-        torch.autograd.backward([out], [dout])
+        torch.autograd.grad([out], xs, [dout])
 
     for _ in range(warmup):
         step()
