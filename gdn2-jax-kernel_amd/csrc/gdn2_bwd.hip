@@ -969,7 +969,21 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
       sKH[t * LD1 + ch] = kv[x] * __expf(sTot[I * GP + ch] - loc[x]);
     }
   }
-  __syncthreads();
+  // operands of the chain rule below, loaded now so that they arrive while the
+  // products run
+  const size_t wrow_t = ((size_t)cid * BT + t) * D + ch0;
+  f32x4 pv[NDT], pw[NDT], pdqg[NDT], pdkg[NDT], pdkbd[NDT], pdwv[NDT];
+#pragma unroll
+  for (int j = 0; j < NDT; ++j) {
+    const int c0 = j * 16 + lg * 4;
+    pv[j] = load4f(a.v + rowo + c0);
+    pw[j] = load4f(a.w + rowo + c0);
+    pdqg[j] = load4f(a.DQG + wrow_t + c0);
+    pdkg[j] = load4f(a.DKG + wrow_t + c0);
+    pdkbd[j] = load4f(a.DKBD + wrow_t + c0);
+    pdwv[j] = load4f(a.DWV + wrow_t + c0);
+  }
+  lds_barrier();
 
   // ---- off-diagonal pairs on MFMA --------------------------------------------
 #pragma unroll
@@ -1078,15 +1092,13 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   // score gradients of its own rows, written by its own lanes above.  dgc is summed
   // from each token to the block end by a row scan; the block totals cross the
   // waves through LDS.
-  const size_t wrow_t = ((size_t)cid * BT + t) * D + ch0;
 #pragma unroll
   for (int j = 0; j < NDT; ++j) {
     const int c0 = j * 16 + lg * 4;
     const f32x4 qv = load4f(a.q + rowo + c0), kv = load4f(a.k + rowo + c0),
-                vv = load4f(a.v + rowo + c0), wvv = load4f(a.w + rowo + c0),
                 bv = load4f(a.b + rowo + c0);
-    const f32x4 dqg = load4f(a.DQG + wrow_t + c0), dkg = load4f(a.DKG + wrow_t + c0),
-                dkbd = load4f(a.DKBD + wrow_t + c0), dwv = load4f(a.DWV + wrow_t + c0);
+    const f32x4 vv = pv[j], wvv = pw[j], dqg = pdqg[j], dkg = pdkg[j], dkbd = pdkbd[j],
+                dwv = pdwv[j];
     const f32x4 gq = load4f(&sAQ[t * LD1 + c0]), gbk = load4f(&sABK[t * LD1 + c0]),
                 gk = load4f(&sKH[t * LD1 + c0]);
     f32x4 lc = load4f(a.g + rowo + c0);   // in-block cumsum again, as at the start
