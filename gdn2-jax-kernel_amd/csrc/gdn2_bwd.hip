@@ -9,7 +9,7 @@
 //        dh = e^{gl} dh' + scale qg^T do - W^T dv_new                         serial)
 //   B3   dqg = scale do h^T, dW = -dv_new h^T, dkg = v_new dh'^T,
 //        dA = dW (b k e^gc)^T + dv_new (w v)^T, d(bke^gc) = A^T dW, d(wv) = A^T dv_new,
-//        dAkk = -(A^T dA A^T) . strict                                        (bwd_wy)
+//        dv = d(wv) w, dw = d(wv) v, dAkk = -(A^T dA A^T) . strict             (bwd_wy)
 //   B4   gradients of Aqk/Akk wrt q, k, b k, gc, then the chain rule through
 //        the exponentials (B3 tail) and the reverse cumsum of dgc (B5)       (gram_bwd)
 
@@ -556,7 +556,7 @@ __global__ void __launch_bounds__(256) bwd_b2(B2Args<T> a) {
 // element-wise b k e^{gc}, w v, with dW, dA and dA A^T kept on chip:
 //   dqg  = scale do h^T              dW    = -dv_new h^T
 //   dkg  = v_new dh'^T               dA    = (dW (b k e^gc)^T + dv_new (w v)^T) . strict
-//   d(bke^gc) = A^T dW               d(wv) = A^T dv_new
+//   d(bke^gc) = A^T dW               d(wv) = A^T dv_new -> dv = d(wv) w, dw = d(wv) v
 //   dAkk = -(A^T (dA A^T)) . strict
 // Stored operands per chunk: do in (B,T,H,D) rows; h^T, dh'^T as [e][d]; v_new^T,
 // dv_new^T as [e][t]; A as [t][s].  One workgroup per chunk; wave w owns the
@@ -579,8 +579,9 @@ struct WyArgs {
   const float* DVNT;  // dv_new^T [cid][D][BT]
   int T_len, H, N;
   float scale;
-  float *DQG, *DKG, *DKBD, *DWV, *DAKK;  // [cid][BT][D] x 4, [cid][BT][BT]
+  float *DQG, *DKG, *DKBD, *DAKK;  // [cid][BT][D] x 3, [cid][BT][BT]
   float* SDH;         // [cid][D]: sum_e dh'[d][e] h[d][e] (the g_last term of dgc)
+  T *dv, *dw;         // gradients (B,T,H,D): d(wv) w, d(wv) v (gdn2_bwd.py:204-205)
 };
 
 template <typename T, typename TG, int D>
@@ -805,14 +806,26 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
         mma(awv[nt], x, rowop(sR1, LDV, nt * 16, kt * 16));   // dv_new^T[e][t]
       }
     }
+    // dv = d(wv) w, dw = d(wv) v: w and v re-read in this layout (L2: step 3
+    // read them), so the element-wise pass does not need them
     float* dkbd = a.DKBD + (size_t)cid * BT * D;
-    float* dwv = a.DWV + (size_t)cid * BT * D;
+    float wl[NDT][4], vl[NDT][4];
 #pragma unroll
     for (int nt = 0; nt < NDT; ++nt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        const size_t o = tok0 + (size_t)orow(r) * HD + nt * 16 + li;
+        wl[nt][r] = to_f(a.w[o]);
+        vl[nt][r] = to_f(a.v[o]);
+      }
+#pragma unroll
+    for (int nt = 0; nt < NDT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const size_t o = tok0 + (size_t)orow(r) * HD + nt * 16 + li;
         dkbd[orow(r) * D + nt * 16 + li] = akb[nt][r];
-        dwv[orow(r) * D + nt * 16 + li] = awv[nt][r];
+        a.dv[o] = from_f<T>(sanitize(awv[nt][r] * wl[nt][r]));
+        a.dw[o] = from_f<T>(sanitize(awv[nt][r] * vl[nt][r]));
       }
   }
   {
@@ -870,20 +883,21 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 // Every wave does three block pairs per 16-channel slice, so a barrier after each
 // slice frees that slice of AQ / ABK / Khat and RQ / RBK / RK take its place in LDS.
 // Diagonal blocks are summed per channel (one lane per channel), factorised around
-// the block's 8th token as in the forward.  The same lane then applies the chain
-// rule through the exponentials of qg, kg and b k e^gc (gdn2_bwd.py:186-210; dqg,
-// dkg, d(b k e^gc), d(w v) and sum_e dh' h come from bwd_wy) and the reverse cumsum
-// of dgc (gdn2_bwd.py:32-41): suffix sums inside the block, block totals across the
-// waves through LDS.  Wave w owns row block w (BT = 64).
+// the block's 8th token as in the forward, and added in place.  Then, one lane per
+// token and four channels per 16-byte access, the chain rule through the
+// exponentials of qg, kg and b k e^gc (gdn2_bwd.py:186-210; dqg, dkg, d(b k e^gc)
+// and sum_e dh' h come from bwd_wy, which also forms dv and dw) and the reverse
+// cumsum of dgc (gdn2_bwd.py:32-41): DPP suffix sums inside each 16-token block,
+// block totals across the waves through LDS.  Wave w owns row block w (BT = 64).
 // ============================================================================
 template <typename T, typename TG>
 struct GramArgs {
-  const T *q, *k, *v, *w, *b;
+  const T *q, *k, *b;
   const TG* g;
-  const float *DAQK, *DAKK, *SDH, *DQG, *DKG, *DKBD, *DWV;
+  const float *DAQK, *DAKK, *SDH, *DQG, *DKG, *DKBD;
   int T_len, H, N;
   float scale;
-  T *dq, *dk, *dv, *dw, *db;
+  T *dq, *dk, *db;
   TG* dg;
 };
 
@@ -972,16 +986,13 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   // operands of the chain rule below, loaded now so that they arrive while the
   // products run
   const size_t wrow_t = ((size_t)cid * BT + t) * D + ch0;
-  f32x4 pv[NDT], pw[NDT], pdqg[NDT], pdkg[NDT], pdkbd[NDT], pdwv[NDT];
+  f32x4 pdqg[NDT], pdkg[NDT], pdkbd[NDT];
 #pragma unroll
   for (int j = 0; j < NDT; ++j) {
     const int c0 = j * 16 + lg * 4;
-    pv[j] = load4f(a.v + rowo + c0);
-    pw[j] = load4f(a.w + rowo + c0);
     pdqg[j] = load4f(a.DQG + wrow_t + c0);
     pdkg[j] = load4f(a.DKG + wrow_t + c0);
     pdkbd[j] = load4f(a.DKBD + wrow_t + c0);
-    pdwv[j] = load4f(a.DWV + wrow_t + c0);
   }
   lds_barrier();
 
@@ -1088,7 +1099,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   }
 
   // ---- chain rule, lane = token t of block I, channels chan(x) -----------------
-  // (gdn2_bwd.py:186-210; dqg, dkg, dkbd, dwv come from bwd_wy).  Wave I reads the
+  // (gdn2_bwd.py:186-210; dqg, dkg, dkbd come from bwd_wy).  Wave I reads the
   // score gradients of its own rows, written by its own lanes above.  dgc is summed
   // from each token to the block end by a row scan; the block totals cross the
   // waves through LDS.
@@ -1097,8 +1108,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
     const int c0 = j * 16 + lg * 4;
     const f32x4 qv = load4f(a.q + rowo + c0), kv = load4f(a.k + rowo + c0),
                 bv = load4f(a.b + rowo + c0);
-    const f32x4 vv = pv[j], wvv = pw[j], dqg = pdqg[j], dkg = pdkg[j], dkbd = pdkbd[j],
-                dwv = pdwv[j];
+    const f32x4 dqg = pdqg[j], dkg = pdkg[j], dkbd = pdkbd[j];
     const f32x4 gq = load4f(&sAQ[t * LD1 + c0]), gbk = load4f(&sABK[t * LD1 + c0]),
                 gk = load4f(&sKH[t * LD1 + c0]);
     f32x4 lc = load4f(a.g + rowo + c0);   // in-block cumsum again, as at the start
@@ -1114,7 +1124,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
         pre[e] += m < I ? tm[e] : 0.f;
       }
     }
-    f32x4 odq, odk, odb, odw, odv, suf;
+    f32x4 odq, odk, odb, suf;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float gc = pre[e] + lc[e];
@@ -1123,8 +1133,6 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
       odq[e] = sanitize(dqg[e] * eg + gq[e]);
       odk[e] = sanitize(dkbd[e] * bv[e] * eg + dkg[e] * ekg + gk[e] + gbk[e] * bv[e]);
       odb[e] = sanitize(dkbd[e] * kv[e] * eg + gbk[e] * kv[e]);
-      odw[e] = sanitize(dwv[e] * vv[e]);
-      odv[e] = sanitize(dwv[e] * wvv[e]);
       const float dgc = dkbd[e] * bv[e] * kv[e] * eg + dqg[e] * qv[e] * eg - dkg[e] * kgv +
                         qv[e] * gq[e] + bv[e] * kv[e] * gbk[e] - kv[e] * gk[e];
       suf[e] = row_suffix16(dgc);
@@ -1138,8 +1146,6 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
     store4(a.dq + rowo + c0, odq);
     store4(a.dk + rowo + c0, odk);
     store4(a.db + rowo + c0, odb);
-    store4(a.dw + rowo + c0, odw);
-    store4(a.dv + rowo + c0, odv);
   }
   lds_barrier();
   // dg[t] = sum_{s >= t} dgc[s] + sum_t dkg kg + e^{gl} sum_e dh' h  (the last two
@@ -1224,17 +1230,16 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
       WyArgs<T, TG> wa{(const T*)k,  (const T*)w,     (const T*)v,  (const T*)b, (const TG*)g,
                        dout,         (const T*)fHT,   (const T*)fVnT,
                        reinterpret_cast<const float*>(fA), buf(B_DHT), buf(B_DVNT),
-                       T_len, H, N, scale, buf(B_DQG), buf(B_DKG), buf(B_DKBD), buf(B_DWV),
-                       buf(B_DAKK), buf(B_SDH)};
+                       T_len, H, N, scale, buf(B_DQG), buf(B_DKG), buf(B_DKBD),
+                       buf(B_DAKK), buf(B_SDH), (T*)dv, (T*)dw};
       hipLaunchKernelGGL((bwd_wy<T, TG, D>), dim3(NC), dim3(256), 0, st, wa);
       launch_mark(st);
       // B4 + B3 elementwise tail + B5
-      GramArgs<T, TG> gr{(const T*)q,  (const T*)k,  (const T*)v,  (const T*)w,
-                         (const T*)b,  (const TG*)g, buf(B_DAQK),  buf(B_DAKK),
-                         buf(B_SDH),   buf(B_DQG),   buf(B_DKG),   buf(B_DKBD),
-                         buf(B_DWV),   T_len,        H,            N,
-                         scale,        (T*)dq,       (T*)dk,       (T*)dv,
-                         (T*)dw,       (T*)db,       (TG*)dg};
+      GramArgs<T, TG> gr{(const T*)q,  (const T*)k,  (const T*)b,  (const TG*)g,
+                         buf(B_DAQK),  buf(B_DAKK),  buf(B_SDH),   buf(B_DQG),
+                         buf(B_DKG),   buf(B_DKBD),  T_len,        H,
+                         N,            scale,        (T*)dq,       (T*)dk,
+                         (T*)db,       (TG*)dg};
       hipLaunchKernelGGL((gram_bwd<T, TG, D>), dim3(NC * (D / gram_panel())), dim3(256), 0,
                          st, gr);
       launch_mark(st);

@@ -21,7 +21,7 @@
 // Backward workspace (all f32, chunk-major, one region per name):
 //   DAQK [BT][BT] dAqk (causal)      DVPT [D][BT] (Aqk^T do)^T    QDOT [D][D] (scale qg^T do)^T
 //   DHT  [D][D]  dh_{c+1}^T           DVNT [D][BT] dv_new^T
-//   DQG, DKG, DKBD, DWV [BT][D]       DAKK [BT][BT]
+//   DQG, DKG, DKBD [BT][D]            DAKK [BT][BT]
 //   SDH  [D]      sum_e dh_{c+1}[d][e] h_c[d][e]
 #pragma once
 
@@ -97,8 +97,7 @@ inline int state_segments(long long BH, int N, int D, int forced) {
 namespace gdn2 {
 
 enum BwdBuf {
-  B_DAQK, B_DVPT, B_QDOT, B_DHT, B_DVNT, B_DQG, B_DKG, B_DKBD, B_DWV, B_DAKK,
-  B_SDH, B_COUNT
+  B_DAQK, B_DVPT, B_QDOT, B_DHT, B_DVNT, B_DQG, B_DKG, B_DKBD, B_DAKK, B_SDH, B_COUNT
 };
 
 struct BwdLayout {
@@ -110,7 +109,7 @@ struct BwdLayout {
 inline BwdLayout bwd_layout(size_t nchunks, int BT, int D) {
   BwdLayout L;
   const size_t tt = (size_t)BT * BT, td = (size_t)BT * D, dd = (size_t)D * D;
-  const size_t per[B_COUNT] = {tt, td, dd, dd, td, td, td, td, td, tt, (size_t)D};
+  const size_t per[B_COUNT] = {tt, td, dd, dd, td, td, td, td, tt, (size_t)D};
   size_t off = 0;
   for (int i = 0; i < B_COUNT; ++i) {
     L.off[i] = off;
