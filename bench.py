@@ -132,14 +132,15 @@ def time_train(gp, xs, steps, warmup):
 
 
 # Algorithmic MFMA flops per chunk of the float32 training kernels (chunk 64,
-# D = 128; masked triangular products counted in full, as the kernels run them):
-#   bwd_b2:    dAqk, Aqk^T do (2 BT BT D each), qg^T do (2 D D BT)
+# D = 128; products counted as the kernels run them):
+#   bwd_b2:    dAqk, Aqk^T do (2 BT BT D each, only the 10 of 16 16x16 blocks on or
+#              below the diagonal), qg^T do (2 D D BT)
 #   bwd_state: kg dh and W^T dv_new per chunk (2 BT D D each)
 #   bwd_wy:    three (BT, D, D), two (BT, BT, D), two (BT, D, BT), two (BT, BT, BT)
 TRAIN_CHUNK = 64
 _C = TRAIN_CHUNK
 TRAIN_FLOPS = {
-    "bwd_b2": 2 * 2 * _C * _C * D + 2 * D * D * _C,
+    "bwd_b2": 2 * 2 * _C * _C * D * (_C // 16 + 1) // (2 * (_C // 16)) + 2 * D * D * _C,
     "bwd_state": 2 * 2 * _C * D * D,
     "bwd_wy": 3 * 2 * _C * D * D + 2 * 2 * _C * _C * D + 2 * 2 * _C * D * _C + 2 * 2 * _C ** 3,
 }

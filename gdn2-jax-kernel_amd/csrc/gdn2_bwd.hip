@@ -459,7 +459,8 @@ __global__ void __launch_bounds__(256) bwd_b2(B2Args<T> a) {
   __shared__ __align__(16) float sV[D * LDV];
   __shared__ __align__(16) float sA[BT * LDA];
   __shared__ __align__(16) float sQ[BT * LDQ];
-  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: MFMA under branches
   const int cid = blockIdx.x;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
   const size_t HD = (size_t)a.H * D;
@@ -486,39 +487,46 @@ __global__ void __launch_bounds__(256) bwd_b2(B2Args<T> a) {
     stage_load(s2, mV, (size_t)cid * D * BT, D, BT, tid);
     stage_store(sDo, LDO, s1, mDo, BT, D, 0, 0, false, tid);
     stage_store(sV, LDV, s2, mV, D, BT, 0, 0, false, tid);
+    // qg and Aqk are in flight while dAqk is formed (LDS-only barrier)
     stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
     stage_load(s2, mA, (size_t)cid * BT * BT, BT, BT, tid);
+    lds_barrier();
+    // dAqk[t][s] = sum_e do[t][e] v_new[s][e], s <= t: column blocks right of
+    // the own row block are zero and not formed
+    {
+      f32x4 acc[NKT];
+#pragma unroll
+      for (int st = 0; st < NKT; ++st) acc[st] = z4;
+#pragma unroll
+      for (int kg = 0; kg < NDT; ++kg) {
+        const f32x4 x = rowop(sDo, LDO, wv * 16, kg * 16);
+#pragma unroll
+        for (int st = 0; st < NKT; ++st)
+          if (st <= wv) mma(acc[st], x, colop(sV, LDV, kg * 16, st * 16));
+      }
+      float* o = a.DAQK + (size_t)cid * BT * BT;
+#pragma unroll
+      for (int st = 0; st < NKT; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = wv * 16 + 4 * lg + r, s2 = st * 16 + li;
+          o[row * BT + s2] = s2 <= row ? acc[st][r] : 0.f;
+        }
+    }
     stage_store(sQ, LDQ, s1, mQ, BT, D, 0, 0, false, tid);
     stage_store(sA, LDA, s2, mA, BT, BT, 0, 0, false, tid);
   }
-  __syncthreads();
-  // dAqk[t][s] = sum_e do[t][e] v_new[s][e], s <= t
-  {
-    f32x4 acc[NKT];
-#pragma unroll
-    for (int st = 0; st < NKT; ++st) acc[st] = z4;
-#pragma unroll
-    for (int kg = 0; kg < NDT; ++kg) {
-      const f32x4 x = rowop(sDo, LDO, wv * 16, kg * 16);
-#pragma unroll
-      for (int st = 0; st < NKT; ++st) mma(acc[st], x, colop(sV, LDV, kg * 16, st * 16));
-    }
-    float* o = a.DAQK + (size_t)cid * BT * BT;
-#pragma unroll
-    for (int st = 0; st < NKT; ++st)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = wv * 16 + 4 * lg + r, s2 = st * 16 + li;
-        o[row * BT + s2] = s2 <= row ? acc[st][r] : 0.f;
-      }
-  }
-  // dvp^T[e][s] = sum_t Aqk[t][s] do[t][e]: rows s of the own block, stored as [e][s]
+  lds_barrier();
+  // dvp^T[e][s] = sum_t Aqk[t][s] do[t][e]: rows s of the own block, stored as
+  // [e][s]; Aqk[t][s] = 0 for t < s, so token blocks before the own one add nothing
+  // (with dAqk's skipped blocks: 5 of 8 block-products per wave, on every wave)
   {
     f32x4 acc[NDT];
 #pragma unroll
     for (int nt = 0; nt < NDT; ++nt) acc[nt] = z4;
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
+      if (kt < wv) continue;
       const f32x4 x = colop(sA, LDA, kt * 16, wv * 16);      // Aqk^T rows s, k = t
 #pragma unroll
       for (int nt = 0; nt < NDT; ++nt) mma(acc[nt], x, colop(sDo, LDO, kt * 16, nt * 16));
