@@ -949,39 +949,45 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   auto chan = [&](int x) { return (x / 4) * 16 + lg * 4 + (x % 4); };
   const int I = wv;
 
-  // stage the score gradients
-  {
-    const float* dq = a.DAQK + (size_t)cid * BT * BT;
-    const float* dk = a.DAKK + (size_t)cid * BT * BT;
-#pragma unroll
-    for (int u = 0; u < BT * BT / 4 / 256; ++u) {
-      const int i = tid + 256 * u, r = i / (BT / 4), cc = (i % (BT / 4)) * 4;
-      *reinterpret_cast<f32x4*>(&sDQK[r * LD2 + cc]) = load4f(dq + r * BT + cc);
-      *reinterpret_cast<f32x4*>(&sDKK[r * LD2 + cc]) = load4f(dk + r * BT + cc);
-    }
-  }
-  // in-block cumsum of g for own rows (lane li = token)
+  // score gradients, then this lane's g, q, k, b (token t, channels chan(x)), all
+  // in flight together; the staged tiles go to LDS first (they arrive first), the
+  // cumsum then waits for g alone while q, k, b arrive behind it
+  constexpr int SU = BT * BT / 4 / 256;
   const int t = I * 16 + li;
   const size_t rowo = tok0 + (size_t)t * HD;
   {
-    float loc[DQ];
+    const float* dq = a.DAQK + (size_t)cid * BT * BT;
+    const float* dk = a.DAKK + (size_t)cid * BT * BT;
+    f32x4 sq[SU], sk[SU];
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int i = tid + 256 * u, r = i / (BT / 4), cc = (i % (BT / 4)) * 4;
+      sq[u] = load4f(dq + r * BT + cc);
+      sk[u] = load4f(dk + r * BT + cc);
+    }
+    float loc[DQ], qv[DQ], kv[DQ], bv[DQ];
 #pragma unroll
     for (int j = 0; j < NDT; ++j) load_f<4>(a.g + rowo + j * 16 + lg * 4, &loc[j * 4]);
-#pragma unroll
-    for (int x = 0; x < DQ; ++x) loc[x] = row_scan16(loc[x]);
-    if (li == 15) {
-#pragma unroll
-      for (int x = 0; x < DQ; ++x) sTot[I * GP + chan(x)] = loc[x];
-    }
-    __syncthreads();
-    for (int i = tid; i < NB * GP; i += 256) sETot[i] = __expf(sTot[i]);
-    float qv[DQ], kv[DQ], bv[DQ];
 #pragma unroll
     for (int j = 0; j < NDT; ++j) {
       load_f<4>(a.q + rowo + j * 16 + lg * 4, &qv[j * 4]);
       load_f<4>(a.k + rowo + j * 16 + lg * 4, &kv[j * 4]);
       load_f<4>(a.b + rowo + j * 16 + lg * 4, &bv[j * 4]);
     }
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int i = tid + 256 * u, r = i / (BT / 4), cc = (i % (BT / 4)) * 4;
+      *reinterpret_cast<f32x4*>(&sDQK[r * LD2 + cc]) = sq[u];
+      *reinterpret_cast<f32x4*>(&sDKK[r * LD2 + cc]) = sk[u];
+    }
+#pragma unroll
+    for (int x = 0; x < DQ; ++x) loc[x] = row_scan16(loc[x]);
+    if (li == 15) {
+#pragma unroll
+      for (int x = 0; x < DQ; ++x) sTot[I * GP + chan(x)] = loc[x];
+    }
+    lds_barrier();
+    for (int i = tid; i < NB * GP; i += 256) sETot[i] = __expf(sTot[i]);
 #pragma unroll
     for (int x = 0; x < DQ; ++x) {
       const int ch = chan(x);

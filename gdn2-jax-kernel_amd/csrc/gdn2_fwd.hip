@@ -186,15 +186,18 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
     const bool last_pn = pn == NPN - 1;
     if (pn > 0) __syncthreads();          // the previous panel's LDS reads are done
 
-    // all loads needed before the inverse, issued together
+    // all loads needed before the inverse, issued together, g first: the cumsum
+    // waits for g alone (memory operations complete in order) while q, k, b
+    // arrive behind it
     float loc[NBW][DQ];
     Op qo[NBW][NKD], ko[NBW][NKD], bo[NBW][NKD];
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
       const size_t off = load_row(i) + d0;
 #pragma unroll
+      for (int j = 0; j < NKD; ++j) load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
+#pragma unroll
       for (int j = 0; j < NKD; ++j) {
-        load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
         qo[i][j] = op_load<T>(a.q + off + j * KS + lg * KC);
         ko[i][j] = op_load<T>(a.k + off + j * KS + lg * KC);
         bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
@@ -236,7 +239,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
         for (int x = 0; x < DQ; ++x) sTot[I * DP + chan(x)] = loc[i][x];
       }
     }
-    __syncthreads();
+    lds_barrier();   // LDS only: q, k, b may still be in flight
     for (int i = tid; i < NB * DP; i += NT) {
       sETot[i] = __expf(sTot[i]);
     }
@@ -249,7 +252,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
 #pragma unroll
       for (int m = NB - 1; m >= 0; --m) { sF1[m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- 2. per-token factors: qg, kbd, kg, khat; diagonal score blocks -----
     float aq[NBW][DQ], ak[NBW][DQ];
