@@ -1233,7 +1233,7 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     // variable-length batch (B = 1): one scan unit per (head, sequence)
     BStateArgs<T> sa{(const T*)fW, (const T*)fKgT, fGL, buf(B_DVPT), buf(B_QDOT), dh_final, N,
                      buf(B_DHT), buf(B_DVNT), dh0, cu_chunks, cu_chunks ? nseq : 1, H};
-    constexpr int BW = 2, BP = 2;  // column slices and producer waves per scan workgroup
+    constexpr int BW = 2, BP = 4;  // column slices and producer waves per scan workgroup
     constexpr int BK = bstate_ksplit<T, D>();   // compute waves per column slice
     const size_t units = cu_chunks ? (size_t)H * nseq : (size_t)B * H;
     hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP, BK>), dim3(units * (D / (16 * BW))),

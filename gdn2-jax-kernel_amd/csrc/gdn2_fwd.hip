@@ -1276,7 +1276,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   }
   launch_mark(st);
   constexpr int SW = 2;  // compute waves (16 value columns each) per state workgroup
-  constexpr int SP = 2;  // producer waves
+  constexpr int SP = 4;  // producer waves (DMA issue: 4 beat 2 by 14 % on float32 scans)
   constexpr int SK = state_ksplit<T, D>();   // compute waves per column slice
   constexpr int NVS = D / (16 * SW);
   const size_t BH = (size_t)B * H;
