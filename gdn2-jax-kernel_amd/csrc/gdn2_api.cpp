@@ -111,8 +111,8 @@ struct BwdRun {
                  float scale, const float* dout, const float* dh_final, void* dq, void* dk,
                  void* dv, void* dw, void* db, void* dg, float* dh0, const char* fws,
                  char* ws, const int* cu_chunks, int nseq) {
-    if constexpr (D > 128) {
-      return GDN2_ERR_HEAD_DIM;  // the backward kernels are built for D <= 128
+    if constexpr (D > 128 && BT != 64) {
+      return GDN2_ERR_CHUNK;  // D = 256 runs at chunk 64 only
     } else {
       hipError_t e = launch_bwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale,
                                               dout, dh_final, dq, dk, dv, dw, db, dg, dh0, fws,
@@ -158,7 +158,7 @@ const char* gdn2_strerror(int code) {
   switch (code) {
     case GDN2_OK: return "ok";
     case GDN2_ERR_HEAD_DIM:
-      return "head dim D must be 64, 128 or 256 (256: forward and decode only)";
+      return "head dim D must be 64, 128 or 256";
     case GDN2_ERR_SEQ_LEN: return "sequence length T must be divisible by the chunk size BT";
     case GDN2_ERR_CHUNK:
       return "chunk size BT must be 64 or 128 (128 needs bfloat16 inputs and D <= 128)";
@@ -244,7 +244,6 @@ int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtyp
 }
 
 size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {
-  if (D > 128) return 0;  // forward only at D = 256
   if (gdn2_validate(B, T, H, D, BT, in_dtype, in_dtype) != GDN2_OK &&
       gdn2_validate(B, T, H, D, BT, in_dtype, GDN2_F32) != GDN2_OK)
     return 0;
@@ -260,7 +259,6 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
   EventScope scope;
   int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
-  if (D > 128) return GDN2_ERR_HEAD_DIM;  // forward only at D = 256
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, dout, dq, dk, dv, dw, db, dg}))) return rc;
   if ((rc = check_ptrs({dh0}))) return rc;
   if ((rc = check_opt({h0, dh_final}))) return rc;
@@ -293,7 +291,6 @@ int gdn2_bwd_varlen(void* stream, int num_seqs, const int* cu_chunks, int total_
   const int T = total_chunks * BT;
   int rc = gdn2_validate(1, T, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
-  if (D > 128) return GDN2_ERR_HEAD_DIM;
   if (BT != 64) return GDN2_ERR_CHUNK;
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, dout, dq, dk, dv, dw, db, dg}))) return rc;
   if ((rc = check_ptrs({dh0, cu_chunks}))) return rc;

@@ -136,14 +136,23 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
   constexpr int WBYTES = BT * D * (int)sizeof(T);
   constexpr int BUF = 2 * WBYTES;
   constexpr int PIECES = BUF / 1024;
+  // two tile buffers where they fit (float32 at D = 256: one, with a third
+  // barrier E per chunk after which the producers refill it)
+  constexpr int NBUF = 2 * BUF <= 132 * 1024 ? 2 : 1;
+  // qdot straight from global memory by the compute waves (K-split: its LDS goes
+  // to the exchange buffer; D = 256: it does not fit beside the tiles); one step
+  // ahead in spare registers up to 8 row tiles per wave, else loaded right before
+  // the dh update that uses it (registers)
+  constexpr bool QG = KS > 1 || D > 128;
+  constexpr bool QAHEAD = NDH <= 8;
   static_assert(BUF % 1024 == 0, "tiles must split into 1 KB pieces");
   __shared__ __align__(16) char sbuf0[BUF];
-  __shared__ __align__(16) char sbuf1[BUF];
+  __shared__ __align__(16) char sbuf1[NBUF == 2 ? BUF : 16];
   __shared__ __align__(16) f32x4 sDV[NW * NB * 64];    // dvp^T in compute-lane order
-  __shared__ __align__(16) f32x4 sQD[KS == 1 ? NW * NDT * 64 : 1];   // (scale qg^T do)^T, same
+  __shared__ __align__(16) f32x4 sQD[QG ? 1 : NW * NDT * 64];   // (scale qg^T do)^T, same
   __shared__ __align__(16) f32x4 sX[KS > 1 ? NCW * NB * 64 : 1];     // K-split partials of kg dh
   __shared__ __align__(16) float sGL0[D];
-  __shared__ __align__(16) float sGL1[D];
+  __shared__ __align__(16) float sGL1[NBUF == 2 ? D : 4];
   __shared__ __align__(16) float sJunk[64];
 
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
@@ -214,7 +223,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         lds_dma16(dsrc + (size_t)w * 16 * BT + it * 16, &sDV[q * 64]);
       }
       // (scale qg^T do)^T[col][d]: wave w, tile at -> sQD[(w NDT + at) 64 + lane]
-      if constexpr (KS == 1) {
+      if constexpr (!QG) {
         const float* qsrc = a.QDOT + cid * D * D + (size_t)(vs * 16 * NW + li) * D + 4 * lg;
 #pragma unroll
         for (int j = 0; j < NW * NDT / NP; ++j) {
@@ -268,6 +277,21 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
     // The dvp / qdot buffer is single: the next chunk's gather goes out after B.
     if (n > 0) issue(0, sbuf0, sGL0);
     if (n > 1) touch(1);
+    if constexpr (NBUF == 1) {
+      for (int i = 0; i < n; ++i) {
+        wait_step(i);
+        exp_gl(sGL0);
+        barrier();  // A(i)
+        barrier();  // B(i)
+        if constexpr (KS > 1) barrier();  // X(i)
+        barrier();  // E(i): chunk i's tiles are no longer read
+        if (i + 1 < n) {
+          issue(i + 1, sbuf0, sGL0);
+          if (i + 2 < n) touch(i + 2);
+        }
+      }
+      return;
+    }
     for (int i = 0; i < n; i += 2) {
       wait_step(i);
       exp_gl(sGL0);
@@ -316,34 +340,34 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
 #pragma unroll
     for (int j = 0; j < NDH; ++j) dh[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // K-split: this wave's qdot pieces, loaded one step ahead
-  f32x4 qnext[KS > 1 ? NDH : 1];
-  auto load_qd = [&](int i) __attribute__((always_inline)) {
+  // this wave's qdot pieces from global memory (QG), loaded ahead
+  f32x4 qnext[QG && QAHEAD ? NDH : 1], qd[NDH];
+  auto load_qd = [&](int i, f32x4* dst) __attribute__((always_inline)) {
     const float* qsrc = a.QDOT + chunk_id(i) * D * D + (size_t)col * D + 4 * lg;
 #pragma unroll
-    for (int j = 0; j < NDH; ++j) qnext[j] = load4f(qsrc + (ks * NDH + j) * 16);
+    for (int j = 0; j < NDH; ++j) dst[j] = load4f(qsrc + (ks * NDH + j) * 16);
   };
-  if constexpr (KS > 1) {
-    if (n > 0) load_qd(0);
+  if constexpr (QG && QAHEAD) {
+    if (n > 0) load_qd(0, qnext);
   }
 
   auto step = [&](int i, const char* cur, const float* eglc) __attribute__((always_inline)) {
     const size_t cid = chunk_id(i);
-    // K-split: LDS-only barriers, so the qdot loads of the next step stay in
-    // flight (the producers order their DMA with their own vmcnt waits)
-    if constexpr (KS > 1) lds_barrier(); else __syncthreads();  // A(i)
-    f32x4 dvn[NB], qd[NDH];
+    // qdot from global: LDS-only barriers, so its loads stay in flight (the
+    // producers order their DMA with their own vmcnt waits)
+    if constexpr (QG) lds_barrier(); else __syncthreads();  // A(i)
+    f32x4 dvn[NB];
 #pragma unroll
     for (int it = 0; it < NB; ++it) dvn[it] = sDV[(wcol * NB + it) * 64 + lane];
-    if constexpr (KS > 1) {
+    if constexpr (QG && QAHEAD) {
 #pragma unroll
       for (int j = 0; j < NDH; ++j) qd[j] = qnext[j];
-      if (i + 1 < n) load_qd(i + 1);
-    } else {
+      if (i + 1 < n) load_qd(i + 1, qnext);
+    } else if constexpr (!QG) {
 #pragma unroll
       for (int at = 0; at < NDT; ++at) qd[at] = sQD[(wv * NDT + at) * 64 + lane];
     }
-    if constexpr (KS > 1) lds_barrier(); else __syncthreads();  // B(i)
+    if constexpr (QG) lds_barrier(); else __syncthreads();  // B(i)
     const T* sW = reinterpret_cast<const T*>(cur);
     const T* sK = reinterpret_cast<const T*>(cur + WBYTES);
 
@@ -392,6 +416,8 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) dvn[it][r] = sanitize(dvn[it][r]);
+        // D = 256: keep the operand reads of one row block in flight at a time
+        if constexpr (NDT > 8) __builtin_amdgcn_sched_barrier(0);
       }
     }
     float* dvo = a.DVNT + cid * D * BT + (size_t)col * BT;
@@ -400,6 +426,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       store4(dvo + it * 16 + 4 * lg, dvn[it]);
 
     // dh <- e^{gl} dh + qdot - W^T dv_new: X[d][t] = W[t][d]
+    if constexpr (QG && !QAHEAD) load_qd(i, qd);
 #pragma unroll
     for (int j = 0; j < NDH; ++j) {
       const int at = ks * NDH + j;
@@ -414,12 +441,22 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       const f32x4 egl = load4f(eglc + at * 16 + 4 * lg);
 #pragma unroll
       for (int r = 0; r < 4; ++r) dh[j][r] = sanitize(egl[r] * dh[j][r] + qd[j][r] - acc[r]);
+      if constexpr (NDT > 8) {
+        if (j % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+      }
     }
   };
 
-  for (int i = 0; i < n; i += 2) {
-    step(i, sbuf0, sGL0);
-    if (i + 1 < n) step(i + 1, sbuf1, sGL1);
+  if constexpr (NBUF == 1) {
+    for (int i = 0; i < n; ++i) {
+      step(i, sbuf0, sGL0);
+      lds_barrier();  // E(i)
+    }
+  } else {
+    for (int i = 0; i < n; i += 2) {
+      step(i, sbuf0, sGL0);
+      if (i + 1 < n) step(i + 1, sbuf1, sGL1);
+    }
   }
 #pragma unroll
   for (int j = 0; j < NDH; ++j)
@@ -1188,12 +1225,279 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
 }
 
 // ============================================================================
+// Wide heads (D = 256): the backward as per-chunk products on a generic kernel.
+// The fused per-chunk kernels above hold D x D and BT x D float32 tiles whole in
+// LDS, which at D = 256 would need up to 266 KB; here every product of B2 and B3
+// is one launch of chunk_gemm over all chunks, with K walked in 64-wide slices,
+// plus three element-wise kernels.  bwd_state (single-buffered at this width)
+// and gram_bwd (32-channel panels) run unchanged.
+// ============================================================================
+// One operand of a per-chunk product: logical X(r, k) (r = row of the result for
+// A, column for B) stored at [k*ld + r] (kmajor) or [r*ld + k], element offset
+// bb*sb + hh*sh + c*sc for chunk c of head hh of batch bb.
+struct WMat {
+  const void* p;
+  int bf16;                 // element type in memory
+  long long sb, sh, sc;
+  int ld;
+  int kmajor;
+  int mask;                 // on the stored (row, col): 1 keep col <= row, 2 keep col < row
+  int chained;              // bfloat16: stored columns in chained order (kpos)
+};
+// C[m][n] = alpha sum_k A(m,k) B(n,k) (+ C), stored [m*ld + n], mask on (m, n)
+struct WOut {
+  float* p;
+  long long sb, sh, sc;
+  int ld;
+  int mask;
+  float alpha;
+  int accum;
+};
+struct WGemmArgs {
+  WMat A, B;
+  WOut C;
+  int M, N, K, H, Nc;
+};
+
+// Stage a 64 x 64 slice (rows r0.., k0..) of an operand into registers: four
+// 16-byte runs per thread.
+__device__ __forceinline__ void wide_load(f32x4 (&v)[4], const WMat& m, size_t off, int r0,
+                                          int k0, int tid) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = tid + 256 * u, a = i >> 4, b = (i & 15) * 4;   // stored row a, col b
+    const int srow = m.kmajor ? k0 + a : r0 + a;
+    const int scol = m.kmajor ? r0 + b : k0 + b;
+    const int pcol = m.chained ? kpos<bf16_t>(scol) : scol;
+    float t[4];
+    load4_any(m.p, m.bf16, off + (size_t)srow * m.ld + pcol, t);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[u][e] = ((m.mask == 1 && scol + e > srow) || (m.mask == 2 && scol + e >= srow)) ? 0.f : t[e];
+  }
+}
+// ... and into LDS as [r][k] (pitch 68)
+__device__ __forceinline__ void wide_store(float* dst, const f32x4 (&v)[4], const WMat& m,
+                                           int tid) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = tid + 256 * u, a = i >> 4, b = (i & 15) * 4;
+    if (!m.kmajor) {
+      *reinterpret_cast<f32x4*>(&dst[a * 68 + b]) = v[u];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[(b + e) * 68 + a] = v[u][e];
+    }
+  }
+}
+
+// One workgroup per chunk and 64 x 64 output tile; wave w owns output rows
+// 16w..16w+15 (four 16 x 16 accumulators).  The next K slice's loads are in
+// flight while the current slice's products run.
+__global__ void __launch_bounds__(256) chunk_gemm(WGemmArgs a) {
+  __shared__ __align__(16) float sX[64 * 68];
+  __shared__ __align__(16) float sY[64 * 68];
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int MT = a.M / 64, NT = a.N / 64;
+  const int id = blockIdx.x;
+  const int cid = id / (MT * NT), mt = (id / NT) % MT, nt = id % NT;
+  const int c = cid % a.Nc, bh = cid / a.Nc, hh = bh % a.H, bb = bh / a.H;
+  const size_t offA = bb * a.A.sb + hh * a.A.sh + c * a.A.sc;
+  const size_t offB = bb * a.B.sb + hh * a.B.sh + c * a.B.sc;
+  const size_t offC = bb * a.C.sb + hh * a.C.sh + c * a.C.sc;
+  const int m0 = mt * 64, n0 = nt * 64;
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 ra[4], rb[4];
+  wide_load(ra, a.A, offA, m0, 0, tid);
+  wide_load(rb, a.B, offB, n0, 0, tid);
+  for (int k0 = 0; k0 < a.K; k0 += 64) {
+    wide_store(sX, ra, a.A, tid);
+    wide_store(sY, rb, a.B, tid);
+    __syncthreads();
+    if (k0 + 64 < a.K) {
+      wide_load(ra, a.A, offA, m0, k0 + 64, tid);
+      wide_load(rb, a.B, offB, n0, k0 + 64, tid);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f32x4 x = load4f(&sX[(wv * 16 + li) * 68 + ks * 16 + 4 * lg]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mma(acc[j], x, load4f(&sY[(j * 16 + li) * 68 + ks * 16 + 4 * lg]));
+    }
+    lds_barrier();   // the slice is read before the next one is stored
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + wv * 16 + 4 * lg + r, n = n0 + j * 16 + li;
+      float val = a.C.alpha * acc[j][r];
+      if ((a.C.mask == 1 && n > m) || (a.C.mask == 2 && n >= m)) val = 0.f;
+      float* dst = a.C.p + offC + (size_t)m * a.C.ld + n;
+      if (a.C.accum) val += *dst;
+      *dst = val;
+    }
+}
+
+// b k e^{gc} and w v per token, chunk-major [t][d] float32; one thread per channel
+// (gc: running sum of g over the chunk's tokens)
+template <typename T, typename TG>
+__global__ void __launch_bounds__(256) wide_kbd_wv(const T* k, const T* w, const T* v,
+                                                  const T* b, const TG* g, int T_len, int H,
+                                                  int N, int D, float* KBD, float* WV) {
+  constexpr int BT = 64;
+  const int d = threadIdx.x, cid = blockIdx.x;
+  if (d >= D) return;
+  const int c = cid % N, bh = cid / N, hh = bh % H, bb = bh / H;
+  const size_t HD = (size_t)H * D;
+  const size_t tok0 = ((size_t)bb * T_len + (size_t)c * BT) * HD + (size_t)hh * D + d;
+  float gc = 0.f;
+  for (int t = 0; t < BT; ++t) {
+    const size_t o = tok0 + (size_t)t * HD, wo = ((size_t)cid * BT + t) * D + d;
+    gc += to_f(g[o]);
+    KBD[wo] = to_f(b[o]) * to_f(k[o]) * __expf(gc);
+    WV[wo] = to_f(w[o]) * to_f(v[o]);
+  }
+}
+
+// sum_e dh'[d][e] h[d][e] per chunk and channel d (dh'^T float32 [e][d], h^T [e][d]
+// in the residual type); one thread per channel
+template <typename T>
+__global__ void __launch_bounds__(256) wide_sdh(const float* DHT, const T* HT, int D, float* SDH) {
+  const int d = threadIdx.x, cid = blockIdx.x;
+  if (d >= D) return;
+  const size_t base = (size_t)cid * D * D;
+  const int pd = sizeof(T) == 2 ? kpos<bf16_t>(d) : d;
+  float s = 0.f;
+  for (int e = 0; e < D; ++e) s += DHT[base + (size_t)e * D + d] * to_f(HT[base + (size_t)e * D + pd]);
+  SDH[(size_t)cid * D + d] = s;
+}
+
+// dv = d(wv) w, dw = d(wv) v (gdn2_bwd.py:204-205), d(wv) chunk-major [t][e]
+template <typename T>
+__global__ void __launch_bounds__(256) wide_dvdw(const float* DWV, const T* w, const T* v,
+                                                int T_len, int H, int N, int D, T* dv, T* dw) {
+  constexpr int BT = 64;
+  const int d = threadIdx.x, cid = blockIdx.x;
+  if (d >= D) return;
+  const int c = cid % N, bh = cid / N, hh = bh % H, bb = bh / H;
+  const size_t HD = (size_t)H * D;
+  const size_t tok0 = ((size_t)bb * T_len + (size_t)c * BT) * HD + (size_t)hh * D + d;
+  for (int t = 0; t < BT; ++t) {
+    const size_t o = tok0 + (size_t)t * HD;
+    const float x = DWV[((size_t)cid * BT + t) * D + d];
+    dv[o] = from_f<T>(sanitize(x * to_f(w[o])));
+    dw[o] = from_f<T>(sanitize(x * to_f(v[o])));
+  }
+}
+
+// ============================================================================
 // Host side
 // ============================================================================
 size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t) {
   return BT == 64 ? bwd_layout(nchunks, BT, D).total : 0;
 }
 
+
+// The backward at D = 256 (chunk 64): B2 and B3 as chunk_gemm launches, the
+// reverse scan and gram_bwd as at D <= 128.  Launch marks: before B2, after B2,
+// after the scan, after B3, after gram_bwd (as the fused path).
+template <typename T, typename TG>
+hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* q,
+                           const void* k, const void* v, const void* w, const void* b,
+                           const void* g, float scale, const float* dout,
+                           const float* dh_final, void* dq, void* dk, void* dv, void* dw,
+                           void* db, void* dg, float* dh0, const char* fws, char* ws,
+                           const int* cu_chunks, int nseq) {
+  constexpr int BT = 64, D = 256, BF = sizeof(T) == 2;
+  const int N = T_len / BT;
+  const size_t NC = (size_t)B * H * N;
+  const FwdLayout F = fwd_layout(NC, BT, D, sizeof(T));
+  const BwdLayout L = bwd_layout(NC, BT, D);
+  auto buf = [&](BwdBuf i) { return reinterpret_cast<float*>(ws + L.off[i]); };
+  const long long td = (long long)BT * D, tt = (long long)BT * BT, dd = (long long)D * D;
+  // chunk-major tiles of `per` elements; (B,T,H,D) token rows
+  auto cm = [&](const void* p, int bf, long long per, int ld, int kmajor, int mask,
+                int chained) {
+    return WMat{p, bf, (long long)H * N * per, (long long)N * per, per, ld, kmajor, mask,
+                chained};
+  };
+  auto tok = [&](const void* p, int kmajor) {
+    return WMat{p, 0, (long long)T_len * H * D, D, (long long)BT * H * D, H * D, kmajor, 0, 0};
+  };
+  auto out = [&](float* p, long long per, int ld, int mask, float alpha, int accum) {
+    return WOut{p, (long long)H * N * per, (long long)N * per, per, ld, mask, alpha, accum};
+  };
+  auto gemm = [&](const WMat& A, const WMat& Bm, const WOut& C, int M, int Nn, int K) {
+    WGemmArgs ga{A, Bm, C, M, Nn, K, H, N};
+    hipLaunchKernelGGL(chunk_gemm, dim3(NC * (M / 64) * (Nn / 64)), dim3(256), 0, st, ga);
+  };
+  const void* fVnT = fws + F.VnT;
+  const void* fHT = fws + F.HT;
+  const float* fA = reinterpret_cast<const float*>(fws + F.A);
+  launch_mark(st);
+  if (NC > 0) {
+    // B2: dAqk = (do v_new^T) . causal, dvp^T = (Aqk^T do)^T, qdot = scale (qg^T do)^T
+    gemm(tok(dout, 0), cm(fVnT, BF, td, BT, 1, 0, BF), out(buf(B_DAQK), tt, BT, 1, 1.f, 0), BT,
+         BT, D);
+    gemm(tok(dout, 1), cm(fws + F.Aqk, BF, tt, BT, 1, 1, 0), out(buf(B_DVPT), td, BT, 0, 1.f, 0),
+         D, BT, BT);
+    gemm(tok(dout, 1), cm(fws + F.Qg, BF, td, D, 1, 0, 0), out(buf(B_QDOT), dd, D, 0, scale, 0),
+         D, D, BT);
+    launch_mark(st);
+  }
+  BStateArgs<T> sa{(const T*)(fws + F.W), (const T*)(fws + F.KgT),
+                   reinterpret_cast<const float*>(fws + F.GL), buf(B_DVPT), buf(B_QDOT),
+                   dh_final, N, buf(B_DHT), buf(B_DVNT), dh0, cu_chunks, cu_chunks ? nseq : 1, H};
+  constexpr int BW = 2, BP = 2;
+  const size_t units = cu_chunks ? (size_t)H * nseq : (size_t)B * H;
+  hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP, 1>), dim3(units * (D / (16 * BW))),
+                     dim3(64 * (BW + BP)), 0, st, sa);
+  launch_mark(st);
+  if (NC > 0) {
+    // B3 (gdn2_bwd.py:126-210), products as in bwd_wy
+    const WMat hT = cm(fHT, BF, dd, D, 1, 0, BF);         // h(d, e) = h^T[e][d]
+    const WMat dvn = cm(buf(B_DVNT), 0, td, BT, 1, 0, 0);  // dv_new(t, e) = dv_new^T[e][t]
+    const WMat Ats = cm(fA, 0, tt, BT, 1, 0, 0);          // A^T(s, t) = A[t][s]
+    gemm(tok(dout, 0), hT, out(buf(B_DQG), td, D, 0, scale, 0), BT, D, D);       // dqg
+    gemm(dvn, hT, out(buf(B_DW), td, D, 0, -1.f, 0), BT, D, D);                   // dW
+    gemm(cm(fVnT, BF, td, BT, 1, 0, BF), cm(buf(B_DHT), 0, dd, D, 1, 0, 0),
+         out(buf(B_DKG), td, D, 0, 1.f, 0), BT, D, D);                            // dkg
+    hipLaunchKernelGGL((wide_sdh<T>), dim3(NC), dim3(D), 0, st, (const float*)buf(B_DHT),
+                       (const T*)fHT, D, buf(B_SDH));
+    hipLaunchKernelGGL((wide_kbd_wv<T, TG>), dim3(NC), dim3(D), 0, st, (const T*)k,
+                       (const T*)w, (const T*)v, (const T*)b, (const TG*)g, T_len, H, N, D,
+                       buf(B_KBD), buf(B_WV));
+    gemm(cm(buf(B_DW), 0, td, D, 0, 0, 0), cm(buf(B_KBD), 0, td, D, 0, 0, 0),
+         out(buf(B_DA), tt, BT, 2, 1.f, 0), BT, BT, D);                           // dA = dW kbd^T
+    gemm(dvn, cm(buf(B_WV), 0, td, D, 0, 0, 0), out(buf(B_DA), tt, BT, 2, 1.f, 1), BT, BT,
+         D);                                                                      // + dv_new wv^T
+    gemm(Ats, cm(buf(B_DW), 0, td, D, 1, 0, 0), out(buf(B_DKBD), td, D, 0, 1.f, 0), BT, D,
+         BT);                                                                     // A^T dW
+    gemm(Ats, cm(buf(B_DVNT), 0, td, BT, 0, 0, 0), out(buf(B_DWV), td, D, 0, 1.f, 0), BT, D,
+         BT);                                                                     // A^T dv_new
+    hipLaunchKernelGGL((wide_dvdw<T>), dim3(NC), dim3(D), 0, st, (const float*)buf(B_DWV),
+                       (const T*)w, (const T*)v, T_len, H, N, D, (T*)dv, (T*)dw);
+    gemm(cm(buf(B_DA), 0, tt, BT, 0, 0, 0), cm(fA, 0, tt, BT, 0, 0, 0),
+         out(buf(B_TMP), tt, BT, 0, 1.f, 0), BT, BT, BT);                         // dA A^T
+    gemm(Ats, cm(buf(B_TMP), 0, tt, BT, 1, 0, 0), out(buf(B_DAKK), tt, BT, 2, -1.f, 0), BT, BT,
+         BT);                                                                     // dAkk
+    launch_mark(st);
+    // B4 + B3 element-wise tail + B5
+    GramArgs<T, TG> gr{(const T*)q,  (const T*)k,  (const T*)b,  (const TG*)g,
+                       buf(B_DAQK),  buf(B_DAKK),  buf(B_SDH),   buf(B_DQG),
+                       buf(B_DKG),   buf(B_DKBD),  T_len,        H,
+                       N,            scale,        (T*)dq,       (T*)dk,
+                       (T*)db,       (TG*)dg};
+    hipLaunchKernelGGL((gram_bwd<T, TG, D>), dim3(NC * (D / gram_panel())), dim3(256), 0, st,
+                       gr);
+    launch_mark(st);
+  }
+  return hipGetLastError();
+}
 
 template <typename T, typename TG, int BT, int D>
 hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
@@ -1203,6 +1507,10 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       const char* fws, char* ws, const int* cu_chunks, int nseq) {
   if constexpr (BT != 64) {
     return hipErrorNotSupported;
+  } else if constexpr (D > 128) {
+    (void)h0;
+    return launch_bwd_wide<T, TG>(st, B, T_len, H, q, k, v, w, b, g, scale, dout, dh_final, dq,
+                                  dk, dv, dw, db, dg, dh0, fws, ws, cu_chunks, nseq);
   } else {
     (void)h0;
     const int N = T_len / BT;
@@ -1233,8 +1541,12 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     // variable-length batch (B = 1): one scan unit per (head, sequence)
     BStateArgs<T> sa{(const T*)fW, (const T*)fKgT, fGL, buf(B_DVPT), buf(B_QDOT), dh_final, N,
                      buf(B_DHT), buf(B_DVNT), dh0, cu_chunks, cu_chunks ? nseq : 1, H};
-    constexpr int BW = 2, BP = 4;  // column slices and producer waves per scan workgroup
+    constexpr int BW = 2;                       // column slices per scan workgroup
     constexpr int BK = bstate_ksplit<T, D>();   // compute waves per column slice
+    // producer waves: four with the K-split (float32: the next chunk's DMA is bound
+    // by how fast it is issued), else two, which leaves the compute waves one per
+    // SIMD with 512 registers
+    constexpr int BP = BK > 1 ? 4 : 2;
     const size_t units = cu_chunks ? (size_t)H * nseq : (size_t)B * H;
     hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP, BK>), dim3(units * (D / (16 * BW))),
                        dim3(64 * (BW * BK + BP)), 0, st, sa);
@@ -1277,5 +1589,8 @@ GDN2_INST_BWD(bf16_t, bf16_t, 64, 64)
 GDN2_INST_BWD(bf16_t, bf16_t, 64, 128)
 GDN2_INST_BWD(bf16_t, bf16_t, 128, 64)
 GDN2_INST_BWD(bf16_t, bf16_t, 128, 128)
+GDN2_INST_BWD(float, float, 64, 256)
+GDN2_INST_BWD(bf16_t, float, 64, 256)
+GDN2_INST_BWD(bf16_t, bf16_t, 64, 256)
 
 }  // namespace gdn2

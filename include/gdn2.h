@@ -39,7 +39,7 @@ extern "C" {
 
 /* Error codes. */
 #define GDN2_OK                0
-#define GDN2_ERR_HEAD_DIM     -1  /* D not in {64,128,256} (256: forward and decode only);
+#define GDN2_ERR_HEAD_DIM     -1  /* D not in {64,128,256};
                                      ref asserts D==128, gdn2_fwd.py:145, gdn2_bwd.py:348 */
 #define GDN2_ERR_SEQ_LEN      -2  /* T % BT != 0; ref asserts, gdn2_fwd.py:146 */
 #define GDN2_ERR_CHUNK        -3  /* BT not in {64,128}, or BT=128 with float32 inputs or D=256 */
@@ -126,7 +126,9 @@ size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
  * first).  BT must be 64.  dh_final and h0 may be NULL (zero).  dq,dk,dv,dw,db
  * are in_dtype, dg is g_dtype, dh0 is float32 (B,H,D,D); all gradients are
  * sanitized as gdn2_pipeline.py:129-135.  Computes in float32 throughout.
- * Launches 4 kernels (see gdn2_set_launch_events). */
+ * Launches 4 kernels at D <= 128 (see gdn2_set_launch_events); at D = 256 the
+ * per-chunk products run as separate launches (the launch marks still bracket
+ * the same four stages). */
 int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
              const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, const float* h0, float scale, const float* dout,

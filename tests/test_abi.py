@@ -122,9 +122,9 @@ def test_bwd_rejects_before_launch():
     call = lambda d, dout, fwsb: L.gdn2_bwd(None, *d, *fake, None, 0.125, dout, None, *grads,
                                             0x5000, 0x6000, fwsb, 0x7000, bws)
     assert call((1, 512, 2, 96, 64, F32, F32), 0x4000, fws) == _lib.ERR_HEAD_DIM
-    # D = 256 is forward-only: the backward refuses it before touching anything
-    assert L.gdn2_bwd_workspace_bytes(1, 512, 2, 256, 64, F32) == 0
-    assert call((1, 512, 2, 256, 64, F32, F32), 0x4000, 1 << 30) == _lib.ERR_HEAD_DIM
+    # D = 256: a larger backward workspace, checked before anything is launched
+    assert L.gdn2_bwd_workspace_bytes(1, 512, 2, 256, 64, F32) > bws
+    assert call((1, 512, 2, 256, 64, F32, F32), 0x4000, 1 << 30) == _lib.ERR_WORKSPACE
     assert call(dims, None, fws) == _lib.ERR_NULL
     assert call(dims, 0x4000, fws - 1) == _lib.ERR_WORKSPACE
 
@@ -209,7 +209,7 @@ def test_bwd_varlen_rejects_before_launch():
     assert call(0, 4) == _lib.ERR_SHAPE                     # no sequences
     assert call(2, -1) == _lib.ERR_SHAPE
     assert call(2, 4, D=96) == _lib.ERR_HEAD_DIM
-    assert call(2, 4, D=256) == _lib.ERR_HEAD_DIM           # forward only at D = 256
+    assert call(2, 4, D=256) == _lib.ERR_WORKSPACE          # D = 256 needs a larger one
     assert call(2, 4, BT=128) == _lib.ERR_CHUNK             # float32 needs chunk 64
     assert call(2, 4, cu=None) == _lib.ERR_NULL
     assert call(2, 4, dh0=None) == _lib.ERR_NULL

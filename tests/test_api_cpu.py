@@ -52,11 +52,16 @@ def test_partial_last_chunk_passes_validation():
     assert not isinstance(e.value, gp.GDN2ShapeError)
 
 
-def test_trainable_d256_is_refused():
-    """D = 256 runs forward only; the trainable path refuses it with the shape
-    error (its backward kernels are built for D <= 128)."""
+def test_bwd_workspace_d256():
+    """D = 256 trains too: its backward adds six per-chunk regions (dW, b k e^gc,
+    w v, d(wv), dA, dA A^T) to the layout of D <= 128, each 256-byte aligned."""
     from gdn2_package import _lib
-    assert _lib.lib().gdn2_bwd_workspace_bytes(1, 128, 2, 256, 64, _lib.GDN2_F32) == 0
+    al = lambda x: (x + 255) // 256 * 256
+    nc, BT, D = 1 * 2 * (128 // 64), 64, 256
+    tt, td, dd = BT * BT, BT * D, D * D
+    per = [tt, td, dd, dd, td, td, td, td, tt, D, td, td, td, td, tt, tt]
+    assert _lib.lib().gdn2_bwd_workspace_bytes(1, 128, 2, 256, 64, _lib.GDN2_F32) == \
+        sum(al(nc * p * 4) for p in per)
 
 
 def test_no_cpu_fallback():

@@ -104,6 +104,7 @@ def test_varlen_bad_tables_stay_in_bounds(dev):
     (torch.float32, 64, [70, 1, 128, 33], True),   # tails, one token, whole chunks
     (torch.float32, 128, [200, 64], False),
     (torch.bfloat16, 64, [100, 29], True),
+    (torch.float32, 256, [90, 64], True),          # D = 256: the backward of per-chunk products
 ])
 def test_varlen_trainable_matches_per_sequence_oracle(dev, dtype, D, lens, h0):
     """gdn2_pallas_forward_varlen_trainable: out, h_final and every gradient
