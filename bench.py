@@ -323,7 +323,14 @@ def extras(gp, steps=10, warmup=3):
     res["d256_fwd"] = {"shape": "B8 T8192 H3 D256 bf16, chunk 64", "ms": ms,
                        "tokens_per_s": B * T / (ms * 1e-3),
                        "kernels_ms": dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms))}
-    del x256
+    # D = 256 training step, float32 (chunk 64): forward with residuals + backward
+    x256f = [x.float().detach().requires_grad_(True) for x in x256]
+    do256 = r((B, T, 3, 256))
+    ms = _time(lambda: torch.autograd.grad(
+        [gp.gdn2_pallas_forward_trainable(*x256f, 256 ** -0.5)[0]], x256f, [do256]), 3, 1)
+    res["d256_train"] = {"shape": "B8 T8192 H3 D256 float32, forward + backward", "ms": ms,
+                         "tokens_per_s": B * T / (ms * 1e-3)}
+    del x256, x256f, do256
     # T % BT != 0: 8100 tokens per sequence, the last chunk of each 36 tokens short
     xp = dist((B, 8100, H, D))
     ms = _time(lambda: gp.gdn2_pallas_forward(*xp, D ** -0.5), steps, warmup)
