@@ -567,37 +567,35 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
     }
 
     // ---- 6. w_pseudo = A (b k e^gc), u = A (w v), the panel's columns ---------
+    // Items (row block I, 16-channel tile dt) are dealt round-robin over the waves
+    // (I-major), so every wave gets the same mix of short and long (triangular,
+    // K = 16 (I+1)) products; all operands are in LDS.
+    constexpr int NDTT = DP / 16;                    // channel tiles of the panel
+    static_assert((NB * NDTT) % PW == 0, "W/U items must split over the waves");
+    T* Wc = a.W + (size_t)cid * BT * D;
+    T* Uc = a.UT + (size_t)cid * D * BT;
 #pragma unroll
-    for (int i = 0; i < NBW; ++i) {
-      const int I = own_block<NB>(wv, i);
+    for (int step = 0; step < NB * NDTT / PW; ++step) {
+      const int j = wv + step * PW, I = j / NDTT, dt = j % NDTT;
       const int kgmax = (I * 16 + 15) / KS;
-      Op af[NKT];
+      const int dg = d0 + dt * 16;      // first channel of the tile
+      f32x4 accw = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kg = 0; kg < NKT; ++kg) {
-        float tmp[KC];
+        if (kg <= kgmax) {
+          float tmp[KC];
 #pragma unroll
-        for (int e = 0; e < KC; e += 4) {
-          const f32x4 v4 = load4f(&sA[(I * 16 + li) * A_LD + kg * KS + lg * KC + e]);
-          tmp[e] = v4[0]; tmp[e + 1] = v4[1]; tmp[e + 2] = v4[2]; tmp[e + 3] = v4[3];
-        }
-        af[kg] = op_from<T>(tmp);
-      }
-      T* Wc = a.W + (size_t)cid * BT * D;
-      T* Uc = a.UT + (size_t)cid * D * BT;
-#pragma unroll
-      for (int dt = 0; dt < DP / 16; ++dt) {
-        const int dg = d0 + dt * 16;      // first channel of the tile
-        f32x4 accw = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kg = 0; kg < NKT; ++kg) {
-          if (kg <= kgmax) {
-            mma(accw, op_load<T>(&sKbdT[(dg + li) * TT_LD + kg * KS + lg * KC]), af[kg]);
-            mma(accu, af[kg], op_load<T>(&sWVT[(dt * 16 + li) * TT_LD + kg * KS + lg * KC]));
+          for (int e = 0; e < KC; e += 4) {
+            const f32x4 v4 = load4f(&sA[(I * 16 + li) * A_LD + kg * KS + lg * KC + e]);
+            tmp[e] = v4[0]; tmp[e + 1] = v4[1]; tmp[e + 2] = v4[2]; tmp[e + 3] = v4[3];
           }
+          const Op af = op_from<T>(tmp);
+          mma(accw, op_load<T>(&sKbdT[(dg + li) * TT_LD + kg * KS + lg * KC]), af);
+          mma(accu, af, op_load<T>(&sWVT[(dt * 16 + li) * TT_LD + kg * KS + lg * KC]));
         }
-        store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dg + 4 * lg), accw);
-        store4(Uc + (size_t)(dg + li) * BT + kpos<T>(I * 16 + 4 * lg), accu);
       }
+      store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dg + 4 * lg), accw);
+      store4(Uc + (size_t)(dg + li) * BT + kpos<T>(I * 16 + 4 * lg), accu);
     }
   }
 }
