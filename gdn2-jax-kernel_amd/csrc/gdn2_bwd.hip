@@ -124,7 +124,7 @@ struct BStateArgs {
 // pieces (four per step) straight from global memory one step ahead, hitting
 // L2 behind the producers' touch.
 template <typename T, int D>
-constexpr int bstate_ksplit() { return (sizeof(T) == 4 && D <= 128) ? 2 : 1; }
+constexpr int bstate_ksplit() { return sizeof(T) == 4 ? 2 : 1; }
 
 template <typename T, int BT, int D, int NW, int NP, int KS>
 __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a) {
@@ -141,10 +141,10 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
   constexpr int NBUF = 2 * BUF <= 132 * 1024 ? 2 : 1;
   // qdot straight from global memory by the compute waves (K-split: its LDS goes
   // to the exchange buffer; D = 256: it does not fit beside the tiles); one step
-  // ahead in spare registers up to 8 row tiles per wave, else loaded right before
+  // ahead in spare registers up to 4 row tiles per wave, else loaded right before
   // the dh update that uses it (registers)
   constexpr bool QG = KS > 1 || D > 128;
-  constexpr bool QAHEAD = NDH <= 8;
+  constexpr bool QAHEAD = NDH <= 4;
   static_assert(BUF % 1024 == 0, "tiles must split into 1 KB pieces");
   __shared__ __align__(16) char sbuf0[BUF];
   __shared__ __align__(16) char sbuf1[NBUF == 2 ? BUF : 16];
@@ -1452,10 +1452,10 @@ hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* 
   BStateArgs<T> sa{(const T*)(fws + F.W), (const T*)(fws + F.KgT),
                    reinterpret_cast<const float*>(fws + F.GL), buf(B_DVPT), buf(B_QDOT),
                    dh_final, N, buf(B_DHT), buf(B_DVNT), dh0, cu_chunks, cu_chunks ? nseq : 1, H};
-  constexpr int BW = 2, BP = 2;
+  constexpr int BW = 2, BK = bstate_ksplit<T, D>(), BP = BK > 1 ? 4 : 2;
   const size_t units = cu_chunks ? (size_t)H * nseq : (size_t)B * H;
-  hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP, 1>), dim3(units * (D / (16 * BW))),
-                     dim3(64 * (BW + BP)), 0, st, sa);
+  hipLaunchKernelGGL((bwd_state<T, BT, D, BW, BP, BK>), dim3(units * (D / (16 * BW))),
+                     dim3(64 * (BW * BK + BP)), 0, st, sa);
   launch_mark(st);
   if (NC > 0) {
     // B3 (gdn2_bwd.py:126-210), products as in bwd_wy

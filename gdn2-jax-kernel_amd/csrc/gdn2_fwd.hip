@@ -664,7 +664,7 @@ struct StateArgs {
 template <typename T, int BT, int D>
 constexpr int state_bufs() { return 4 * BT * D * (int)sizeof(T) <= 132 * 1024 ? 2 : 1; }
 template <typename T, int D>
-constexpr int state_ksplit() { return (sizeof(T) == 4 && D <= 128) ? 2 : 1; }
+constexpr int state_ksplit() { return sizeof(T) == 4 ? 2 : 1; }
 
 template <typename T, int BT, int D, int NW, int NP, int KS>
 __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a) {
