@@ -927,9 +927,10 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 // strictly between J and I), Khat = k e^{T-loc}, AQ = q e^{loc}, ABK = b k e^{loc}.
 // Every wave does three block pairs per 16-channel slice, so a barrier after each
 // slice frees that slice of AQ / ABK / Khat and RQ / RBK / RK take its place in LDS.
-// Diagonal blocks are summed per channel (one lane per channel), factorised around
-// the block's 8th token as in the forward, and added in place.  Then, one lane per
-// token and four channels per 16-byte access, the chain rule through the
+// Diagonal blocks, factorised around the block's 8th token as in the forward, run
+// first on MFMA, transposed (channel x token) so that their sums arrive in the
+// token layout of the chain rule, which adds them.  Then, one lane per token and
+// four channels per 16-byte access, the chain rule through the
 // exponentials of qg, kg and b k e^gc (gdn2_bwd.py:186-210; dqg, dkg, d(b k e^gc)
 // and sum_e dh' h come from bwd_wy, which also forms dv and dw) and the reverse
 // cumsum of dgc (gdn2_bwd.py:32-41): DPP suffix sums inside each 16-token block,
@@ -947,7 +948,7 @@ struct GramArgs {
 };
 
 // Channels are independent in all of this, so a workgroup takes one chunk and
-// one panel of GP = 32 channels (62 KB of LDS: two workgroups per CU, one
+// one panel of GP = 32 channels (63 KB of LDS: two workgroups per CU, one
 // streaming while the other computes).  The panels of a chunk run on one XCD,
 // sharing the chunk's dAqk / dAkk tiles in its L2.
 constexpr int gram_panel() { return 32; }
@@ -965,6 +966,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   __shared__ __align__(16) float sTot[NB * GP];
   __shared__ __align__(16) float sETot[NB * GP];   // e^{T_m}, then per-block sums of dgc
   __shared__ __align__(16) float sSkg[NB * GP];    // per-block sums of dkg kg
+  __shared__ __align__(16) float sLm[NB * GP];     // in-block cumsum at the block's 8th token
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   int cid, pn;
@@ -992,6 +994,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   constexpr int SU = BT * BT / 4 / 256;
   const int t = I * 16 + li;
   const size_t rowo = tok0 + (size_t)t * HD;
+  f32x4 dqd[NDT], dbd[NDT], dkd[NDT];   // diagonal-block sums, token t, channels chan()
   {
     const float* dq = a.DAQK + (size_t)cid * BT * BT;
     const float* dk = a.DAKK + (size_t)cid * BT * BT;
@@ -1023,8 +1026,59 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
 #pragma unroll
       for (int x = 0; x < DQ; ++x) sTot[I * GP + chan(x)] = loc[x];
     }
+    if (li == 7) {
+#pragma unroll
+      for (int x = 0; x < DQ; ++x) sLm[I * GP + chan(x)] = loc[x];
+    }
     lds_barrier();
     for (int i = tid; i < NB * GP; i += 256) sETot[i] = __expf(sTot[i]);
+    // Diagonal block first, on MFMA, with e^{lc_i - lc_j} = e^{lc_i - lm} e^{lm - lc_j}
+    // around the block's 8th token (as the forward's diagonal blocks): this wave's
+    // own rows of sAQ, sABK, sKH take QE = scale q e^{loc-lm}, BE = b k e^{loc-lm},
+    // KE = k e^{lm-loc} (only this wave reads them), and the products are formed
+    // transposed (channel x token), so that lane li holds token li, channels
+    // dt*16 + 4lg + r: the layout of the chain rule below, where the row factors
+    // are applied.
+#pragma unroll
+    for (int x = 0; x < DQ; ++x) {
+      const int ch = chan(x);
+      const float lm = sLm[I * GP + ch];
+      const float fl = __expf(loc[x] - lm), fr = __expf(lm - loc[x]);
+      sAQ[t * LD1 + ch] = a.scale * qv[x] * fl;
+      sABK[t * LD1 + ch] = bv[x] * kv[x] * fl;
+      sKH[t * LD1 + ch] = kv[x] * fr;
+    }
+    {
+      const int dblk = I * 16 * LD2 + I * 16;
+      const f32x4 rq = load4f(&sDQK[dblk + li * LD2 + 4 * lg]);   // row li, cols 4lg + e
+      const f32x4 rk = load4f(&sDKK[dblk + li * LD2 + 4 * lg]);
+      f32x4 mq, mk, cq, ck;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int s = 4 * lg + e;
+        mq[e] = s <= li ? rq[e] : 0.f;                          // dAqk[li][s], s <= li
+        mk[e] = s < li ? rk[e] : 0.f;                           // dAkk[li][s], s < li
+        cq[e] = s >= li ? sDQK[dblk + s * LD2 + li] : 0.f;     // dAqk[s][li], s >= li
+        ck[e] = s > li ? sDKK[dblk + s * LD2 + li] : 0.f;      // dAkk[s][li], s > li
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        f32x4 ke, qe, be;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int o = (I * 16 + 4 * lg + e) * LD1 + dt * 16 + li;
+          ke[e] = sKH[o];
+          qe[e] = sAQ[o];
+          be[e] = sABK[o];
+        }
+        dqd[dt] = dbd[dt] = dkd[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        mma(dqd[dt], ke, mq);   // sum_{j <= i} dAqk[i][j] KE_j
+        mma(dbd[dt], ke, mk);   // sum_{j < i}  dAkk[i][j] KE_j
+        mma(dkd[dt], qe, cq);   // sum_{i >= j} dAqk[i][j] QE_i
+        mma(dkd[dt], be, ck);   //  + sum_{i > j} dAkk[i][j] BE_i
+      }
+    }
+    // then the off-diagonal operands in the same rows (in order within the wave)
 #pragma unroll
     for (int x = 0; x < DQ; ++x) {
       const int ch = chan(x);
@@ -1093,87 +1147,42 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
     }
   }
 
-  // ---- diagonal block, one lane per channel ------------------------------------
-  // Wave I reads back only its own rows of RQ / RBK / RK (written by its own
-  // lanes above).
-  if (lane < GP) {
-    const int d = lane;
-    const float totI = sTot[I * GP + d];
-    // e^{lc_i - lc_j} = e^{lc_i - lm} e^{lm - lc_j} around the block's 8th token
-    // (as the forward's diagonal blocks): 32 exponentials per channel and block
-    float qe[16], ke[16], be[16], fl[16], fr[16], lc[16], dq[16], dk[16], db[16];
-    float run = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const size_t o = tok0 + (size_t)(I * 16 + i) * HD + d;
-      qe[i] = to_f(a.q[o]);
-      ke[i] = to_f(a.k[o]);
-      be[i] = to_f(a.b[o]) * ke[i];
-      run += to_f(a.g[o]);
-      lc[i] = run;
-      dq[i] = dk[i] = db[i] = 0.f;
-    }
-    const float lm = lc[7];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      fr[i] = __expf(lm - lc[i]);
-      fl[i] = __expf(lc[i] - lm);
-      qe[i] *= a.scale * fl[i];   // scale q_i e^{lc_i - lm}
-      be[i] *= fl[i];             // (b k)_i e^{lc_i - lm}
-      ke[i] *= fr[i];             // k_j e^{lm - lc_j}
-    }
-    const int dblk = I * 16 * LD2 + I * 16;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-#pragma unroll
-      for (int j = 0; j <= i; ++j) {
-        const float aq = sDQK[dblk + i * LD2 + j];
-        dq[i] += aq * ke[j];
-        dk[j] += aq * qe[i];
-        if (j < i) {
-          const float ak = sDKK[dblk + i * LD2 + j];
-          dk[j] += ak * be[i];
-          db[i] += ak * ke[j];
-        }
-      }
-    }
-    // score gradients wrt q, b k, k: off-diagonal sums with their row factors plus
-    // the diagonal block, in place of RQ, RBK, RK
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int so = (I * 16 + i) * LD1 + d;
-      const float el = __expf(lc[i]), ek = __expf(totI - lc[i]);
-      sAQ[so] = a.scale * (el * sAQ[so] + dq[i] * fl[i]);
-      sABK[so] = el * sABK[so] + db[i] * fl[i];
-      sKH[so] = ek * sKH[so] + dk[i] * fr[i];
-    }
-  }
-
   // ---- chain rule, lane = token t of block I, channels chan(x) -----------------
-  // (gdn2_bwd.py:186-210; dqg, dkg, dkbd come from bwd_wy).  Wave I reads the
-  // score gradients of its own rows, written by its own lanes above.  dgc is summed
-  // from each token to the block end by a row scan; the block totals cross the
-  // waves through LDS.
+  // (gdn2_bwd.py:186-210; dqg, dkg, dkbd come from bwd_wy).  First the score
+  // gradients wrt q, b k, k: the off-diagonal sums (wave I reads its own rows,
+  // written by its own lanes above) with their row factors, plus the diagonal
+  // block's.  dgc is summed from each token to the block end by a row scan; the
+  // block totals cross the waves through LDS.
 #pragma unroll
   for (int j = 0; j < NDT; ++j) {
     const int c0 = j * 16 + lg * 4;
     const f32x4 qv = load4f(a.q + rowo + c0), kv = load4f(a.k + rowo + c0),
                 bv = load4f(a.b + rowo + c0);
     const f32x4 dqg = pdqg[j], dkg = pdkg[j], dkbd = pdkbd[j];
-    const f32x4 gq = load4f(&sAQ[t * LD1 + c0]), gbk = load4f(&sABK[t * LD1 + c0]),
-                gk = load4f(&sKH[t * LD1 + c0]);
+    const f32x4 rq = load4f(&sAQ[t * LD1 + c0]), rbk = load4f(&sABK[t * LD1 + c0]),
+                rk = load4f(&sKH[t * LD1 + c0]), lm = load4f(&sLm[I * GP + c0]);
     f32x4 lc = load4f(a.g + rowo + c0);   // in-block cumsum again, as at the start
 #pragma unroll
     for (int e = 0; e < 4; ++e) lc[e] = row_scan16(lc[e]);
-    f32x4 pre = {0.f, 0.f, 0.f, 0.f}, gl = {0.f, 0.f, 0.f, 0.f};
+    f32x4 pre = {0.f, 0.f, 0.f, 0.f}, gl = {0.f, 0.f, 0.f, 0.f}, totI;
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
       const f32x4 tm = load4f(&sTot[m * GP + c0]);
+      if (m == I) totI = tm;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         gl[e] += tm[e];
         pre[e] += m < I ? tm[e] : 0.f;
       }
+    }
+    f32x4 gq, gbk, gk;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float fl = __expf(lc[e] - lm[e]), fr = __expf(lm[e] - lc[e]);
+      const float el = __expf(lc[e]), ek = __expf(totI[e] - lc[e]);
+      gq[e] = a.scale * (el * rq[e] + fl * dqd[j][e]);
+      gbk[e] = el * rbk[e] + fl * dbd[j][e];
+      gk[e] = ek * rk[e] + fr * dkd[j][e];
     }
     f32x4 odq, odk, odb, suf;
 #pragma unroll
