@@ -995,6 +995,9 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   const int t = I * 16 + li;
   const size_t rowo = tok0 + (size_t)t * HD;
   f32x4 dqd[NDT], dbd[NDT], dkd[NDT];   // diagonal-block sums, token t, channels chan()
+  // this lane's in-block cumsum of g and q, k, b (token t, channels chan(x)), kept
+  // for the chain rule
+  float loc[DQ], qv[DQ], kv[DQ], bv[DQ];
   {
     const float* dq = a.DAQK + (size_t)cid * BT * BT;
     const float* dk = a.DAKK + (size_t)cid * BT * BT;
@@ -1005,7 +1008,6 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
       sq[u] = load4f(dq + r * BT + cc);
       sk[u] = load4f(dk + r * BT + cc);
     }
-    float loc[DQ], qv[DQ], kv[DQ], bv[DQ];
 #pragma unroll
     for (int j = 0; j < NDT; ++j) load_f<4>(a.g + rowo + j * 16 + lg * 4, &loc[j * 4]);
 #pragma unroll
@@ -1091,13 +1093,14 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   // operands of the chain rule below, loaded now so that they arrive while the
   // products run
   const size_t wrow_t = ((size_t)cid * BT + t) * D + ch0;
-  f32x4 pdqg[NDT], pdkg[NDT], pdkbd[NDT];
+  f32x4 pdqg[NDT], pdkg[NDT], pdkbd[NDT], psdh[NDT];
 #pragma unroll
   for (int j = 0; j < NDT; ++j) {
     const int c0 = j * 16 + lg * 4;
     pdqg[j] = load4f(a.DQG + wrow_t + c0);
     pdkg[j] = load4f(a.DKG + wrow_t + c0);
     pdkbd[j] = load4f(a.DKBD + wrow_t + c0);
+    psdh[j] = load4f(a.SDH + (size_t)cid * D + ch0 + c0);
   }
   lds_barrier();
 
@@ -1156,14 +1159,14 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
 #pragma unroll
   for (int j = 0; j < NDT; ++j) {
     const int c0 = j * 16 + lg * 4;
-    const f32x4 qv = load4f(a.q + rowo + c0), kv = load4f(a.k + rowo + c0),
-                bv = load4f(a.b + rowo + c0);
     const f32x4 dqg = pdqg[j], dkg = pdkg[j], dkbd = pdkbd[j];
     const f32x4 rq = load4f(&sAQ[t * LD1 + c0]), rbk = load4f(&sABK[t * LD1 + c0]),
                 rk = load4f(&sKH[t * LD1 + c0]), lm = load4f(&sLm[I * GP + c0]);
-    f32x4 lc = load4f(a.g + rowo + c0);   // in-block cumsum again, as at the start
-#pragma unroll
-    for (int e = 0; e < 4; ++e) lc[e] = row_scan16(lc[e]);
+    // channel c0 + e is x = 4j + e of the start's registers
+    const float* const lc = &loc[4 * j];
+    const float* const xq = &qv[4 * j];
+    const float* const xk = &kv[4 * j];
+    const float* const xb = &bv[4 * j];
     f32x4 pre = {0.f, 0.f, 0.f, 0.f}, gl = {0.f, 0.f, 0.f, 0.f}, totI;
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
@@ -1189,12 +1192,12 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
     for (int e = 0; e < 4; ++e) {
       const float gc = pre[e] + lc[e];
       const float eg = __expf(gc), ekg = __expf(gl[e] - gc);
-      const float kgv = kv[e] * ekg;
+      const float kgv = xk[e] * ekg;
       odq[e] = sanitize(dqg[e] * eg + gq[e]);
-      odk[e] = sanitize(dkbd[e] * bv[e] * eg + dkg[e] * ekg + gk[e] + gbk[e] * bv[e]);
-      odb[e] = sanitize(dkbd[e] * kv[e] * eg + gbk[e] * kv[e]);
-      const float dgc = dkbd[e] * bv[e] * kv[e] * eg + dqg[e] * qv[e] * eg - dkg[e] * kgv +
-                        qv[e] * gq[e] + bv[e] * kv[e] * gbk[e] - kv[e] * gk[e];
+      odk[e] = sanitize(dkbd[e] * xb[e] * eg + dkg[e] * ekg + gk[e] + gbk[e] * xb[e]);
+      odb[e] = sanitize(dkbd[e] * xk[e] * eg + gbk[e] * xk[e]);
+      const float dgc = dkbd[e] * xb[e] * xk[e] * eg + dqg[e] * xq[e] * eg - dkg[e] * kgv +
+                        xq[e] * gq[e] + xb[e] * xk[e] * gbk[e] - xk[e] * gk[e];
       suf[e] = row_suffix16(dgc);
       const float skg = row_suffix16(dkg[e] * kgv);   // lane 0: the block's sum
       if (li == 0) {
@@ -1213,7 +1216,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
 #pragma unroll
   for (int j = 0; j < NDT; ++j) {
     const int c0 = j * 16 + lg * 4;
-    const f32x4 sdh = load4f(a.SDH + (size_t)cid * D + ch0 + c0);
+    const f32x4 sdh = psdh[j];
     f32x4 gl = {0.f, 0.f, 0.f, 0.f}, tail = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
