@@ -87,9 +87,10 @@ __device__ __forceinline__ int own_block(int wv, int i) {
 // Channels are processed in panels of up to 128 (D = 256: two panels).  The
 // cumsum, decay factors, q_g / kg^T / (b k e^gc)^T and khat are per channel, so
 // steps 1-3 run once per panel; the score blocks Aqk, Akk are sums over
-// channels, accumulated over the panels in float32 LDS (sA, sQA) and stored
-// after the last one.  u = A (w v) is computed per panel of (w v)^T.  With one
-// panel (D <= 128) every score block is stored as soon as it is computed.
+// channels, accumulated over the panels (Akk in float32 LDS, sA; Aqk in the
+// registers of the wave that owns the row block) and stored after the last
+// one.  u = A (w v) is computed per panel of (w v)^T.  With one panel every
+// score block is stored as soon as it is computed.
 constexpr int prep_waves(int BT) { return BT >= 128 ? 8 : 4; }
 
 template <typename T, typename TG, int BT, int D>
@@ -100,7 +101,10 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   constexpr int PW = prep_waves(BT), NT = 64 * PW;   // waves, threads
   constexpr int NBW = NB / PW;            // row blocks per wave
   static_assert(NB % PW == 0 && (NBW == 1 || NBW == 2), "row blocks must split over waves");
-  constexpr int DP = D < 128 ? D : 128;   // channels per panel
+  // channels per panel: up to 128; float32 at chunk 64 and D = 128 takes two
+  // 64-channel panels, which brings its LDS under half a CU (two workgroups per
+  // CU, one loading while the other computes)
+  constexpr int DP = D < 128 ? D : (sizeof(T) == 4 && BT == 64 && D == 128 ? 64 : 128);
   constexpr int NPN = D / DP;             // panels
   static_assert(D % DP == 0 && DP <= NT, "panels must tile D");
   constexpr int NKD = DP / KS;            // k-groups over a panel's channels
@@ -115,7 +119,6 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   __shared__ __align__(16) T sR0[R0];         // khat [t][d]; later (w v)^T [d][t], one panel
   __shared__ __align__(16) T sKbdT[D * TT_LD];  // (b k e^gc)^T [d][t]
   __shared__ __align__(16) float sA[BT * A_LD];
-  __shared__ __align__(16) float sQA[NPN > 1 ? BT * A_LD : 4];  // Aqk partial sums
   // per-(block, channel) decay factors of steps 1-3, then (free after step 3)
   // the parked T = L_BA X_AA blocks of the inverse's doubling steps
   constexpr int PARK = 16 * 20;   // one parked 16 x 16 block, rows padded to 20 floats
@@ -177,6 +180,17 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
         ikn[i] = 1.f / fmaxf(sqrtf(sk), 1e-12f);
       }
     }
+  }
+
+  // Aqk partial sums over the panels: the diagonal block and the blocks J < I of
+  // this wave's row blocks (several panels only, all at chunk 64)
+  static_assert(NPN == 1 || NB == 4, "panel sums of Aqk are held for 4 row blocks");
+  f32x4 qdiag[NBW], qoff[NBW][NB];
+#pragma unroll
+  for (int i = 0; i < NBW; ++i) {
+    qdiag[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int J = 0; J < NB; ++J) qoff[i][J] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
 #pragma unroll
@@ -343,11 +357,11 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
         store4(&sA[e0], sk);
       } else {
         if (pn > 0) {
-          sq += load4f(&sQA[e0]);
+          sq += qdiag[i];
           sk += load4f(&sA[e0]);
         }
         if (last_pn) store4(aqk + (size_t)t * BT + I * 16 + 4 * lg, sq);
-        else store4(&sQA[e0], sq);
+        else qdiag[i] = sq;
         store4(&sA[e0], sk);
       }
     }
@@ -361,7 +375,8 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
       float F[DQ];
 #pragma unroll
       for (int x = 0; x < DQ; ++x) F[x] = 1.f;
-      for (int J = I - 1; J >= 0; --J) {
+      // block pair (I, J), J < I, in descending J (F carries the decay between)
+      auto pair = [&](int J, f32x4& qp) __attribute__((always_inline)) {
         f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < NKD; ++j) {
@@ -382,15 +397,22 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
         } else {
           f32x4 sq = accq * a.scale;
           if (pn > 0) {
-            sq += load4f(&sQA[e0]);
+            sq += qp;
             acck += load4f(&sA[e0]);
           }
           if (last_pn) store4(aqk + (size_t)t * BT + J * 16 + 4 * lg, sq);
-          else store4(&sQA[e0], sq);
+          else qp = sq;
           store4(&sA[e0], acck);
         }
 #pragma unroll
         for (int x = 0; x < DQ; ++x) F[x] *= sETot[J * DP + chan(x)];
+      };
+      if constexpr (one) {
+        for (int J = I - 1; J >= 0; --J) pair(J, qoff[i][0]);   // qoff unused here
+      } else {
+#pragma unroll
+        for (int J = NB - 2; J >= 0; --J)   // static J: the sums stay in registers
+          if (J < I) pair(J, qoff[i][J]);
       }
     }
   }
