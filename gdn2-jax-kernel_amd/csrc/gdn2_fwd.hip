@@ -92,9 +92,15 @@ __device__ __forceinline__ int own_block(int wv, int i) {
 // one.  u = A (w v) is computed per panel of (w v)^T.  With one panel every
 // score block is stored as soon as it is computed.
 constexpr int prep_waves(int BT) { return BT >= 128 ? 8 : 4; }
+// Workgroups per CU the register allocation is held to: three for bfloat16 at
+// chunk 64 and D = 128 (50 KB of LDS each), else what the kernel needs.
+constexpr int prep_min_blocks(int esize, int BT, int D) {
+  return esize == 2 && BT == 64 && D == 128 ? 3 : 1;
+}
 
 template <typename T, typename TG, int BT, int D>
-__global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> a) {
+__global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T), BT, D))
+    fwd_prep(PrepArgs<T, TG> a) {
   using Op = typename Tr<T>::Op;
   constexpr int KC = Tr<T>::KC, KS = Tr<T>::KS;
   constexpr int NB = BT / 16;             // 16-token row blocks
@@ -104,7 +110,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT)) fwd_prep(PrepArgs<T, TG> 
   // channels per panel: up to 128; float32 at chunk 64 and D = 128 takes two
   // 64-channel panels, which brings its LDS under half a CU (two workgroups per
   // CU, one loading while the other computes)
-  constexpr int DP = D < 128 ? D : (sizeof(T) == 4 && BT == 64 && D == 128 ? 64 : 128);
+  constexpr int DP = D < 128 ? D : (BT == 64 && D == 128 ? 64 : 128);
   constexpr int NPN = D / DP;             // panels
   static_assert(D % DP == 0 && DP <= NT, "panels must tile D");
   constexpr int NKD = DP / KS;            // k-groups over a panel's channels
