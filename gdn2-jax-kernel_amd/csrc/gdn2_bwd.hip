@@ -472,7 +472,11 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
 //   qdot = scale do^T qg                [e][d]   ((scale qg^T do)^T)
 // with do, v_new^T, Aqk and qg staged once in LDS as float32.  Wave w owns the
 // 16-row block w of dAqk and of Aqk^T do, and row blocks 2w, 2w+1 (over e) of
-// qdot (D = 128; one block per wave at D = 64).
+// qdot (D = 128; one block per wave at D = 64).  do stays in LDS throughout; the
+// second operand of each product takes one region in turn (v_new^T, then Aqk,
+// then qg, each loaded into registers ahead and stored after a barrier), so the
+// kernel needs 67 KB of LDS at D = 128: two workgroups per CU, one streaming
+// while the other computes.
 // ============================================================================
 template <typename T>
 struct B2Args {
@@ -487,15 +491,18 @@ struct B2Args {
 };
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256) bwd_b2(B2Args<T> a) {
+__global__ void __launch_bounds__(256, 2) bwd_b2(B2Args<T> a) {
   constexpr int BT = 64, NDT = D / 16, NKT = BT / 16;
   constexpr int LDO = D + 4, LDV = BT + 4, LDA = BT + 4, LDQ = D + 4;
   constexpr int BF = sizeof(T) == 2;
   constexpr int QB = NDT / 4;               // qdot row blocks per wave
+  constexpr int RV = D * LDV, RA = BT * LDA, RQ = BT * LDQ;
+  constexpr int RS = RV > RQ ? (RV > RA ? RV : RA) : (RQ > RA ? RQ : RA);
   __shared__ __align__(16) float sDo[BT * LDO];
-  __shared__ __align__(16) float sV[D * LDV];
-  __shared__ __align__(16) float sA[BT * LDA];
-  __shared__ __align__(16) float sQ[BT * LDQ];
+  __shared__ __align__(16) float sR[RS];   // v_new^T [e][s], then Aqk [t][s], then qg [t][d]
+  float* const sV = sR;
+  float* const sA = sR;
+  float* const sQ = sR;
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: MFMA under branches
   const int cid = blockIdx.x;
@@ -512,19 +519,19 @@ __global__ void __launch_bounds__(256) bwd_b2(B2Args<T> a) {
     return y;
   };
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  const GMat mQ{a.Qg, BF, D, 0, 0};
+  Staged s1, s2;   // s1: do, then qg (stored after the dvp^T product)
   {
     // do rows are (B,T,H,D) token rows: pitch H*D
     const GMat mDo{a.dout, 0, (int)HD, 0, 0};
     const GMat mV{a.VnT, BF, BT, 0, BF};
-    const GMat mQ{a.Qg, BF, D, 0, 0};
     // Aqk: blocks right of the diagonal block are unwritten; causal mask on load
     const GMat mA{a.Aqk, BF, BT, 1, 0};
-    Staged s1, s2;
     stage_load(s1, mDo, tok0, BT, D, tid);
     stage_load(s2, mV, (size_t)cid * D * BT, D, BT, tid);
     stage_store(sDo, LDO, s1, mDo, BT, D, 0, 0, false, tid);
     stage_store(sV, LDV, s2, mV, D, BT, 0, 0, false, tid);
-    // qg and Aqk are in flight while dAqk is formed (LDS-only barrier)
+    // qg and Aqk are in flight while dAqk is formed (LDS-only barriers)
     stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
     stage_load(s2, mA, (size_t)cid * BT * BT, BT, BT, tid);
     lds_barrier();
@@ -550,7 +557,7 @@ __global__ void __launch_bounds__(256) bwd_b2(B2Args<T> a) {
           o[row * BT + s2] = s2 <= row ? acc[st][r] : 0.f;
         }
     }
-    stage_store(sQ, LDQ, s1, mQ, BT, D, 0, 0, false, tid);
+    lds_barrier();  // every wave is done with v_new^T
     stage_store(sA, LDA, s2, mA, BT, BT, 0, 0, false, tid);
   }
   lds_barrier();
@@ -573,6 +580,9 @@ __global__ void __launch_bounds__(256) bwd_b2(B2Args<T> a) {
     for (int nt = 0; nt < NDT; ++nt)
       store4(o + (size_t)(nt * 16 + li) * BT + wv * 16 + 4 * lg, acc[nt]);
   }
+  lds_barrier();  // every wave is done with Aqk
+  stage_store(sQ, LDQ, s1, mQ, BT, D, 0, 0, false, tid);
+  lds_barrier();
   // qdot[e][d] = scale sum_t do[t][e] qg[t][d]
   {
 #pragma unroll
