@@ -265,8 +265,9 @@ def extras(gp, steps=10, warmup=3):
     """The paths beyond the headline, each timed on the GPU in the same run:
     configs[4] (1 x 131072 x 8 heads, segmented state scan), the forward with
     the input activations fused (vs torch activations + forward), a
-    variable-length batch with the headline's token count, D = 256, a partial
-    last chunk, and the decode step (state read + written per token)."""
+    variable-length batch with the headline's token count, D = 256, the bfloat16
+    training step, a partial last chunk, and the decode step (state read +
+    written per token)."""
     import torch
     f = torch.nn.functional
     res = {}
@@ -331,6 +332,15 @@ def extras(gp, steps=10, warmup=3):
     res["d256_train"] = {"shape": "B8 T8192 H3 D256 float32, forward + backward", "ms": ms,
                          "tokens_per_s": B * T / (ms * 1e-3)}
     del x256, x256f, do256
+    # bfloat16 training step at the headline shape (chunk 64: bf16 residuals, float32
+    # backward arithmetic, gradients in the input dtypes)
+    xb = [x.detach().requires_grad_(True) for x in dist((B, T, H, D))]
+    dob = r((B, T, H, D))
+    ms = _time(lambda: torch.autograd.grad(
+        [gp.gdn2_pallas_forward_trainable(*xb, D ** -0.5)[0]], xb, [dob]), 5, 2)
+    res["bf16_train"] = {"shape": "B8 T8192 H6 D128 bf16 inputs (fp32 g), forward + backward",
+                         "ms": ms, "tokens_per_s": B * T / (ms * 1e-3)}
+    del xb, dob
     # T % BT != 0: 8100 tokens per sequence, the last chunk of each 36 tokens short
     xp = dist((B, 8100, H, D))
     ms = _time(lambda: gp.gdn2_pallas_forward(*xp, D ** -0.5), steps, warmup)

@@ -117,21 +117,21 @@ struct BStateArgs {
 // for bfloat16 residuals, chained column order) LDS read per element, which
 // the XOR swizzle of the 16-byte chunks keeps free of bank conflicts.
 //
-// K-split (KS = 2, float32 residuals), as in fwd_state: two compute waves per
+// K-split (KS = 2; bfloat16 residuals only up to D = 128, where its registers
+// fit), as in fwd_state: two compute waves per
 // 16-column slice, each holding half of dh's rows; the halves of kg dh are
 // exchanged through LDS (barrier X, after B).  The exchange buffer takes the
 // place of the qdot gather: each compute wave then loads its own 16-byte qdot
 // pieces (four per step) straight from global memory one step ahead, hitting
 // L2 behind the producers' touch.
 template <typename T, int D>
-constexpr int bstate_ksplit() { return sizeof(T) == 4 ? 2 : 1; }
+constexpr int bstate_ksplit() { return sizeof(T) == 4 || D <= 128 ? 2 : 1; }
 
 template <typename T, int BT, int D, int NW, int NP, int KS>
 __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a) {
   constexpr int NB = BT / 16, NDT = D / 16;
   constexpr int NCW = NW * KS, NDH = NDT / KS;
-  static_assert(KS == 1 || (sizeof(T) == 4 && NDT % KS == 0 && NB % KS == 0),
-                "K-split: float32 only");
+  static_assert(KS == 1 || (NDT % KS == 0 && NB % KS == 0), "K-split must tile dh and dv_new");
   constexpr int NVS = D / (16 * NW);
   constexpr int WBYTES = BT * D * (int)sizeof(T);
   constexpr int BUF = 2 * WBYTES;
