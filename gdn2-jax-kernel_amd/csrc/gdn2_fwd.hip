@@ -84,7 +84,8 @@ __device__ __forceinline__ int own_block(int wv, int i) {
 // exponentials are evaluated (e^{loc}, e^{T_I - loc} and the two diagonal-block
 // factors); the block-level factors e^{P_{I-1}}, e^{S_{I+1}} come from LDS.
 //
-// Channels are processed in panels of up to 128 (D = 256: two panels).  The
+// Channels are processed in panels of up to 128 (D = 256: two panels; chunk 64
+// at D = 128: two panels of 64).  The
 // cumsum, decay factors, q_g / kg^T / (b k e^gc)^T and khat are per channel, so
 // steps 1-3 run once per panel; the score blocks Aqk, Akk are sums over
 // channels, accumulated over the panels (Akk in float32 LDS, sA; Aqk in the
@@ -107,9 +108,9 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
   constexpr int PW = prep_waves(BT), NT = 64 * PW;   // waves, threads
   constexpr int NBW = NB / PW;            // row blocks per wave
   static_assert(NB % PW == 0 && (NBW == 1 || NBW == 2), "row blocks must split over waves");
-  // channels per panel: up to 128; float32 at chunk 64 and D = 128 takes two
-  // 64-channel panels, which brings its LDS under half a CU (two workgroups per
-  // CU, one loading while the other computes)
+  // channels per panel: up to 128; chunk 64 at D = 128 takes two 64-channel
+  // panels, which brings the LDS under half a CU (float32: two workgroups per CU,
+  // bfloat16: three, one loading while the others compute)
   constexpr int DP = D < 128 ? D : (BT == 64 && D == 128 ? 64 : 128);
   constexpr int NPN = D / DP;             // panels
   static_assert(D % DP == 0 && DP <= NT, "panels must tile D");
