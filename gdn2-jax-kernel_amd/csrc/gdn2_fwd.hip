@@ -137,11 +137,16 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
   float* const sF1 = sSmall + 3 * NB * DP;     // e^{S_{I+1}}
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  // Chunks are dealt last-first across all (b,h): the state scan reads chunk 0
-  // first, and that is then the most recently written (still in the last-level
-  // cache).  The grid is (b,h) pairs x N chunks.
-  const int nbh = gridDim.x / a.N;
-  const int cid = (blockIdx.x % nbh) * a.N + (a.N - 1 - blockIdx.x / nbh);
+  // Chunk order (the grid is (b,h) pairs x N chunks).  bfloat16: dealt last-first
+  // across all (b,h), so the state scan's first chunks are the most recently
+  // written (still in the last-level cache): the latency-bound bf16 scan gains 5 %.
+  // float32: (b,h)-major, neighbouring workgroups on neighbouring memory; its scan
+  // is bound by the MFMA chain, and the last-first order only cost this kernel 5 %.
+  int cid = blockIdx.x;
+  if constexpr (sizeof(T) == 2) {
+    const int nbh = gridDim.x / a.N;
+    cid = (blockIdx.x % nbh) * a.N + (a.N - 1 - blockIdx.x / nbh);
+  }
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
   const size_t HD = (size_t)a.H * D;
   const ChunkRows cr = chunk_rows(a.cstart, c, bb, a.T_len, BT);
