@@ -77,6 +77,67 @@ def kernel_table(dtype_bytes, chunk):
     }
 
 
+# Compulsory HBM bytes per token-head of the bf16 forward: q,k,v,w,b bf16 and g
+# fp32 read once, out fp32 written once (h_final adds 4*D*D per (b,h), under
+# 0.1 % here).  Algorithmic flops per token-head at chunk C.
+def compulsory_fwd_bytes():
+    return 5 * 2 * D + 4 * D + 4 * D + 4 * D * D / T
+
+
+def fwd_flops(C):
+    return 5 * C * D + 6 * D * D + C * C / 3
+
+
+def roofline(per, ms):
+    """The headline roofline on compulsory bytes: the forward must move
+    compulsory_fwd_bytes() per token-head (906 MB at B8 T8192 H6 D128) and is
+    HBM-bound (about 80 flop/B against a bf16 ridge of about 315).  `achieved`
+    divides those bytes by the dominant kernel's event time; `end_to_end` by
+    the whole forward's time (the lower bound 906 MB / 8 TB/s over ms_per_step).
+    `kernel_io` keeps the dominant kernel's own algorithmic traffic (its inputs
+    and workspace tiles), and `traffic` the counter-measured bytes per launch."""
+    th = B * T * H
+    comp = compulsory_fwd_bytes() * th
+    dom = max(per, key=per.get)
+    ksec = per[dom] * 1e-3
+    roof = {"bound": "hbm", "achieved": comp / ksec / 1e9, "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s", "kernel": dom, "compulsory_bytes": comp}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof["end_to_end"] = {"lower_bound_ms": comp / HBM_PEAK * 1e3,
+                          "frac": comp / HBM_PEAK / (ms * 1e-3)}
+    tab = kernel_table(2, CHUNK)
+    if dom in tab:
+        kb = tab[dom]["bytes"] * th
+        roof["kernel_io"] = {"bytes": kb, "GB/s": kb / ksec / 1e9, "frac": kb / ksec / HBM_PEAK}
+    roof["traffic"] = None
+    pmc = ROOT / "profiles" / f"traffic_{dom}_b8t8192h6d128_bf16.json"
+    if pmc.exists():
+        roof["traffic"] = json.loads(pmc.read_text()).get("bytes_per_launch")
+    return roof
+
+
+def train_roofline(tms):
+    """configs[3] (float32 fwd+bwd): algorithmic flops per token-head (forward
+    5CD + 6D^2 + C^2/3, backward twice that) on the float32 MFMA peak, against
+    compulsory bytes (80 D per token-head) on HBM; the larger time is the bound.
+    `frac` uses C = 128 (the published lower bound, 219 GFLOP -> 1.392 ms);
+    `at_chunk_64` the same formula at the chunk this path runs (166 GFLOP)."""
+    th = B * T * H
+    nbytes = 80 * D * th
+
+    def at(C):
+        flops = 3 * fwd_flops(C) * th
+        t_mfma, t_hbm = flops / (FP32_MFMA_PEAK * 1e12), nbytes / HBM_PEAK
+        lb = max(t_mfma, t_hbm)
+        return {"bound": "mfma" if t_mfma >= t_hbm else "hbm", "flops": flops,
+                "lower_bound_ms": lb * 1e3, "frac": lb / (tms * 1e-3)}
+
+    r = at(128)
+    r.update({"bytes": nbytes, "achieved_tflops": r["flops"] / (tms * 1e-3) / 1e12,
+              "peak_tflops": FP32_MFMA_PEAK, "at_chunk_64": at(TRAIN_CHUNK)})
+    return r
+
+
 def time_forward(gp, xs, steps, warmup, chunk):
     import torch
     from gdn2_package import _lib
@@ -332,13 +393,15 @@ def extras(gp, steps=10, warmup=3):
     res["d256_train"] = {"shape": "B8 T8192 H3 D256 float32, forward + backward", "ms": ms,
                          "tokens_per_s": B * T / (ms * 1e-3)}
     del x256, x256f, do256
-    # bfloat16 training step at the headline shape (chunk 64: bf16 residuals, float32
-    # backward arithmetic, gradients in the input dtypes)
+    # bfloat16 training step at the headline shape (the inputs are widened and run
+    # through the float32 forward and backward, as the reference upcasts; gradients
+    # in the input dtypes)
     xb = [x.detach().requires_grad_(True) for x in dist((B, T, H, D))]
     dob = r((B, T, H, D))
     ms = _time(lambda: torch.autograd.grad(
         [gp.gdn2_pallas_forward_trainable(*xb, D ** -0.5)[0]], xb, [dob]), 5, 2)
-    res["bf16_train"] = {"shape": "B8 T8192 H6 D128 bf16 inputs (fp32 g), forward + backward",
+    res["bf16_train"] = {"shape": "B8 T8192 H6 D128 bf16 inputs (fp32 g), forward + backward "
+                                  "computed in float32, bf16 gradients",
                          "ms": ms, "tokens_per_s": B * T / (ms * 1e-3)}
     del xb, dob
     # T % BT != 0: 8100 tokens per sequence, the last chunk of each 36 tokens short
@@ -359,10 +422,25 @@ def extras(gp, steps=10, warmup=3):
     return res
 
 
-def cpu_baseline(min_seconds=10.0):
-    """The numpy restatement of the reference's chunked forward (kernels A-D
-    with the 3-D decay tensor, float32) on one batch element of the headline
-    workload (B=1, T, H, D as above), repeated until `min_seconds` have passed."""
+def _cpu_model():
+    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(min_seconds=10.0, bwd_tokens=1024, bwd_min_seconds=8.0):
+    """The numpy restatement of the reference's chunked algorithm on this host:
+    the forward (kernels A-D with the 3-D decay tensor, float32) on one batch
+    element of the headline workload (B=1, T, H, D as above), repeated until
+    `min_seconds` have passed; and the training step of configs[3] (float32
+    forward recompute + B1-B5, oracle.chunked_bwd, chunk 64) on a bounded
+    prefix of one batch element (`bwd_tokens` tokens of the 8192, all 6 heads),
+    scaled linearly -- the work is linear in T."""
     import numpy as np
     from oracle import gdn2_oracle as O
     try:
@@ -378,11 +456,29 @@ def cpu_baseline(min_seconds=10.0):
         dt = time.perf_counter() - t0
         if dt >= min_seconds:
             break
+    xb = [x[:, :bwd_tokens] for x in xs]
+    do = np.random.default_rng(1).standard_normal(xb[0].shape).astype(np.float32)
+    bruns, t1 = 0, time.perf_counter()
+    while True:
+        O.chunked_bwd(*xb, D ** -0.5, do, BT=TRAIN_CHUNK, clip=True, dtype=np.float32)
+        bruns += 1
+        bdt = time.perf_counter() - t1
+        if bdt >= bwd_min_seconds:
+            break
+    btps = bruns * bwd_tokens / bdt
     return {"value": runs * T / dt, "unit": "tokens/s", "cores": int(cores), "kind": "port",
+            "cpu": _cpu_model(), "os_cpu_count": os.cpu_count(),
             "sample": f"{runs} x forward of one batch element (B=1 T={T} H={H} D={D} "
                       f"BT={CHUNK}, float32) of the headline workload, numpy restatement of "
                       f"gdn2_fwd.py kernels A-D (oracle.chunked_fwd), {dt:.1f} s; "
-                      f"tokens/s comparable to value (same T, H, D)"}
+                      f"tokens/s comparable to value (same T, H, D)",
+            "fwd_bwd": {"value": btps, "unit": "tokens/s",
+                        "ms_per_step_scaled": B * T / btps * 1e3,
+                        "sample": f"{bruns} x forward + backward (oracle.chunked_bwd: recompute, "
+                                  f"B2, B1, B3, B4, B5; float32, chunk {TRAIN_CHUNK}) of "
+                                  f"B=1 T={bwd_tokens} H={H} D={D}, the first {bwd_tokens} "
+                                  f"tokens of one batch element of configs[3], {bdt:.1f} s; "
+                                  f"tokens/s comparable to train.tokens_per_s"}}
 
 
 COPY_BYTES = 1 << 30           # calibration copy: reads and writes this many bytes
@@ -498,25 +594,7 @@ def main():
     tokens = B * T
     value = tokens / (ms * 1e-3)
 
-    tab = kernel_table(2, CHUNK)
-    dom = max(per, key=per.get)
-    th = B * T * H
-    kb = tab[dom]["bytes"] * th
-    kf = tab[dom]["flops"] * th
-    t_hbm, t_mfma = kb / HBM_PEAK, kf / MFMA_PEAK["bf16"]
-    ksec = per[dom] * 1e-3
-    if t_hbm >= t_mfma:
-        roof = {"bound": "hbm", "achieved": kb / ksec / 1e9, "peak": HBM_PEAK / 1e9,
-                "unit": "GB/s"}
-    else:
-        roof = {"bound": "mfma", "achieved": kf / ksec / 1e12, "peak": MFMA_PEAK["bf16"] / 1e12,
-                "unit": "TFLOP/s"}
-    roof["frac"] = roof["achieved"] / roof["peak"]
-    roof["kernel"] = dom
-    roof["traffic"] = None
-    pmc = ROOT / "profiles" / f"traffic_{dom}_b8t8192h6d128_bf16.json"
-    if pmc.exists():
-        roof["traffic"] = json.loads(pmc.read_text()).get("bytes_per_launch")
+    roof = roofline(per, ms)
 
     del xs
     torch.cuda.empty_cache()
@@ -528,7 +606,7 @@ def main():
             kms, mfma = train_kernels(gp, xs32)
             train = {"config": "B8 T8192 H6 D128 float32, forward + backward (trainable)",
                      "ms_per_step": tms, "tokens_per_s": tokens / (tms * 1e-3),
-                     "kernels_ms": kms, "mfma": mfma}
+                     "kernels_ms": kms, "mfma": mfma, "roofline": train_roofline(tms)}
             del xs32
         except Exception as e:  # backward entry point not available in this build
             train = {"error": f"{type(e).__name__}: {e}"[:200]}

@@ -192,7 +192,7 @@ static size_t fwd_ws_need(int B, int T, int H, int D, int BT, int in_dtype, int 
   const int N = chunks_per_seq(T, BT);
   const int S = state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
   return fwd_layout(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype),
-                    S > 1 ? (size_t)B * H * S : 0).total;
+                    S > 1 ? (size_t)B * H * S : 0, !(flags & kFwdNoARegion)).total;
 }
 
 size_t gdn2_fwd_workspace_bytes_ex(int B, int T, int H, int D, int BT, int in_dtype, int flags) {
@@ -206,11 +206,15 @@ size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
   return gdn2_fwd_workspace_bytes_ex(B, T, H, D, BT, in_dtype, 0);
 }
 
-static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
-                      int g_dtype, const void* q, const void* k, const void* v, const void* w,
-                      const void* b, const void* g, const float* h0, float scale, float* out,
-                      float* h_final, void* ws, size_t ws_bytes, float* a_dbg,
-                      int flags) {
+}  // extern "C"
+
+namespace gdn2 {
+// The forward behind gdn2_fwd, gdn2_fwd_debug and gdn2_fwd_noalloc; `flags` may
+// carry kFwdNoARegion here (the public entry points clear it).
+int fwd_entry(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
+              const void* q, const void* k, const void* v, const void* w, const void* b,
+              const void* g, const float* h0, float scale, float* out, float* h_final,
+              void* ws, size_t ws_bytes, float* a_dbg, int flags) {
   EventScope scope;
   int rc = validate_fwd(B, T, H, D, BT, in_dtype, g_dtype, flags);
   if (rc) return rc;
@@ -226,12 +230,23 @@ static int fwd_common(void* stream, int B, int T, int H, int D, int BT, int in_d
                           (const Varlen*)nullptr);
 }
 
+// Workspace bytes of the forward for `flags` (kFwdNoARegion included), or 0 for
+// shapes the forward rejects.
+size_t fwd_workspace_need(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
+                          int flags) {
+  if (validate_fwd(B, T, H, D, BT, in_dtype, g_dtype, flags) != GDN2_OK) return 0;
+  return fwd_ws_need(B, T, H, D, BT, in_dtype, flags);
+}
+}  // namespace gdn2
+
+extern "C" {
+
 int gdn2_fwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
              const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, const float* h0, float scale, float* out, float* h_final,
              void* ws, size_t ws_bytes, int flags) {
-  return fwd_common(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale,
-                    out, h_final, ws, ws_bytes, nullptr, flags);
+  return fwd_entry(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale,
+                   out, h_final, ws, ws_bytes, nullptr, flags & ~kFwdNoARegion);
 }
 
 int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
@@ -239,8 +254,8 @@ int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtyp
                    const void* b, const void* g, const float* h0, float scale, float* out,
                    float* h_final, void* ws, size_t ws_bytes, float* a_out) {
   if (!a_out && T > 0) return GDN2_ERR_NULL;
-  return fwd_common(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale,
-                    out, h_final, ws, ws_bytes, a_out, GDN2_FWD_PARTIAL_CHUNK);
+  return fwd_entry(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale,
+                   out, h_final, ws, ws_bytes, a_out, GDN2_FWD_PARTIAL_CHUNK);
 }
 
 size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {

@@ -176,11 +176,9 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
   if (a.cu) {
     const int sg = unit % a.S;
     bh = unit / a.S;
-    c0 = a.cu[sg];
-    c0 = c0 < 0 ? 0 : (c0 > a.N ? a.N : c0);
-    n = a.cu[sg + 1] - c0;
-    n = n < a.N - c0 ? n : a.N - c0;
-    n = n > 0 ? n : 0;
+    const SeqChunks sc = seq_chunks(a.cu, sg, a.N);
+    c0 = sc.c0;
+    n = sc.n;
     st_idx = (size_t)sg * a.H + bh;
   }
   // step i works on chunk c0 + n-1-i
@@ -554,7 +552,7 @@ __global__ void __launch_bounds__(256, 2) bwd_b2(B2Args<T> a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = wv * 16 + 4 * lg + r, s2 = st * 16 + li;
-          o[row * BT + s2] = s2 <= row ? acc[st][r] : 0.f;
+          o[row * BT + s2] = s2 <= row ? sanitize(acc[st][r]) : 0.f;   // gdn2_bwd.py:95
         }
     }
     lds_barrier();  // every wave is done with v_new^T
@@ -578,7 +576,7 @@ __global__ void __launch_bounds__(256, 2) bwd_b2(B2Args<T> a) {
     float* o = a.DVPT + (size_t)cid * D * BT;
 #pragma unroll
     for (int nt = 0; nt < NDT; ++nt)
-      store4(o + (size_t)(nt * 16 + li) * BT + wv * 16 + 4 * lg, acc[nt]);
+      store4(o + (size_t)(nt * 16 + li) * BT + wv * 16 + 4 * lg, sanitize4(acc[nt]));  // :96
   }
   lds_barrier();  // every wave is done with Aqk
   stage_store(sQ, LDQ, s1, mQ, BT, D, 0, 0, false, tid);
@@ -838,7 +836,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int s2 = st2 * 16 + li;
-        sR4[orow(r) * LD4 + s2] = s2 < orow(r) ? ada[st2][r] : 0.f;
+        sR4[orow(r) * LD4 + s2] = s2 < orow(r) ? sanitize(ada[st2][r]) : 0.f;   // :168
       }
   }
   lds_barrier();   // dA complete; (b k e^gc | w v) no longer read
@@ -897,7 +895,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 #pragma unroll
     for (int nt = 0; nt < NKT; ++nt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sR4[orow(r) * LD4 + nt * 16 + li] = atm[nt][r];
+      for (int r = 0; r < 4; ++r) sR4[orow(r) * LD4 + nt * 16 + li] = sanitize(atm[nt][r]);  // :174
   }
   lds_barrier();
 
@@ -918,7 +916,7 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n2 = nt * 16 + li;
-        dakk[orow(r) * BT + n2] = n2 < orow(r) ? -aak[nt][r] : 0.f;
+        dakk[orow(r) * BT + n2] = n2 < orow(r) ? sanitize(-aak[nt][r]) : 0.f;   // :209
       }
   }
 }
@@ -977,6 +975,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
   __shared__ __align__(16) float sETot[NB * GP];   // e^{T_m}, then per-block sums of dgc
   __shared__ __align__(16) float sSkg[NB * GP];    // per-block sums of dkg kg
   __shared__ __align__(16) float sLm[NB * GP];     // in-block cumsum at the block's 8th token
+  __shared__ __align__(16) float sB3L[GP];         // B3's dgc at the chunk's last token
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   int cid, pn;
@@ -1203,12 +1202,17 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
       const float gc = pre[e] + lc[e];
       const float eg = __expf(gc), ekg = __expf(gl[e] - gc);
       const float kgv = xk[e] * ekg;
-      odq[e] = sanitize(dqg[e] * eg + gq[e]);
-      odk[e] = sanitize(dkbd[e] * xb[e] * eg + dkg[e] * ekg + gk[e] + gbk[e] * xb[e]);
-      odb[e] = sanitize(dkbd[e] * xk[e] * eg + gbk[e] * xk[e]);
-      const float dgc = dkbd[e] * xb[e] * xk[e] * eg + dqg[e] * xq[e] * eg - dkg[e] * kgv +
-                        xq[e] * gq[e] + xb[e] * xk[e] * gbk[e] - xk[e] * gk[e];
-      suf[e] = row_suffix16(dgc);
+      // B3's and B4's parts are sanitized as each kernel's output, then their
+      // sum (gdn2_bwd.py:212-218, 333-338; gdn2_pipeline.py:121-133)
+      odq[e] = sanitize(sanitize(dqg[e] * eg) + sanitize(gq[e]));
+      odk[e] = sanitize(sanitize(dkbd[e] * xb[e] * eg + dkg[e] * ekg) +
+                        sanitize(gk[e] + gbk[e] * xb[e]));
+      odb[e] = sanitize(sanitize(dkbd[e] * xk[e] * eg) + sanitize(gbk[e] * xk[e]));
+      const float dgc3 = dkbd[e] * xb[e] * xk[e] * eg + dqg[e] * xq[e] * eg - dkg[e] * kgv;
+      const float dgc4 = xq[e] * gq[e] + xb[e] * xk[e] * gbk[e] - xk[e] * gk[e];
+      // the last token's B3 part still lacks the g_last terms: kept for the end
+      if (I == NB - 1 && li == 15) sB3L[c0 + e] = dgc3;
+      suf[e] = row_suffix16(sanitize(dgc3) + sanitize(dgc4));
       const float skg = row_suffix16(dkg[e] * kgv);   // lane 0: the block's sum
       if (li == 0) {
         sETot[I * GP + c0 + e] = suf[e];
@@ -1221,13 +1225,15 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
     store4(a.db + rowo + c0, odb);
   }
   lds_barrier();
-  // dg[t] = sum_{s >= t} dgc[s] + sum_t dkg kg + e^{gl} sum_e dh' h  (the last two
-  // enter at the chunk's last token, gdn2_bwd.py:196-199)
+  // dg[t] = sum_{s >= t} dgc[s], where the chunk's last token also carries
+  // dgl = sum_t dkg kg + e^{gl} sum_e dh' h (gdn2_bwd.py:196-201) inside its B3
+  // part: that part was summed as sanitize(b3), and becomes sanitize(b3 + dgl)
+  // -- exactly b3 + dgl whenever neither saturates
 #pragma unroll
   for (int j = 0; j < NDT; ++j) {
     const int c0 = j * 16 + lg * 4;
-    const f32x4 sdh = psdh[j];
-    f32x4 gl = {0.f, 0.f, 0.f, 0.f}, tail = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 sdh = psdh[j], b3l = load4f(&sB3L[c0]);
+    f32x4 gl = {0.f, 0.f, 0.f, 0.f}, skg = {0.f, 0.f, 0.f, 0.f}, later = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
       const f32x4 tm = load4f(&sTot[m * GP + c0]), sk = load4f(&sSkg[m * GP + c0]),
@@ -1235,13 +1241,20 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         gl[e] += tm[e];
-        tail[e] += sk[e] + (m > I ? bt[e] : 0.f);
+        skg[e] += sk[e];
+        later[e] += m > I ? bt[e] : 0.f;
       }
     }
     const f32x4 suf = load4f(&sAQ[t * LD1 + c0]);
     f32x4 odg;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) odg[e] = sanitize(suf[e] + tail[e] + __expf(gl[e]) * sdh[e]);
+    for (int e = 0; e < 4; ++e) {
+      const float dgl = skg[e] + __expf(gl[e]) * sdh[e];
+      const float b3 = b3l[e], b3g = b3 + dgl;
+      const float corr = (fabsf(b3) < kClip && fabsf(b3g) < kClip)
+                             ? dgl : sanitize(b3g) - sanitize(b3);
+      odg[e] = sanitize(suf[e] + later[e] + corr);
+    }
     store4(a.dg + rowo + c0, odg);
   }
 }
@@ -1274,6 +1287,7 @@ struct WOut {
   int mask;
   float alpha;
   int accum;
+  int sat;                  // sanitize the stored value (a stage output the reference clips)
 };
 struct WGemmArgs {
   WMat A, B;
@@ -1360,7 +1374,7 @@ __global__ void __launch_bounds__(256) chunk_gemm(WGemmArgs a) {
       if ((a.C.mask == 1 && n > m) || (a.C.mask == 2 && n >= m)) val = 0.f;
       float* dst = a.C.p + offC + (size_t)m * a.C.ld + n;
       if (a.C.accum) val += *dst;
-      *dst = val;
+      *dst = a.C.sat ? sanitize(val) : val;
     }
 }
 
@@ -1450,8 +1464,9 @@ hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* 
   auto tok = [&](const void* p, int kmajor) {
     return WMat{p, 0, (long long)T_len * H * D, D, (long long)BT * H * D, H * D, kmajor, 0, 0};
   };
-  auto out = [&](float* p, long long per, int ld, int mask, float alpha, int accum) {
-    return WOut{p, (long long)H * N * per, (long long)N * per, per, ld, mask, alpha, accum};
+  auto out = [&](float* p, long long per, int ld, int mask, float alpha, int accum,
+                 int sat = 0) {
+    return WOut{p, (long long)H * N * per, (long long)N * per, per, ld, mask, alpha, accum, sat};
   };
   auto gemm = [&](const WMat& A, const WMat& Bm, const WOut& C, int M, int Nn, int K) {
     WGemmArgs ga{A, Bm, C, M, Nn, K, H, N};
@@ -1463,10 +1478,10 @@ hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* 
   launch_mark(st);
   if (NC > 0) {
     // B2: dAqk = (do v_new^T) . causal, dvp^T = (Aqk^T do)^T, qdot = scale (qg^T do)^T
-    gemm(tok(dout, 0), cm(fVnT, BF, td, BT, 1, 0, BF), out(buf(B_DAQK), tt, BT, 1, 1.f, 0), BT,
-         BT, D);
-    gemm(tok(dout, 1), cm(fws + F.Aqk, BF, tt, BT, 1, 1, 0), out(buf(B_DVPT), td, BT, 0, 1.f, 0),
-         D, BT, BT);
+    gemm(tok(dout, 0), cm(fVnT, BF, td, BT, 1, 0, BF), out(buf(B_DAQK), tt, BT, 1, 1.f, 0, 1),
+         BT, BT, D);
+    gemm(tok(dout, 1), cm(fws + F.Aqk, BF, tt, BT, 1, 1, 0),
+         out(buf(B_DVPT), td, BT, 0, 1.f, 0, 1), D, BT, BT);
     gemm(tok(dout, 1), cm(fws + F.Qg, BF, td, D, 1, 0, 0), out(buf(B_QDOT), dd, D, 0, scale, 0),
          D, D, BT);
     launch_mark(st);
@@ -1495,7 +1510,7 @@ hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* 
                        buf(B_KBD), buf(B_WV));
     gemm(cm(buf(B_DW), 0, td, D, 0, 0, 0), cm(buf(B_KBD), 0, td, D, 0, 0, 0),
          out(buf(B_DA), tt, BT, 2, 1.f, 0), BT, BT, D);                           // dA = dW kbd^T
-    gemm(dvn, cm(buf(B_WV), 0, td, D, 0, 0, 0), out(buf(B_DA), tt, BT, 2, 1.f, 1), BT, BT,
+    gemm(dvn, cm(buf(B_WV), 0, td, D, 0, 0, 0), out(buf(B_DA), tt, BT, 2, 1.f, 1, 1), BT, BT,
          D);                                                                      // + dv_new wv^T
     gemm(Ats, cm(buf(B_DW), 0, td, D, 1, 0, 0), out(buf(B_DKBD), td, D, 0, 1.f, 0), BT, D,
          BT);                                                                     // A^T dW
@@ -1504,9 +1519,9 @@ hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* 
     hipLaunchKernelGGL((wide_dvdw<T>), dim3(NC), dim3(D), 0, st, (const float*)buf(B_DWV),
                        (const T*)w, (const T*)v, T_len, H, N, D, (T*)dv, (T*)dw);
     gemm(cm(buf(B_DA), 0, tt, BT, 0, 0, 0), cm(fA, 0, tt, BT, 0, 0, 0),
-         out(buf(B_TMP), tt, BT, 0, 1.f, 0), BT, BT, BT);                         // dA A^T
-    gemm(Ats, cm(buf(B_TMP), 0, tt, BT, 1, 0, 0), out(buf(B_DAKK), tt, BT, 2, -1.f, 0), BT, BT,
-         BT);                                                                     // dAkk
+         out(buf(B_TMP), tt, BT, 0, 1.f, 0, 1), BT, BT, BT);                      // dA A^T
+    gemm(Ats, cm(buf(B_TMP), 0, tt, BT, 1, 0, 0), out(buf(B_DAKK), tt, BT, 2, -1.f, 0, 1), BT,
+         BT, BT);                                                                 // dAkk
     launch_mark(st);
     // B4 + B3 element-wise tail + B5
     GramArgs<T, TG> gr{(const T*)q,  (const T*)k,  (const T*)b,  (const TG*)g,

@@ -39,6 +39,9 @@ __device__ __forceinline__ float sanitize(float x) {
   x = (x != x) ? 0.f : x;
   return fminf(fmaxf(x, -kClip), kClip);
 }
+__device__ __forceinline__ f32x4 sanitize4(f32x4 v) {
+  return f32x4{sanitize(v[0]), sanitize(v[1]), sanitize(v[2]), sanitize(v[3])};
+}
 
 template <typename T> struct Tr;
 template <> struct Tr<float> {

@@ -17,6 +17,12 @@
 // subtract two large prefix sums.  This is exact math; the reference's +-20
 // clip of gc_i - gc_j (gdn2_fwd.py:125) is not applied (it changes results by
 // < exp(-20) * |q||k| in the documented input domain).
+//
+// Saturation.  Every stage output the reference sanitizes (clip to +-1e4,
+// nan -> 0) is sanitized here too before it is stored: the score blocks Aqk,
+// Akk (gdn2_fwd.py:138-139), the blocks of A = (I + Akk)^{-1} (:183,199,208-211,
+// 236-238, at the blocks of this kernel's own inversion order), W, u, kg, qg
+// and gc_last (:281-289), each chunk state h and each output tile (:359-360).
 
 #include "gdn2_common.h"
 #include "gdn2_layout.h"
@@ -42,27 +48,6 @@ struct PrepArgs {
   const int* cstart;  // variable-length batch: token row where chunk c starts
                       // ([N+1], B = 1); rows past cstart[c+1] are neutral padding
 };
-
-// First token row of chunk c and its number of real tokens: from the chunk table
-// of a variable-length batch (clamped to [0, BT] and to the T rows), else
-// c*BT within batch element bb, with min(BT, T_len - c*BT) real tokens.
-struct ChunkRows {
-  size_t row0;
-  int valid;
-};
-__device__ __forceinline__ ChunkRows chunk_rows(const int* cstart, int c, int bb, int T_len,
-                                                int BT) {
-  if (!cstart) {  // equal sequences of T_len tokens; the last chunk may be short
-    const int rest = T_len - c * BT;
-    return ChunkRows{(size_t)bb * T_len + (size_t)c * BT, rest < BT ? rest : BT};
-  }
-  const int r0 = cstart[c];
-  int v = cstart[c + 1] - r0;
-  v = v < BT ? v : BT;
-  v = v < T_len - r0 ? v : T_len - r0;
-  if (v <= 0 || r0 < 0) return ChunkRows{0, 0};  // no real rows: point at row 0
-  return ChunkRows{(size_t)r0, v};
-}
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
 // -softplus(x) = -(max(x,0) + log(1 + e^{-|x|}))
@@ -277,7 +262,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       float run = 0.f;
 #pragma unroll
       for (int m = 0; m < NB; ++m) { sF0[m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
-      a.GL[(size_t)cid * D + d0 + tid] = run;
+      a.GL[(size_t)cid * D + d0 + tid] = sanitize(run);
       run = 0.f;
 #pragma unroll
       for (int m = NB - 1; m >= 0; --m) { sF1[m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
@@ -338,9 +323,10 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
           const float ekh = __expf(sTot[I * DP + ch] - lc);
           const float egc = eloc * sF0[I * DP + ch];
           const float bk = bv * kv;
-          qg[e] = qv * egc;
+          qg[e] = sanitize(qv * egc);
           sKbdT[(d0 + ch) * TT_LD + t] = from_f<T>(bk * egc);
-          kgT[(size_t)(d0 + ch) * BT + kpos<T>(t)] = from_f<T>(kv * ekh * sF1[I * DP + ch]);
+          kgT[(size_t)(d0 + ch) * BT + kpos<T>(t)] =
+              from_f<T>(sanitize(kv * ekh * sF1[I * DP + ch]));
           kh[e] = kv * ekh;
           aq[i][x] = qv * eloc;
           ak[i][x] = bk * eloc;
@@ -369,16 +355,16 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       }
       const int e0 = t * A_LD + I * 16 + 4 * lg;
       if constexpr (one) {
-        store4(aqk + (size_t)t * BT + I * 16 + 4 * lg, sq);
-        store4(&sA[e0], sk);
+        store4(aqk + (size_t)t * BT + I * 16 + 4 * lg, sanitize4(sq));
+        store4(&sA[e0], sanitize4(sk));
       } else {
         if (pn > 0) {
           sq += qdiag[i];
           sk += load4f(&sA[e0]);
         }
-        if (last_pn) store4(aqk + (size_t)t * BT + I * 16 + 4 * lg, sq);
+        if (last_pn) store4(aqk + (size_t)t * BT + I * 16 + 4 * lg, sanitize4(sq));
         else qdiag[i] = sq;
-        store4(&sA[e0], sk);
+        store4(&sA[e0], last_pn ? sanitize4(sk) : sk);
       }
     }
     __syncthreads();
@@ -408,17 +394,17 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
         }
         const int e0 = t * A_LD + J * 16 + 4 * lg;
         if constexpr (one) {
-          store4(aqk + (size_t)t * BT + J * 16 + 4 * lg, accq * a.scale);
-          store4(&sA[e0], acck);
+          store4(aqk + (size_t)t * BT + J * 16 + 4 * lg, sanitize4(accq * a.scale));
+          store4(&sA[e0], sanitize4(acck));
         } else {
           f32x4 sq = accq * a.scale;
           if (pn > 0) {
             sq += qp;
             acck += load4f(&sA[e0]);
           }
-          if (last_pn) store4(aqk + (size_t)t * BT + J * 16 + 4 * lg, sq);
+          if (last_pn) store4(aqk + (size_t)t * BT + J * 16 + 4 * lg, sanitize4(sq));
           else qp = sq;
-          store4(&sA[e0], acck);
+          store4(&sA[e0], last_pn ? sanitize4(acck) : acck);
         }
 #pragma unroll
         for (int x = 0; x < DQ; ++x) F[x] *= sETot[J * DP + chan(x)];
@@ -483,7 +469,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     const f32x4 M = mul(M2t, E + P8);                        // M2 (I + L^8)
     (void)M2;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) blk[(4 * lg + r) * A_LD + li] = M[r];
+    for (int r = 0; r < 4; ++r) blk[(4 * lg + r) * A_LD + li] = sanitize(M[r]);
   }
   __syncthreads();
 
@@ -517,7 +503,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       f32x4 t = {0.f, 0.f, 0.f, 0.f}, x = {0.f, 0.f, 0.f, 0.f};
       mma(t, rowop(B0, A0), Xc(A0, A0));
       mma(x, rowop(B0, B0), t);
-      put(&sA[(B0 * 16) * A_LD + A0 * 16], A_LD, -x);
+      put(&sA[(B0 * 16) * A_LD + A0 * 16], A_LD, sanitize4(-x));
     }
     __syncthreads();
     auto level = [&](auto hc) __attribute__((always_inline)) {
@@ -538,7 +524,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
 #pragma unroll
         for (int k = 0; k < h; ++k)
           if (k <= i) mma(x, rowop(B0 + i, B0 + k), colop(&sSmall[((g * h + k) * h + j) * PARK], 20));
-        put(&sA[((B0 + i) * 16) * A_LD + (A0 + j) * 16], A_LD, -x);
+        put(&sA[((B0 + i) * 16) * A_LD + (A0 + j) * 16], A_LD, sanitize4(-x));
       };
       if constexpr (NOUT <= PW) {
         const int g = wv / (h * h), i = (wv / h) % h, j = wv % h;
@@ -632,8 +618,8 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
           mma(accu, af, op_load<T>(&sWVT[(dt * 16 + li) * TT_LD + kg * KS + lg * KC]));
         }
       }
-      store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dg + 4 * lg), accw);
-      store4(Uc + (size_t)(dg + li) * BT + kpos<T>(I * 16 + 4 * lg), accu);
+      store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dg + 4 * lg), sanitize4(accw));
+      store4(Uc + (size_t)(dg + li) * BT + kpos<T>(I * 16 + 4 * lg), sanitize4(accu));
     }
   }
 }
@@ -755,10 +741,9 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
   if (mslice) vs -= NVS;
   int c0, n;                                 // chunks [c0, c0 + n) of this unit
   if (a.cu) {
-    c0 = a.cu[sg];
-    c0 = c0 < 0 ? 0 : (c0 > a.N ? a.N : c0);
-    n = a.cu[sg + 1] - c0;
-    n = n < a.N - c0 ? n : a.N - c0;
+    const SeqChunks sc = seq_chunks(a.cu, sg, a.N);
+    c0 = sc.c0;
+    n = sc.n;
   } else {
     c0 = sg * a.L;
     n = a.N - c0;
@@ -1291,7 +1276,8 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   const int N = vl ? vl->total_chunks : (T_len + BT - 1) / BT;
   const size_t NC = (size_t)B * H * N;
   const int S_ws = vl ? 1 : state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
-  const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), S_ws > 1 ? (size_t)B * H * S_ws : 0);
+  const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), S_ws > 1 ? (size_t)B * H * S_ws : 0,
+                                 !(flags & kFwdNoARegion));
   T* W = reinterpret_cast<T*>(ws + L.W);
   T* UT = reinterpret_cast<T*>(ws + L.UT);
   T* KgT = reinterpret_cast<T*>(ws + L.KgT);

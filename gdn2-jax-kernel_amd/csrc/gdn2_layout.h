@@ -37,11 +37,19 @@ struct FwdLayout {
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Internal launch flag, never accepted from callers (the public entry points
+// clear it): the workspace has no A region, because nothing will read the
+// residuals (the no-allocation inference entry point, whose workspace is a
+// fixed device array).
+constexpr int kFwdNoARegion = 1 << 24;
+
 // SEG (only with a segmented state scan, S > 1): per (b,h) and segment the end
 // state from h = 0 and the transition M_seg ([bh][S][2][D][D] f32), then the
 // segment entry states ([bh][S][D][D] f32).  It comes last, so the offsets the
-// backward reads do not depend on S.
-inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem, size_t seg_units = 0) {
+// backward reads do not depend on S.  Without `a_region` the A tiles take no
+// space (SEG moves up accordingly).
+inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem, size_t seg_units = 0,
+                            bool a_region = true) {
   FwdLayout L;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
@@ -53,7 +61,7 @@ inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem, size_t s
   L.GL = take(nchunks * D * 4);
   L.HT = take(nchunks * D * D * elem);
   L.VnT = take(nchunks * D * BT * elem);
-  L.A = take(nchunks * BT * BT * 4);
+  L.A = take(a_region ? nchunks * BT * BT * 4 : 0);
   L.SEG = take(seg_units * 3 * (size_t)D * D * 4);
   L.total = off;
   return L;
@@ -69,6 +77,47 @@ struct Varlen {
   int nseq;
   int total_chunks;
 };
+
+// Table clamps of a variable-length batch.  The kernels read their chunk
+// tables through these two functions only, so a malformed table can give wrong
+// numbers but never an access outside the buffers.  They are constexpr, which
+// makes them callable from device code and from a plain host compiler (the CPU
+// test of the clamps compiles this header with g++).
+//
+// First token row of chunk c and its number of real tokens: from the chunk
+// table of a variable-length batch (row0 in [0, T_len), valid in [0, BT] with
+// row0 + valid <= T_len; valid = 0 points at row 0), else c*BT within batch
+// element bb, with min(BT, T_len - c*BT) real tokens.
+struct ChunkRows {
+  size_t row0;
+  int valid;
+};
+constexpr ChunkRows chunk_rows(const int* cstart, int c, int bb, int T_len, int BT) {
+  if (!cstart) {  // equal sequences of T_len tokens; the last chunk may be short
+    const int rest = T_len - c * BT;
+    return ChunkRows{(size_t)bb * T_len + (size_t)c * BT, rest < BT ? rest : BT};
+  }
+  const int r0 = cstart[c];
+  if (r0 < 0 || r0 >= T_len) return ChunkRows{0, 0};  // no real rows: point at row 0
+  long long v = (long long)cstart[c + 1] - r0;
+  v = v < BT ? v : BT;
+  v = v < T_len - r0 ? v : T_len - r0;
+  if (v <= 0) return ChunkRows{0, 0};
+  return ChunkRows{(size_t)r0, (int)v};
+}
+
+// Chunks [c0, c0 + n) of sequence s in a list of N chunks, from the sequence
+// table cu (cu[s], cu[s+1]) clamped to [0, N].
+struct SeqChunks {
+  int c0, n;
+};
+constexpr SeqChunks seq_chunks(const int* cu, int s, int N) {
+  int c0 = cu[s];
+  c0 = c0 < 0 ? 0 : (c0 > N ? N : c0);
+  long long n = (long long)cu[s + 1] - c0;
+  n = n < N - c0 ? n : N - c0;
+  return SeqChunks{c0, n > 0 ? (int)n : 0};
+}
 
 // Segments of the forward state scan for BH (b,h) pairs of N chunks.  Automatic
 // choice: as many as fill a 256-CU device in the final pass when the plain

@@ -82,17 +82,40 @@ def _dtype_code(dt):
 
 def chunk_size_for(dtype, chunk_size=None, D=128) -> int:
     """Chunk size: explicit, else the module-level BT override, else 128 for
-    bfloat16 inputs with D <= 128 and 64 otherwise (float32, and D = 256)."""
+    bfloat16 inputs with D <= 128 and 64 otherwise (float32, and D = 256).
+
+    The reference's default BT = 256 (gdn2_fwd.py:29) is refused with a
+    GDN2ShapeError: its 256 x 256 float32 inverse does not fit a gfx950
+    workgroup's LDS.  Results do not depend on the chunk size beyond rounding,
+    so callers that set BT = 256 lose nothing by leaving BT at None."""
     bt = chunk_size if chunk_size is not None else BT
     if bt is None:
         return 128 if dtype == torch.bfloat16 and D <= 128 else 64
+    if int(bt) == 256:
+        raise GDN2ShapeError(
+            "gdn2: chunk size 256 (the reference default, gdn2_fwd.py:29) is not supported "
+            "on gfx950; use None (automatic), 64, or 128 with bfloat16 inputs -- results do "
+            "not depend on the chunk size beyond rounding")
     return int(bt)
+
+
+def _check_clip():
+    """The kernels saturate at 1e4 (gdn2_fwd.py:33); an override of the module
+    constant CLIP (README.md:87-92) is refused instead of silently ignored."""
+    if float(CLIP) != 1e4:
+        raise GDN2Error(f"gdn2: CLIP = {CLIP!r} is not supported; the gfx950 kernels clip "
+                        f"stage outputs at the reference value 1e4 (gdn2_fwd.py:33)")
 
 
 class _Prepared:
     """Inputs normalised for the C ABI (contiguous, supported dtypes)."""
 
-    def __init__(self, q, k, v, w, b, g, scale, h0, chunk_size):
+    def __init__(self, q, k, v, w, b, g, scale, h0, chunk_size, compute_dtype=None):
+        """``compute_dtype=torch.float32`` runs bfloat16 inputs through the
+        float32 kernels (the trainable path: the reference upcasts every input
+        before any arithmetic, gdn2_fwd.py:100-103,266-272, gdn2_bwd.py:130-142);
+        ``in_dtypes`` keeps the caller's dtypes for the gradients."""
+        _check_clip()
         xs = (q, k, v, w, b, g)
         for x in xs:
             if not isinstance(x, torch.Tensor):
@@ -109,6 +132,8 @@ class _Prepared:
         g_dt = torch.float32
         if in_dt == torch.bfloat16 and g.dtype == torch.bfloat16:
             g_dt = torch.bfloat16
+        if compute_dtype == torch.float32:
+            in_dt = g_dt = torch.float32
         self.B, self.T, self.H, self.D = q.shape
         self.BT = chunk_size_for(in_dt, chunk_size, self.D)
         self.args = (self.B, self.T, self.H, self.D, self.BT, _dtype_code(in_dt),
@@ -186,9 +211,16 @@ def gdn2_pallas_forward(q, k, v, w, b, g, scale, h0=None, debug_tag="", chunk_si
                           ("kernel_B_wy_inverse_A", "A"), ("kernel_C_w_pseudo", "w_pseudo"),
                           ("kernel_C_u", "u"), ("kernel_C_kg", "kg"), ("kernel_C_qg", "qg")):
             _stage_diag(f"{debug_tag}:{name}", res[key])
+        _diag_kernel_d(debug_tag, out, h_final)
         return out, h_final
     out, h_final, _, _ = _run_forward(p)
     return out, h_final
+
+
+def _diag_kernel_d(tag: str, out, h_final):
+    """The reference's kernel-D reports (gdn2_fwd.py:363,365)."""
+    _stage_diag(f"{tag}:kernel_D_h_final", h_final)
+    _stage_diag(f"{tag}:kernel_D_o", out)
 
 
 def _residual_views(p: _Prepared, ws: torch.Tensor):

@@ -7,6 +7,12 @@ A ``torch.autograd.Function`` plays the role of the reference's
 the cotangents are (d out, d h_final), and the gradients of
 (q, k, v, w, b, g, h0) come back in each input's dtype (:129-135).
 
+Arithmetic.  The trainable path computes in float32 whatever the input dtype:
+bfloat16 inputs are widened before the forward, as the reference upcasts every
+input before any arithmetic (gdn2_fwd.py:100-103,266-272; gdn2_bwd.py:130-142),
+so the residuals the backward contracts against the state cotangent are
+float32.  Gradients are cast back to each input's dtype.
+
 Residuals.  By default the forward keeps its per-chunk workspace (WY factors,
 chunk states, v_new) for the backward.  ``recompute=True`` keeps only the
 inputs, as the reference does (:64-67), and re-runs the forward kernels in the
@@ -52,7 +58,7 @@ class _GDN2Core(torch.autograd.Function):
     def forward(ctx, q, k, v, w, b, g, h0, scale, chunk_size, recompute):
         # the backward kernels tile 64-token chunks
         p = _Prepared(q, k, v, w, b, g, scale, h0, TRAIN_CHUNK if chunk_size is None
-                      else chunk_size)
+                      else chunk_size, compute_dtype=torch.float32)
         out, h_final, ws, _ = _run_forward(p, flags=_lib.FWD_SAVE_A)
         ctx.prep = p
         ctx.ws = None if recompute else ws
@@ -104,7 +110,7 @@ class _GDN2VarlenCore(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, w, b, g, h0, scale, cu_chunks):
-        p = _Prepared(q, k, v, w, b, g, scale, None, TRAIN_CHUNK)
+        p = _Prepared(q, k, v, w, b, g, scale, None, TRAIN_CHUNK, compute_dtype=torch.float32)
         S = cu_chunks.numel() - 1
         total = p.T // p.BT
         dev = p.device

@@ -125,7 +125,13 @@ size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
  * gdn2_pipeline.py:77-83; a caller that kept no residuals re-runs gdn2_fwd
  * first).  BT must be 64.  dh_final and h0 may be NULL (zero).  dq,dk,dv,dw,db
  * are in_dtype, dg is g_dtype, dh0 is float32 (B,H,D,D); all gradients are
- * sanitized as gdn2_pipeline.py:129-135.  Computes in float32 throughout.
+ * sanitized as gdn2_pipeline.py:129-135.  The arithmetic is float32; the
+ * residuals it reads from fwd_ws are in the forward's operand type, so with
+ * in_dtype = GDN2_BF16 they are bfloat16-rounded (h_c, v_new, W, kg, qg, Aqk)
+ * and gradients contracted against a large dh_final lose accuracy.  The
+ * reference upcasts every input to float32 first (gdn2_fwd.py:100-103,
+ * gdn2_bwd.py:130-142); the Python trainable path does the same, running
+ * bfloat16 inputs through the float32 forward and backward.
  * Launches 4 kernels at D <= 128 (see gdn2_set_launch_events); at D = 256 the
  * per-chunk products run as separate launches (the launch marks still bracket
  * the same four stages). */

@@ -95,15 +95,48 @@ def test_bwd_partial_last_chunk(dev, T, h0):
 
 
 def test_bwd_bf16_inputs(dev):
-    xs = O.make_inputs(1, 256, 2, 128, seed=21)
+    """bfloat16 inputs with a unit-scale h0 and dh_final: the trainable path
+    computes in float32 (the reference upcasts, gdn2_fwd.py:100-103) and
+    returns bfloat16 gradients, within 2e-2 of the oracle on the same
+    bf16-rounded inputs."""
+    B, T, H, D = 1, 256, 2, 128
+    xs = O.make_inputs(B, T, H, D, seed=21)
     rng = np.random.default_rng(3)
     do = rng.standard_normal(xs[0].shape).astype(np.float32)
-    _, grads, xt = run_grads(xs, 128 ** -0.5, do, dtype=torch.bfloat16, dev=dev)
+    dhn = rng.standard_normal((B, H, D, D)).astype(np.float32)
+    h0n = rng.standard_normal((B, H, D, D)).astype(np.float32)
+    _, grads, xt = run_grads(xs, D ** -0.5, do, dhn, h0=h0n, dtype=torch.bfloat16, dev=dev)
     for x in xt[:5]:
         assert x.grad.dtype == torch.bfloat16
     xin = [x.detach().float().cpu().numpy() for x in xt]
-    ref = O.chunked_bwd(*xin, 128 ** -0.5, do, BT=64, clip=False)
+    ref = O.chunked_bwd(*xin, D ** -0.5, do, dhn, h0=h0n, BT=64, clip=False)
     check(grads, ref, 2e-2)
+
+
+def test_config4_training_path_bf16(dev):
+    """The training path at BASELINE configs[3]'s shape (8,8192,6,128) with
+    bfloat16 q,k,v,w,b, float32 g, an N(0,1) cotangent on out and a unit N(0,1)
+    cotangent on h_final.  Two sampled (batch, head) pairs are checked against
+    the oracle's B1-B5 on the bf16-rounded inputs at 2e-2."""
+    B, T, H, D = 8, 8192, 6, 128
+    gen = torch.Generator(device=dev).manual_seed(4)
+    r = lambda *s: torch.randn(s or (B, T, H, D), generator=gen, device=dev)
+    q, k, v, w, b, g = r(), r(), r(), r(), r(), r()
+    q, k = q / q.norm(dim=-1, keepdim=True), k / k.norm(dim=-1, keepdim=True)
+    w, b, g = torch.sigmoid(w), torch.sigmoid(b), -torch.nn.functional.softplus(g)
+    xt = [x.to(torch.bfloat16).detach().requires_grad_(True) for x in (q, k, v, w, b)] + \
+        [g.detach().requires_grad_(True)]
+    do, dh = r(), r(B, H, D, D)
+    out, hf = gp().gdn2_pallas_forward_trainable(*xt, D ** -0.5)
+    torch.autograd.backward([out, hf], [do, dh])
+    for x in xt:
+        assert torch.isfinite(x.grad.float()).all()
+    for bb, hh in [(2, 1), (6, 5)]:
+        sl = [x.detach()[bb:bb + 1, :, hh:hh + 1].float().cpu().numpy() for x in xt]
+        ref = O.chunked_bwd(*sl, D ** -0.5, do[bb:bb + 1, :, hh:hh + 1].cpu().numpy(),
+                            dh[bb:bb + 1, hh:hh + 1].cpu().numpy(), BT=64, clip=False)
+        got = [x.grad[bb:bb + 1, :, hh:hh + 1].float().cpu().numpy() for x in xt]
+        check(got, ref[:6], 2e-2, NAMES[:6])
 
 
 def test_bwd_recompute_matches_saved_residuals(dev):
@@ -162,14 +195,12 @@ def test_grad_of_h0_only_when_given(dev):
 @pytest.mark.parametrize("T,H,h0,dh,dtype", [
     (128, 2, True, 1.0, torch.float32),
     (192, 1, False, 0.0, torch.float32),
-    (128, 1, False, 0.1, torch.bfloat16),
+    (128, 1, True, 1.0, torch.bfloat16),
 ])
 def test_bwd_d256_matches_oracle(dev, T, H, h0, dh, dtype):
     """D = 256 (beyond the reference, which asserts D == 128): the backward of
-    per-chunk products, against the oracle's B1-B5 in float64.  With bfloat16
-    residuals a unit-scale dh_final cotangent exceeds the 2e-2 bar on dk (as at
-    D = 128 in the variable-length test: the bf16 rounding of kg and W meets a
-    large dh), so that case takes dh_final at 0.1."""
+    per-chunk products, against the oracle's B1-B5 in float64, with unit-scale
+    h0 and dh_final also for bfloat16 inputs (computed in float32)."""
     B, D = 1, 256
     xs = O.make_inputs(B, T, H, D, seed=T + H)
     rng = np.random.default_rng(13)

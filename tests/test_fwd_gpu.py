@@ -114,7 +114,8 @@ def test_config3_headline_bf16(dev):
     xt = [x.to(torch.bfloat16) for x in (q, k, v, w, b)] + [g]
     out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5)
     assert torch.isfinite(out).all() and torch.isfinite(hf).all()
-    _sampled_pairs_check(out, hf, xt, [(0, 0), (7, 5), (3, 2)], D)
+    _sampled_pairs_check(out, hf, xt, [(0, 0), (7, 5), (3, 2), (1, 4), (2, 1), (4, 3),
+                                       (5, 0), (6, 2), (7, 0), (0, 5)], D)
     # chaining: second half from the first half's final state reproduces the full run
     o1, h1 = gp().gdn2_pallas_forward(*[x[:, :T // 2] for x in xt], D ** -0.5)
     o2, h2 = gp().gdn2_pallas_forward(*[x[:, T // 2:] for x in xt], D ** -0.5, h0=h1)
@@ -134,7 +135,7 @@ def test_config5_long_context_bf16(dev):
     xt = [x.to(torch.bfloat16) for x in (q, k, v, w, b)] + [g]
     out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5)
     assert torch.isfinite(out).all() and torch.isfinite(hf).all()
-    _sampled_pairs_check(out, hf, xt, [(0, 3)], D)
+    _sampled_pairs_check(out, hf, xt, [(0, 3), (0, 6)], D)
 
 
 # ----------------------------------------------------------------------------- intermediates
@@ -385,3 +386,55 @@ def test_raw_inputs_fused_activations(dev, dtype, BT, D):
     ok_o, e_o = close(out_r.cpu().numpy(), ro, TOL[dtype])
     ok_h, e_h = close(h_r.cpu().numpy(), rh, TOL[dtype])
     assert ok_o and ok_h, ("vs oracle", e_o, e_h)
+
+
+# ----------------------------------------------------------------------------- saturation
+def test_stage_sanitize_matches_reference_clipping(dev):
+    """Values past the reference's clip (v x 1e5, scale 20, slow decay): u, the
+    outputs and the states saturate at +-1e4 (gdn2_fwd.py:42-44 applied at
+    :281-289 and :359-360) while every exponential stays finite.  The float32
+    forward matches the oracle's restatement with the same sanitize points
+    (oracle.chunked_fwd, clip=True), which differs from the unclipped math by
+    orders of magnitude here.  Tolerances act on the saturation scale:
+    |got - ref| <= 1e-4 * 1e4 + 1e-4 * |ref|."""
+    B, T, H, D, scale = 1, 256, 2, 64, 20.0
+    xs = list(O.make_inputs(B, T, H, D, seed=40, g_scale=0.05))
+    xs[2] = xs[2] * 1e5
+    xt = to_dev(xs, dev, torch.float32)
+    out, hf = gp().gdn2_pallas_forward(*xt, scale, chunk_size=64)
+    ro, rh, res = O.chunked_fwd(*host(xt), scale, BT=64, clip=True, return_residuals=True)
+    assert np.abs(res["u"]).max() == 1e4 and np.abs(ro).max() == 1e4 and np.abs(rh).max() == 1e4
+    assert np.abs(O.recurrent_fwd(*host(xt), scale)[0]).max() > 1e5   # clipping is active
+    ok_o, e_o = close(out.cpu().numpy() * 1e-4, ro * 1e-4, 1e-4)
+    ok_h, e_h = close(hf.cpu().numpy() * 1e-4, rh * 1e-4, 1e-4)
+    assert ok_o and ok_h, (e_o, e_h)
+    # the trainable path on the same inputs: finite gradients within the clip
+    xg = [x.detach().requires_grad_(True) for x in xt]
+    o2, h2 = gp().gdn2_pallas_forward_trainable(*xg, scale)
+    (o2.sum() + h2.sum()).backward()
+    for x in xg:
+        assert torch.isfinite(x.grad).all() and x.grad.abs().max().item() <= 1e4
+
+
+def test_stage_sanitize_bf16_saturates_like_reference(dev):
+    """The bfloat16 forward (chunk 128) on saturating inputs (v x 1e5, scale 1,
+    slow decay: u, 1 % of the outputs and of the states reach the clip): outputs
+    and states stay finite within +-1e4, every state entry the oracle saturates
+    is saturated here with the same sign, and the rest agrees within the bf16
+    bar on the saturation scale (2e-2 * 1e4: bf16 operands of magnitude 1e4
+    carry rounding steps of 2^-8 * 1e4)."""
+    B, T, H, D, scale = 1, 256, 2, 64, 1.0
+    xs = list(O.make_inputs(B, T, H, D, seed=40, g_scale=0.05))
+    xs[2] = xs[2] * 1e5
+    xt = to_dev(xs, dev, torch.bfloat16)
+    out, hf = gp().gdn2_pallas_forward(*xt, scale, chunk_size=128)
+    ro, rh = O.chunked_fwd(*host(xt), scale, BT=128, clip=True)
+    o, h = out.cpu().numpy(), hf.cpu().numpy()
+    assert np.isfinite(o).all() and np.isfinite(h).all()
+    assert np.abs(o).max() <= 1e4 and np.abs(h).max() <= 1e4
+    sat = np.abs(rh) == 1e4
+    assert sat.any() and np.array_equal(np.sign(h[sat]), np.sign(rh[sat]))
+    assert (np.abs(h[sat]) >= 0.98e4).all()
+    e_o, e_h = np.abs(o - ro).max() * 1e-4, np.abs(h - rh).max() * 1e-4
+    print(f"bf16 saturation: max|dout|/1e4={e_o:.3e} max|dh|/1e4={e_h:.3e}")
+    assert close(o * 1e-4, ro * 1e-4, 2e-2)[0] and close(h * 1e-4, rh * 1e-4, 2e-2)[0], (e_o, e_h)
