@@ -168,7 +168,9 @@ const char* gdn2_strerror(int code) {
     case GDN2_ERR_WORKSPACE: return "workspace too small";
     case GDN2_ERR_SHAPE: return "invalid shape (B and H must be >= 1, T >= 0)";
     case GDN2_ERR_LAUNCH: return "HIP kernel launch failed";
-    case GDN2_ERR_FLAGS: return "invalid flags (GDN2_FWD_RAW_INPUTS cannot be combined with GDN2_FWD_SAVE_A)";
+    case GDN2_ERR_FLAGS: return "invalid flags (GDN2_FWD_RAW_INPUTS cannot be combined with GDN2_FWD_SAVE_A; gdn2_fwd_noalloc takes no GDN2_FWD_SAVE_A)";
+    case GDN2_ERR_SCRATCH:
+      return "workload too large for gdn2_fwd_noalloc's fixed scratch (GDN2_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown error";
   }
 }

@@ -38,6 +38,8 @@ ERR_WORKSPACE = -7
 ERR_SHAPE = -8
 ERR_LAUNCH = -9
 ERR_FLAGS = -10
+ERR_SCRATCH = -11
+NOALLOC_SCRATCH_BYTES = 128 << 20
 
 _c_int, _c_float, _c_size, _vp = ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
 
@@ -57,6 +59,8 @@ SIGNATURES = {
     "gdn2_bwd": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7
                  + [_c_float, _vp, _vp] + [_vp] * 7 + [_vp, _c_size, _vp, _c_size]),
     "gdn2_decode": (_c_int, [_vp] + [_c_int] * 5 + [_vp] * 6 + [_c_float, _vp, _vp, _vp]),
+    "gdn2_fwd_noalloc": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7
+                         + [_c_float, _vp, _vp, _c_int]),
     "gdn2_fwd_varlen_workspace_bytes": (_c_size, [_c_int] * 5),
     "gdn2_fwd_varlen": (_c_int, [_vp, _c_int, _vp, _vp] + [_c_int] * 7 + [_vp] * 7
                         + [_c_float, _vp, _vp, _vp, _c_size, _c_int]),

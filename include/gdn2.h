@@ -50,6 +50,7 @@ extern "C" {
 #define GDN2_ERR_SHAPE        -8  /* B<1, H<1, T<0, or sizes overflow */
 #define GDN2_ERR_LAUNCH       -9  /* HIP launch failure */
 #define GDN2_ERR_FLAGS       -10  /* invalid flag combination */
+#define GDN2_ERR_SCRATCH     -11  /* gdn2_fwd_noalloc: workload needs more than its scratch */
 
 /* Library version string, e.g. "0.1.0". */
 const char* gdn2_version(void);
@@ -175,6 +176,25 @@ int gdn2_bwd_varlen(void* stream, int num_seqs, const int* cu_chunks, int total_
                     float scale, const float* dout, const float* dh_final, void* dq, void* dk,
                     void* dv, void* dw, void* db, void* dg, float* dh0, const void* fwd_ws,
                     size_t fwd_ws_bytes, void* ws, size_t ws_bytes);
+
+/* Forward that allocates nothing: gdn2_fwd's kernels with the workspace in a
+ * fixed device array of the library (GDN2_NOALLOC_SCRATCH_BYTES per GPU, held
+ * until the process ends).  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Arguments as gdn2_fwd
+ * without ws / ws_bytes; flags: GDN2_FWD_RAW_INPUTS, GDN2_FWD_PARTIAL_CHUNK,
+ * GDN2_FWD_SEGMENTS(n) -- GDN2_FWD_SAVE_A is GDN2_ERR_FLAGS (the residuals would
+ * not survive the next call).  A workload whose inference workspace exceeds the
+ * scratch returns GDN2_ERR_SCRATCH before any launch (128 MiB: about 74 k
+ * token-heads B*T*H for bfloat16 inputs at chunk 128 and D = 128, e.g.
+ * B = 1, T = 8192, H = 8).
+ * All calls on one GPU share its scratch: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller. */
+#define GDN2_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+int gdn2_fwd_noalloc(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
+                     int g_dtype, const void* q, const void* k, const void* v, const void* w,
+                     const void* b, const void* g, const float* h0, float scale, float* out,
+                     float* h_final, int flags);
 
 /* Single-token recurrent step on the (B,H,D,D) float32 state, for serving:
  * the reference has no decode entry; this is gdn2_pallas_forward with T = 1

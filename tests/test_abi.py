@@ -30,7 +30,7 @@ def test_version_and_strerror():
     import gdn2_package
     L = _lib.lib()
     assert L.gdn2_version().decode() == gdn2_package.__version__
-    for code in range(0, -11, -1):
+    for code in range(0, -12, -1):
         assert L.gdn2_strerror(code) and L.gdn2_strerror(code) != b"unknown error"
     assert L.gdn2_strerror(-1234) == b"unknown error"
 
