@@ -35,9 +35,13 @@ typedef __bf16 bf16_t;
 constexpr float kClip = 1e4f;
 
 // nan -> 0, +-inf -> +-kClip, clip to [-kClip, kClip]: gdn2_fwd.py:42-44.
+// max(x, 0) + min(x, 0) is x, or 0 for NaN (IEEE maxNum / minNum return the
+// non-NaN operand); v_med3 then clamps (+-inf included).  Four independent
+// VALU operations per value and no compare: a NaN test through VCC would
+// serialise every element of a tile behind one register.
 __device__ __forceinline__ float sanitize(float x) {
-  x = (x != x) ? 0.f : x;
-  return fminf(fmaxf(x, -kClip), kClip);
+  const float y = fmaxf(x, 0.f) + fminf(x, 0.f);
+  return __builtin_amdgcn_fmed3f(y, -kClip, kClip);
 }
 __device__ __forceinline__ f32x4 sanitize4(f32x4 v) {
   return f32x4{sanitize(v[0]), sanitize(v[1]), sanitize(v[2]), sanitize(v[3])};

@@ -149,6 +149,8 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     return rowp(t < last ? t : last);
   };
   const bool raw = a.raw != 0;
+  // Barriers order LDS data only (lds_barrier): no wave reads global memory
+  // another wave of this workgroup wrote, so stores stay in flight across them.
   T* kgT = a.KgT + (size_t)cid * D * BT;
   T* aqk = a.Aqk + (size_t)cid * BT * BT;
 
@@ -199,7 +201,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     const int d0 = pn * DP;               // first channel of the panel
     constexpr bool one = NPN == 1;
     const bool last_pn = pn == NPN - 1;
-    if (pn > 0) __syncthreads();          // the previous panel's LDS reads are done
+    if (pn > 0) lds_barrier();            // the previous panel's LDS reads are done
 
     // all loads needed before the inverse, issued together, g first: the cumsum
     // waits for g alone (memory operations complete in order) while q, k, b
@@ -367,30 +369,23 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
         store4(&sA[e0], last_pn ? sanitize4(sk) : sk);
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- 3. off-diagonal score blocks (I > J) on MFMA ------------------------
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
       const int I = own_block<NB>(wv, i);
       const int t = I * 16 + li;
-      float F[DQ];
-#pragma unroll
-      for (int x = 0; x < DQ; ++x) F[x] = 1.f;
-      // block pair (I, J), J < I, in descending J (F carries the decay between)
+      // block pair (I, J), J < I, in descending J; after each pair aq and ak
+      // take the decay e^{T_J} of block J in place (they are not needed after
+      // the last pair)
       auto pair = [&](int J, f32x4& qp) __attribute__((always_inline)) {
         f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < NKD; ++j) {
-          float yq[KC], yk[KC];
-#pragma unroll
-          for (int e = 0; e < KC; ++e) {
-            yq[e] = aq[i][j * KC + e] * F[j * KC + e];
-            yk[e] = ak[i][j * KC + e] * F[j * KC + e];
-          }
           const Op xo = op_load<T>(&sR0[(J * 16 + li) * KH_LD + j * KS + lg * KC]);
-          mma(accq, xo, op_from<T>(yq));
-          mma(acck, xo, op_from<T>(yk));
+          mma(accq, xo, op_from<T>(&aq[i][j * KC]));
+          mma(acck, xo, op_from<T>(&ak[i][j * KC]));
         }
         const int e0 = t * A_LD + J * 16 + 4 * lg;
         if constexpr (one) {
@@ -407,7 +402,11 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
           store4(&sA[e0], last_pn ? sanitize4(acck) : acck);
         }
 #pragma unroll
-        for (int x = 0; x < DQ; ++x) F[x] *= sETot[J * DP + chan(x)];
+        for (int x = 0; x < DQ; ++x) {
+          const float e = sETot[J * DP + chan(x)];
+          aq[i][x] *= e;
+          ak[i][x] *= e;
+        }
       };
       if constexpr (one) {
         for (int J = I - 1; J >= 0; --J) pair(J, qoff[i][0]);   // qoff unused here
@@ -418,7 +417,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
 
   // w, v of the first panel: in flight during the inverse (issued earlier they
@@ -471,7 +470,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
 #pragma unroll
     for (int r = 0; r < 4; ++r) blk[(4 * lg + r) * A_LD + li] = sanitize(M[r]);
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 4b. off-diagonal blocks by recursive doubling ------------------------
   // For h = 1, 2, 4, ... 16-row blocks and each group [A0, A0 + 2h) with
@@ -505,7 +504,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       mma(x, rowop(B0, B0), t);
       put(&sA[(B0 * 16) * A_LD + A0 * 16], A_LD, sanitize4(-x));
     }
-    __syncthreads();
+    lds_barrier();
     auto level = [&](auto hc) __attribute__((always_inline)) {
       constexpr int h = decltype(hc)::value;
       constexpr int NOUT = NB * h / 2;          // blocks X_BA of this h, all groups
@@ -529,9 +528,9 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       if constexpr (NOUT <= PW) {
         const int g = wv / (h * h), i = (wv / h) % h, j = wv % h;
         if (wv < NOUT) tblock(g, i, j);
-        __syncthreads();
+        lds_barrier();
         if (wv < NOUT) xblock(g, i, j);
-        __syncthreads();
+        lds_barrier();
       } else {
         // one group (h = NB/2), two blocks per wave: T_ij costs h - j products,
         // so a wave takes T_{i,q} and T_{i,h-1-q}; X_ij costs i + 1, so it takes
@@ -540,10 +539,10 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
         const int i1 = wv / (h / 2), q = wv % (h / 2);
         tblock(0, i1, q);
         tblock(0, i1, h - 1 - q);
-        __syncthreads();
+        lds_barrier();
         xblock(0, q, i1);
         xblock(0, h - 1 - q, i1);
-        __syncthreads();
+        lds_barrier();
       }
     };
     if constexpr (NB >= 4) level(std::integral_constant<int, 2>{});
@@ -556,7 +555,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     const int d0 = pn * DP;
     if (pn > 0) {
       load_wv(d0);
-      __syncthreads();  // the previous panel's (w v)^T reads are done
+      lds_barrier();  // the previous panel's (w v)^T reads are done
     }
     // ---- 5. (w v)^T of the panel into LDS (khat's region, free since step 3) --
     if (padded) {
@@ -583,7 +582,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
         sWVT[chan(x) * TT_LD + t] =
             from_f<T>(to_f(wo[i][x / KC][x % KC]) * to_f(vo[i][x / KC][x % KC]));
     }
-    __syncthreads();
+    lds_barrier();
 
     if (pn == 0 && a.a_dbg) {
       float* dst = a.a_dbg + (size_t)cid * BT * BT;

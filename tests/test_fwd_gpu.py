@@ -438,3 +438,17 @@ def test_stage_sanitize_bf16_saturates_like_reference(dev):
     e_o, e_h = np.abs(o - ro).max() * 1e-4, np.abs(h - rh).max() * 1e-4
     print(f"bf16 saturation: max|dout|/1e4={e_o:.3e} max|dh|/1e4={e_h:.3e}")
     assert close(o * 1e-4, ro * 1e-4, 2e-2)[0] and close(h * 1e-4, rh * 1e-4, 2e-2)[0], (e_o, e_h)
+
+
+def test_sanitize_map_on_the_initial_state(dev):
+    """The sanitize map (gdn2_fwd.py:42-44: nan -> 0, +-inf -> +-1e4, clip to
+    +-1e4) on h0, which an empty sequence passes to h_final unchanged otherwise
+    (gdn2_fwd.py:334-335)."""
+    vals = [float("nan"), float("inf"), -float("inf"), 2e4, -3e4, 9999.5, -5.0, 0.0]
+    h0 = torch.zeros((1, 1, 64, 64), device=dev)
+    h0.view(-1)[:len(vals)] = torch.tensor(vals, device=dev)
+    xs = [torch.zeros((1, 0, 1, 64), device=dev) for _ in range(6)]
+    _, hf = gp().gdn2_pallas_forward(*xs, 0.1, h0=h0)
+    got = hf.view(-1)[:len(vals)].cpu().tolist()
+    assert got == [0.0, 1e4, -1e4, 1e4, -1e4, 9999.5, -5.0, 0.0], got
+    assert torch.count_nonzero(hf.view(-1)[len(vals):]).item() == 0
