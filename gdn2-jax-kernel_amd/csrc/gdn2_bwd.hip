@@ -158,6 +158,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   int unit, vs;
+  bool one_xcd = false;   // all slices of the unit on this workgroup's XCD
   {
     const int nwg = gridDim.x, id = blockIdx.x;
     const int per_xcd = nwg / 8;
@@ -165,6 +166,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       const int xcd = id % 8, slot = id / 8;
       unit = xcd * (per_xcd / NVS) + slot / NVS;
       vs = slot % NVS;
+      one_xcd = true;
     } else {
       unit = id / NVS;
       vs = id % NVS;
@@ -235,8 +237,13 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
     constexpr int LDV = 16 * NW * (BT * 4 / LINE);
     constexpr int LQD = 16 * NW * (D * 4 / LINE);
     constexpr int LG = (D * 4 + LINE - 1) / LINE;
-    constexpr int LTOT = 2 * LW + LDV + LQD + LG;
+    constexpr int LTOT = 2 * LW + LDV + LQD + LG;           // at most (one slice)
     constexpr int NTP = ((LTOT + 63) / 64 + NP - 1) / NP;
+    // W / kg^T lines are read by every column slice of the unit: when the
+    // slices share an XCD (one L2), slice v touches only the v-th share of them
+    const int lws = one_xcd ? (2 * LW + NVS - 1) / NVS : 2 * LW;
+    const int lw0 = one_xcd ? vs * lws : 0;
+    const int ltot = lws + LDV + LQD + LG;
     auto touch = [&](int i) __attribute__((always_inline)) {
       const size_t cid = chunk_id(i);
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
@@ -249,12 +256,12 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
 #pragma unroll
       for (int j = 0; j < NTP; ++j) {
         int l = (j * NP + p) * 64 + lane;
-        l = l < LTOT ? l : LTOT - 1;
-        const char* src = l < LW ? wsrc + l * LINE
-                        : l < 2 * LW ? ksrc + (l - LW) * LINE
-                        : l < 2 * LW + LDV ? dsrc + (l - 2 * LW) * LINE
-                        : l < 2 * LW + LDV + LQD ? qsrc + (l - 2 * LW - LDV) * LINE
-                        : gsrc + (l - 2 * LW - LDV - LQD) * LINE;
+        l = l < ltot ? l : ltot - 1;
+        const int lw = min(lw0 + l, 2 * LW - 1);               // line of W | kg^T
+        const char* src = l < lws ? (lw < LW ? wsrc + lw * LINE : ksrc + (lw - LW) * LINE)
+                        : l < lws + LDV ? dsrc + (l - lws) * LINE
+                        : l < lws + LDV + LQD ? qsrc + (l - lws - LDV) * LINE
+                        : gsrc + (l - lws - LDV - LQD) * LINE;
         lds_dma4(src, sJunk);
       }
     };

@@ -678,16 +678,21 @@ struct StateArgs {
 // the compute waves' reads, after which the producers move the next chunk, by
 // then in L2 through the touch issued one chunk ahead.
 //
-// K-split (KS = 2, float32): on float32 MFMA the two chained products of a
-// chunk are the step's critical path (256 16x16x4 instructions per compute wave
-// at BT = 64, D = 128).  Each 16-column slice then has two compute waves, each
+// K-split (KS = 2): the two chained products of a chunk are the step's
+// critical path.  Each 16-column slice then has two compute waves, each
 // holding half of h's rows: both form their half of W h, exchange it through
-// LDS (barrier X, after B), form the same v_new = u - (W h)_lo - (W h)_hi and
-// update their own rows of h -- half the MFMA chain per wave.
+// LDS, form the same v_new = u - (W h)_lo - (W h)_hi and update their own rows
+// of h -- half the MFMA chain per wave, and all four SIMDs' matrix cores busy.
+// float32 exchanges through sX (barrier X, after B); bfloat16, whose two tile
+// buffers leave no room for sX, through the W tile of the current buffer once
+// every compute wave has read it (barriers X1, X2).  Not at D = 64 in
+// bfloat16, where the W tile is smaller than the exchanged partials.
 template <typename T, int BT, int D>
 constexpr int state_bufs() { return 4 * BT * D * (int)sizeof(T) <= 132 * 1024 ? 2 : 1; }
-template <typename T, int D>
-constexpr int state_ksplit() { return sizeof(T) == 4 ? 2 : 1; }
+template <typename T, int BT, int D>
+constexpr int state_ksplit() {
+  return sizeof(T) == 4 ? 2 : (4 * (BT / 16) * 1024 <= BT * D * 2 ? 2 : 1);
+}
 
 template <typename T, int BT, int D, int NW, int NP, int KS>
 __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a) {
@@ -702,14 +707,20 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
   constexpr int NCW = NW * KS;                       // compute waves
   constexpr int NDH = NDT / KS;                      // row tiles of h per compute wave
   static_assert(BUF % 1024 == 0, "tiles must split into 1 KB pieces");
-  static_assert(KS == 1 || (F32 && NDT % KS == 0 && NB % KS == 0), "K-split: float32 only");
+  // barriers per chunk of the K-split exchange: X (float32) or X1, X2 (bfloat16)
+  constexpr int NXB = KS == 1 ? 0 : (F32 ? 1 : 2);
+  static_assert(KS == 1 || (NDT % KS == 0 && NB % KS == 0 &&
+                            (F32 || (KS == 2 && NDH % 2 == 0 && NB % 4 == 0 &&
+                                     NCW * NB * 1024 <= WBYTES))),
+                "K-split: the halves must split into whole k-steps (bfloat16: the W "
+                "tile must hold the exchanged partials)");
   __shared__ __align__(16) char sbuf0[BUF];
   __shared__ __align__(16) char sbuf1[NBUF == 2 ? BUF : 16];
   // u^T in compute-lane order: 16 bytes per lane and row block (float32) or
   // row-block pair (bfloat16, chained order)
   constexpr int UB = F32 ? NB : NB / 2;              // u^T pieces per compute wave
   __shared__ __align__(16) uint4 sU[NW * UB * 64];
-  __shared__ __align__(16) f32x4 sX[KS > 1 ? NCW * NB * 64 : 1];   // K-split partials of W h
+  __shared__ __align__(16) f32x4 sX[KS > 1 && F32 ? NCW * NB * 64 : 1];   // K-split partials of W h
   __shared__ __align__(16) float sGL0[D];
   __shared__ __align__(16) float sGL1[NBUF == 2 ? D : 4];
   __shared__ __align__(16) float sJunk[64];        // target of the L2 touches
@@ -722,6 +733,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
   // tiles they all stream are fetched into that XCD's L2 once.
   const int NSL = a.summary ? 2 * NVS : NVS;
   int unit, vs;
+  bool one_xcd = false;   // all slices of the unit on this workgroup's XCD
   {
     const int nwg = gridDim.x, id = blockIdx.x;
     const int per_xcd = nwg / 8;
@@ -729,6 +741,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
       const int xcd = id % 8, slot = id / 8;
       unit = xcd * (per_xcd / NSL) + slot / NSL;
       vs = slot % NSL;
+      one_xcd = true;
     } else {
       unit = id / NSL;
       vs = id % NSL;
@@ -794,13 +807,21 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
     // L2 touch of chunk c: one 4-byte DMA into a junk slot per 128-byte line of
     // everything issue(c) will read, spread over the producers.  Issued one
     // chunk ahead of the DMA, it turns the DMA's HBM latency into L2 latency.
+    // The W / kg^T lines are read by every column slice of the unit: when the
+    // slices share an XCD (one L2) slice v touches only the v-th share of them
+    // (a touch per line and workgroup cost the scan a fifth of its time), every
+    // slice its own u^T rows.
     constexpr int LINE = 128;
     constexpr int LW = WBYTES / LINE;                       // lines per W / kg^T tile
     constexpr int LUR = BT * (int)sizeof(T) / LINE;         // lines per u^T row
     constexpr int LU = 16 * NW * LUR;                       // this workgroup's u^T rows
     constexpr int LG = (D * 4 + LINE - 1) / LINE;           // g_last
-    constexpr int LTOT = 2 * LW + LU + LG;
+    constexpr int LTOT = 2 * LW + LU + LG;                  // at most (one slice)
     constexpr int NTP = ((LTOT + 63) / 64 + NP - 1) / NP;   // touch instructions per producer
+    const int vsl = vs + (mslice ? NVS : 0);                // slice index within the unit
+    const int lws = one_xcd ? (2 * LW + NSL - 1) / NSL : 2 * LW;   // W | kg^T lines touched here
+    const int lw0 = one_xcd ? vsl * lws : 0;
+    const int ltot = lws + LU + LG;
     auto touch = [&](int c) __attribute__((always_inline)) {
       const size_t cid = (size_t)bh * a.N + c0 + c;
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
@@ -811,11 +832,11 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
 #pragma unroll
       for (int j = 0; j < NTP; ++j) {
         int l = (j * NP + p) * 64 + lane;
-        l = l < LTOT ? l : LTOT - 1;
-        const char* src = l < LW ? wsrc + l * LINE
-                        : l < 2 * LW ? ksrc + (l - LW) * LINE
-                        : l < 2 * LW + LU ? usrc + (l - 2 * LW) * LINE
-                        : gsrc + (l - 2 * LW - LU) * LINE;
+        l = l < ltot ? l : ltot - 1;
+        const int lw = min(lw0 + l, 2 * LW - 1);                // line of W | kg^T
+        const char* src = l < lws ? (lw < LW ? wsrc + lw * LINE : ksrc + (lw - LW) * LINE)
+                        : l < lws + LU ? usrc + (l - lws) * LINE
+                        : gsrc + (l - lws - LU) * LINE;
         lds_dma4(src, sJunk);
       }
     };
@@ -845,7 +866,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
         exp_gl(sGL0);
         barrier();  // A(c)
         barrier();  // B(c)
-        if constexpr (KS > 1) barrier();  // X(c)
+        for (int x = 0; x < NXB; ++x) barrier();  // X(c)
         barrier();  // E(c): chunk c's tiles are no longer read
         if (c + 1 < n) {
           issue(c + 1, sbuf0, sGL0);
@@ -862,16 +883,16 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
       if (c + 1 < n) {
         issue(c + 1, sbuf1, sGL1);
         if (c + 2 < n) touch(c + 2);
-        if constexpr (KS > 1) barrier();  // X(c)
+        for (int x = 0; x < NXB; ++x) barrier();  // X(c)
         wait_chunk(c + 1);
         exp_gl(sGL1);
         barrier();  // A(c+1)
         barrier();  // B(c+1)
         if (c + 2 < n) issue(c + 2, sbuf0, sGL0);
         if (c + 3 < n) touch(c + 3);
-        if constexpr (KS > 1) barrier();  // X(c+1)
+        for (int x = 0; x < NXB; ++x) barrier();  // X(c+1)
       } else {
-        if constexpr (KS > 1) barrier();  // X(c)
+        for (int x = 0; x < NXB; ++x) barrier();  // X(c)
       }
     }
     return;
@@ -944,15 +965,16 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
       for (int i = 0; i < NDH; ++i) store4(hT + (ks * NDH + i) * 16 + 4 * lg, h[i]);
     } else {
 #pragma unroll
-      for (int p = 0; p < NDT / 2; ++p)
-        *reinterpret_cast<Op*>(hT + p * 32 + 8 * lg) = op_from_c(h[2 * p], h[2 * p + 1], (Op*)nullptr);
+      for (int p = 0; p < NDH / 2; ++p)
+        *reinterpret_cast<Op*>(hT + (ks * NDH / 2 + p) * 32 + 8 * lg) =
+            op_from_c(h[2 * p], h[2 * p + 1], (Op*)nullptr);
     }
 
     // v_new -= W h.  The NB row blocks are independent accumulators: the k-step
     // loop is outermost, so consecutive MFMAs never wait on each other, and the
     // next k-step's W operands are read while this one's MFMAs run.
     {
-      constexpr int NKD = F32 ? NDH : NDT / 2;   // k-steps over this wave's d
+      constexpr int NKD = F32 ? NDH : NDH / 2;   // k-steps over this wave's d
       Op hb[NKD];
 #pragma unroll
       for (int kk = 0; kk < NKD; ++kk) {
@@ -962,35 +984,61 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
       auto wop = [&](int it, int kk) __attribute__((always_inline)) {
         const int r = it * 16 + li;
         if constexpr (F32) return load4f(&sW[swz(r, (ks * NDH + kk) * 16 + 4 * lg, D)]);
-        else return op_load<T>(&sW[swz(r, kk * 32 + 8 * lg, D)]);
+        else return op_load<T>(&sW[swz(r, (ks * NKD + kk) * 32 + 8 * lg, D)]);
       };
       f32x4 acc[NB];
-      Op wc[NB], wn[NB];
+      if constexpr (F32) {
+        Op wc[NB], wn[NB];
 #pragma unroll
-      for (int it = 0; it < NB; ++it) {
-        acc[it] = f32x4{0.f, 0.f, 0.f, 0.f};
-        wc[it] = wop(it, 0);
-      }
-#pragma unroll
-      for (int kk = 0; kk < NKD; ++kk) {
-        if (kk + 1 < NKD) {
-#pragma unroll
-          for (int it = 0; it < NB; ++it) wn[it] = wop(it, kk + 1);
+        for (int it = 0; it < NB; ++it) {
+          acc[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+          wc[it] = wop(it, 0);
         }
 #pragma unroll
-        for (int it = 0; it < NB; ++it) mma(acc[it], wc[it], hb[kk]);
+        for (int kk = 0; kk < NKD; ++kk) {
+          if (kk + 1 < NKD) {
 #pragma unroll
-        for (int it = 0; it < NB; ++it) wc[it] = wn[it];
+            for (int it = 0; it < NB; ++it) wn[it] = wop(it, kk + 1);
+          }
+#pragma unroll
+          for (int it = 0; it < NB; ++it) mma(acc[it], wc[it], hb[kk]);
+#pragma unroll
+          for (int it = 0; it < NB; ++it) wc[it] = wn[it];
+        }
+      } else {
+        // bfloat16: one accumulator chain at a time (a chain of dependent
+        // 16x16x32 MFMAs issues faster than interleaved accumulators); the next
+        // row block's W operands are read while this one's chain runs
+        Op wc[NKD], wn[NKD];
+#pragma unroll
+        for (int kk = 0; kk < NKD; ++kk) wc[kk] = wop(0, kk);
+#pragma unroll
+        for (int it = 0; it < NB; ++it) {
+          if (it + 1 < NB) {
+#pragma unroll
+            for (int kk = 0; kk < NKD; ++kk) wn[kk] = wop(it + 1, kk);
+          }
+          acc[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kk = 0; kk < NKD; ++kk) mma(acc[it], wc[kk], hb[kk]);
+#pragma unroll
+          for (int kk = 0; kk < NKD; ++kk) wc[kk] = wn[kk];
+        }
       }
       if constexpr (KS > 1) {
         // exchange the halves; both waves form v_new in the same order
+        f32x4* xb = sX;
+        if constexpr (!F32) {
+          lds_barrier();  // X1(c): every compute wave is done with the W tile
+          xb = reinterpret_cast<f32x4*>(const_cast<char*>(cur));
+        }
 #pragma unroll
-        for (int it = 0; it < NB; ++it) sX[(wv * NB + it) * 64 + lane] = acc[it];
-        lds_barrier();  // X(c)
+        for (int it = 0; it < NB; ++it) xb[(wv * NB + it) * 64 + lane] = acc[it];
+        lds_barrier();  // X(c), X2(c)
         const int pw = (1 - ks) * NW + wcol;
 #pragma unroll
         for (int it = 0; it < NB; ++it) {
-          const f32x4 o = sX[(pw * NB + it) * 64 + lane];
+          const f32x4 o = xb[(pw * NB + it) * 64 + lane];
           vn[it] -= ks == 0 ? acc[it] + o : o + acc[it];
         }
       } else {
@@ -1006,7 +1054,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
         store4(vT + it * 16 + 4 * lg, vn[it]);
     } else {
 #pragma unroll
-      for (int p = 0; p < NB / 2; ++p)
+      for (int p = ks * (NB / 2 / KS); p < (ks + 1) * (NB / 2 / KS); ++p)
         *reinterpret_cast<Op*>(vT + p * 32 + 8 * lg) = op_from_c(vn[2 * p], vn[2 * p + 1], (Op*)nullptr);
     }
 
@@ -1027,6 +1075,26 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
         if constexpr (F32) return load4f(&sK[swz(r, kk * 16 + 4 * lg, BT)]);
         else return op_load<T>(&sK[swz(r, kk * 32 + 8 * lg, BT)]);
       };
+      if constexpr (!F32) {
+        // bfloat16: one chain per row tile of h, as for W h above
+        Op vb[NKT], kc2[NKT], kn2[NKT];
+#pragma unroll
+        for (int kk = 0; kk < NKT; ++kk) {
+          vb[kk] = op_from_c(vn[2 * kk], vn[2 * kk + 1], (Op*)nullptr);
+          kc2[kk] = kop(0, kk);
+        }
+#pragma unroll
+        for (int at = 0; at < NDH; ++at) {
+          if (at + 1 < NDH) {
+#pragma unroll
+            for (int kk = 0; kk < NKT; ++kk) kn2[kk] = kop(at + 1, kk);
+          }
+#pragma unroll
+          for (int kk = 0; kk < NKT; ++kk) mma(h[at], kc2[kk], vb[kk]);
+#pragma unroll
+          for (int kk = 0; kk < NKT; ++kk) kc2[kk] = kn2[kk];
+        }
+      } else {
       Op kc[NDH], kn[AHEAD ? NDH : 1];
       if constexpr (AHEAD) {
 #pragma unroll
@@ -1050,6 +1118,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
 #pragma unroll
           for (int at = 0; at < NDH; ++at) mma(h[at], kop(at, kk), vb);
         }
+      }
       }
       if (!mslice) {
 #pragma unroll
@@ -1298,7 +1367,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   launch_mark(st);
   constexpr int SW = 2;  // compute waves (16 value columns each) per state workgroup
   constexpr int SP = 4;  // producer waves (DMA issue: 4 beat 2 by 14 % on float32 scans)
-  constexpr int SK = state_ksplit<T, D>();   // compute waves per column slice
+  constexpr int SK = state_ksplit<T, BT, D>();   // compute waves per column slice
   constexpr int NVS = D / (16 * SW);
   const size_t BH = (size_t)B * H;
   const int S = S_ws;
