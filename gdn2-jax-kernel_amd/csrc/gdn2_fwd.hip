@@ -1379,19 +1379,26 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
       hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * vl->nseq * NVS),
                          dim3(64 * (SW * SK + SP)), 0, st, va);
   } else if (S > 1) {
+    // Segmented passes (several workgroups per CU's worth of units): bfloat16 at
+    // D >= 128 takes 64 columns per workgroup (four compute waves, no K-split),
+    // so the summary pass, which doubles the units with the M slices, fits the
+    // device in one round (1.1x faster than 32-column workgroups in two rounds)
+    constexpr int GW = sizeof(T) == 2 && D >= 128 ? 4 : SW;
+    constexpr int GK = GW == SW ? SK : 1;
+    constexpr int GVS = D / (16 * GW);
     const int Lseg = (N + S - 1) / S;
     float* seg = reinterpret_cast<float*>(ws + L.SEG);          // [bh][S][2][D][D]
     float* hin = seg + BH * S * 2 * (size_t)D * D;               // [bh][S][D][D]
     StateArgs<T> sum{W, UT, KgT, GL, h0, N, S, Lseg, 1, nullptr, seg, HT, VnT, h_final,
                      nullptr, H};
-    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * S * 2 * NVS),
-                       dim3(64 * (SW * SK + SP)), 0, st, sum);
+    hipLaunchKernelGGL((fwd_state<T, BT, D, GW, SP, GK>), dim3(BH * S * 2 * GVS),
+                       dim3(64 * (GW * GK + SP)), 0, st, sum);
     hipLaunchKernelGGL((seg_combine<D>), dim3(BH * (D / 16)), dim3(256), 0, st, seg, h0, hin,
                        S);
     StateArgs<T> fin{W, UT, KgT, GL, h0, N, S, Lseg, 0, hin, nullptr, HT, VnT, h_final,
                      nullptr, H};
-    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * S * NVS), dim3(64 * (SW * SK + SP)),
-                       0, st, fin);
+    hipLaunchKernelGGL((fwd_state<T, BT, D, GW, SP, GK>), dim3(BH * S * GVS),
+                       dim3(64 * (GW * GK + SP)), 0, st, fin);
   } else {
     StateArgs<T> sa{W, UT, KgT, GL, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT, h_final,
                     nullptr, H};
