@@ -43,15 +43,17 @@ __device__ __forceinline__ void load4_any(const void* p, int bf16, size_t idx, f
 // runs, all loads issued before any LDS store (one memory round trip per chunk).
 // dst (pitch ld) <- S: dst[r][c] = S[r][c], or dst[c][r] when `transposed`.
 // (r0, c0) place the tile in the stored matrix for the masks.
+// Up to 4096 16-byte runs (64 KB of float32) per call, over NT threads.
 struct Staged {
   float v[16][4];
 };
+template <int NT = 256>
 __device__ __forceinline__ void stage_load(Staged& s, const GMat& m, size_t off, int R, int Cc,
                                            int tid) {
   const int cq = Cc >> 2, total = R * cq;
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int i = tid + 256 * u;
+  for (int u = 0; u < 4096 / NT; ++u) {
+    const int i = tid + NT * u;
     if (i < total) {
       const int r = i / cq, c = (i - r * cq) * 4;
       const int sc = m.chained ? kpos<bf16_t>(c) : c;
@@ -59,13 +61,14 @@ __device__ __forceinline__ void stage_load(Staged& s, const GMat& m, size_t off,
     }
   }
 }
+template <int NT = 256>
 __device__ __forceinline__ void stage_store(float* dst, int ld, const Staged& s, const GMat& m,
                                             int R, int Cc, int r0, int c0, bool transposed,
                                             int tid) {
   const int cq = Cc >> 2, total = R * cq;
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int i = tid + 256 * u;
+  for (int u = 0; u < 4096 / NT; ++u) {
+    const int i = tid + NT * u;
     if (i < total) {
       const int r = i / cq, c = (i - r * cq) * 4;
       float v[4];
@@ -1267,12 +1270,316 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
 }
 
 // ============================================================================
-// Wide heads (D = 256): the backward as per-chunk products on a generic kernel.
-// The fused per-chunk kernels above hold D x D and BT x D float32 tiles whole in
-// LDS, which at D = 256 would need up to 266 KB; here every product of B2 and B3
-// is one launch of chunk_gemm over all chunks, with K walked in 64-wide slices,
-// plus three element-wise kernels.  bwd_state (single-buffered at this width)
-// and gram_bwd (32-channel panels) run unchanged.
+// bwd_wy_wide (B3 at D = 256, chunk 64): the products of bwd_wy with the D x D
+// and BT x D operands streamed through LDS in slices, one workgroup of eight
+// waves per chunk.  Wave (rb, hf) owns the 16-token row block rb and half hf of
+// every product's output column tiles.
+//   1-2. e-slices of 32: h^T and dh'^T rows [e][d] staged together; dqg, dW
+//        (both against h) and dkg (against dh') accumulate over the slices;
+//        sum_e dh' h is formed from the staged registers.  dW then sits whole in
+//        LDS (R_W, [t][d]).
+//   3.   d-slices of 64: b k e^{gc} and w v of the slice's channels into LDS
+//        ([s][d]); dA accumulates dW (b k e^gc)^T + dv_new (w v)^T.
+//   4.   A and dv_new^T staged: d(bke^gc) = A^T dW, d(wv) = A^T dv_new -> dv, dw.
+//   5.   dA A^T and dAkk = -(A^T (dA A^T)) . strict, as in bwd_wy.
+// LDS: R_S 68 KB (the slices, then dv_new^T, then dA / dA A^T), R_W 65 KB, A 17 KB.
+// ============================================================================
+template <typename T, typename TG>
+__global__ void __launch_bounds__(512) bwd_wy_wide(WyArgs<T, TG> a) {
+  constexpr int BT = 64, D = 256, NB = BT / 16, NKT = BT / 16, NT = 512;
+  constexpr int HDT = D / 32;                  // output column tiles per wave (half of D/16)
+  constexpr int HKT = NKT / 2;                 // token column tiles per wave
+  constexpr int ES = 32, LDE = D + 4;          // e-slices of phases 1-2: [ES][D] x 2
+  constexpr int DS = 64, LDD = DS + 4;         // d-slices of phase 3: [BT][DS] x 2
+  constexpr int LDV = BT + 4, LDW = D + 4, LDA = BT + 4;
+  constexpr int RS = (2 * ES * LDE > D * LDV) ? 2 * ES * LDE : D * LDV;
+  static_assert(2 * BT * LDD <= RS && BT * LDA <= RS, "slices must fit R_S");
+  constexpr int BF = sizeof(T) == 2;
+  __shared__ __align__(16) float sS[RS];
+  __shared__ __align__(16) float sW[BT * LDW];
+  __shared__ __align__(16) float sA[BT * LDA];
+  __shared__ __align__(16) float sTot[NB * DS];
+  __shared__ __align__(16) float sSdh[D];
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rb = wv & 3, hf = wv >> 2;
+  const int cid = blockIdx.x;
+  const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
+  const size_t HD = (size_t)a.H * D;
+  const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D;
+  const int t = rb * 16 + li;                  // this lane's row for row operands
+  const int tp = BF ? kpos<bf16_t>(t) : t;     // stored column of token t (v_new^T)
+  // Barriers order LDS data only: no wave reads global memory another wave of
+  // this workgroup wrote.
+  if (tid < D) sSdh[tid] = 0.f;
+
+  auto rowop = [&](const float* base, int ld, int r0, int k0) __attribute__((always_inline)) {
+    return load4f(&base[(r0 + li) * ld + k0 + 4 * lg]);
+  };
+  auto colop = [&](const float* base, int ld, int k0, int c0) __attribute__((always_inline)) {
+    f32x4 y;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = base[(k0 + 4 * lg + r) * ld + c0 + li];
+    return y;
+  };
+  auto orow = [&](int r) { return rb * 16 + 4 * lg + r; };
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  // dv_new rows t, k = e (dv_new^T [e][t] read across rows)
+  auto dvn_op = [&](int e0) __attribute__((always_inline)) {
+    f32x4 x;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = a.DVNT[((size_t)cid * D + e0 + 4 * lg + r) * BT + t];
+    return x;
+  };
+
+  // ---- 1-2. dqg = scale do h^T, dW = -dv_new h^T, dkg = v_new dh'^T ----------------
+  const GMat mH{a.HT, BF, D, 0, BF};
+  const GMat mDH{a.DHT, 0, D, 0, 0};
+  const GMat mA{a.A, 0, BT, 0, 0};
+  float* sH = sS;                 // h^T slice [ES][D]
+  float* sDH = sS + ES * LDE;     // dh'^T slice [ES][D]
+  f32x4 aq[HDT], aw[HDT], ak[HDT];
+#pragma unroll
+  for (int n = 0; n < HDT; ++n) aq[n] = aw[n] = ak[n] = z4;
+  float part[4] = {0.f, 0.f, 0.f, 0.f};   // sum_e dh' h, column group tid mod D/4
+  {
+    Staged sa;
+    stage_load<NT>(sa, mA, (size_t)cid * BT * BT, BT, BT, tid);
+    stage_store<NT>(sA, LDA, sa, mA, BT, BT, 0, 0, false, tid);
+  }
+  for (int es = 0; es < D / ES; ++es) {
+    const int e0 = es * ES;
+    Staged sh, sd;
+    stage_load<NT>(sh, mH, (size_t)cid * D * D + (size_t)e0 * D, ES, D, tid);
+    stage_load<NT>(sd, mDH, (size_t)cid * D * D + (size_t)e0 * D, ES, D, tid);
+    f32x4 xdo[ES / 16], xdv[ES / 16], xvn[ES / 16];
+#pragma unroll
+    for (int kk = 0; kk < ES / 16; ++kk) {
+      xdo[kk] = load4f(a.dout + tok0 + (size_t)t * HD + e0 + kk * 16 + 4 * lg);
+      xdv[kk] = dvn_op(e0 + kk * 16);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        xvn[kk][r] = to_f(a.VnT[((size_t)cid * D + e0 + kk * 16 + 4 * lg + r) * BT + tp]);
+    }
+    static_assert(NT % (D / 4) == 0, "column group must stay fixed over the pieces");
+#pragma unroll
+    for (int u = 0; u < ES * D / 4 / NT; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) part[e] += sd.v[u][e] * sh.v[u][e];
+    if (es > 0) lds_barrier();   // the previous slice is read
+    stage_store<NT>(sH, LDE, sh, mH, ES, D, 0, 0, false, tid);
+    stage_store<NT>(sDH, LDE, sd, mDH, ES, D, 0, 0, false, tid);
+    lds_barrier();
+#pragma unroll
+    for (int kk = 0; kk < ES / 16; ++kk)
+#pragma unroll
+      for (int n = 0; n < HDT; ++n) {
+        const int c0 = (hf * HDT + n) * 16;
+        const f32x4 y = colop(sH, LDE, kk * 16, c0);    // h[d][e] as (n = d, k = e)
+        mma(aq[n], xdo[kk], y);
+        mma(aw[n], xdv[kk], y);
+        mma(ak[n], xvn[kk], colop(sDH, LDE, kk * 16, c0));
+      }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) atomicAdd(&sSdh[(tid % (D / 4)) * 4 + e], part[e]);
+  {
+    float* dqg = a.DQG + (size_t)cid * BT * D;
+    float* dkg = a.DKG + (size_t)cid * BT * D;
+#pragma unroll
+    for (int n = 0; n < HDT; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int col = (hf * HDT + n) * 16 + li;
+        dqg[orow(r) * D + col] = a.scale * aq[n][r];
+        dkg[orow(r) * D + col] = ak[n][r];
+        sW[orow(r) * LDW + col] = -aw[n][r];
+      }
+  }
+  lds_barrier();   // dW and sum_e dh' h complete; the e-slices are read
+  if (tid < D) a.SDH[(size_t)cid * D + tid] = sSdh[tid];
+
+  // ---- 3. dA = (dW (b k e^gc)^T + dv_new (w v)^T) . strict, over d-slices ---------
+  // lane (li, lg): token s = t; channels d0 + 32 hf + 16 j + 4 lg + e of the slice
+  float* sK = sS;                 // b k e^gc [s][DS]
+  float* sV = sS + BT * LDD;      // w v [s][DS]
+  f32x4 ada[HKT];
+#pragma unroll
+  for (int n = 0; n < HKT; ++n) ada[n] = z4;
+  for (int ds = 0; ds < D / DS; ++ds) {
+    const int d0 = ds * DS;
+    float loc[2][4], bk[2][4];
+    {
+      const size_t row = tok0 + (size_t)t * HD;
+      float gv[2][4], bv[2][4], kv[2][4], wvv[2][4], vv[2][4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const size_t o = row + d0 + hf * 32 + j * 16 + 4 * lg;
+        load_f<4>(a.g + o, gv[j]);
+        load_f<4>(a.b + o, bv[j]);
+        load_f<4>(a.k + o, kv[j]);
+        load_f<4>(a.w + o, wvv[j]);
+        load_f<4>(a.v + o, vv[j]);
+      }
+      lds_barrier();   // the previous slice's b k e^gc, w v and sums are read
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int cl = hf * 32 + j * 16 + 4 * lg;   // channel within the slice
+        f32x4 wvo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          loc[j][e] = row_scan16(gv[j][e]);
+          bk[j][e] = bv[j][e] * kv[j][e];
+          wvo[e] = wvv[j][e] * vv[j][e];
+        }
+        *reinterpret_cast<f32x4*>(&sV[t * LDD + cl]) = wvo;
+        if (li == 15) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sTot[rb * DS + cl + e] = loc[j][e];
+        }
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int m = 0; m < NB - 1; ++m) {
+      if (m < rb) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const f32x4 tv = load4f(&sTot[m * DS + hf * 32 + j * 16 + 4 * lg]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) loc[j][e] += tv[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f32x4 kb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kb[e] = bk[j][e] * __expf(loc[j][e]);
+      *reinterpret_cast<f32x4*>(&sK[t * LDD + hf * 32 + j * 16 + 4 * lg]) = kb;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int kg = 0; kg < DS / 16; ++kg) {
+      const f32x4 x1 = rowop(sW, LDW, rb * 16, d0 + kg * 16);   // dW rows, k = d
+      const f32x4 x2 = dvn_op(d0 + kg * 16);                    // dv_new rows, k = e
+#pragma unroll
+      for (int n = 0; n < HKT; ++n) {
+        const int s0 = (hf * HKT + n) * 16;
+        mma(ada[n], x1, rowop(sK, LDD, s0, kg * 16));
+        mma(ada[n], x2, rowop(sV, LDD, s0, kg * 16));
+      }
+    }
+  }
+  // dA . strict (gdn2_bwd.py:168), kept in registers until step 5
+#pragma unroll
+  for (int n = 0; n < HKT; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int s2 = (hf * HKT + n) * 16 + li;
+      ada[n][r] = s2 < orow(r) ? sanitize(ada[n][r]) : 0.f;
+    }
+
+  // ---- 4. d(bke^gc) = A^T dW, d(wv) = A^T dv_new -> dv, dw --------------------------
+  const GMat mDV{a.DVNT, 0, BT, 0, 0};
+  {
+    Staged sv;
+    stage_load<NT>(sv, mDV, (size_t)cid * D * BT, D, BT, tid);
+    lds_barrier();   // the last d-slice is read
+    stage_store<NT>(sS, LDV, sv, mDV, D, BT, 0, 0, false, tid);
+  }
+  lds_barrier();
+  {
+    f32x4 akb[HDT], awv[HDT];
+#pragma unroll
+    for (int n = 0; n < HDT; ++n) akb[n] = awv[n] = z4;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+      const f32x4 x = colop(sA, LDA, kt * 16, rb * 16);   // A^T rows m, k = t
+#pragma unroll
+      for (int n = 0; n < HDT; ++n) {
+        const int c0 = (hf * HDT + n) * 16;
+        mma(akb[n], x, colop(sW, LDW, kt * 16, c0));   // dW[t][d] as (n = d, k = t)
+        mma(awv[n], x, rowop(sS, LDV, c0, kt * 16));   // dv_new^T[e][t]
+      }
+    }
+    float* dkbd = a.DKBD + (size_t)cid * BT * D;
+#pragma unroll
+    for (int n = 0; n < HDT; ++n) {
+      float wl[4], vl[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const size_t o = tok0 + (size_t)orow(r) * HD + (hf * HDT + n) * 16 + li;
+        wl[r] = to_f(a.w[o]);
+        vl[r] = to_f(a.v[o]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int col = (hf * HDT + n) * 16 + li;
+        const size_t o = tok0 + (size_t)orow(r) * HD + col;
+        dkbd[orow(r) * D + col] = akb[n][r];
+        a.dv[o] = from_f<T>(sanitize(awv[n][r] * wl[r]));
+        a.dw[o] = from_f<T>(sanitize(awv[n][r] * vl[r]));
+      }
+    }
+  }
+  lds_barrier();   // dv_new^T is read
+
+  // ---- 5. dA A^T, dAkk = -(A^T (dA A^T)) . strict -----------------------------------
+  float* sDA = sS;   // dA, then dA A^T [t][s]
+#pragma unroll
+  for (int n = 0; n < HKT; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sDA[orow(r) * LDA + (hf * HKT + n) * 16 + li] = ada[n][r];
+  lds_barrier();
+  {
+    f32x4 atm[HKT];
+#pragma unroll
+    for (int n = 0; n < HKT; ++n) atm[n] = z4;
+#pragma unroll
+    for (int ks = 0; ks < NKT; ++ks) {
+      const f32x4 x = rowop(sDA, LDA, rb * 16, ks * 16);    // dA rows t, k = s
+#pragma unroll
+      for (int n = 0; n < HKT; ++n)
+        mma(atm[n], x, rowop(sA, LDA, (hf * HKT + n) * 16, ks * 16));   // A[n][s]
+    }
+    lds_barrier();   // both waves of the row block have read its rows of dA
+#pragma unroll
+    for (int n = 0; n < HKT; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sDA[orow(r) * LDA + (hf * HKT + n) * 16 + li] = sanitize(atm[n][r]);   // :174
+  }
+  lds_barrier();
+  {
+    f32x4 aak[HKT];
+#pragma unroll
+    for (int n = 0; n < HKT; ++n) aak[n] = z4;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+      const f32x4 x = colop(sA, LDA, kt * 16, rb * 16);    // A^T rows m, k
+#pragma unroll
+      for (int n = 0; n < HKT; ++n)
+        mma(aak[n], x, colop(sDA, LDA, kt * 16, (hf * HKT + n) * 16));
+    }
+    float* dakk = a.DAKK + (size_t)cid * BT * BT;
+#pragma unroll
+    for (int n = 0; n < HKT; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n2 = (hf * HKT + n) * 16 + li;
+        dakk[orow(r) * BT + n2] = n2 < orow(r) ? sanitize(-aak[n][r]) : 0.f;   // :209
+      }
+  }
+}
+
+// ============================================================================
+// Wide heads (D = 256): B2 as per-chunk products on a generic kernel.  The fused
+// B2 kernel holds D x D and BT x D float32 tiles whole in LDS, which at D = 256
+// would need up to 266 KB; here each of its three products is one launch of
+// chunk_gemm over all chunks, with K walked in 64-wide slices.  B3 is
+// bwd_wy_wide; bwd_state (single-buffered at this width) and gram_bwd (32-channel
+// panels) run unchanged.
 // ============================================================================
 // One operand of a per-chunk product: logical X(r, k) (r = row of the result for
 // A, column for B) stored at [k*ld + r] (kmajor) or [r*ld + k], element offset
@@ -1385,58 +1692,6 @@ __global__ void __launch_bounds__(256) chunk_gemm(WGemmArgs a) {
     }
 }
 
-// b k e^{gc} and w v per token, chunk-major [t][d] float32; one thread per channel
-// (gc: running sum of g over the chunk's tokens)
-template <typename T, typename TG>
-__global__ void __launch_bounds__(256) wide_kbd_wv(const T* k, const T* w, const T* v,
-                                                  const T* b, const TG* g, int T_len, int H,
-                                                  int N, int D, float* KBD, float* WV) {
-  constexpr int BT = 64;
-  const int d = threadIdx.x, cid = blockIdx.x;
-  if (d >= D) return;
-  const int c = cid % N, bh = cid / N, hh = bh % H, bb = bh / H;
-  const size_t HD = (size_t)H * D;
-  const size_t tok0 = ((size_t)bb * T_len + (size_t)c * BT) * HD + (size_t)hh * D + d;
-  float gc = 0.f;
-  for (int t = 0; t < BT; ++t) {
-    const size_t o = tok0 + (size_t)t * HD, wo = ((size_t)cid * BT + t) * D + d;
-    gc += to_f(g[o]);
-    KBD[wo] = to_f(b[o]) * to_f(k[o]) * __expf(gc);
-    WV[wo] = to_f(w[o]) * to_f(v[o]);
-  }
-}
-
-// sum_e dh'[d][e] h[d][e] per chunk and channel d (dh'^T float32 [e][d], h^T [e][d]
-// in the residual type); one thread per channel
-template <typename T>
-__global__ void __launch_bounds__(256) wide_sdh(const float* DHT, const T* HT, int D, float* SDH) {
-  const int d = threadIdx.x, cid = blockIdx.x;
-  if (d >= D) return;
-  const size_t base = (size_t)cid * D * D;
-  const int pd = sizeof(T) == 2 ? kpos<bf16_t>(d) : d;
-  float s = 0.f;
-  for (int e = 0; e < D; ++e) s += DHT[base + (size_t)e * D + d] * to_f(HT[base + (size_t)e * D + pd]);
-  SDH[(size_t)cid * D + d] = s;
-}
-
-// dv = d(wv) w, dw = d(wv) v (gdn2_bwd.py:204-205), d(wv) chunk-major [t][e]
-template <typename T>
-__global__ void __launch_bounds__(256) wide_dvdw(const float* DWV, const T* w, const T* v,
-                                                int T_len, int H, int N, int D, T* dv, T* dw) {
-  constexpr int BT = 64;
-  const int d = threadIdx.x, cid = blockIdx.x;
-  if (d >= D) return;
-  const int c = cid % N, bh = cid / N, hh = bh % H, bb = bh / H;
-  const size_t HD = (size_t)H * D;
-  const size_t tok0 = ((size_t)bb * T_len + (size_t)c * BT) * HD + (size_t)hh * D + d;
-  for (int t = 0; t < BT; ++t) {
-    const size_t o = tok0 + (size_t)t * HD;
-    const float x = DWV[((size_t)cid * BT + t) * D + d];
-    dv[o] = from_f<T>(sanitize(x * to_f(w[o])));
-    dw[o] = from_f<T>(sanitize(x * to_f(v[o])));
-  }
-}
-
 // ============================================================================
 // Host side
 // ============================================================================
@@ -1445,8 +1700,8 @@ size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t) {
 }
 
 
-// The backward at D = 256 (chunk 64): B2 and B3 as chunk_gemm launches, the
-// reverse scan and gram_bwd as at D <= 128.  Launch marks: before B2, after B2,
+// The backward at D = 256 (chunk 64): B2 as chunk_gemm launches, B3 fused
+// (bwd_wy_wide), the reverse scan and gram_bwd as at D <= 128.  Launch marks: before B2, after B2,
 // after the scan, after B3, after gram_bwd (as the fused path).
 template <typename T, typename TG>
 hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* q,
@@ -1502,33 +1757,13 @@ hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* 
                      dim3(64 * (BW * BK + BP)), 0, st, sa);
   launch_mark(st);
   if (NC > 0) {
-    // B3 (gdn2_bwd.py:126-210), products as in bwd_wy
-    const WMat hT = cm(fHT, BF, dd, D, 1, 0, BF);         // h(d, e) = h^T[e][d]
-    const WMat dvn = cm(buf(B_DVNT), 0, td, BT, 1, 0, 0);  // dv_new(t, e) = dv_new^T[e][t]
-    const WMat Ats = cm(fA, 0, tt, BT, 1, 0, 0);          // A^T(s, t) = A[t][s]
-    gemm(tok(dout, 0), hT, out(buf(B_DQG), td, D, 0, scale, 0), BT, D, D);       // dqg
-    gemm(dvn, hT, out(buf(B_DW), td, D, 0, -1.f, 0), BT, D, D);                   // dW
-    gemm(cm(fVnT, BF, td, BT, 1, 0, BF), cm(buf(B_DHT), 0, dd, D, 1, 0, 0),
-         out(buf(B_DKG), td, D, 0, 1.f, 0), BT, D, D);                            // dkg
-    hipLaunchKernelGGL((wide_sdh<T>), dim3(NC), dim3(D), 0, st, (const float*)buf(B_DHT),
-                       (const T*)fHT, D, buf(B_SDH));
-    hipLaunchKernelGGL((wide_kbd_wv<T, TG>), dim3(NC), dim3(D), 0, st, (const T*)k,
-                       (const T*)w, (const T*)v, (const T*)b, (const TG*)g, T_len, H, N, D,
-                       buf(B_KBD), buf(B_WV));
-    gemm(cm(buf(B_DW), 0, td, D, 0, 0, 0), cm(buf(B_KBD), 0, td, D, 0, 0, 0),
-         out(buf(B_DA), tt, BT, 2, 1.f, 0), BT, BT, D);                           // dA = dW kbd^T
-    gemm(dvn, cm(buf(B_WV), 0, td, D, 0, 0, 0), out(buf(B_DA), tt, BT, 2, 1.f, 1, 1), BT, BT,
-         D);                                                                      // + dv_new wv^T
-    gemm(Ats, cm(buf(B_DW), 0, td, D, 1, 0, 0), out(buf(B_DKBD), td, D, 0, 1.f, 0), BT, D,
-         BT);                                                                     // A^T dW
-    gemm(Ats, cm(buf(B_DVNT), 0, td, BT, 0, 0, 0), out(buf(B_DWV), td, D, 0, 1.f, 0), BT, D,
-         BT);                                                                     // A^T dv_new
-    hipLaunchKernelGGL((wide_dvdw<T>), dim3(NC), dim3(D), 0, st, (const float*)buf(B_DWV),
-                       (const T*)w, (const T*)v, T_len, H, N, D, (T*)dv, (T*)dw);
-    gemm(cm(buf(B_DA), 0, tt, BT, 0, 0, 0), cm(fA, 0, tt, BT, 0, 0, 0),
-         out(buf(B_TMP), tt, BT, 0, 1.f, 0, 1), BT, BT, BT);                      // dA A^T
-    gemm(Ats, cm(buf(B_TMP), 0, tt, BT, 1, 0, 0), out(buf(B_DAKK), tt, BT, 2, -1.f, 0, 1), BT,
-         BT, BT);                                                                 // dAkk
+    // B3 (gdn2_bwd.py:126-210): one fused kernel with the D x D operands streamed
+    WyArgs<T, TG> wa{(const T*)k,  (const T*)w,     (const T*)v,  (const T*)b, (const TG*)g,
+                     dout,         (const T*)fHT,   (const T*)fVnT,
+                     fA,           buf(B_DHT),      buf(B_DVNT),
+                     T_len, H, N, scale, buf(B_DQG), buf(B_DKG), buf(B_DKBD),
+                     buf(B_DAKK), buf(B_SDH), (T*)dv, (T*)dw};
+    hipLaunchKernelGGL((bwd_wy_wide<T, TG>), dim3(NC), dim3(512), 0, st, wa);
     launch_mark(st);
     // B4 + B3 element-wise tail + B5
     GramArgs<T, TG> gr{(const T*)q,  (const T*)k,  (const T*)b,  (const TG*)g,

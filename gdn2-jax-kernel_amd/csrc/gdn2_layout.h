@@ -23,8 +23,6 @@
 //   DHT  [D][D]  dh_{c+1}^T           DVNT [D][BT] dv_new^T
 //   DQG, DKG, DKBD [BT][D]            DAKK [BT][BT]
 //   SDH  [D]      sum_e dh_{c+1}[d][e] h_c[d][e]
-// and, for D > 128 only (the backward of per-chunk products): DW, KBD, WV, DWV
-// [BT][D] (dW, b k e^gc, w v, d(wv)), DA, TMP [BT][BT] (dA, dA A^T).
 #pragma once
 
 #include <stddef.h>
@@ -148,8 +146,7 @@ inline int state_segments(long long BH, int N, int D, int forced) {
 namespace gdn2 {
 
 enum BwdBuf {
-  B_DAQK, B_DVPT, B_QDOT, B_DHT, B_DVNT, B_DQG, B_DKG, B_DKBD, B_DAKK, B_SDH,
-  B_DW, B_KBD, B_WV, B_DWV, B_DA, B_TMP, B_COUNT
+  B_DAQK, B_DVPT, B_QDOT, B_DHT, B_DVNT, B_DQG, B_DKG, B_DKBD, B_DAKK, B_SDH, B_COUNT
 };
 
 struct BwdLayout {
@@ -161,10 +158,7 @@ struct BwdLayout {
 inline BwdLayout bwd_layout(size_t nchunks, int BT, int D) {
   BwdLayout L;
   const size_t tt = (size_t)BT * BT, td = (size_t)BT * D, dd = (size_t)D * D;
-  const size_t w = D > 128 ? 1 : 0;   // regions of the wide-head backward only
-  const size_t per[B_COUNT] = {tt,     td,     dd,     dd,     td,     td,    td,    td,
-                               tt,     (size_t)D, w * td, w * td, w * td, w * td, w * tt,
-                               w * tt};
+  const size_t per[B_COUNT] = {tt, td, dd, dd, td, td, td, td, tt, (size_t)D};
   size_t off = 0;
   for (int i = 0; i < B_COUNT; ++i) {
     L.off[i] = off;

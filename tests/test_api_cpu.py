@@ -53,13 +53,13 @@ def test_partial_last_chunk_passes_validation():
 
 
 def test_bwd_workspace_d256():
-    """D = 256 trains too: its backward adds six per-chunk regions (dW, b k e^gc,
-    w v, d(wv), dA, dA A^T) to the layout of D <= 128, each 256-byte aligned."""
+    """D = 256 trains with the layout of D <= 128 (B3 is fused at every width):
+    ten per-chunk float32 regions, each 256-byte aligned."""
     from gdn2_package import _lib
     al = lambda x: (x + 255) // 256 * 256
     nc, BT, D = 1 * 2 * (128 // 64), 64, 256
     tt, td, dd = BT * BT, BT * D, D * D
-    per = [tt, td, dd, dd, td, td, td, td, tt, D, td, td, td, td, tt, tt]
+    per = [tt, td, dd, dd, td, td, td, td, tt, D]
     assert _lib.lib().gdn2_bwd_workspace_bytes(1, 128, 2, 256, 64, _lib.GDN2_F32) == \
         sum(al(nc * p * 4) for p in per)
 
