@@ -480,11 +480,11 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
 //   qdot = scale do^T qg                [e][d]   ((scale qg^T do)^T)
 // with do, v_new^T, Aqk and qg staged once in LDS as float32.  Wave w owns the
 // 16-row block w of dAqk and of Aqk^T do, and row blocks 2w, 2w+1 (over e) of
-// qdot (D = 128; one block per wave at D = 64).  do stays in LDS throughout; the
-// second operand of each product takes one region in turn (v_new^T, then Aqk,
-// then qg, each loaded into registers ahead and stored after a barrier), so the
-// kernel needs 67 KB of LDS at D = 128: two workgroups per CU, one streaming
-// while the other computes.
+// qdot (D = 128; one block per wave at D = 64, four at D = 256).  do stays in LDS
+// throughout; the second operand of each product takes one region in turn
+// (v_new^T, then Aqk, then qg, each loaded into registers ahead and stored after a
+// barrier), so the kernel needs 67 KB of LDS at D = 128: two workgroups per CU, one
+// streaming while the other computes (136 KB and one at D = 256).
 // ============================================================================
 template <typename T>
 struct B2Args {
@@ -499,7 +499,7 @@ struct B2Args {
 };
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 2) bwd_b2(B2Args<T> a) {
+__global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
   constexpr int BT = 64, NDT = D / 16, NKT = BT / 16;
   constexpr int LDO = D + 4, LDV = BT + 4, LDA = BT + 4, LDQ = D + 4;
   constexpr int BF = sizeof(T) == 2;
@@ -539,8 +539,10 @@ __global__ void __launch_bounds__(256, 2) bwd_b2(B2Args<T> a) {
     stage_load(s2, mV, (size_t)cid * D * BT, D, BT, tid);
     stage_store(sDo, LDO, s1, mDo, BT, D, 0, 0, false, tid);
     stage_store(sV, LDV, s2, mV, D, BT, 0, 0, false, tid);
-    // qg and Aqk are in flight while dAqk is formed (LDS-only barriers)
-    stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
+    // qg and Aqk are in flight while dAqk is formed (LDS-only barriers); at
+    // D = 256 qg (64 KB) is loaded after the Aqk^T do product instead, which
+    // would otherwise spill the registers that hold it
+    if constexpr (D <= 128) stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
     stage_load(s2, mA, (size_t)cid * BT * BT, BT, BT, tid);
     lds_barrier();
     // dAqk[t][s] = sum_e do[t][e] v_new[s][e], s <= t: column blocks right of
@@ -588,12 +590,14 @@ __global__ void __launch_bounds__(256, 2) bwd_b2(B2Args<T> a) {
     for (int nt = 0; nt < NDT; ++nt)
       store4(o + (size_t)(nt * 16 + li) * BT + wv * 16 + 4 * lg, sanitize4(acc[nt]));  // :96
   }
+  if constexpr (D > 128) stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
   lds_barrier();  // every wave is done with Aqk
   stage_store(sQ, LDQ, s1, mQ, BT, D, 0, 0, false, tid);
   lds_barrier();
-  // qdot[e][d] = scale sum_t do[t][e] qg[t][d]
+  // qdot[e][d] = scale sum_t do[t][e] qg[t][d] (one row block at a time: at
+  // D = 256 a block's sixteen accumulator tiles are 64 registers)
   {
-#pragma unroll
+#pragma unroll (D <= 128 ? QB : 1)
     for (int qb = 0; qb < QB; ++qb) {
       const int eb = wv * QB + qb;
       f32x4 acc[NDT];
@@ -1574,125 +1578,6 @@ __global__ void __launch_bounds__(512) bwd_wy_wide(WyArgs<T, TG> a) {
 }
 
 // ============================================================================
-// Wide heads (D = 256): B2 as per-chunk products on a generic kernel.  The fused
-// B2 kernel holds D x D and BT x D float32 tiles whole in LDS, which at D = 256
-// would need up to 266 KB; here each of its three products is one launch of
-// chunk_gemm over all chunks, with K walked in 64-wide slices.  B3 is
-// bwd_wy_wide; bwd_state (single-buffered at this width) and gram_bwd (32-channel
-// panels) run unchanged.
-// ============================================================================
-// One operand of a per-chunk product: logical X(r, k) (r = row of the result for
-// A, column for B) stored at [k*ld + r] (kmajor) or [r*ld + k], element offset
-// bb*sb + hh*sh + c*sc for chunk c of head hh of batch bb.
-struct WMat {
-  const void* p;
-  int bf16;                 // element type in memory
-  long long sb, sh, sc;
-  int ld;
-  int kmajor;
-  int mask;                 // on the stored (row, col): 1 keep col <= row, 2 keep col < row
-  int chained;              // bfloat16: stored columns in chained order (kpos)
-};
-// C[m][n] = alpha sum_k A(m,k) B(n,k) (+ C), stored [m*ld + n], mask on (m, n)
-struct WOut {
-  float* p;
-  long long sb, sh, sc;
-  int ld;
-  int mask;
-  float alpha;
-  int accum;
-  int sat;                  // sanitize the stored value (a stage output the reference clips)
-};
-struct WGemmArgs {
-  WMat A, B;
-  WOut C;
-  int M, N, K, H, Nc;
-};
-
-// Stage a 64 x 64 slice (rows r0.., k0..) of an operand into registers: four
-// 16-byte runs per thread.
-__device__ __forceinline__ void wide_load(f32x4 (&v)[4], const WMat& m, size_t off, int r0,
-                                          int k0, int tid) {
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int i = tid + 256 * u, a = i >> 4, b = (i & 15) * 4;   // stored row a, col b
-    const int srow = m.kmajor ? k0 + a : r0 + a;
-    const int scol = m.kmajor ? r0 + b : k0 + b;
-    const int pcol = m.chained ? kpos<bf16_t>(scol) : scol;
-    float t[4];
-    load4_any(m.p, m.bf16, off + (size_t)srow * m.ld + pcol, t);
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v[u][e] = ((m.mask == 1 && scol + e > srow) || (m.mask == 2 && scol + e >= srow)) ? 0.f : t[e];
-  }
-}
-// ... and into LDS as [r][k] (pitch 68)
-__device__ __forceinline__ void wide_store(float* dst, const f32x4 (&v)[4], const WMat& m,
-                                           int tid) {
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int i = tid + 256 * u, a = i >> 4, b = (i & 15) * 4;
-    if (!m.kmajor) {
-      *reinterpret_cast<f32x4*>(&dst[a * 68 + b]) = v[u];
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dst[(b + e) * 68 + a] = v[u][e];
-    }
-  }
-}
-
-// One workgroup per chunk and 64 x 64 output tile; wave w owns output rows
-// 16w..16w+15 (four 16 x 16 accumulators).  The next K slice's loads are in
-// flight while the current slice's products run.
-__global__ void __launch_bounds__(256) chunk_gemm(WGemmArgs a) {
-  __shared__ __align__(16) float sX[64 * 68];
-  __shared__ __align__(16) float sY[64 * 68];
-  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int MT = a.M / 64, NT = a.N / 64;
-  const int id = blockIdx.x;
-  const int cid = id / (MT * NT), mt = (id / NT) % MT, nt = id % NT;
-  const int c = cid % a.Nc, bh = cid / a.Nc, hh = bh % a.H, bb = bh / a.H;
-  const size_t offA = bb * a.A.sb + hh * a.A.sh + c * a.A.sc;
-  const size_t offB = bb * a.B.sb + hh * a.B.sh + c * a.B.sc;
-  const size_t offC = bb * a.C.sb + hh * a.C.sh + c * a.C.sc;
-  const int m0 = mt * 64, n0 = nt * 64;
-  f32x4 acc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  f32x4 ra[4], rb[4];
-  wide_load(ra, a.A, offA, m0, 0, tid);
-  wide_load(rb, a.B, offB, n0, 0, tid);
-  for (int k0 = 0; k0 < a.K; k0 += 64) {
-    wide_store(sX, ra, a.A, tid);
-    wide_store(sY, rb, a.B, tid);
-    __syncthreads();
-    if (k0 + 64 < a.K) {
-      wide_load(ra, a.A, offA, m0, k0 + 64, tid);
-      wide_load(rb, a.B, offB, n0, k0 + 64, tid);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const f32x4 x = load4f(&sX[(wv * 16 + li) * 68 + ks * 16 + 4 * lg]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) mma(acc[j], x, load4f(&sY[(j * 16 + li) * 68 + ks * 16 + 4 * lg]));
-    }
-    lds_barrier();   // the slice is read before the next one is stored
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = m0 + wv * 16 + 4 * lg + r, n = n0 + j * 16 + li;
-      float val = a.C.alpha * acc[j][r];
-      if ((a.C.mask == 1 && n > m) || (a.C.mask == 2 && n >= m)) val = 0.f;
-      float* dst = a.C.p + offC + (size_t)m * a.C.ld + n;
-      if (a.C.accum) val += *dst;
-      *dst = a.C.sat ? sanitize(val) : val;
-    }
-}
-
-// ============================================================================
 // Host side
 // ============================================================================
 size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t) {
@@ -1700,8 +1585,10 @@ size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t) {
 }
 
 
-// The backward at D = 256 (chunk 64): B2 as chunk_gemm launches, B3 fused
-// (bwd_wy_wide), the reverse scan and gram_bwd as at D <= 128.  Launch marks: before B2, after B2,
+// The backward at D = 256 (chunk 64): B2 by bwd_b2 (its tiles still fit LDS,
+// 136 KB), B3 by bwd_wy_wide (the D x D operands streamed in slices: the D = 128
+// kernel would need 266 KB), the reverse scan (single-buffered at this width) and
+// gram_bwd (32-channel panels) as at D <= 128.  Launch marks: before B2, after B2,
 // after the scan, after B3, after gram_bwd (as the fused path).
 template <typename T, typename TG>
 hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* q,
@@ -1710,42 +1597,21 @@ hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* 
                            const float* dh_final, void* dq, void* dk, void* dv, void* dw,
                            void* db, void* dg, float* dh0, const char* fws, char* ws,
                            const int* cu_chunks, int nseq) {
-  constexpr int BT = 64, D = 256, BF = sizeof(T) == 2;
+  constexpr int BT = 64, D = 256;
   const int N = T_len / BT;
   const size_t NC = (size_t)B * H * N;
   const FwdLayout F = fwd_layout(NC, BT, D, sizeof(T));
   const BwdLayout L = bwd_layout(NC, BT, D);
   auto buf = [&](BwdBuf i) { return reinterpret_cast<float*>(ws + L.off[i]); };
-  const long long td = (long long)BT * D, tt = (long long)BT * BT, dd = (long long)D * D;
-  // chunk-major tiles of `per` elements; (B,T,H,D) token rows
-  auto cm = [&](const void* p, int bf, long long per, int ld, int kmajor, int mask,
-                int chained) {
-    return WMat{p, bf, (long long)H * N * per, (long long)N * per, per, ld, kmajor, mask,
-                chained};
-  };
-  auto tok = [&](const void* p, int kmajor) {
-    return WMat{p, 0, (long long)T_len * H * D, D, (long long)BT * H * D, H * D, kmajor, 0, 0};
-  };
-  auto out = [&](float* p, long long per, int ld, int mask, float alpha, int accum,
-                 int sat = 0) {
-    return WOut{p, (long long)H * N * per, (long long)N * per, per, ld, mask, alpha, accum, sat};
-  };
-  auto gemm = [&](const WMat& A, const WMat& Bm, const WOut& C, int M, int Nn, int K) {
-    WGemmArgs ga{A, Bm, C, M, Nn, K, H, N};
-    hipLaunchKernelGGL(chunk_gemm, dim3(NC * (M / 64) * (Nn / 64)), dim3(256), 0, st, ga);
-  };
   const void* fVnT = fws + F.VnT;
   const void* fHT = fws + F.HT;
   const float* fA = reinterpret_cast<const float*>(fws + F.A);
   launch_mark(st);
   if (NC > 0) {
     // B2: dAqk = (do v_new^T) . causal, dvp^T = (Aqk^T do)^T, qdot = scale (qg^T do)^T
-    gemm(tok(dout, 0), cm(fVnT, BF, td, BT, 1, 0, BF), out(buf(B_DAQK), tt, BT, 1, 1.f, 0, 1),
-         BT, BT, D);
-    gemm(tok(dout, 1), cm(fws + F.Aqk, BF, tt, BT, 1, 1, 0),
-         out(buf(B_DVPT), td, BT, 0, 1.f, 0, 1), D, BT, BT);
-    gemm(tok(dout, 1), cm(fws + F.Qg, BF, td, D, 1, 0, 0), out(buf(B_QDOT), dd, D, 0, scale, 0),
-         D, D, BT);
+    B2Args<T> ba{dout, (const T*)fVnT, (const T*)(fws + F.Aqk), (const T*)(fws + F.Qg), T_len,
+                 H, N, scale, buf(B_DAQK), buf(B_DVPT), buf(B_QDOT)};
+    hipLaunchKernelGGL((bwd_b2<T, D>), dim3(NC), dim3(256), 0, st, ba);
     launch_mark(st);
   }
   BStateArgs<T> sa{(const T*)(fws + F.W), (const T*)(fws + F.KgT),

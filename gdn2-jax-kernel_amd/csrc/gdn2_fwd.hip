@@ -707,20 +707,22 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
   constexpr int NCW = NW * KS;                       // compute waves
   constexpr int NDH = NDT / KS;                      // row tiles of h per compute wave
   static_assert(BUF % 1024 == 0, "tiles must split into 1 KB pieces");
-  // barriers per chunk of the K-split exchange: X (float32) or X1, X2 (bfloat16)
-  constexpr int NXB = KS == 1 ? 0 : (F32 ? 1 : 2);
+  // K-split exchange: through sX (float32, two parts; barrier X) or through the W
+  // tile of the current buffer (barriers X1, X2)
+  constexpr bool XSX = F32 && KS == 2;
+  constexpr int NXB = KS == 1 ? 0 : (XSX ? 1 : 2);
   static_assert(KS == 1 || (NDT % KS == 0 && NB % KS == 0 &&
-                            (F32 || (KS == 2 && NDH % 2 == 0 && NB % 4 == 0 &&
-                                     NCW * NB * 1024 <= WBYTES))),
-                "K-split: the halves must split into whole k-steps (bfloat16: the W "
-                "tile must hold the exchanged partials)");
+                            (XSX || NCW * NB * 1024 <= WBYTES) &&
+                            (F32 || (KS == 2 && NDH % 2 == 0 && NB % 4 == 0))),
+                "K-split: the parts must split into whole k-steps, and the W tile "
+                "must hold the exchanged partials");
   __shared__ __align__(16) char sbuf0[BUF];
   __shared__ __align__(16) char sbuf1[NBUF == 2 ? BUF : 16];
   // u^T in compute-lane order: 16 bytes per lane and row block (float32) or
   // row-block pair (bfloat16, chained order)
   constexpr int UB = F32 ? NB : NB / 2;              // u^T pieces per compute wave
   __shared__ __align__(16) uint4 sU[NW * UB * 64];
-  __shared__ __align__(16) f32x4 sX[KS > 1 && F32 ? NCW * NB * 64 : 1];   // K-split partials of W h
+  __shared__ __align__(16) f32x4 sX[XSX ? NCW * NB * 64 : 1];   // K-split partials of W h
   __shared__ __align__(16) float sGL0[D];
   __shared__ __align__(16) float sGL1[NBUF == 2 ? D : 4];
   __shared__ __align__(16) float sJunk[64];        // target of the L2 touches
@@ -1026,20 +1028,23 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
         }
       }
       if constexpr (KS > 1) {
-        // exchange the halves; both waves form v_new in the same order
+        // exchange the parts; every wave of the slice sums them in the order of
+        // the k-parts, so all form the same v_new
         f32x4* xb = sX;
-        if constexpr (!F32) {
+        if constexpr (!XSX) {
           lds_barrier();  // X1(c): every compute wave is done with the W tile
           xb = reinterpret_cast<f32x4*>(const_cast<char*>(cur));
         }
 #pragma unroll
         for (int it = 0; it < NB; ++it) xb[(wv * NB + it) * 64 + lane] = acc[it];
         lds_barrier();  // X(c), X2(c)
-        const int pw = (1 - ks) * NW + wcol;
 #pragma unroll
         for (int it = 0; it < NB; ++it) {
-          const f32x4 o = xb[(pw * NB + it) * 64 + lane];
-          vn[it] -= ks == 0 ? acc[it] + o : o + acc[it];
+          f32x4 sum = ks == 0 ? acc[it] : xb[(wcol * NB + it) * 64 + lane];
+#pragma unroll
+          for (int q = 1; q < KS; ++q)
+            sum += ks == q ? acc[it] : xb[((q * NW + wcol) * NB + it) * 64 + lane];
+          vn[it] -= sum;
         }
       } else {
 #pragma unroll
