@@ -47,21 +47,28 @@ __device__ __forceinline__ void load4_any(const void* p, int bf16, size_t idx, f
 struct Staged {
   float v[16][4];
 };
-template <int NT = 256>
+// Run i = tid + nt u of a staging loop (tid < nt) exists.  With `ct` it is
+// decided at compile time for whole rounds (total constant after inlining), so
+// full rounds carry no branch and rounds past the end no code; without it each
+// run tests i < total (branches the scheduler does not move loads across).
+__device__ __forceinline__ bool run_in(bool ct, int u, int i, int total, int nt) {
+  return ct ? (u + 1) * nt <= total || (u * nt < total && i < total) : i < total;
+}
+template <int NT = 256, bool CT = false>
 __device__ __forceinline__ void stage_load(Staged& s, const GMat& m, size_t off, int R, int Cc,
                                            int tid) {
   const int cq = Cc >> 2, total = R * cq;
 #pragma unroll
   for (int u = 0; u < 4096 / NT; ++u) {
     const int i = tid + NT * u;
-    if (i < total) {
+    if (run_in(CT, u, i, total, NT)) {
       const int r = i / cq, c = (i - r * cq) * 4;
       const int sc = m.chained ? kpos<bf16_t>(c) : c;
       load4_any(m.p, m.bf16, off + (size_t)r * m.ld + sc, s.v[u]);
     }
   }
 }
-template <int NT = 256>
+template <int NT = 256, bool CT = false>
 __device__ __forceinline__ void stage_store(float* dst, int ld, const Staged& s, const GMat& m,
                                             int R, int Cc, int r0, int c0, bool transposed,
                                             int tid) {
@@ -69,7 +76,7 @@ __device__ __forceinline__ void stage_store(float* dst, int ld, const Staged& s,
 #pragma unroll
   for (int u = 0; u < 4096 / NT; ++u) {
     const int i = tid + NT * u;
-    if (i < total) {
+    if (run_in(CT, u, i, total, NT)) {
       const int r = i / cq, c = (i - r * cq) * 4;
       float v[4];
 #pragma unroll
@@ -627,10 +634,17 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
 //   dAkk = -(A^T (dA A^T)) . strict
 // Stored operands per chunk: do in (B,T,H,D) rows; h^T, dh'^T as [e][d]; v_new^T,
 // dv_new^T as [e][t]; A as [t][s].  One workgroup per chunk; wave w owns the
-// 16-token row block w of every product (up to 2 x 8 independent 16 x 16
-// accumulators).  Shared operands sit in LDS:
-//   R1: h^T, then dh'^T, then (b k e^gc | w v) as [s][d], then dv_new^T
-//   R2: dW [t][d]     R4: dA [t][s], then dA A^T     R5: A [t][s]
+// 16-token row block w of every product.
+// The channels are taken in halves of 64 (two at D = 128): every product above
+// except dA is separable over them (dqg, dW, dkg, d(bke^gc) over the key channel
+// d; d(wv), dv, dw over the value channel e), and dA's two half sums accumulate in
+// registers.  Per half: h^T[:, half] staged (dqg, dW of the half), dh'^T[:, half]
+// staged over it (dkg, sum_e dh' h), (b k e^gc | w v) of the half (dA half sum),
+// then A and dv_new^T[half] (d(bke^gc), d(wv)); after the last half dA A^T and
+// dAkk.  71 KB of LDS and under 256 registers: two workgroups per CU, one
+// streaming while the other computes (the next half's h^T and step 5's operands
+// are also loaded one phase ahead).  The triangular products skip the 16 x 16
+// blocks that A (lower triangular) and the strict masks make zero.
 // A stored matrix read with its row index as the MFMA k index is read per lane
 // as four scalars (colop); one read with k contiguous is one 16-byte load (rowop).
 // ============================================================================
@@ -652,26 +666,37 @@ struct WyArgs {
 };
 
 template <typename T, typename TG, int D>
-__global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
+__global__ void __launch_bounds__(256, 2) bwd_wy(WyArgs<T, TG> a) {
   constexpr int BT = 64, NB = BT / 16, NDT = D / 16, NKT = BT / 16;
-  constexpr int LD1 = D + 4, LDV = BT + 4, LD2 = D + 4, LD4 = BT + 4;
-  constexpr int R1 = (D * LD1 > 2 * BT * LD1) ? D * LD1 : 2 * BT * LD1;
+  constexpr int DH = D < 64 ? D : 64, NH = D / DH, NDH = DH / 16;   // channel halves
+  constexpr int LDH = DH + 4;   // [e][d of the half], [s][d of the half]
+  constexpr int LD4 = BT + 4;   // [t][s], [e][t]
   constexpr int BF = sizeof(T) == 2;
+  // R1 in turn: h^T[:, half] (D x DH), dh'^T[:, half], (b k e^gc | w v) of the half
+  // (2 x BT x DH), A (BT x BT) with dv_new^T[half] (DH x BT)
+  constexpr int R1 = (D * LDH > 2 * BT * LD4) ? D * LDH : 2 * BT * LD4;
+  static_assert(2 * BT * LDH <= R1, "(b k e^gc | w v) must fit R1");
   __shared__ __align__(16) float sR1[R1];
-  __shared__ __align__(16) float sR2[BT * LD2];
-  __shared__ __align__(16) float sR4[BT * LD4];
-  __shared__ __align__(16) float sR5[BT * LD4];
-  __shared__ __align__(16) float sTot[NB * D];
-  __shared__ __align__(16) float sSdh[D];
+  __shared__ __align__(16) float sW[BT * LDH];    // dW[:, half] [t][d]
+  __shared__ __align__(16) float sDA[BT * LD4];   // dA, then dA A^T
+  __shared__ __align__(16) float sTot[NB * DH];
+  __shared__ __align__(16) float sSdh[DH];
+  float* const sKB = sR1;                // (b k e^gc)[s][d]
+  float* const sWV = sR1 + BT * LDH;     // (w v)[s][e]
+  float* const sA = sR1;                 // A [t][s]
+  float* const sDV = sR1 + BT * LD4;     // dv_new^T[e][t]
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  // the wave's row block as a scalar: the triangular products below skip the
+  // blocks that A (lower triangular) and the strict masks make zero, by uniform
+  // branches (every skipped term is an exact zero, so results are unchanged)
+  const int wb = __builtin_amdgcn_readfirstlane(wv);
   const int cid = blockIdx.x;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
   const size_t HD = (size_t)a.H * D;
   const size_t tok0 = ((size_t)bb * a.T_len + (size_t)c * BT) * HD + (size_t)hh * D;
-  const int t = wv * 16 + li;   // this lane's row for row operands of the own block
+  const int t0 = wv * 16 + li;   // this lane's row for row operands of the own block
   // Barriers order LDS data only (lds_barrier): no wave reads global memory
   // another wave of this workgroup wrote.
-  if (tid < D) sSdh[tid] = 0.f;
 
   auto rowop = [&](const float* base, int ld, int r0, int k0) __attribute__((always_inline)) {
     return load4f(&base[(r0 + li) * ld + k0 + 4 * lg]);
@@ -682,115 +707,147 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
     for (int r = 0; r < 4; ++r) y[r] = base[(k0 + 4 * lg + r) * ld + c0 + li];
     return y;
   };
-  // C-layout element (r) of the own block's tile at column tile nt: row, column
-  auto orow = [&](int r) { return wv * 16 + 4 * lg + r; };
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 
-  // ---- 1. dqg = scale do h^T, dW = -dv_new h^T --------------------------------
-  Staged st;
   const GMat mH{a.HT, BF, D, 0, BF};
-  stage_load(st, mH, (size_t)cid * D * D, D, D, tid);
-  f32x4 xdo[NDT], xdv[NDT];
-#pragma unroll
-  for (int kg = 0; kg < NDT; ++kg) {
-    xdo[kg] = load4f(a.dout + tok0 + (size_t)t * HD + kg * 16 + 4 * lg);
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      xdv[kg][r] = a.DVNT[((size_t)cid * D + kg * 16 + 4 * lg + r) * BT + t];
-  }
-  stage_store(sR1, LD1, st, mH, D, D, 0, 0, false, tid);
-  lds_barrier();
-  {
-    f32x4 aq[NDT], aw[NDT];
-#pragma unroll
-    for (int nt = 0; nt < NDT; ++nt) aq[nt] = aw[nt] = z4;
-#pragma unroll
-    for (int kg = 0; kg < NDT; ++kg)
-#pragma unroll
-      for (int nt = 0; nt < NDT; ++nt) {
-        const f32x4 y = colop(sR1, LD1, kg * 16, nt * 16);    // h[d][e] as (n = d, k = e)
-        mma(aq[nt], xdo[kg], y);
-        mma(aw[nt], xdv[kg], y);
-      }
-    float* dqg = a.DQG + (size_t)cid * BT * D;
-#pragma unroll
-    for (int nt = 0; nt < NDT; ++nt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        dqg[orow(r) * D + nt * 16 + li] = a.scale * aq[nt][r];
-        sR2[orow(r) * LD2 + nt * 16 + li] = -aw[nt][r];
-      }
-  }
-  lds_barrier();   // every wave is done with h^T
-
-  // ---- 2. dkg = v_new dh'^T ------------------------------------------------------
   const GMat mDH{a.DHT, 0, D, 0, 0};
   const GMat mA{a.A, 0, BT, 0, 0};
-  Staged sa;
-  stage_load(st, mDH, (size_t)cid * D * D, D, D, tid);
-  stage_load(sa, mA, (size_t)cid * BT * BT, BT, BT, tid);
-  {
-    f32x4 xvn[NDT];
-    const int tp = BF ? kpos<bf16_t>(t) : t;   // stored column of token t
+  const GMat mDV{a.DVNT, 0, BT, 0, 0};
+  const size_t offDD = (size_t)cid * D * D;
+  // tid, opaque to the compiler: each staging computes its own addresses (the
+  // stagings share their offset pattern, and one shared set of 64-bit addresses
+  // would stay live through the kernel)
+  auto otid = [&]() __attribute__((always_inline)) {
+    int x = tid;
+    asm volatile("" : "+v"(x));
+    return x;
+  };
+
+  // The own rows of do, dv_new and v_new (k = value channel e) are loaded per half
+  // (from L2 the second time) ahead of the step using them: the registers stay
+  // within two workgroups per CU.
+  Staged st;
+  stage_load<256, true>(st, mH, offDD, D, DH, otid());   // h^T[:, half 0]
+  // rows e0 .. e0 + 16 n of a stored [e][t] matrix at column col, as k = e operands
+  // (lane offsets from the chunk's tile, opaque per call like the stagings)
+  auto load_rows = [&](f32x4* x, auto src, int e0, int n, int col) __attribute__((always_inline)) {
+    const auto* tile = src + (size_t)cid * D * BT;
+    int off = (e0 + 4 * lg) * BT + col;
+    asm volatile("" : "+v"(off));
+#pragma unroll
+    for (int kg = 0; kg < n; ++kg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[kg][r] = to_f(tile[off + (kg * 16 + r) * BT]);
+  };
+  f32x4 ada[NKT];   // dA rows of the own block, summed over the halves
+#pragma unroll
+  for (int s2 = 0; s2 < NKT; ++s2) ada[s2] = z4;
+
+#pragma unroll
+  for (int hf = 0; hf < NH; ++hf) {
+    // the half's own token row and first channel, opaque to the compiler: the two
+    // halves then compute their addresses where they use them instead of sharing
+    // them (a shared address stays live across the whole kernel)
+    int t = t0, d0 = hf * DH;
+    asm volatile("" : "+v"(t), "+v"(d0));
+    // C-layout element (r) of the own block's tile: its row
+    auto orow = [&](int r) { return t - li + 4 * lg + r; };
+    // ---- 1. dqg = scale do h^T, dW = -dv_new h^T (columns d of the half) -------
+    f32x4 xdo[NDT], xdv[NDT], xvn[NDT];
 #pragma unroll
     for (int kg = 0; kg < NDT; ++kg)
+      xdo[kg] = load4f(a.dout + tok0 + (size_t)t * HD + kg * 16 + 4 * lg);
+    load_rows(xdv, a.DVNT, 0, NDT, t);
+    if (hf > 0) lds_barrier();   // the previous half's A, dv_new^T and dW reads are done
+    if (tid < DH) sSdh[tid] = 0.f;
+    stage_store<256, true>(sR1, LDH, st, mH, D, DH, 0, 0, false, tid);
+    lds_barrier();
+    {
+      f32x4 aq[NDH], aw[NDH];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        xvn[kg][r] = to_f(a.VnT[((size_t)cid * D + kg * 16 + 4 * lg + r) * BT + tp]);
-    // sum_e dh'[d][e] h[d][e]: each thread multiplies the dh'^T runs it staged
-    // with the h^T runs still at the same places in R1 (the thread's column
-    // group is fixed: index tid + 256 u keeps tid mod D/4), then one LDS add per
-    // column
+      for (int nt = 0; nt < NDH; ++nt) aq[nt] = aw[nt] = z4;
+#pragma unroll
+      for (int kg = 0; kg < NDT; ++kg) {
+#pragma unroll
+        for (int nt = 0; nt < NDH; ++nt) {
+          const f32x4 y = colop(sR1, LDH, kg * 16, nt * 16);   // h[d][e] as (n = d, k = e)
+          mma(aq[nt], xdo[kg], y);
+          mma(aw[nt], xdv[kg], y);
+        }
+      }
+      float* dqg = a.DQG + (size_t)cid * BT * D + d0;
+#pragma unroll
+      for (int nt = 0; nt < NDH; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          dqg[orow(r) * D + nt * 16 + li] = a.scale * aq[nt][r];
+          sW[orow(r) * LDH + nt * 16 + li] = -aw[nt][r];
+        }
+    }
+
+    // ---- 2. dkg = v_new dh'^T, sum_e dh'[d][e] h[d][e] (columns d of the half) --
+    Staged sd;   // dh'^T[:, half]
+    stage_load<256, true>(sd, mDH, offDD + d0, D, DH, otid());
+    load_rows(xvn, a.VnT, 0, NDT, BF ? kpos<bf16_t>(t) : t);
+    // each thread multiplies the dh'^T runs it staged with the h^T runs still at
+    // the same places in R1 (its column group is fixed: index tid + 256 u keeps
+    // tid mod DH/4), then one LDS add per column
     {
       float part[4] = {0.f, 0.f, 0.f, 0.f};
-      constexpr int CQ = D / 4;
+      constexpr int CQ = DH / 4;
+      static_assert(256 % CQ == 0, "a thread's column group must stay fixed");
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         const int i = tid + 256 * u;
         if (i < D * CQ) {
-          const f32x4 hv = load4f(&sR1[(i / CQ) * LD1 + (i % CQ) * 4]);
+          const f32x4 hv = load4f(&sR1[(i / CQ) * LDH + (i % CQ) * 4]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) part[e] += st.v[u][e] * hv[e];
+          for (int e = 0; e < 4; ++e) part[e] += sd.v[u][e] * hv[e];
         }
       }
+      lds_barrier();   // every wave is done with h^T
 #pragma unroll
       for (int e = 0; e < 4; ++e) atomicAdd(&sSdh[(tid % CQ) * 4 + e], part[e]);
     }
-    stage_store(sR1, LD1, st, mDH, D, D, 0, 0, false, tid);
-    stage_store(sR5, LD4, sa, mA, BT, BT, 0, 0, false, tid);
+    stage_store<256, true>(sR1, LDH, sd, mDH, D, DH, 0, 0, false, tid);
     lds_barrier();
-    if (tid < D) a.SDH[(size_t)cid * D + tid] = sSdh[tid];
-    f32x4 ak[NDT];
+    if (tid < DH) a.SDH[(size_t)cid * D + d0 + tid] = sSdh[tid];
+    {
+      f32x4 ak[NDH];
 #pragma unroll
-    for (int nt = 0; nt < NDT; ++nt) ak[nt] = z4;
+      for (int nt = 0; nt < NDH; ++nt) ak[nt] = z4;
 #pragma unroll
-    for (int kg = 0; kg < NDT; ++kg)
+      for (int kg = 0; kg < NDT; ++kg) {
 #pragma unroll
-      for (int nt = 0; nt < NDT; ++nt) mma(ak[nt], xvn[kg], colop(sR1, LD1, kg * 16, nt * 16));
-    float* dkg = a.DKG + (size_t)cid * BT * D;
+        for (int nt = 0; nt < NDH; ++nt)
+          mma(ak[nt], xvn[kg], colop(sR1, LDH, kg * 16, nt * 16));
+      }
+      float* dkg = a.DKG + (size_t)cid * BT * D + d0;
 #pragma unroll
-    for (int nt = 0; nt < NDT; ++nt)
+      for (int nt = 0; nt < NDH; ++nt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dkg[orow(r) * D + nt * 16 + li] = ak[nt][r];
-  }
-
-  // ---- 3. b k e^{gc} and w v into R1 (rows s of the own block) ------------------
-  // lane (li, lg): token s = t, channels 16 j + 4 lg + e; gc = in-block cumsum over
-  // the 16 lanes li (DPP) + the sums of the earlier blocks (sTot)
-  constexpr int NJ = D / 16;
-  float loc[NJ][4], bk[NJ][4];
-  {
-    const size_t row = tok0 + (size_t)t * HD;
-    float gv[NJ][4], bv[NJ][4], kv[NJ][4], wvv[NJ][4], vv[NJ][4];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const size_t o = row + j * 16 + 4 * lg;
-      load_f<4>(a.g + o, gv[j]);
-      load_f<4>(a.b + o, bv[j]);
-      load_f<4>(a.k + o, kv[j]);
-      load_f<4>(a.w + o, wvv[j]);
-      load_f<4>(a.v + o, vv[j]);
+        for (int r = 0; r < 4; ++r) dkg[orow(r) * D + nt * 16 + li] = ak[nt][r];
     }
+    // step 3's inputs (channels of the half)
+    constexpr int NJ = NDH;
+    float gv[NJ][4], bv[NJ][4], kv[NJ][4], wvv[NJ][4], vv[NJ][4];
+    {
+      const size_t row = tok0 + (size_t)t * HD + d0;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const size_t o = row + j * 16 + 4 * lg;
+        load_f<4>(a.g + o, gv[j]);
+        load_f<4>(a.b + o, bv[j]);
+        load_f<4>(a.k + o, kv[j]);
+        load_f<4>(a.w + o, wvv[j]);
+        load_f<4>(a.v + o, vv[j]);
+      }
+    }
+
+    // ---- 3. b k e^{gc} and w v of the half into R1 (rows s of the own block) ---
+    // lane (li, lg): token s = t, channels d0 + 16 j + 4 lg + e; gc = in-block
+    // cumsum over the 16 lanes li (DPP) + the sums of the earlier blocks (sTot)
+    float loc[NJ][4], bk[NJ][4];
     lds_barrier();   // every wave is done with dh'^T
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -801,128 +858,148 @@ __global__ void __launch_bounds__(256) bwd_wy(WyArgs<T, TG> a) {
         bk[j][e] = bv[j][e] * kv[j][e];
         wvo[e] = wvv[j][e] * vv[j][e];
       }
-      *reinterpret_cast<f32x4*>(&sR1[(BT + t) * LD1 + j * 16 + 4 * lg]) = wvo;
+      *reinterpret_cast<f32x4*>(&sWV[t * LDH + j * 16 + 4 * lg]) = wvo;
       if (li == 15) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sTot[wv * D + j * 16 + 4 * lg + e] = loc[j][e];
+        for (int e = 0; e < 4; ++e) sTot[wv * DH + j * 16 + 4 * lg + e] = loc[j][e];
       }
     }
-  }
-  lds_barrier();
-  // gc = loc + sums of the earlier blocks: independent 16-byte LDS reads per
-  // (block, channel group), all issued before the exponentials
+    lds_barrier();
+    // gc = loc + sums of the earlier blocks: independent 16-byte LDS reads per
+    // (block, channel group), all issued before the exponentials
 #pragma unroll
-  for (int m = 0; m < NB - 1; ++m) {
-    if (m < wv) {
+    for (int m = 0; m < NB - 1; ++m) {
+      if (m < wv) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const f32x4 tv = load4f(&sTot[m * D + j * 16 + 4 * lg]);
+        for (int j = 0; j < NJ; ++j) {
+          const f32x4 tv = load4f(&sTot[m * DH + j * 16 + 4 * lg]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) loc[j][e] += tv[e];
+          for (int e = 0; e < 4; ++e) loc[j][e] += tv[e];
+        }
       }
     }
-  }
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    f32x4 kb;
+    for (int j = 0; j < NJ; ++j) {
+      f32x4 kb;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) kb[e] = bk[j][e] * __expf(loc[j][e]);
-    *reinterpret_cast<f32x4*>(&sR1[t * LD1 + j * 16 + 4 * lg]) = kb;
-  }
-  lds_barrier();
+      for (int e = 0; e < 4; ++e) kb[e] = bk[j][e] * __expf(loc[j][e]);
+      *reinterpret_cast<f32x4*>(&sKB[t * LDH + j * 16 + 4 * lg]) = kb;
+    }
+    // the own rows of dv_new in the half, and step 5's A and dv_new^T[half], in
+    // flight during the dA products
+    f32x4 xdh[NDH];
+    load_rows(xdh, a.DVNT, d0, NDH, t);
+    Staged sa, sv;
+    stage_load<256, true>(sa, mA, (size_t)cid * BT * BT, BT, BT, otid());
+    stage_load<256, true>(sv, mDV, ((size_t)cid * D + d0) * BT, DH, BT, otid());
+    lds_barrier();
 
-  // ---- 4. dA = (dW (b k e^gc)^T + dv_new (w v)^T) . strict ----------------------
-  {
-    f32x4 ada[NKT];
+    // ---- 4. dA += dW[:, half] (b k e^gc)[:, half]^T + dv_new[:, half] (w v)[:, half]^T
 #pragma unroll
-    for (int st2 = 0; st2 < NKT; ++st2) ada[st2] = z4;
+    for (int kg = 0; kg < NDH; ++kg) {
+      const f32x4 x1 = rowop(sW, LDH, wv * 16, kg * 16);   // dW rows, k = d
 #pragma unroll
-    for (int kg = 0; kg < NDT; ++kg) {
-      const f32x4 x1 = rowop(sR2, LD2, wv * 16, kg * 16);   // dW rows, k = d
-#pragma unroll
-      for (int st2 = 0; st2 < NKT; ++st2) {
-        mma(ada[st2], x1, rowop(sR1, LD1, st2 * 16, kg * 16));           // (b k e^gc)[s][d]
-        mma(ada[st2], xdv[kg], rowop(sR1, LD1, BT + st2 * 16, kg * 16));  // (w v)[s][e]
+      for (int s2 = 0; s2 < NKT; ++s2) {
+        if (s2 <= wb) {   // dA is strictly lower: blocks s > t are masked
+          mma(ada[s2], x1, rowop(sKB, LDH, s2 * 16, kg * 16));       // (b k e^gc)[s][d]
+          mma(ada[s2], xdh[kg], rowop(sWV, LDH, s2 * 16, kg * 16));  // (w v)[s][e]
+        }
       }
     }
+    if (hf == NH - 1) {
 #pragma unroll
-    for (int st2 = 0; st2 < NKT; ++st2)
+      for (int s2 = 0; s2 < NKT; ++s2)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int s2 = st2 * 16 + li;
-        sR4[orow(r) * LD4 + s2] = s2 < orow(r) ? sanitize(ada[st2][r]) : 0.f;   // :168
-      }
-  }
-  lds_barrier();   // dA complete; (b k e^gc | w v) no longer read
+        for (int r = 0; r < 4; ++r) {
+          const int sc = s2 * 16 + li;
+          sDA[orow(r) * LD4 + sc] = sc < orow(r) ? sanitize(ada[s2][r]) : 0.f;   // :168
+        }
+    }
+    lds_barrier();   // (b k e^gc | w v) no longer read
 
-  // ---- 5. d(bke^gc) = A^T dW, d(wv) = A^T dv_new, TMP = dA A^T -------------------
-  const GMat mDV{a.DVNT, 0, BT, 0, 0};
-  stage_load(st, mDV, (size_t)cid * D * BT, D, BT, tid);
-  stage_store(sR1, LDV, st, mDV, D, BT, 0, 0, false, tid);
-  lds_barrier();
-  {
-    f32x4 akb[NDT], awv[NDT];
+    // ---- 5. d(bke^gc)[:, half] = A^T dW[:, half], d(wv)[:, half] = A^T dv_new[:, half]
+    stage_store<256, true>(sA, LD4, sa, mA, BT, BT, 0, 0, false, tid);
+    stage_store<256, true>(sDV, LD4, sv, mDV, DH, BT, 0, 0, false, tid);
+    if (hf + 1 < NH) stage_load<256, true>(st, mH, offDD + d0 + DH, D, DH, otid());   // next half's h^T
+    lds_barrier();
+    {
+      f32x4 akb[NDH], awv[NDH];
 #pragma unroll
-    for (int nt = 0; nt < NDT; ++nt) akb[nt] = awv[nt] = z4;
+      for (int nt = 0; nt < NDH; ++nt) akb[nt] = awv[nt] = z4;
 #pragma unroll
-    for (int kt = 0; kt < NKT; ++kt) {
-      const f32x4 x = colop(sR5, LD4, kt * 16, wv * 16);   // A^T rows m, k = t
+      for (int kt = 0; kt < NKT; ++kt) {
+        if (kt >= wb) {   // A[t][m] = 0 for t < m
+          const f32x4 x = colop(sA, LD4, kt * 16, wv * 16);   // A^T rows m, k = t
 #pragma unroll
-      for (int nt = 0; nt < NDT; ++nt) {
-        mma(akb[nt], x, colop(sR2, LD2, kt * 16, nt * 16));   // dW[t][d] as (n = d, k = t)
-        mma(awv[nt], x, rowop(sR1, LDV, nt * 16, kt * 16));   // dv_new^T[e][t]
+          for (int nt = 0; nt < NDH; ++nt) {
+            mma(akb[nt], x, colop(sW, LDH, kt * 16, nt * 16));   // dW[t][d] as (n = d, k = t)
+            mma(awv[nt], x, rowop(sDV, LD4, nt * 16, kt * 16));  // dv_new^T[e][t]
+          }
+        }
       }
+      // dv = d(wv) w, dw = d(wv) v: w and v re-read in this layout (L2: step 3
+      // read them), so the element-wise pass does not need them
+      float* dkbd = a.DKBD + (size_t)cid * BT * D + d0;
+      float wl[NDH][4], vl[NDH][4];
+#pragma unroll
+      for (int nt = 0; nt < NDH; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const size_t o = tok0 + (size_t)orow(r) * HD + d0 + nt * 16 + li;
+          wl[nt][r] = to_f(a.w[o]);
+          vl[nt][r] = to_f(a.v[o]);
+        }
+#pragma unroll
+      for (int nt = 0; nt < NDH; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const size_t o = tok0 + (size_t)orow(r) * HD + d0 + nt * 16 + li;
+          dkbd[orow(r) * D + nt * 16 + li] = akb[nt][r];
+          a.dv[o] = from_f<T>(sanitize(awv[nt][r] * wl[nt][r]));
+          a.dw[o] = from_f<T>(sanitize(awv[nt][r] * vl[nt][r]));
+        }
     }
-    // dv = d(wv) w, dw = d(wv) v: w and v re-read in this layout (L2: step 3
-    // read them), so the element-wise pass does not need them
-    float* dkbd = a.DKBD + (size_t)cid * BT * D;
-    float wl[NDT][4], vl[NDT][4];
-#pragma unroll
-    for (int nt = 0; nt < NDT; ++nt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const size_t o = tok0 + (size_t)orow(r) * HD + nt * 16 + li;
-        wl[nt][r] = to_f(a.w[o]);
-        vl[nt][r] = to_f(a.v[o]);
-      }
-#pragma unroll
-    for (int nt = 0; nt < NDT; ++nt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const size_t o = tok0 + (size_t)orow(r) * HD + nt * 16 + li;
-        dkbd[orow(r) * D + nt * 16 + li] = akb[nt][r];
-        a.dv[o] = from_f<T>(sanitize(awv[nt][r] * wl[nt][r]));
-        a.dw[o] = from_f<T>(sanitize(awv[nt][r] * vl[nt][r]));
-      }
   }
+
+  // ---- 6. TMP = dA A^T (the own rows of dA are read only by this wave) ----------
+  // Only the columns n < m <= t of TMP enter dAkk[m][n] (strict), so columns past
+  // the own block are not formed (those entries keep dA's zeros)
+  auto orow = [&](int r) { return wv * 16 + 4 * lg + r; };
   {
     f32x4 atm[NKT];
 #pragma unroll
     for (int nt = 0; nt < NKT; ++nt) atm[nt] = z4;
 #pragma unroll
     for (int ks = 0; ks < NKT; ++ks) {
-      const f32x4 x = rowop(sR4, LD4, wv * 16, ks * 16);    // dA rows t, k = s
+      if (ks <= wb) {   // dA[t][s] = 0 for s > t
+        const f32x4 x = rowop(sDA, LD4, wv * 16, ks * 16);    // dA rows t, k = s
 #pragma unroll
-      for (int nt = 0; nt < NKT; ++nt) mma(atm[nt], x, rowop(sR5, LD4, nt * 16, ks * 16));  // A[n][s]
+        for (int nt = 0; nt < NKT; ++nt)
+          if (nt <= wb) mma(atm[nt], x, rowop(sA, LD4, nt * 16, ks * 16));  // A[n][s]
+      }
     }
-    // the own rows of dA are read only by this wave: overwrite them with dA A^T
 #pragma unroll
     for (int nt = 0; nt < NKT; ++nt)
+      if (nt <= wb) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sR4[orow(r) * LD4 + nt * 16 + li] = sanitize(atm[nt][r]);  // :174
+        for (int r = 0; r < 4; ++r) sDA[orow(r) * LD4 + nt * 16 + li] = sanitize(atm[nt][r]);  // :174
+      }
   }
   lds_barrier();
 
-  // ---- 6. dAkk = -(A^T (dA A^T)) . strict -----------------------------------------
+  // ---- 7. dAkk = -(A^T (dA A^T)) . strict -----------------------------------------
   {
     f32x4 aak[NKT];
 #pragma unroll
     for (int nt = 0; nt < NKT; ++nt) aak[nt] = z4;
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
-      const f32x4 x = colop(sR5, LD4, kt * 16, wv * 16);    // A^T rows m, k
+      if (kt >= wb) {   // A[t][m] = 0 for t < m; columns n >= m are masked
+        const f32x4 x = colop(sA, LD4, kt * 16, wv * 16);    // A^T rows m, k
 #pragma unroll
-      for (int nt = 0; nt < NKT; ++nt) mma(aak[nt], x, colop(sR4, LD4, kt * 16, nt * 16));
+        for (int nt = 0; nt < NKT; ++nt)
+          if (nt <= wb) mma(aak[nt], x, colop(sDA, LD4, kt * 16, nt * 16));
+      }
     }
     float* dakk = a.DAKK + (size_t)cid * BT * BT;
 #pragma unroll
