@@ -1546,9 +1546,11 @@ __global__ void __launch_bounds__(512) bwd_wy_wide(WyArgs<T, TG> a) {
       const f32x4 x2 = dvn_op(d0 + kg * 16);                    // dv_new rows, k = e
 #pragma unroll
       for (int n = 0; n < HKT; ++n) {
-        const int s0 = (hf * HKT + n) * 16;
-        mma(ada[n], x1, rowop(sK, LDD, s0, kg * 16));
-        mma(ada[n], x2, rowop(sV, LDD, s0, kg * 16));
+        if (hf * HKT + n <= rb) {   // dA is strictly lower: blocks s > t are masked
+          const int s0 = (hf * HKT + n) * 16;
+          mma(ada[n], x1, rowop(sK, LDD, s0, kg * 16));
+          mma(ada[n], x2, rowop(sV, LDD, s0, kg * 16));
+        }
       }
     }
   }
@@ -1576,6 +1578,7 @@ __global__ void __launch_bounds__(512) bwd_wy_wide(WyArgs<T, TG> a) {
     for (int n = 0; n < HDT; ++n) akb[n] = awv[n] = z4;
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
+      if (kt < rb) continue;   // A[t][m] = 0 for t < m
       const f32x4 x = colop(sA, LDA, kt * 16, rb * 16);   // A^T rows m, k = t
 #pragma unroll
       for (int n = 0; n < HDT; ++n) {
@@ -1618,18 +1621,24 @@ __global__ void __launch_bounds__(512) bwd_wy_wide(WyArgs<T, TG> a) {
 #pragma unroll
     for (int n = 0; n < HKT; ++n) atm[n] = z4;
 #pragma unroll
+    // dA[t][s] = 0 for s > t; only the columns n < m <= t of dA A^T enter dAkk,
+    // so columns past the own row block are not formed (they keep dA's zeros)
     for (int ks = 0; ks < NKT; ++ks) {
+      if (ks > rb) continue;
       const f32x4 x = rowop(sDA, LDA, rb * 16, ks * 16);    // dA rows t, k = s
 #pragma unroll
       for (int n = 0; n < HKT; ++n)
-        mma(atm[n], x, rowop(sA, LDA, (hf * HKT + n) * 16, ks * 16));   // A[n][s]
+        if (hf * HKT + n <= rb)
+          mma(atm[n], x, rowop(sA, LDA, (hf * HKT + n) * 16, ks * 16));   // A[n][s]
     }
     lds_barrier();   // both waves of the row block have read its rows of dA
 #pragma unroll
     for (int n = 0; n < HKT; ++n)
+      if (hf * HKT + n <= rb) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sDA[orow(r) * LDA + (hf * HKT + n) * 16 + li] = sanitize(atm[n][r]);   // :174
+        for (int r = 0; r < 4; ++r)
+          sDA[orow(r) * LDA + (hf * HKT + n) * 16 + li] = sanitize(atm[n][r]);   // :174
+      }
   }
   lds_barrier();
   {
@@ -1638,10 +1647,11 @@ __global__ void __launch_bounds__(512) bwd_wy_wide(WyArgs<T, TG> a) {
     for (int n = 0; n < HKT; ++n) aak[n] = z4;
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
+      if (kt < rb) continue;   // A[t][m] = 0 for t < m; columns n >= m are masked
       const f32x4 x = colop(sA, LDA, kt * 16, rb * 16);    // A^T rows m, k
 #pragma unroll
       for (int n = 0; n < HKT; ++n)
-        mma(aak[n], x, colop(sDA, LDA, kt * 16, (hf * HKT + n) * 16));
+        if (hf * HKT + n <= rb) mma(aak[n], x, colop(sDA, LDA, kt * 16, (hf * HKT + n) * 16));
     }
     float* dakk = a.DAKK + (size_t)cid * BT * BT;
 #pragma unroll
