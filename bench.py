@@ -197,13 +197,20 @@ def time_train(gp, xs, steps, warmup):
 #   bwd_b2:    dAqk, Aqk^T do (2 BT BT D each, only the 10 of 16 16x16 blocks on or
 #              below the diagonal), qg^T do (2 D D BT)
 #   bwd_state: kg dh and W^T dv_new per chunk (2 BT D D each)
-#   bwd_wy:    three (BT, D, D), two (BT, BT, D), two (BT, D, BT), two (BT, BT, BT)
+#   bwd_wy:    three (BT, D, D) in full; dA (two (BT, BT, D)) and A^T dW, A^T dv_new
+#              (two (BT, D, BT)) on the 10 of 16 16x16 blocks A's triangle and the
+#              strict mask leave; dA A^T and A^T (dA A^T) (two (BT, BT, BT)) on 30 and
+#              20 of 64 block products
 TRAIN_CHUNK = 64
 _C = TRAIN_CHUNK
+_NB = _C // 16
+_TRI = _NB * (_NB + 1) // 2                       # blocks on or below the diagonal
+_SQ = _NB * (_NB + 1) * (2 * _NB + 1) // 6        # dA A^T: sum over row blocks of (I+1)^2
 TRAIN_FLOPS = {
     "bwd_b2": 2 * 2 * _C * _C * D * (_C // 16 + 1) // (2 * (_C // 16)) + 2 * D * D * _C,
     "bwd_state": 2 * 2 * _C * D * D,
-    "bwd_wy": 3 * 2 * _C * D * D + 2 * 2 * _C * _C * D + 2 * 2 * _C * D * _C + 2 * 2 * _C ** 3,
+    "bwd_wy": 3 * 2 * _C * D * D + 2 * (2 * 2 * _C * _C * D) * _TRI // (_NB * _NB)
+              + 2 * _C ** 3 * (_SQ + ((_NB + 1) * _TRI - _SQ)) // _NB ** 3,
 }
 FP32_MFMA_PEAK = 157.3   # TFLOP/s, MI355X dense float32 matrix
 
