@@ -1348,7 +1348,8 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       float* a_dbg, int flags, const Varlen* vl) {
   const int N = vl ? vl->total_chunks : (T_len + BT - 1) / BT;
   const size_t NC = (size_t)B * H * N;
-  const int S_ws = vl ? 1 : state_segments((long long)B * H, N, D, (flags >> 8) & 0xff);
+  const int S_ws =
+      vl ? 1 : state_segments((long long)B * H, N, D, (int)sizeof(T), (flags >> 8) & 0xff);
   const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), S_ws > 1 ? (size_t)B * H * S_ws : 0,
                                  !(flags & kFwdNoARegion));
   T* W = reinterpret_cast<T*>(ws + L.W);
@@ -1388,7 +1389,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     // D >= 128 takes 64 columns per workgroup (four compute waves, no K-split),
     // so the summary pass, which doubles the units with the M slices, fits the
     // device in one round (1.1x faster than 32-column workgroups in two rounds)
-    constexpr int GW = sizeof(T) == 2 && D >= 128 ? 4 : SW;
+    constexpr int GW = seg_pass_cols(sizeof(T), D) / 16;
     constexpr int GK = GW == SW ? SK : 1;
     constexpr int GVS = D / (16 * GW);
     const int Lseg = (N + S - 1) / S;

@@ -117,20 +117,23 @@ constexpr SeqChunks seq_chunks(const int* cu, int s, int N) {
   return SeqChunks{c0, n > 0 ? (int)n : 0};
 }
 
-// Segments of the forward state scan for BH (b,h) pairs of N chunks.  Automatic
-// choice: as many as fill a 256-CU device in the final pass when the plain
-// pass's BH * D/32 workgroups cannot, each at least 16 chunks, and only when
-// that gives 4 or more (the segmented scan costs about 3/S of the serial
-// chain plus a small combine).  `forced` (1..255) overrides it.  The result is
-// adjusted so that no segment is empty.  Depends on shapes only, so the
-// workspace size is known without a device.
-inline int state_segments(long long BH, int N, int D, int forced) {
+// Columns of a segmented-pass workgroup: 64 for bfloat16 tiles at D >= 128, else 32.
+constexpr int seg_pass_cols(int esize, int D) { return esize == 2 && D >= 128 ? 64 : 32; }
+
+// Segments of the forward state scan for BH (b,h) pairs of N chunks with
+// `esize`-byte tiles.  Automatic choice: as many as fill a 256-CU device in the
+// final pass (BH * D/seg_pass_cols workgroups per segment), each at least 16
+// chunks, and only when that gives 4 or more (the segmented scan costs about 3/S
+// of the serial chain plus a small combine).  `forced` (1..255) overrides it.
+// The result is adjusted so that no segment is empty.  Depends on shapes only,
+// so the workspace size is known without a device.
+inline int state_segments(long long BH, int N, int D, int esize, int forced) {
   if (N <= 1) return 1;
   long long s;
   if (forced > 0) {
     s = forced;
   } else {
-    const long long slices = BH * (D / 32);
+    const long long slices = BH * (D / seg_pass_cols(esize, D));
     s = slices > 0 ? 256 / slices : 1;
     if (s > N / 16) s = N / 16;
     if (s < 4) s = 1;
