@@ -349,7 +349,7 @@ def extras(gp, steps=10, warmup=3):
     xs = [x.to(torch.bfloat16) for x in (q, k, v, w, b)] + [g]
     ms = _time(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5), steps, warmup)
     kms = _event_ms(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5), 4)
-    res["config5_fwd"] = {"shape": "B1 T131072 H8 D128 bf16, chunk 128 (state scan in 8 "
+    res["config5_fwd"] = {"shape": "B1 T131072 H8 D128 bf16, chunk 128 (state scan in 16 "
                                    "segments)", "ms": ms, "tokens_per_s": B5 * T5 / (ms * 1e-3),
                           "kernels_ms": dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms))}
     del q, k, v, w, b, g, xs
