@@ -609,7 +609,10 @@ def main():
     if not args.no_train:
         try:
             xs32 = make_inputs(torch.float32)
-            tms = time_train(gp, xs32, max(1, args.steps // 4), max(1, args.warmup // 2))
+            # the first steps after the allocation of the gradient and workspace
+            # tensors run up to 15 % slower (first touch of fresh memory): warm up as
+            # many steps as the forward does
+            tms = time_train(gp, xs32, max(1, args.steps // 2), max(1, args.warmup))
             kms, mfma = train_kernels(gp, xs32)
             train = {"config": "B8 T8192 H6 D128 float32, forward + backward (trainable)",
                      "ms_per_step": tms, "tokens_per_s": tokens / (tms * 1e-3),
