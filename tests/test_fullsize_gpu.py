@@ -1,7 +1,8 @@
 """Full-size parity over every (batch, head) pair.
 
-The gfx950 forward at the BASELINE configs[2] and configs[4] shapes, and the training
-path's gradients at configs[3], are compared with the token recurrence
+The gfx950 forward at the BASELINE configs[2] and configs[4] shapes, the training
+path's gradients at configs[3], and the D = 256 forward and training path (B8 T8192
+H3), are compared with the token recurrence
 (gdn2_fwd.py:342-360, restated by oracle.recurrent_fwd) and its adjoint, evaluated in
 float64 with torch on the same GPU: the CPU oracle cannot finish these sizes in
 seconds, so test_fwd_gpu.py / test_bwd_gpu.py check sampled pairs there; this file
@@ -189,4 +190,36 @@ def test_config4_training_bf16_all_pairs(dev):
     ref = recurrence_grads_fp64(*[x.detach() for x in xt], D ** -0.5, do, dh)
     for n, x, rg in zip(["dq", "dk", "dv", "dw", "db", "dg"], xt, ref):
         ok, e = within(x.grad, rg, 2e-2)
+        assert ok, (n, e, float(rg.abs().max()))
+
+
+def test_d256_forward_all_pairs(dev):
+    """D = 256 (beyond the reference's D = 128 assert) at B8 T8192 H3, bf16 inputs,
+    chunk 64: all 24 pairs against the float64 recurrence."""
+    B, T, H, D = 8, 8192, 3, 256
+    xt = baseline_inputs(B, T, H, D, dev, seed=6)
+    out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5)
+    ro, rh = recurrence_fp64(*xt, D ** -0.5)
+    ok_o, e_o = within(out, ro, 2e-2)
+    ok_h, e_h = within(hf, rh, 2e-2)
+    assert ok_o and ok_h, (e_o, e_h)
+
+
+def test_d256_training_all_pairs(dev):
+    """D = 256 float32 training path at B8 T8192 H3 with an N(0,1) cotangent on out
+    and on h_final: the six input gradients of all 24 pairs against the float64
+    adjoint at 1e-4."""
+    B, T, H, D = 8, 8192, 3, 256
+    gen = torch.Generator(device=dev).manual_seed(7)
+    r = lambda *s: torch.randn(s or (B, T, H, D), generator=gen, device=dev)
+    q, k, v, w, b, g = r(), r(), r(), r(), r(), r()
+    q, k = q / q.norm(dim=-1, keepdim=True), k / k.norm(dim=-1, keepdim=True)
+    w, b, g = torch.sigmoid(w), torch.sigmoid(b), -torch.nn.functional.softplus(g)
+    xt = [x.detach().requires_grad_(True) for x in (q, k, v, w, b, g)]
+    do, dh = r(), r(B, H, D, D)
+    out, hf = gp().gdn2_pallas_forward_trainable(*xt, D ** -0.5)
+    torch.autograd.backward([out, hf], [do, dh])
+    ref = recurrence_grads_fp64(*[x.detach() for x in xt], D ** -0.5, do, dh)
+    for n, x, rg in zip(["dq", "dk", "dv", "dw", "db", "dg"], xt, ref):
+        ok, e = within(x.grad, rg, 1e-4)
         assert ok, (n, e, float(rg.abs().max()))
