@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <type_traits>
 #include <stddef.h>
 #include <stdint.h>
 

@@ -47,7 +47,26 @@ struct PrepArgs {
                  // g <- -softplus(g), applied here as the values are read
   const int* cstart;  // variable-length batch: token row where chunk c starts
                       // ([N+1], B = 1); rows past cstart[c+1] are neutral padding
+  int frag;           // Qg and Aqk in operand-fragment order (qg_frag / aqk_frag):
+                      // for the scan's output waves, which then read 1 KB per load
 };
+
+// Operand-fragment order of a chunk's q_g [BT][D] tile: the 16-byte operand
+// run a lane (li, lg) feeds a 16 x 16 MFMA for row block I and k-group j
+// (channels j*KS + lg*KC + e, e < KC) sits at fragment (I, j), lane 16 lg + li,
+// so the 64 lanes' operands of one fragment are 1 KB contiguous.
+template <typename T, int BT, int D>
+__host__ __device__ constexpr size_t qg_frag(int I, int j, int lane) {
+  return ((size_t)(I * (D / Tr<T>::KS) + j) * 64 + lane) * Tr<T>::KC;
+}
+// The same for Aqk [BT][BT], in the chained order of C-layout tiles: lane
+// (li, lg) holds row I*16 + li, columns 16 J + 4 lg + r of block J, which for
+// bfloat16 is half J % 2 of fragment (I, J / 2) (float32: fragment (I, J)).
+template <typename T, int BT>
+__host__ __device__ constexpr size_t aqk_frag(int I, int J, int lane) {
+  return sizeof(T) == 4 ? ((size_t)(I * (BT / 16) + J) * 64 + lane) * 4
+                        : ((size_t)(I * (BT / 32) + J / 2) * 64 + lane) * 8 + (J % 2) * 4;
+}
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
 // -softplus(x) = -(max(x,0) + log(1 + e^{-|x|}))
@@ -153,6 +172,10 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
   // another wave of this workgroup wrote, so stores stay in flight across them.
   T* kgT = a.KgT + (size_t)cid * D * BT;
   T* aqk = a.Aqk + (size_t)cid * BT * BT;
+  // offset of row I*16 + li, columns 16 J + 4 lg .. + 3 of Aqk
+  auto aqk_at = [&](int I, int J) {
+    return a.frag ? aqk_frag<T, BT>(I, J, lane) : (size_t)(I * 16 + li) * BT + J * 16 + 4 * lg;
+  };
 
   // raw inputs with several panels: 1 / max(|q|_2, 1e-12) and the same for k over
   // all D channels, before the panel loop
@@ -278,6 +301,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       const int I = own_block<NB>(wv, i);
       const int t = I * 16 + li;
       T* qgp = a.Qg + (size_t)cid * BT * D + (size_t)t * D + d0;
+      T* qgf = a.Qg + (size_t)cid * BT * D;
       f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
       // raw inputs: q,k <- q,k / max(|.|_2, 1e-12) over D (F.normalize) and
       // b <- sigmoid(b), in place in the loaded registers; a token's channels sit
@@ -340,7 +364,8 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
           db[e] = bk * edq;
           dk[e] = kv * edk;
         }
-        *reinterpret_cast<Op*>(qgp + j * KS + lg * KC) = op_from<T>(qg);
+        *reinterpret_cast<Op*>(a.frag ? qgf + qg_frag<T, BT, D>(I, d0 / KS + j, lane)
+                                      : qgp + j * KS + lg * KC) = op_from<T>(qg);
         *reinterpret_cast<Op*>(&sR0[t * KH_LD + j * KS + lg * KC]) = op_from<T>(kh);
         // diagonal block, factorised around its 8th token: X = k rows (j),
         // Y = q / bk rows (i) -> lane holds [i=li][j=4lg+r]
@@ -357,14 +382,14 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       }
       const int e0 = t * A_LD + I * 16 + 4 * lg;
       if constexpr (one) {
-        store4(aqk + (size_t)t * BT + I * 16 + 4 * lg, sanitize4(sq));
+        store4(aqk + aqk_at(I, I), sanitize4(sq));
         store4(&sA[e0], sanitize4(sk));
       } else {
         if (pn > 0) {
           sq += qdiag[i];
           sk += load4f(&sA[e0]);
         }
-        if (last_pn) store4(aqk + (size_t)t * BT + I * 16 + 4 * lg, sanitize4(sq));
+        if (last_pn) store4(aqk + aqk_at(I, I), sanitize4(sq));
         else qdiag[i] = sq;
         store4(&sA[e0], last_pn ? sanitize4(sk) : sk);
       }
@@ -389,7 +414,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
         }
         const int e0 = t * A_LD + J * 16 + 4 * lg;
         if constexpr (one) {
-          store4(aqk + (size_t)t * BT + J * 16 + 4 * lg, sanitize4(accq * a.scale));
+          store4(aqk + aqk_at(I, J), sanitize4(accq * a.scale));
           store4(&sA[e0], sanitize4(acck));
         } else {
           f32x4 sq = accq * a.scale;
@@ -397,7 +422,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
             sq += qp;
             acck += load4f(&sA[e0]);
           }
-          if (last_pn) store4(aqk + (size_t)t * BT + J * 16 + 4 * lg, sanitize4(sq));
+          if (last_pn) store4(aqk + aqk_at(I, J), sanitize4(sq));
           else qp = sq;
           store4(&sA[e0], last_pn ? sanitize4(acck) : acck);
         }
@@ -642,6 +667,14 @@ struct StateArgs {
   const int* cu;    // variable-length batch (B = 1): unit (h, sequence s) scans chunks
                     // [cu[s], cu[s+1]); h0 / h_final are [s][h][D][D]
   int H;
+  // Output waves (NO > 0): o = scale qg h_c + Aqk v_new formed in this kernel
+  // (h^T / v_new^T are then not written)
+  const T* Qg;
+  const T* Aqk;
+  float* out;
+  float scale;
+  int T_len;
+  const int* cstart;  // variable-length chunk table (see PrepArgs)
 };
 
 // One workgroup = one (b,h) and 16*NW value columns: NW compute waves (16
@@ -687,15 +720,43 @@ struct StateArgs {
 // buffers leave no room for sX, through the W tile of the current buffer once
 // every compute wave has read it (barriers X1, X2).  Not at D = 64 in
 // bfloat16, where the W tile is smaller than the exchanged partials.
+//
+// Output waves (NO > 0, inference: nothing reads h^T / v_new^T afterwards).
+// The outputs o = scale qg h_c + Aqk v_new of the workgroup's columns are
+// formed here instead of by fwd_out, so h_c and v_new never reach HBM.  The
+// compute waves keep h_c (bfloat16, natural d order) and v_new (chained order)
+// of chunk c in registers and put them into LDS (sHo, sVo) between barriers
+// A and B of chunk c+1; NO output waves, each owning the row blocks
+// {ow, NB-1-ow} (equal triangular work), read them from B(c+1) to A(c+2): one
+// row block while the compute waves form W h (B..X), the other during their h
+// update (after the last X barrier), so neither phase of the chain waits for
+// them.  q_g and Aqk rows come from global memory one chunk ahead, in the
+// operand-fragment order the prep writes for this path (qg_frag, aqk_frag).
+// Two barriers A(n), B(n) after the last chunk hand over its tiles.  Needs a
+// K-split (an X barrier per chunk) and both tile buffers.
 template <typename T, int BT, int D>
 constexpr int state_bufs() { return 4 * BT * D * (int)sizeof(T) <= 132 * 1024 ? 2 : 1; }
 template <typename T, int BT, int D>
 constexpr int state_ksplit() {
   return sizeof(T) == 4 ? 2 : (4 * (BT / 16) * 1024 <= BT * D * 2 ? 2 : 1);
 }
+// Output waves of the fused scan for the plain and variable-length passes
+// (32 value columns per workgroup), or 0 where fwd_out runs instead: no K-split
+// (bfloat16 at D = 64), a single tile buffer, or LDS beyond 160 KB (D = 256).
+template <typename T, int BT, int D>
+constexpr int state_out_waves() {
+  constexpr int NW = 2, PADT = 16 / (int)sizeof(T);
+  constexpr int tiles = 2 * 2 * BT * D * (int)sizeof(T);                  // W, kg^T x 2
+  constexpr int ub = NW * (sizeof(T) == 4 ? BT / 16 : BT / 32) * 1024;    // sU
+  constexpr int xs = sizeof(T) == 4 ? 2 * NW * (BT / 16) * 1024 : 0;     // sX
+  constexpr int fo = 16 * NW * (D + BT + 2 * PADT) * (int)sizeof(T);     // sHo, sVo
+  constexpr int lds = tiles + ub + xs + fo + 2 * D * 4 + 256;
+  return (state_ksplit<T, BT, D>() == 2 && state_bufs<T, BT, D>() == 2 && D <= 128 &&
+          lds <= 160 * 1024) ? BT / 32 : 0;
+}
 
-template <typename T, int BT, int D, int NW, int NP, int KS>
-__global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a) {
+template <typename T, int BT, int D, int NW, int NP, int KS, int NO = 0>
+__global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<T> a) {
   using Op = typename Tr<T>::Op;
   constexpr int NB = BT / 16, NDT = D / 16;
   constexpr int NVS = D / (16 * NW);
@@ -726,6 +787,14 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
   __shared__ __align__(16) float sGL0[D];
   __shared__ __align__(16) float sGL1[NBUF == 2 ? D : 4];
   __shared__ __align__(16) float sJunk[64];        // target of the L2 touches
+  // output waves: h_c^T [col][d] (natural order) and v_new^T [col][t] (chained
+  // order, as the v_new^T workspace tile) of the workgroup's columns
+  constexpr int PADO = 16 / (int)sizeof(T);
+  constexpr int HO_LD = D + PADO, VO_LD = BT + PADO;
+  __shared__ __align__(16) T sHo[NO > 0 ? 16 * NW * HO_LD : 8];
+  __shared__ __align__(16) T sVo[NO > 0 ? 16 * NW * VO_LD : 8];
+  static_assert(NO == 0 || (NXB > 0 && NBUF == 2 && NO == NB / 2),
+                "output waves need an X barrier per chunk, two tile buffers and NB/2 waves");
 
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -764,6 +833,96 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
     n = n < a.L ? n : a.L;
   }
   n = n > 0 ? n : 0;
+
+  if constexpr (NO > 0) {
+    if (wv >= NCW + NP) {
+      // ---- output waves --------------------------------------------------------
+      // wave ow owns row blocks {ow, NB-1-ow} of every chunk and all 16 NW
+      // columns of the workgroup; out(c) is formed during chunk c+1 (after F for
+      // the last chunk) from sHo / sVo and the q_g / Aqk rows loaded one chunk
+      // ahead.  The barriers mirror the compute waves' A, B, X.. per chunk and F.
+      constexpr int TKC = Tr<T>::KC, TKS = Tr<T>::KS;
+      constexpr int OKD = D / TKS, OKT = BT / TKS;
+      const int ow = wv - NCW - NP;
+      const int hh = bh % a.H, bb = bh / a.H;
+      const size_t HD = (size_t)a.H * D;
+      auto oblock = [&](int i) { return i == 0 ? ow : NB - 1 - ow; };
+      Op qf[2][OKD], af[2][OKT];
+      // q_g and Aqk in operand-fragment order (the prep's frag layout): one
+      // 16-byte load per operand, 1 KB contiguous per wave
+      auto load_ops = [&](int c) __attribute__((always_inline)) {
+        const size_t cid = (size_t)bh * a.N + c0 + c;
+        const T* qc = a.Qg + cid * BT * D;
+        const T* ac = a.Aqk + cid * BT * BT;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int It = oblock(i);
+#pragma unroll
+          for (int kg = 0; kg < OKD; ++kg) qf[i][kg] = op_load<T>(qc + qg_frag<T, BT, D>(It, kg, lane));
+          // Aqk blocks right of the diagonal block are never written: masked
+#pragma unroll
+          for (int kg = 0; kg < OKT; ++kg) {
+            if constexpr (sizeof(T) == 4) {
+              af[i][kg] = kg <= It ? op_load<T>(ac + aqk_frag<T, BT>(It, kg, lane)) : op_zero<T>();
+            } else {
+              af[i][kg] = 2 * kg <= It ? op_load<T>(ac + aqk_frag<T, BT>(It, 2 * kg, lane))
+                                       : op_zero<T>();
+            }
+          }
+        }
+      };
+      // out(c) rows of own row block i
+      auto emit = [&](int c, int i) __attribute__((always_inline)) {
+        const ChunkRows cr = chunk_rows(a.cstart, c0 + c, bb, a.T_len, BT);
+        float* obase = a.out + cr.row0 * HD + (size_t)hh * D + vs * 16 * NW;
+        {
+          const int It = oblock(i), t = It * 16 + li;
+          const int kgmax = (It * 16 + 15) / TKS;
+#pragma unroll
+          for (int vt = 0; vt < NW; ++vt) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kg = 0; kg < OKD; ++kg)
+              mma(acc, op_load<T>(&sHo[(vt * 16 + li) * HO_LD + kg * TKS + lg * TKC]), qf[i][kg]);
+            acc *= a.scale;
+#pragma unroll
+            for (int kg = 0; kg < OKT; ++kg)
+              if (kg <= kgmax) {
+                Op y = af[i][kg];
+                if constexpr (sizeof(T) == 2) {
+                  if (2 * kg + 1 > It) {   // block 2kg+1 lies right of the diagonal
+#pragma unroll
+                    for (int e = 4; e < 8; ++e) y[e] = (T)0.f;
+                  }
+                }
+                mma(acc, op_load<T>(&sVo[(vt * 16 + li) * VO_LD + kg * TKS + lg * TKC]), y);
+              }
+            if (t < cr.valid) store4(obase + (size_t)t * HD + vt * 16 + 4 * lg, sanitize4(acc));
+          }
+        }
+      };
+      // chunk c-1's tiles are in sHo / sVo from B(c) to A(c+1): one row block
+      // while the compute waves form W h (B..X), the other during their h update
+      if (n > 0) load_ops(0);
+      for (int c = 0; c < n; ++c) {
+        lds_barrier();  // A(c)
+        lds_barrier();  // B(c)
+        if (c > 0) emit(c - 1, 0);
+        for (int x = 0; x < NXB; ++x) lds_barrier();  // X(c)
+        if (c > 0) {
+          emit(c - 1, 1);
+          load_ops(c);
+        }
+      }
+      lds_barrier();  // A(n)
+      lds_barrier();  // B(n)
+      if (n > 0) {
+        emit(n - 1, 0);
+        emit(n - 1, 1);
+      }
+      return;
+    }
+  }
 
   if (wv >= NCW) {
     // ---- producers ----------------------------------------------------------
@@ -897,6 +1056,10 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
         for (int x = 0; x < NXB; ++x) barrier();  // X(c)
       }
     }
+    if constexpr (NO > 0) {
+      barrier();  // A(n)
+      barrier();  // B(n)
+    }
     return;
   }
 
@@ -938,6 +1101,24 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
   const bool write_tiles = !a.summary;
 
   // One chunk: v_new = u - W h, h <- e^{gl} h + kg^T v_new, with chunk c in `cur`.
+  // output waves: the pieces of chunk c-1's h^T / v_new^T this wave puts into
+  // sHo / sVo between barriers A(c) and B(c)
+  using HP = typename std::conditional<F32, f32x4, bf16x4>::type;
+  constexpr int NVP = F32 ? NB / KS : NB / 2 / KS;
+  HP hp[NO > 0 ? NDH : 1];
+  Op vp[NO > 0 ? NVP : 1];
+  auto put_tiles = [&]() __attribute__((always_inline)) {
+    const int lc = wcol * 16 + li;
+#pragma unroll
+    for (int i = 0; i < NDH; ++i)
+      *reinterpret_cast<HP*>(&sHo[lc * HO_LD + (ks * NDH + i) * 16 + 4 * lg]) = hp[i];
+#pragma unroll
+    for (int j = 0; j < NVP; ++j) {
+      if constexpr (F32) store4(&sVo[lc * VO_LD + (ks * NVP + j) * 16 + 4 * lg], vp[j]);
+      else *reinterpret_cast<Op*>(&sVo[lc * VO_LD + (ks * NVP + j) * 32 + 8 * lg]) = vp[j];
+    }
+  };
+
   auto step = [&](int c, const char* cur, const float* eglc) __attribute__((always_inline)) {
     const size_t cid = (size_t)bh * a.N + c0 + c;
     __syncthreads();  // A(c)
@@ -956,12 +1137,15 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
         }
       }
     }
+    if constexpr (NO > 0) {
+      if (c > 0) put_tiles();
+    }
     __syncthreads();  // B(c)
     const T* sW = reinterpret_cast<const T*>(cur);
     const T* sK = reinterpret_cast<const T*>(cur + WBYTES);
 
     T* hT = a.HT + cid * D * D + (size_t)col * D;
-    if (!write_tiles) {
+    if (!write_tiles || NO > 0) {
     } else if constexpr (F32) {
 #pragma unroll
       for (int i = 0; i < NDH; ++i) store4(hT + (ks * NDH + i) * 16 + 4 * lg, h[i]);
@@ -1052,7 +1236,21 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
       }
     }
     T* vT = a.VnT + cid * D * BT + (size_t)col * BT;
-    if (!write_tiles) {
+    if constexpr (NO > 0) {
+      // h_c and v_new of chunk c, kept for the output waves (put into LDS at the
+      // start of chunk c+1): h^T in natural d order (lane (li, lg) holds
+      // d = 16 i + 4 lg + r of row tile i), v_new^T in chained order
+#pragma unroll
+      for (int i = 0; i < NDH; ++i) {
+        if constexpr (F32) hp[i] = h[i];
+        else hp[i] = HP{(T)h[i][0], (T)h[i][1], (T)h[i][2], (T)h[i][3]};
+      }
+#pragma unroll
+      for (int j = 0; j < NVP; ++j) {
+        if constexpr (F32) vp[j] = vn[ks * NVP + j];
+        else vp[j] = op_from_c(vn[2 * (ks * NVP + j)], vn[2 * (ks * NVP + j) + 1], (Op*)nullptr);
+      }
+    } else if (!write_tiles) {
     } else if constexpr (F32) {
 #pragma unroll
       for (int it = ks * (NB / KS); it < (ks + 1) * (NB / KS); ++it)
@@ -1144,6 +1342,11 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) fwd_state(StateArgs<T> a)
       step(c, sbuf0, sGL0);
       if (c + 1 < n) step(c + 1, sbuf1, sGL1);
     }
+  }
+  if constexpr (NO > 0) {
+    __syncthreads();  // A(n): the output waves are done with chunk n-2's tiles
+    if (n > 0) put_tiles();
+    __syncthreads();  // B(n)
   }
   float* hout = a.cu ? a.h_final + ((size_t)sg * a.H + bh) * D * D
               : a.summary ? a.seg + ((size_t)unit * 2 + (mslice ? 1 : 0)) * D * D
@@ -1360,13 +1563,17 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   float* GL = reinterpret_cast<float*>(ws + L.GL);
   T* HT = reinterpret_cast<T*>(ws + L.HT);
   T* VnT = reinterpret_cast<T*>(ws + L.VnT);
+  // Inference (no residuals kept): the scan forms the outputs itself where its
+  // variant has output waves (state_out_waves), and fwd_out is not launched.
+  constexpr int NO = state_out_waves<T, BT, D>();
+  const bool fuse = NO > 0 && !(flags & 1) && !a_dbg && (vl || S_ws == 1);
   launch_mark(st);
   if (NC > 0) {
     PrepArgs<T, TG> pa{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
                        (const TG*)g, T_len, H, N, (long long)NC, scale, W, UT, KgT, Qg, Aqk, GL,
                        a_dbg ? a_dbg : ((flags & 1) ? reinterpret_cast<float*>(ws + L.A)
                                                     : nullptr),
-                       (flags & 2) ? 1 : 0, vl ? vl->cstart : nullptr};
+                       (flags & 2) ? 1 : 0, vl ? vl->cstart : nullptr, fuse ? 1 : 0};
     hipLaunchKernelGGL((fwd_prep<T, TG, BT, D>), dim3(NC), dim3(64 * prep_waves(BT)), 0, st,
                        pa);
   }
@@ -1377,13 +1584,20 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   constexpr int NVS = D / (16 * SW);
   const size_t BH = (size_t)B * H;
   const int S = S_ws;
+  constexpr int NTH = 64 * (SW * SK + SP), NTHO = 64 * (SW * SK + SP + NO);
   if (vl) {
     // one unit per (head, sequence)
     StateArgs<T> va{W,  UT,      KgT,     GL,     h0,           N,  vl->nseq, 0, 0, nullptr,
-                    nullptr, HT, VnT, h_final, vl->cu_chunks, H};
-    if (vl->nseq > 0)
-      hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * vl->nseq * NVS),
-                         dim3(64 * (SW * SK + SP)), 0, st, va);
+                    nullptr, HT, VnT, h_final, vl->cu_chunks, H, Qg, Aqk, out, scale, T_len,
+                    vl->cstart};
+    if (vl->nseq > 0) {
+      if (fuse)
+        hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK, NO>), dim3(BH * vl->nseq * NVS),
+                           dim3(NTHO), 0, st, va);
+      else
+        hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * vl->nseq * NVS),
+                           dim3(NTH), 0, st, va);
+    }
   } else if (S > 1) {
     // Segmented passes (several workgroups per CU's worth of units): bfloat16 at
     // D >= 128 takes 64 columns per workgroup (four compute waves, no K-split),
@@ -1407,12 +1621,16 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                        dim3(64 * (GW * GK + SP)), 0, st, fin);
   } else {
     StateArgs<T> sa{W, UT, KgT, GL, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT, h_final,
-                    nullptr, H};
-    hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * NVS), dim3(64 * (SW * SK + SP)), 0,
-                       st, sa);
+                    nullptr, H, Qg, Aqk, out, scale, T_len, nullptr};
+    if (fuse)
+      hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK, NO>), dim3(BH * NVS), dim3(NTHO), 0,
+                         st, sa);
+    else
+      hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * NVS), dim3(NTH), 0, st,
+                         sa);
   }
   launch_mark(st);
-  if (NC > 0) {
+  if (NC > 0 && !fuse) {
     OutArgs<T> oa{Qg, Aqk, HT, VnT, T_len, H, N, scale, out, vl ? vl->cstart : nullptr};
     hipLaunchKernelGGL((fwd_out<T, BT, D>), dim3(NC * (D / out_cols<T, D>())), dim3(256), 0,
                        st, oa);
