@@ -74,7 +74,26 @@ def kernel_table(dtype_bytes, chunk):
                       "flops": 4 * D * D},
         "fwd_out": {"bytes": 2 * D * s + aqk + D * D * s / C + D * 4,
                     "flops": 2 * D * D + C * D},
+        # the scan with the outputs formed in it (inference): reads W, u^T, kg^T,
+        # g_last, q_g and Aqk, writes out
+        "fwd_state_out": {"bytes": 4 * D * s + 4 * D / C + aqk + D * 4,
+                          "flops": 6 * D * D + C * D},
     }
+
+
+# Inference forwards whose state scan forms the outputs itself (no fwd_out
+# launch): bfloat16 at D = 128 (chunk 64 or 128) and float32 at D = 64 -- the
+# scan variants whose LDS holds the staged h / v_new tiles (state_out_waves in
+# gdn2_fwd.hip).  Their third launch interval is empty.
+def fused_out(dtype_bytes, d):
+    return (dtype_bytes == 2 and d == 128) or (dtype_bytes == 4 and d == 64)
+
+
+def name_kernels(kms, fused):
+    """Launch intervals (prep, state, out) of one forward, named."""
+    if fused:
+        return {"fwd_prep": kms[0], "fwd_state_out": kms[1]}
+    return dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms))
 
 
 # Compulsory HBM bytes per token-head of the bf16 forward: q,k,v,w,b bf16 and g
@@ -159,10 +178,9 @@ def time_forward(gp, xs, steps, warmup, chunk):
         gp.gdn2_pallas_forward(*xs, scale, chunk_size=chunk)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    names = ["fwd_prep", "fwd_state", "fwd_out"]
-    per = {n: sum(evs[4 * i + j].elapsed_time(evs[4 * i + j + 1]) for i in range(steps)) / steps
-           for j, n in enumerate(names)}
-    return (t1 - t0) / steps * 1e3, per
+    iv = [sum(evs[4 * i + j].elapsed_time(evs[4 * i + j + 1]) for i in range(steps)) / steps
+          for j in range(3)]
+    return (t1 - t0) / steps * 1e3, name_kernels(iv, fused_out(xs[0].element_size(), D))
 
 
 def ctypes_vp(x):
@@ -351,7 +369,7 @@ def extras(gp, steps=10, warmup=3):
     kms = _event_ms(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5), 4)
     res["config5_fwd"] = {"shape": "B1 T131072 H8 D128 bf16, chunk 128 (state scan in 16 "
                                    "segments)", "ms": ms, "tokens_per_s": B5 * T5 / (ms * 1e-3),
-                          "kernels_ms": dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms))}
+                          "kernels_ms": name_kernels(kms, fused_out(2, D))}
     del q, k, v, w, b, g, xs
     # fused input preparation at the headline shape
     raw = [r((B, T, H, D)).to(torch.bfloat16) for _ in range(5)] + [r((B, T, H, D))]
@@ -377,7 +395,7 @@ def extras(gp, steps=10, warmup=3):
     res["varlen_fwd"] = {"shape": f"1 x {B * T} tokens in 16 sequences ({int(lens.min())}.."
                                   f"{int(lens.max())} tokens), H6 D128 bf16, fused activations",
                          "ms": ms_v, "tokens_per_s": B * T / (ms_v * 1e-3),
-                         "kernels_ms": dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms)),
+                         "kernels_ms": name_kernels(kms, fused_out(2, D)),
                          "note": "ms includes building the chunk tables on the host"}
     del raw, packed
     def dist(shape):   # the headline's input distributions at another shape
@@ -391,7 +409,7 @@ def extras(gp, steps=10, warmup=3):
     kms = _event_ms(lambda: gp.gdn2_pallas_forward(*x256, 256 ** -0.5), 4)
     res["d256_fwd"] = {"shape": "B8 T8192 H3 D256 bf16, chunk 64", "ms": ms,
                        "tokens_per_s": B * T / (ms * 1e-3),
-                       "kernels_ms": dict(zip(("fwd_prep", "fwd_state", "fwd_out"), kms))}
+                       "kernels_ms": name_kernels(kms, fused_out(2, 256))}
     # D = 256 training step, float32 (chunk 64): forward with residuals + backward
     x256f = [x.float().detach().requires_grad_(True) for x in x256]
     do256 = r((B, T, 3, 256))
@@ -489,7 +507,9 @@ def cpu_baseline(min_seconds=10.0, bwd_tokens=1024, bwd_min_seconds=8.0):
 
 
 COPY_BYTES = 1 << 30           # calibration copy: reads and writes this many bytes
-KERNELS = ("fwd_prep", "fwd_state", "fwd_out")
+# the headline's launches (its scan forms the outputs): name matched in the
+# kernel symbol -> row of kernel_table
+KERNELS = {"fwd_prep": "fwd_prep", "fwd_state": "fwd_state_out"}
 
 
 def pmc_run(steps):
@@ -542,15 +562,15 @@ def traffic_from(fetch_dir, write_dir):
     tab = kernel_table(2, CHUNK)
     pick = lambda t, k: next(v for n, v in t.items() if k in n)
     out = {}
-    for k in KERNELS:
+    for k, row in KERNELS.items():
         fb = pick(fetch, k) * 1024 * f_scale
         wb = pick(write, k) * 1024 * w_scale
-        rec = {"kernel": k, "workload": "B8 T8192 H6 D128 bf16 chunk 128",
+        rec = {"kernel": row, "workload": "B8 T8192 H6 D128 bf16 chunk 128",
                "fetch_bytes": fb, "write_bytes": wb, "bytes_per_launch": fb + wb,
-               "algorithmic_bytes": tab[k]["bytes"] * B * T * H,
+               "algorithmic_bytes": tab[row]["bytes"] * B * T * H,
                "fetch_scale": f_scale, "write_scale": w_scale,
                "calibration": f"copy kernel reading and writing {COPY_BYTES} bytes"}
-        (ROOT / "profiles" / f"traffic_{k}_b8t8192h6d128_bf16.json").write_text(
+        (ROOT / "profiles" / f"traffic_{row}_b8t8192h6d128_bf16.json").write_text(
             json.dumps(rec, indent=1) + "\n")
         out[k] = rec
     print(json.dumps(out, indent=1))

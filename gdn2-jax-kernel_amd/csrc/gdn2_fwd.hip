@@ -1566,7 +1566,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   // Inference (no residuals kept): the scan forms the outputs itself where its
   // variant has output waves (state_out_waves), and fwd_out is not launched.
   constexpr int NO = state_out_waves<T, BT, D>();
-  const bool fuse = NO > 0 && !(flags & 1) && !a_dbg && (vl || S_ws == 1);
+  const bool fuse = NO > 0 && !(flags & 1) && !a_dbg;
   launch_mark(st);
   if (NC > 0) {
     PrepArgs<T, TG> pa{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
@@ -1616,9 +1616,13 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     hipLaunchKernelGGL((seg_combine<D>), dim3(BH * (D / 16)), dim3(256), 0, st, seg, h0, hin,
                        S);
     StateArgs<T> fin{W, UT, KgT, GL, h0, N, S, Lseg, 0, hin, nullptr, HT, VnT, h_final,
-                     nullptr, H};
-    hipLaunchKernelGGL((fwd_state<T, BT, D, GW, SP, GK>), dim3(BH * S * GVS),
-                       dim3(64 * (GW * GK + SP)), 0, st, fin);
+                     nullptr, H, Qg, Aqk, out, scale, T_len, nullptr};
+    if (fuse)   // final pass with output waves: 32-column workgroups
+      hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK, NO>), dim3(BH * S * NVS), dim3(NTHO),
+                         0, st, fin);
+    else
+      hipLaunchKernelGGL((fwd_state<T, BT, D, GW, SP, GK>), dim3(BH * S * GVS),
+                         dim3(64 * (GW * GK + SP)), 0, st, fin);
   } else {
     StateArgs<T> sa{W, UT, KgT, GL, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT, h_final,
                     nullptr, H, Qg, Aqk, out, scale, T_len, nullptr};
