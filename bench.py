@@ -365,11 +365,18 @@ def extras(gp, steps=10, warmup=3):
     q, k = f.normalize(q, dim=-1), f.normalize(k, dim=-1)
     w, b, g = torch.sigmoid(w), torch.sigmoid(b), -f.softplus(g) * 0.1
     xs = [x.to(torch.bfloat16) for x in (q, k, v, w, b)] + [g]
-    ms = _time(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5), steps, warmup)
-    kms = _event_ms(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5), 4)
-    res["config5_fwd"] = {"shape": "B1 T131072 H8 D128 bf16, chunk 128 (state scan in 16 "
+    ms = _time(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5, chunk_size=CHUNK), steps, warmup)
+    kms = _event_ms(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5, chunk_size=CHUNK), 4)
+    res["config5_fwd"] = {"shape": "B1 T131072 H8 D128 bf16, chunk 128 (state scan in 8 "
                                    "segments)", "ms": ms, "tokens_per_s": B5 * T5 / (ms * 1e-3),
                           "kernels_ms": name_kernels(kms, fused_out(2, D))}
+    # the same at the library's default chunk for bf16 D = 128 (64)
+    ms = _time(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5, chunk_size=64), steps, warmup)
+    kms = _event_ms(lambda: gp.gdn2_pallas_forward(*xs, D ** -0.5, chunk_size=64), 4)
+    res["config5_fwd_chunk64"] = {"shape": "B1 T131072 H8 D128 bf16, chunk 64 (state scan in "
+                                           "8 segments)", "ms": ms,
+                                  "tokens_per_s": B5 * T5 / (ms * 1e-3),
+                                  "kernels_ms": name_kernels(kms, fused_out(2, D))}
     del q, k, v, w, b, g, xs
     # fused input preparation at the headline shape
     raw = [r((B, T, H, D)).to(torch.bfloat16) for _ in range(5)] + [r((B, T, H, D))]
@@ -622,6 +629,9 @@ def main():
     value = tokens / (ms * 1e-3)
 
     roof = roofline(per, ms)
+    # the same workload at the library's default chunk for bf16 D = 128 (64): not
+    # the configuration's BT = 128, reported beside it
+    ms64, per64 = time_forward(gp, xs, args.steps, args.warmup, 64)
 
     del xs
     torch.cuda.empty_cache()
@@ -651,6 +661,11 @@ def main():
                    "B": B, "T": T, "H": H, "D": D, "chunk": CHUNK},
         "kernels_ms": per,
         "roofline": roof,
+        "chunk64": {"ms_per_step": ms64, "tokens_per_s": tokens / (ms64 * 1e-3),
+                    "kernels_ms": per64,
+                    "roofline_end_to_end_frac": roof["end_to_end"]["lower_bound_ms"] / ms64,
+                    "note": "same inputs at chunk 64 (the default chunk for bf16 at D = 128); "
+                            "value above is at the configuration's chunk 128"},
         "train": train,
     }
     if not args.no_extras:

@@ -192,8 +192,10 @@ int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype)
 // when its segment field is 0).
 static size_t fwd_ws_need(int B, int T, int H, int D, int BT, int in_dtype, int flags) {
   const int N = chunks_per_seq(T, BT);
-  const int S = state_segments((long long)B * H, N, D, (int)elem_size(in_dtype),
-                               (flags >> 8) & 0xff);
+  const int es = (int)elem_size(in_dtype);
+  const bool fused = state_out_waves_of(es, BT, D) > 0 && !(flags & GDN2_FWD_SAVE_A);
+  const int S = state_segments((long long)B * H, N, D, es, (flags >> 8) & 0xff,
+                               fused ? 32 : seg_pass_cols(es, D));
   return fwd_layout(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype),
                     S > 1 ? (size_t)B * H * S : 0, !(flags & kFwdNoARegion)).total;
 }

@@ -735,25 +735,11 @@ struct StateArgs {
 // Two barriers A(n), B(n) after the last chunk hand over its tiles.  Needs a
 // K-split (an X barrier per chunk) and both tile buffers.
 template <typename T, int BT, int D>
-constexpr int state_bufs() { return 4 * BT * D * (int)sizeof(T) <= 132 * 1024 ? 2 : 1; }
+constexpr int state_bufs() { return state_bufs_of(sizeof(T), BT, D); }
 template <typename T, int BT, int D>
-constexpr int state_ksplit() {
-  return sizeof(T) == 4 ? 2 : (4 * (BT / 16) * 1024 <= BT * D * 2 ? 2 : 1);
-}
-// Output waves of the fused scan for the plain and variable-length passes
-// (32 value columns per workgroup), or 0 where fwd_out runs instead: no K-split
-// (bfloat16 at D = 64), a single tile buffer, or LDS beyond 160 KB (D = 256).
+constexpr int state_ksplit() { return state_ksplit_of(sizeof(T), BT, D); }
 template <typename T, int BT, int D>
-constexpr int state_out_waves() {
-  constexpr int NW = 2, PADT = 16 / (int)sizeof(T);
-  constexpr int tiles = 2 * 2 * BT * D * (int)sizeof(T);                  // W, kg^T x 2
-  constexpr int ub = NW * (sizeof(T) == 4 ? BT / 16 : BT / 32) * 1024;    // sU
-  constexpr int xs = sizeof(T) == 4 ? 2 * NW * (BT / 16) * 1024 : 0;     // sX
-  constexpr int fo = 16 * NW * (D + BT + 2 * PADT) * (int)sizeof(T);     // sHo, sVo
-  constexpr int lds = tiles + ub + xs + fo + 2 * D * 4 + 256;
-  return (state_ksplit<T, BT, D>() == 2 && state_bufs<T, BT, D>() == 2 && D <= 128 &&
-          lds <= 160 * 1024) ? BT / 32 : 0;
-}
+constexpr int state_out_waves() { return state_out_waves_of(sizeof(T), BT, D); }
 
 template <typename T, int BT, int D, int NW, int NP, int KS, int NO = 0>
 __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<T> a) {
@@ -977,16 +963,30 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
     constexpr int LUR = BT * (int)sizeof(T) / LINE;         // lines per u^T row
     constexpr int LU = 16 * NW * LUR;                       // this workgroup's u^T rows
     constexpr int LG = (D * 4 + LINE - 1) / LINE;           // g_last
-    constexpr int LTOT = 2 * LW + LU + LG;                  // at most (one slice)
+    // At chunk 64 the output waves' q_g and Aqk tiles are touched too, shared
+    // among the slices like W / kg^T (the touch count assumes that sharing;
+    // without it, lines past the count are left to the loads themselves): a
+    // step there (about 1.7 us) is shorter than the HBM latency of the operand
+    // loads issued one step ahead (fused scan 0.265 -> 0.217 ms).  A chunk-128
+    // step lasts long enough, and the extra touches cost more than they save
+    // (0.205 -> 0.213 ms).
+    constexpr bool TQA = NO > 0 && BT == 64;
+    constexpr int LQ = TQA ? BT * D * (int)sizeof(T) / LINE : 0;    // q_g
+    constexpr int LA = TQA ? BT * BT * (int)sizeof(T) / LINE : 0;   // Aqk
+    constexpr int LSH = 2 * LW + LQ + LA;                   // lines shared by the slices
+    constexpr int LTOT = TQA ? (LSH + NVS - 1) / NVS + LU + LG   // at most (one slice)
+                             : LSH + LU + LG;
     constexpr int NTP = ((LTOT + 63) / 64 + NP - 1) / NP;   // touch instructions per producer
     const int vsl = vs + (mslice ? NVS : 0);                // slice index within the unit
-    const int lws = one_xcd ? (2 * LW + NSL - 1) / NSL : 2 * LW;   // W | kg^T lines touched here
+    const int lws = one_xcd ? (LSH + NSL - 1) / NSL : LSH;  // shared lines touched here
     const int lw0 = one_xcd ? vsl * lws : 0;
     const int ltot = lws + LU + LG;
     auto touch = [&](int c) __attribute__((always_inline)) {
       const size_t cid = (size_t)bh * a.N + c0 + c;
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
       const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
+      const char* qsrc = reinterpret_cast<const char*>(a.Qg + cid * BT * D);
+      const char* asrc = reinterpret_cast<const char*>(a.Aqk + cid * BT * BT);
       const char* usrc =
           reinterpret_cast<const char*>(a.UT + cid * D * BT + (size_t)vs * 16 * NW * BT);
       const char* gsrc = reinterpret_cast<const char*>(a.GL + cid * D);
@@ -994,8 +994,12 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
       for (int j = 0; j < NTP; ++j) {
         int l = (j * NP + p) * 64 + lane;
         l = l < ltot ? l : ltot - 1;
-        const int lw = min(lw0 + l, 2 * LW - 1);                // line of W | kg^T
-        const char* src = l < lws ? (lw < LW ? wsrc + lw * LINE : ksrc + (lw - LW) * LINE)
+        const int lw = min(lw0 + l, LSH - 1);                   // shared line
+        const char* sh = lw < LW ? wsrc + lw * LINE
+                       : lw < 2 * LW ? ksrc + (lw - LW) * LINE
+                       : lw < 2 * LW + LQ ? qsrc + (lw - 2 * LW) * LINE
+                       : asrc + (lw - 2 * LW - LQ) * LINE;
+        const char* src = l < lws ? sh
                         : l < lws + LU ? usrc + (l - lws) * LINE
                         : gsrc + (l - lws - LU) * LINE;
         lds_dma4(src, sJunk);
@@ -1551,8 +1555,13 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       float* a_dbg, int flags, const Varlen* vl) {
   const int N = vl ? vl->total_chunks : (T_len + BT - 1) / BT;
   const size_t NC = (size_t)B * H * N;
-  const int S_ws =
-      vl ? 1 : state_segments((long long)B * H, N, D, (int)sizeof(T), (flags >> 8) & 0xff);
+  // the segment count follows flags only (the workspace was sized from them): the
+  // final pass of an inference forward is the 32-column scan with output waves
+  constexpr int NO = state_out_waves<T, BT, D>();
+  const bool fuse_ws = NO > 0 && !(flags & 1);
+  const int S_ws = vl ? 1
+                      : state_segments((long long)B * H, N, D, (int)sizeof(T), (flags >> 8) & 0xff,
+                                       fuse_ws ? 32 : seg_pass_cols(sizeof(T), D));
   const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), S_ws > 1 ? (size_t)B * H * S_ws : 0,
                                  !(flags & kFwdNoARegion));
   T* W = reinterpret_cast<T*>(ws + L.W);
@@ -1565,8 +1574,7 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   T* VnT = reinterpret_cast<T*>(ws + L.VnT);
   // Inference (no residuals kept): the scan forms the outputs itself where its
   // variant has output waves (state_out_waves), and fwd_out is not launched.
-  constexpr int NO = state_out_waves<T, BT, D>();
-  const bool fuse = NO > 0 && !(flags & 1) && !a_dbg;
+  const bool fuse = fuse_ws && !a_dbg;
   launch_mark(st);
   if (NC > 0) {
     PrepArgs<T, TG> pa{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,

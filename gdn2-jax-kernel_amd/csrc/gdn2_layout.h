@@ -120,20 +120,48 @@ constexpr SeqChunks seq_chunks(const int* cu, int s, int N) {
 // Columns of a segmented-pass workgroup: 64 for bfloat16 tiles at D >= 128, else 32.
 constexpr int seg_pass_cols(int esize, int D) { return esize == 2 && D >= 128 ? 64 : 32; }
 
+// Shape of the forward state-scan variants (fwd_state in gdn2_fwd.hip), here so
+// that the host's workspace size follows the same choices.  Tile buffers: two
+// when W and kg^T of two chunks fit LDS.  K-split: two compute waves per
+// column slice for float32, and for bfloat16 where the W tile holds the
+// exchanged partials.
+constexpr int state_bufs_of(int esize, int BT, int D) {
+  return 4 * BT * D * esize <= 132 * 1024 ? 2 : 1;
+}
+constexpr int state_ksplit_of(int esize, int BT, int D) {
+  return esize == 4 ? 2 : (4 * (BT / 16) * 1024 <= BT * D * 2 ? 2 : 1);
+}
+// Output waves of the inference scan (32 value columns per workgroup), which
+// then forms the outputs itself, or 0 where a separate output pass runs: no
+// K-split (bfloat16 at D = 64), a single tile buffer, or more LDS than 160 KB
+// (float32 at D = 128, D = 256).  The LDS count mirrors fwd_state's arrays.
+constexpr int state_out_waves_of(int esize, int BT, int D) {
+  const int NW = 2, PADT = 16 / esize;
+  const int tiles = 2 * 2 * BT * D * esize;                          // W, kg^T x 2
+  const int ub = NW * (esize == 4 ? BT / 16 : BT / 32) * 1024;       // u^T gather
+  const int xs = esize == 4 ? 2 * NW * (BT / 16) * 1024 : 0;        // K-split partials
+  const int fo = 16 * NW * (D + BT + 2 * PADT) * esize;             // staged h, v_new
+  const int lds = tiles + ub + xs + fo + 2 * D * 4 + 256;
+  return (state_ksplit_of(esize, BT, D) == 2 && state_bufs_of(esize, BT, D) == 2 && D <= 128 &&
+          lds <= 160 * 1024) ? BT / 32 : 0;
+}
+
 // Segments of the forward state scan for BH (b,h) pairs of N chunks with
-// `esize`-byte tiles.  Automatic choice: as many as fill a 256-CU device in the
-// final pass (BH * D/seg_pass_cols workgroups per segment), each at least 16
-// chunks, and only when that gives 4 or more (the segmented scan costs about 3/S
-// of the serial chain plus a small combine).  `forced` (1..255) overrides it.
-// The result is adjusted so that no segment is empty.  Depends on shapes only,
-// so the workspace size is known without a device.
-inline int state_segments(long long BH, int N, int D, int esize, int forced) {
+// `esize`-byte tiles, whose final pass runs workgroups of `final_cols` value
+// columns (seg_pass_cols, or 32 for the inference scan with output waves).
+// Automatic choice: as many as fill a 256-CU device in the final pass (BH *
+// D/final_cols workgroups per segment), each at least 16 chunks, and only when
+// that gives 4 or more (the segmented scan costs about 3/S of the serial chain
+// plus a small combine).  `forced` (1..255) overrides it.  The result is
+// adjusted so that no segment is empty.  Depends on shapes and flags only, so
+// the workspace size is known without a device.
+inline int state_segments(long long BH, int N, int D, int esize, int forced, int final_cols) {
   if (N <= 1) return 1;
   long long s;
   if (forced > 0) {
     s = forced;
   } else {
-    const long long slices = BH * (D / seg_pass_cols(esize, D));
+    const long long slices = BH * (D / final_cols);
     s = slices > 0 ? 256 / slices : 1;
     if (s > N / 16) s = N / 16;
     if (s < 4) s = 1;

@@ -141,15 +141,20 @@ def test_launch_events_hook_is_host_only():
 def test_segment_workspace():
     """Forward workspace with a segmented state scan: S segments add
     B*H*S*3*D*D floats (end states, transitions, entry states) after the
-    per-chunk tensors.  The automatic choice uses S = 16 for config 5 with
-    bfloat16 tiles (1 x 131072 x 8 heads, D = 128: 16 workgroups of 64 columns per
-    segment in the final pass), S = 8 with float32 tiles (32 columns per
-    workgroup), and none for the headline shape."""
+    per-chunk tensors.  The automatic choice fills 256 workgroups in the final
+    pass: for config 5 (1 x 131072 x 8 heads, D = 128) with bfloat16 tiles S = 8
+    for inference (the final pass is the 32-column scan with output waves) and
+    S = 16 when the residuals are kept (64-column final pass), S = 8 with
+    float32 tiles (32 columns per workgroup), and none for the headline shape."""
     L = _lib.lib()
     al = lambda x: (x + 255) // 256 * 256
     plain = L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 128, BF16, _lib.FWD_SEGMENTS(1))
     assert L.gdn2_fwd_workspace_bytes(1, 131072, 8, 128, 128, BF16) == \
-        plain + al(8 * 16 * 3 * 128 * 128 * 4)
+        plain + al(8 * 8 * 3 * 128 * 128 * 4)
+    saved = L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 128, BF16,
+                                          _lib.FWD_SEGMENTS(1) | _lib.FWD_SAVE_A)
+    assert L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 128, BF16, _lib.FWD_SAVE_A) == \
+        saved + al(8 * 16 * 3 * 128 * 128 * 4)
     plain32 = L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 64, F32, _lib.FWD_SEGMENTS(1))
     assert L.gdn2_fwd_workspace_bytes(1, 131072, 8, 128, 64, F32) == \
         plain32 + al(8 * 8 * 3 * 128 * 128 * 4)

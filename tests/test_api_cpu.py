@@ -73,13 +73,14 @@ def test_no_cpu_fallback():
 
 def test_chunk_size_resolution():
     from gdn2_package import gdn2_fwd
-    assert gdn2_fwd.chunk_size_for(torch.bfloat16) == 128
+    assert gdn2_fwd.chunk_size_for(torch.bfloat16) == 64
+    assert gdn2_fwd.chunk_size_for(torch.bfloat16, D=64) == 128
     assert gdn2_fwd.chunk_size_for(torch.float32) == 64
     assert gdn2_fwd.chunk_size_for(torch.bfloat16, D=256) == 64
     old = gdn2_fwd.BT
     try:
-        gdn2_fwd.BT = 64              # README.md:87-92 style override, read at call time
-        assert gdn2_fwd.chunk_size_for(torch.bfloat16) == 64
+        gdn2_fwd.BT = 128             # README.md:87-92 style override, read at call time
+        assert gdn2_fwd.chunk_size_for(torch.bfloat16) == 128
     finally:
         gdn2_fwd.BT = old
     import gdn2_package as gp

@@ -133,26 +133,30 @@ def test_recurrence_grads_fp64_matches_oracle(dev):
 
 
 def test_config3_headline_all_pairs(dev):
-    """(8,8192,6,128) bf16 inputs, fp32 g, BT=128; all 48 pairs."""
+    """(8,8192,6,128) bf16 inputs, fp32 g; all 48 pairs, at
+    BT=128 (the configuration's chunk) and at the library's default chunk 64."""
     B, T, H, D = 8, 8192, 6, 128
     xt = baseline_inputs(B, T, H, D, dev)
-    out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5)
     ro, rh = recurrence_fp64(*xt, D ** -0.5)
-    ok_o, e_o = within(out, ro, 2e-2)
-    ok_h, e_h = within(hf, rh, 2e-2)
-    assert ok_o and ok_h, (e_o, e_h)
+    for bt in (128, 64):
+        out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5, chunk_size=bt)
+        ok_o, e_o = within(out, ro, 2e-2)
+        ok_h, e_h = within(hf, rh, 2e-2)
+        assert ok_o and ok_h, (bt, e_o, e_h)
 
 
 def test_config5_long_context_all_heads(dev):
-    """(1,131072,8,128) bf16, g = -softplus * 0.1, BT=128 (the
-    segmented scan); all 8 heads over the full 131072-token chain."""
+    """(1,131072,8,128) bf16, g = -softplus * 0.1 (the
+    segmented scan); all 8 heads over the full 131072-token chain, at BT=128 (the
+    configuration's chunk) and at the default chunk 64."""
     B, T, H, D = 1, 131072, 8, 128
     xt = baseline_inputs(B, T, H, D, dev, g_mul=0.1)
-    out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5)
     ro, rh = recurrence_fp64(*xt, D ** -0.5)
-    ok_o, e_o = within(out, ro, 2e-2)
-    ok_h, e_h = within(hf, rh, 2e-2)
-    assert ok_o and ok_h, (e_o, e_h)
+    for bt in (128, 64):
+        out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5, chunk_size=bt)
+        ok_o, e_o = within(out, ro, 2e-2)
+        ok_h, e_h = within(hf, rh, 2e-2)
+        assert ok_o and ok_h, (bt, e_o, e_h)
 
 
 def test_config4_training_all_pairs(dev):

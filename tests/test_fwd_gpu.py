@@ -112,13 +112,14 @@ def test_config3_headline_bf16(dev):
     q, k = q / q.norm(dim=-1, keepdim=True), k / k.norm(dim=-1, keepdim=True)
     w, b, g = torch.sigmoid(w), torch.sigmoid(b), -torch.nn.functional.softplus(g)
     xt = [x.to(torch.bfloat16) for x in (q, k, v, w, b)] + [g]
-    out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5)
+    out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5, chunk_size=128)
     assert torch.isfinite(out).all() and torch.isfinite(hf).all()
     _sampled_pairs_check(out, hf, xt, [(0, 0), (7, 5), (3, 2), (1, 4), (2, 1), (4, 3),
                                        (5, 0), (6, 2), (7, 0), (0, 5)], D)
     # chaining: second half from the first half's final state reproduces the full run
-    o1, h1 = gp().gdn2_pallas_forward(*[x[:, :T // 2] for x in xt], D ** -0.5)
-    o2, h2 = gp().gdn2_pallas_forward(*[x[:, T // 2:] for x in xt], D ** -0.5, h0=h1)
+    o1, h1 = gp().gdn2_pallas_forward(*[x[:, :T // 2] for x in xt], D ** -0.5, chunk_size=128)
+    o2, h2 = gp().gdn2_pallas_forward(*[x[:, T // 2:] for x in xt], D ** -0.5, h0=h1,
+                                      chunk_size=128)
     assert (torch.cat([o1, o2], 1) - out).abs().max().item() < 1e-5
     assert (h2 - hf).abs().max().item() < 1e-5
 
@@ -133,7 +134,7 @@ def test_config5_long_context_bf16(dev):
     q, k = q / q.norm(dim=-1, keepdim=True), k / k.norm(dim=-1, keepdim=True)
     w, b, g = torch.sigmoid(w), torch.sigmoid(b), -torch.nn.functional.softplus(g) * 0.1
     xt = [x.to(torch.bfloat16) for x in (q, k, v, w, b)] + [g]
-    out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5)
+    out, hf = gp().gdn2_pallas_forward(*xt, D ** -0.5, chunk_size=128)
     assert torch.isfinite(out).all() and torch.isfinite(hf).all()
     _sampled_pairs_check(out, hf, xt, [(0, 3), (0, 6)], D)
 
@@ -288,6 +289,7 @@ def test_partial_last_chunk_equals_zero_padded_inputs(dev):
     (1, 2048, 2, 64, torch.float32, 64, 3, True),      # uneven: 11 + 11 + 10
     (2, 1280, 1, 128, torch.float32, 64, 7, True),     # N=20: 3 x 6 + 2
     (1, 4096, 2, 128, torch.bfloat16, 128, 8, True),   # N=32: 8 x 4
+    (1, 2048, 2, 128, torch.bfloat16, 64, 5, True),    # N=32: 4 x 7 + 4 (fused chunk 64)
     (1, 2560, 2, 64, torch.bfloat16, 128, 5, False),   # N=20: 5 x 4
     (1, 1024, 1, 256, torch.float32, 64, 4, True),     # D = 256, single-buffered scan
     (1, 1024, 2, 256, torch.bfloat16, 64, 3, False),   # N=16: 6 + 6 + 4
