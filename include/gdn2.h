@@ -62,8 +62,11 @@ const char* gdn2_strerror(int code);
  * trace-time assertions gdn2_fwd.py:145-146 and gdn2_bwd.py:348-349. */
 int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype);
 
-/* Bytes of workspace gdn2_fwd needs.  The workspace afterwards holds the
- * per-chunk residuals (WY factors, chunk states, v_new) that gdn2_bwd reads. */
+/* Bytes of workspace gdn2_fwd needs.  After a call with GDN2_FWD_SAVE_A the
+ * workspace holds the per-chunk residuals (WY factors, chunk states, v_new)
+ * that gdn2_bwd reads; after an inference call its contents are unspecified
+ * (where the state scan forms the outputs itself, the chunk states and v_new
+ * never leave the GPU's on-chip memory). */
 size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype);
 
 /* gdn2_fwd flags. */
@@ -96,7 +99,9 @@ size_t gdn2_fwd_workspace_bytes_ex(int B, int T, int H, int D, int BT, int in_dt
 /* Forward: replaces gdn2_pallas_forward (gdn2_fwd.py:400-424), kernels A-D.
  * h0 may be NULL (zero initial state, gdn2_fwd.py:403-404).  out (B,T,H,D)
  * and h_final (B,H,D,D) are float32.  flags: 0 for inference, GDN2_FWD_SAVE_A
- * when gdn2_bwd will consume ws (the trainable forward, gdn2_pipeline.py:64-67). */
+ * when gdn2_bwd will consume ws (the trainable forward, gdn2_pipeline.py:64-67).
+ * Inference at D = 128 with bfloat16 inputs (and float32 at D = 64) runs two
+ * kernels: the state scan forms the outputs itself. */
 int gdn2_fwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
              const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, const float* h0, float scale, float* out, float* h_final,
@@ -112,9 +117,10 @@ int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtyp
 
 /* Timing hook.  For the next gdn2_fwd / gdn2_fwd_debug / gdn2_bwd call made
  * on the calling host thread, record events[0] (hipEvent_t) on the call's
- * stream before its first kernel and events[i] after its i-th kernel, for
- * i < n.  The request is consumed by that call (also when it fails).
- * gdn2_fwd launches 3 kernels (fwd_prep, fwd_state, fwd_out).  Returns 0. */
+ * stream before its first kernel and events[i] after its i-th kernel stage,
+ * for i < n.  The request is consumed by that call (also when it fails).
+ * gdn2_fwd has 3 stages (fwd_prep, the state scan, fwd_out); where the scan
+ * forms the outputs the third stage launches nothing.  Returns 0. */
 int gdn2_set_launch_events(void* const* events, int n);
 
 /* Bytes of workspace gdn2_bwd needs in addition to the forward workspace. */
