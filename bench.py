@@ -425,15 +425,15 @@ def extras(gp, steps=10, warmup=3):
     res["d256_train"] = {"shape": "B8 T8192 H3 D256 float32, forward + backward", "ms": ms,
                          "tokens_per_s": B * T / (ms * 1e-3)}
     del x256, x256f, do256
-    # bfloat16 training step at the headline shape (the inputs are widened and run
-    # through the float32 forward and backward, as the reference upcasts; gradients
-    # in the input dtypes)
+    # bfloat16 training step at the headline shape: float32 arithmetic and residuals
+    # on the bfloat16 inputs as they are (GDN2_BF16_F32), as the reference upcasts;
+    # gradients in the input dtypes
     xb = [x.detach().requires_grad_(True) for x in dist((B, T, H, D))]
     dob = r((B, T, H, D))
     ms = _time(lambda: torch.autograd.grad(
         [gp.gdn2_pallas_forward_trainable(*xb, D ** -0.5)[0]], xb, [dob]), 5, 2)
     res["bf16_train"] = {"shape": "B8 T8192 H6 D128 bf16 inputs (fp32 g), forward + backward "
-                                  "computed in float32, bf16 gradients",
+                                  "in float32 arithmetic on the bf16 data, bf16 gradients",
                          "ms": ms, "tokens_per_s": B * T / (ms * 1e-3)}
     del xb, dob
     # T % BT != 0: 8100 tokens per sequence, the last chunk of each 36 tokens short

@@ -9,13 +9,13 @@
 
 namespace gdn2 {
 
-template <typename T, typename TG, int BT, int D>
+template <typename T, typename TG, int BT, int D, typename TI>
 hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, float* out, float* h_final, char* ws,
                       float* a_dbg, int flags, const Varlen* vl);
 
-template <typename T, typename TG, int BT, int D>
+template <typename T, typename TG, int BT, int D, typename TI>
 hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, const float* dout, const float* dh_final,
@@ -29,7 +29,16 @@ hipError_t launch_decode(hipStream_t st, int B, int H, const void* q, const void
                          const void* v, const void* w, const void* b, const void* g,
                          float scale, const float* h_in, float* h_out, float* out);
 
-static size_t elem_size(int dtype) { return dtype == GDN2_F32 ? 4 : 2; }
+// Workspace element size: the MFMA operand type (float32 for GDN2_BF16_F32).
+static size_t elem_size(int dtype) { return dtype == GDN2_BF16 ? 2 : 4; }
+
+// Tag of GDN2_BF16_F32 in the dispatch: float32 tiles and arithmetic, bfloat16
+// inputs and gradients.  Tile<X> / Stor<X> give the launchers' T and TI.
+struct Bf16F32 {};
+template <typename X> struct Tile { using type = X; };
+template <> struct Tile<Bf16F32> { using type = float; };
+template <typename X> struct Stor { using type = X; };
+template <> struct Stor<Bf16F32> { using type = bf16_t; };
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -87,6 +96,14 @@ static int dispatch(int in_dtype, int g_dtype, int BT, int D, A... args) {
     GDN2_CASE(bf16_t, bf16_t, 128, 64)
     GDN2_CASE(bf16_t, bf16_t, 128, 128)
     GDN2_CASE(bf16_t, bf16_t, 64, 256)
+  } else if (in_dtype == GDN2_BF16_F32 && g_dtype == GDN2_F32) {
+    GDN2_CASE(Bf16F32, float, 64, 64)
+    GDN2_CASE(Bf16F32, float, 64, 128)
+    GDN2_CASE(Bf16F32, float, 64, 256)
+  } else if (in_dtype == GDN2_BF16_F32 && g_dtype == GDN2_BF16) {
+    GDN2_CASE(Bf16F32, bf16_t, 64, 64)
+    GDN2_CASE(Bf16F32, bf16_t, 64, 128)
+    GDN2_CASE(Bf16F32, bf16_t, 64, 256)
   }
 #undef GDN2_CASE
   return GDN2_ERR_CHUNK;
@@ -98,8 +115,8 @@ struct FwdRun {
                  const void* v, const void* w, const void* b, const void* g, const float* h0,
                  float scale, float* out, float* h_final, char* ws, float* a_dbg,
                  int flags, const Varlen* vl) {
-    hipError_t e = launch_fwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale, out,
-                                            h_final, ws, a_dbg, flags, vl);
+    hipError_t e = launch_fwd<typename Tile<T>::type, TG, BT, D, typename Stor<T>::type>(
+        st, B, T_len, H, q, k, v, w, b, g, h0, scale, out, h_final, ws, a_dbg, flags, vl);
     return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
   }
 };
@@ -114,9 +131,9 @@ struct BwdRun {
     if constexpr (D > 128 && BT != 64) {
       return GDN2_ERR_CHUNK;  // D = 256 runs at chunk 64 only
     } else {
-      hipError_t e = launch_bwd<T, TG, BT, D>(st, B, T_len, H, q, k, v, w, b, g, h0, scale,
-                                              dout, dh_final, dq, dk, dv, dw, db, dg, dh0, fws,
-                                              ws, cu_chunks, nseq);
+      hipError_t e = launch_bwd<typename Tile<T>::type, TG, BT, D, typename Stor<T>::type>(
+          st, B, T_len, H, q, k, v, w, b, g, h0, scale, dout, dh_final, dq, dk, dv, dw, db, dg,
+          dh0, fws, ws, cu_chunks, nseq);
       return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
     }
   }
@@ -161,8 +178,8 @@ const char* gdn2_strerror(int code) {
       return "head dim D must be 64, 128 or 256";
     case GDN2_ERR_SEQ_LEN: return "sequence length T must be divisible by the chunk size BT";
     case GDN2_ERR_CHUNK:
-      return "chunk size BT must be 64 or 128 (128 needs bfloat16 inputs and D <= 128)";
-    case GDN2_ERR_DTYPE: return "unsupported dtype (inputs: float32 or bfloat16; g: float32, or bfloat16 with bfloat16 inputs)";
+      return "chunk size BT must be 64 or 128 (128 needs GDN2_BF16 inputs and D <= 128)";
+    case GDN2_ERR_DTYPE: return "unsupported dtype (inputs: GDN2_F32, GDN2_BF16 or GDN2_BF16_F32; g: float32, or bfloat16 with bfloat16 inputs)";
     case GDN2_ERR_NULL: return "required pointer is NULL";
     case GDN2_ERR_ALIGN: return "pointer is not 16-byte aligned";
     case GDN2_ERR_WORKSPACE: return "workspace too small";
@@ -177,12 +194,13 @@ const char* gdn2_strerror(int code) {
 
 int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype) {
   if (B < 1 || H < 1 || T < 0) return GDN2_ERR_SHAPE;
-  if (in_dtype != GDN2_F32 && in_dtype != GDN2_BF16) return GDN2_ERR_DTYPE;
+  if (in_dtype != GDN2_F32 && in_dtype != GDN2_BF16 && in_dtype != GDN2_BF16_F32)
+    return GDN2_ERR_DTYPE;
   if (g_dtype != GDN2_F32 && g_dtype != GDN2_BF16) return GDN2_ERR_DTYPE;
   if (in_dtype == GDN2_F32 && g_dtype != GDN2_F32) return GDN2_ERR_DTYPE;
   if (D != 64 && D != 128 && D != 256) return GDN2_ERR_HEAD_DIM;
   if (BT != 64 && BT != 128) return GDN2_ERR_CHUNK;
-  if (BT == 128 && (in_dtype == GDN2_F32 || D == 256)) return GDN2_ERR_CHUNK;
+  if (BT == 128 && (in_dtype != GDN2_BF16 || D == 256)) return GDN2_ERR_CHUNK;
   if (T % BT != 0) return GDN2_ERR_SEQ_LEN;
   if ((double)B * T * H * D > 9.0e15) return GDN2_ERR_SHAPE;
   return GDN2_OK;
@@ -372,7 +390,7 @@ int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, co
     GDN2_DEC(float, float, 64)
     GDN2_DEC(float, float, 128)
     GDN2_DEC(float, float, 256)
-  } else if (g_dtype == GDN2_F32) {
+  } else if (g_dtype == GDN2_F32) {   // GDN2_BF16 or GDN2_BF16_F32: the step is float32
     GDN2_DEC(bf16_t, float, 64)
     GDN2_DEC(bf16_t, float, 128)
     GDN2_DEC(bf16_t, float, 256)

@@ -648,9 +648,11 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
 // A stored matrix read with its row index as the MFMA k index is read per lane
 // as four scalars (colop); one read with k contiguous is one 16-byte load (rowop).
 // ============================================================================
-template <typename T, typename TG>
+// T: workspace and MFMA operand type; TI: the type of the inputs k, w, v, b and
+// of the gradients dv, dw (T, or bfloat16 with float32 tiles).
+template <typename T, typename TG, typename TI = T>
 struct WyArgs {
-  const T *k, *w, *v, *b;
+  const TI *k, *w, *v, *b;
   const TG* g;
   const float* dout;
   const T* HT;        // forward residual h^T [cid][D][D] (bfloat16: chained columns)
@@ -662,11 +664,11 @@ struct WyArgs {
   float scale;
   float *DQG, *DKG, *DKBD, *DAKK;  // [cid][BT][D] x 3, [cid][BT][BT]
   float* SDH;         // [cid][D]: sum_e dh'[d][e] h[d][e] (the g_last term of dgc)
-  T *dv, *dw;         // gradients (B,T,H,D): d(wv) w, d(wv) v (gdn2_bwd.py:204-205)
+  TI *dv, *dw;        // gradients (B,T,H,D): d(wv) w, d(wv) v (gdn2_bwd.py:204-205)
 };
 
-template <typename T, typename TG, int D>
-__global__ void __launch_bounds__(256, 2) bwd_wy(WyArgs<T, TG> a) {
+template <typename T, typename TG, int D, typename TI>
+__global__ void __launch_bounds__(256, 2) bwd_wy(WyArgs<T, TG, TI> a) {
   constexpr int BT = 64, NB = BT / 16, NDT = D / 16, NKT = BT / 16;
   constexpr int DH = D < 64 ? D : 64, NH = D / DH, NDH = DH / 16;   // channel halves
   constexpr int LDH = DH + 4;   // [e][d of the half], [s][d of the half]
@@ -955,8 +957,8 @@ __global__ void __launch_bounds__(256, 2) bwd_wy(WyArgs<T, TG> a) {
         for (int r = 0; r < 4; ++r) {
           const size_t o = tok0 + (size_t)orow(r) * HD + d0 + nt * 16 + li;
           dkbd[orow(r) * D + nt * 16 + li] = akb[nt][r];
-          a.dv[o] = from_f<T>(sanitize(awv[nt][r] * wl[nt][r]));
-          a.dw[o] = from_f<T>(sanitize(awv[nt][r] * vl[nt][r]));
+          a.dv[o] = from_f<TI>(sanitize(awv[nt][r] * wl[nt][r]));
+          a.dw[o] = from_f<TI>(sanitize(awv[nt][r] * vl[nt][r]));
         }
     }
   }
@@ -1035,14 +1037,14 @@ __global__ void __launch_bounds__(256, 2) bwd_wy(WyArgs<T, TG> a) {
 // cumsum of dgc (gdn2_bwd.py:32-41): DPP suffix sums inside each 16-token block,
 // block totals across the waves through LDS.  Wave w owns row block w (BT = 64).
 // ============================================================================
-template <typename T, typename TG>
+template <typename T, typename TG, typename TI = T>
 struct GramArgs {
-  const T *q, *k, *b;
+  const TI *q, *k, *b;
   const TG* g;
   const float *DAQK, *DAKK, *SDH, *DQG, *DKG, *DKBD;
   int T_len, H, N;
   float scale;
-  T *dq, *dk, *db;
+  TI *dq, *dk, *db;
   TG* dg;
 };
 
@@ -1052,8 +1054,8 @@ struct GramArgs {
 // sharing the chunk's dAqk / dAkk tiles in its L2.
 constexpr int gram_panel() { return 32; }
 
-template <typename T, typename TG, int D>
-__global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
+template <typename T, typename TG, int D, typename TI>
+__global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
   constexpr int BT = 64, NB = 4, GP = gram_panel(), NPN = D / GP, NDT = GP / 16, DQ = GP / 4;
   constexpr int LD1 = GP + 4, LD2 = BT + 4;
   static_assert(D % GP == 0, "panels must tile D");
@@ -1365,8 +1367,8 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG> a) {
 //   5.   dA A^T and dAkk = -(A^T (dA A^T)) . strict, as in bwd_wy.
 // LDS: R_S 68 KB (the slices, then dv_new^T, then dA / dA A^T), R_W 65 KB, A 17 KB.
 // ============================================================================
-template <typename T, typename TG>
-__global__ void __launch_bounds__(512) bwd_wy_wide(WyArgs<T, TG> a) {
+template <typename T, typename TG, typename TI>
+__global__ void __launch_bounds__(512) bwd_wy_wide(WyArgs<T, TG, TI> a) {
   constexpr int BT = 64, D = 256, NB = BT / 16, NKT = BT / 16, NT = 512;
   constexpr int HDT = D / 32;                  // output column tiles per wave (half of D/16)
   constexpr int HKT = NKT / 2;                 // token column tiles per wave
@@ -1602,8 +1604,8 @@ __global__ void __launch_bounds__(512) bwd_wy_wide(WyArgs<T, TG> a) {
         const int col = (hf * HDT + n) * 16 + li;
         const size_t o = tok0 + (size_t)orow(r) * HD + col;
         dkbd[orow(r) * D + col] = akb[n][r];
-        a.dv[o] = from_f<T>(sanitize(awv[n][r] * wl[r]));
-        a.dw[o] = from_f<T>(sanitize(awv[n][r] * vl[r]));
+        a.dv[o] = from_f<TI>(sanitize(awv[n][r] * wl[r]));
+        a.dw[o] = from_f<TI>(sanitize(awv[n][r] * vl[r]));
       }
     }
   }
@@ -1677,7 +1679,7 @@ size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t) {
 // kernel would need 266 KB), the reverse scan (single-buffered at this width) and
 // gram_bwd (32-channel panels) as at D <= 128.  Launch marks: before B2, after B2,
 // after the scan, after B3, after gram_bwd (as the fused path).
-template <typename T, typename TG>
+template <typename T, typename TG, typename TI>
 hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* q,
                            const void* k, const void* v, const void* w, const void* b,
                            const void* g, float scale, const float* dout,
@@ -1711,27 +1713,27 @@ hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* 
   launch_mark(st);
   if (NC > 0) {
     // B3 (gdn2_bwd.py:126-210): one fused kernel with the D x D operands streamed
-    WyArgs<T, TG> wa{(const T*)k,  (const T*)w,     (const T*)v,  (const T*)b, (const TG*)g,
-                     dout,         (const T*)fHT,   (const T*)fVnT,
-                     fA,           buf(B_DHT),      buf(B_DVNT),
-                     T_len, H, N, scale, buf(B_DQG), buf(B_DKG), buf(B_DKBD),
-                     buf(B_DAKK), buf(B_SDH), (T*)dv, (T*)dw};
-    hipLaunchKernelGGL((bwd_wy_wide<T, TG>), dim3(NC), dim3(512), 0, st, wa);
+    WyArgs<T, TG, TI> wa{(const TI*)k, (const TI*)w,   (const TI*)v, (const TI*)b, (const TG*)g,
+                         dout,         (const T*)fHT,   (const T*)fVnT,
+                         fA,           buf(B_DHT),      buf(B_DVNT),
+                         T_len, H, N, scale, buf(B_DQG), buf(B_DKG), buf(B_DKBD),
+                         buf(B_DAKK), buf(B_SDH), (TI*)dv, (TI*)dw};
+    hipLaunchKernelGGL((bwd_wy_wide<T, TG, TI>), dim3(NC), dim3(512), 0, st, wa);
     launch_mark(st);
     // B4 + B3 element-wise tail + B5
-    GramArgs<T, TG> gr{(const T*)q,  (const T*)k,  (const T*)b,  (const TG*)g,
-                       buf(B_DAQK),  buf(B_DAKK),  buf(B_SDH),   buf(B_DQG),
-                       buf(B_DKG),   buf(B_DKBD),  T_len,        H,
-                       N,            scale,        (T*)dq,       (T*)dk,
-                       (T*)db,       (TG*)dg};
-    hipLaunchKernelGGL((gram_bwd<T, TG, D>), dim3(NC * (D / gram_panel())), dim3(256), 0, st,
-                       gr);
+    GramArgs<T, TG, TI> gr{(const TI*)q, (const TI*)k, (const TI*)b, (const TG*)g,
+                           buf(B_DAQK),  buf(B_DAKK),  buf(B_SDH),   buf(B_DQG),
+                           buf(B_DKG),   buf(B_DKBD),  T_len,        H,
+                           N,            scale,        (TI*)dq,      (TI*)dk,
+                           (TI*)db,      (TG*)dg};
+    hipLaunchKernelGGL((gram_bwd<T, TG, D, TI>), dim3(NC * (D / gram_panel())), dim3(256), 0,
+                       st, gr);
     launch_mark(st);
   }
   return hipGetLastError();
 }
 
-template <typename T, typename TG, int BT, int D>
+template <typename T, typename TG, int BT, int D, typename TI>
 hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, const float* dout, const float* dh_final,
@@ -1741,8 +1743,8 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     return hipErrorNotSupported;
   } else if constexpr (D > 128) {
     (void)h0;
-    return launch_bwd_wide<T, TG>(st, B, T_len, H, q, k, v, w, b, g, scale, dout, dh_final, dq,
-                                  dk, dv, dw, db, dg, dh0, fws, ws, cu_chunks, nseq);
+    return launch_bwd_wide<T, TG, TI>(st, B, T_len, H, q, k, v, w, b, g, scale, dout, dh_final,
+                                      dq, dk, dv, dw, db, dg, dh0, fws, ws, cu_chunks, nseq);
   } else {
     (void)h0;
     const int N = T_len / BT;
@@ -1785,20 +1787,20 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     launch_mark(st);
     if (NC > 0) {
       // B3, one fused kernel
-      WyArgs<T, TG> wa{(const T*)k,  (const T*)w,     (const T*)v,  (const T*)b, (const TG*)g,
-                       dout,         (const T*)fHT,   (const T*)fVnT,
-                       reinterpret_cast<const float*>(fA), buf(B_DHT), buf(B_DVNT),
-                       T_len, H, N, scale, buf(B_DQG), buf(B_DKG), buf(B_DKBD),
-                       buf(B_DAKK), buf(B_SDH), (T*)dv, (T*)dw};
-      hipLaunchKernelGGL((bwd_wy<T, TG, D>), dim3(NC), dim3(256), 0, st, wa);
+      WyArgs<T, TG, TI> wa{(const TI*)k, (const TI*)w,   (const TI*)v, (const TI*)b, (const TG*)g,
+                           dout,         (const T*)fHT,   (const T*)fVnT,
+                           reinterpret_cast<const float*>(fA), buf(B_DHT), buf(B_DVNT),
+                           T_len, H, N, scale, buf(B_DQG), buf(B_DKG), buf(B_DKBD),
+                           buf(B_DAKK), buf(B_SDH), (TI*)dv, (TI*)dw};
+      hipLaunchKernelGGL((bwd_wy<T, TG, D, TI>), dim3(NC), dim3(256), 0, st, wa);
       launch_mark(st);
       // B4 + B3 elementwise tail + B5
-      GramArgs<T, TG> gr{(const T*)q,  (const T*)k,  (const T*)b,  (const TG*)g,
-                         buf(B_DAQK),  buf(B_DAKK),  buf(B_SDH),   buf(B_DQG),
-                         buf(B_DKG),   buf(B_DKBD),  T_len,        H,
-                         N,            scale,        (T*)dq,       (T*)dk,
-                         (T*)db,       (TG*)dg};
-      hipLaunchKernelGGL((gram_bwd<T, TG, D>), dim3(NC * (D / gram_panel())), dim3(256), 0,
+      GramArgs<T, TG, TI> gr{(const TI*)q, (const TI*)k, (const TI*)b, (const TG*)g,
+                             buf(B_DAQK),  buf(B_DAKK),  buf(B_SDH),   buf(B_DQG),
+                             buf(B_DKG),   buf(B_DKBD),  T_len,        H,
+                             N,            scale,        (TI*)dq,      (TI*)dk,
+                             (TI*)db,      (TG*)dg};
+      hipLaunchKernelGGL((gram_bwd<T, TG, D, TI>), dim3(NC * (D / gram_panel())), dim3(256), 0,
                          st, gr);
       launch_mark(st);
     }
@@ -1806,23 +1808,30 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   }
 }
 
-#define GDN2_INST_BWD(T, TG, BT, D)                                                        \
-  template hipError_t launch_bwd<T, TG, BT, D>(                                            \
+#define GDN2_INST_BWD(T, TG, BT, D, TI)                                                    \
+  template hipError_t launch_bwd<T, TG, BT, D, TI>(                                        \
       hipStream_t, int, int, int, const void*, const void*, const void*, const void*,      \
       const void*, const void*, const float*, float, const float*, const float*, void*,    \
       void*, void*, void*, void*, void*, float*, const char*, char*, const int*, int);
-GDN2_INST_BWD(float, float, 64, 64)
-GDN2_INST_BWD(float, float, 64, 128)
-GDN2_INST_BWD(bf16_t, float, 64, 64)
-GDN2_INST_BWD(bf16_t, float, 64, 128)
-GDN2_INST_BWD(bf16_t, float, 128, 64)
-GDN2_INST_BWD(bf16_t, float, 128, 128)
-GDN2_INST_BWD(bf16_t, bf16_t, 64, 64)
-GDN2_INST_BWD(bf16_t, bf16_t, 64, 128)
-GDN2_INST_BWD(bf16_t, bf16_t, 128, 64)
-GDN2_INST_BWD(bf16_t, bf16_t, 128, 128)
-GDN2_INST_BWD(float, float, 64, 256)
-GDN2_INST_BWD(bf16_t, float, 64, 256)
-GDN2_INST_BWD(bf16_t, bf16_t, 64, 256)
+GDN2_INST_BWD(float, float, 64, 64, float)
+GDN2_INST_BWD(float, float, 64, 128, float)
+GDN2_INST_BWD(bf16_t, float, 64, 64, bf16_t)
+GDN2_INST_BWD(bf16_t, float, 64, 128, bf16_t)
+GDN2_INST_BWD(bf16_t, float, 128, 64, bf16_t)
+GDN2_INST_BWD(bf16_t, float, 128, 128, bf16_t)
+GDN2_INST_BWD(bf16_t, bf16_t, 64, 64, bf16_t)
+GDN2_INST_BWD(bf16_t, bf16_t, 64, 128, bf16_t)
+GDN2_INST_BWD(bf16_t, bf16_t, 128, 64, bf16_t)
+GDN2_INST_BWD(bf16_t, bf16_t, 128, 128, bf16_t)
+GDN2_INST_BWD(float, float, 64, 256, float)
+GDN2_INST_BWD(bf16_t, float, 64, 256, bf16_t)
+GDN2_INST_BWD(bf16_t, bf16_t, 64, 256, bf16_t)
+// float32 arithmetic on bfloat16 inputs and gradients (GDN2_BF16_F32)
+GDN2_INST_BWD(float, float, 64, 64, bf16_t)
+GDN2_INST_BWD(float, float, 64, 128, bf16_t)
+GDN2_INST_BWD(float, float, 64, 256, bf16_t)
+GDN2_INST_BWD(float, bf16_t, 64, 64, bf16_t)
+GDN2_INST_BWD(float, bf16_t, 64, 128, bf16_t)
+GDN2_INST_BWD(float, bf16_t, 64, 256, bf16_t)
 
 }  // namespace gdn2

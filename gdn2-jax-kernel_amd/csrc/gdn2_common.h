@@ -102,7 +102,25 @@ __device__ __forceinline__ typename Tr<T>::Op op_load(const T* p) {
   return *reinterpret_cast<const typename Tr<T>::Op*>(p);
 }
 
-// Load N consecutive elements of type X as floats (N*sizeof(X) a multiple of 16).
+// Load N consecutive elements of type X as floats (N*sizeof(X) a multiple of 8).
+template <int N>
+__device__ __forceinline__ void load_f(const float* p, float* out);
+template <int N>
+__device__ __forceinline__ void load_f(const bf16_t* p, float* out);
+
+// Operand fragment of tile type T from elements stored as TI (T, or bfloat16
+// widened to a float32 operand).
+template <typename T, typename TI>
+__device__ __forceinline__ typename Tr<T>::Op op_in(const TI* p) {
+  if constexpr (std::is_same<T, TI>::value) {
+    return op_load<T>(p);
+  } else {
+    float x[Tr<T>::KC];
+    load_f<Tr<T>::KC>(p, x);
+    return op_from<T>(x);
+  }
+}
+
 template <int N>
 __device__ __forceinline__ void load_f(const float* p, float* out) {
 #pragma unroll

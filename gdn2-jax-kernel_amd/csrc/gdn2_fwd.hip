@@ -29,9 +29,11 @@
 
 namespace gdn2 {
 
-template <typename T, typename TG>
+// T is the workspace / MFMA operand type; TI the type q, k, v, w, b are stored
+// in (T, or bfloat16 with float32 tiles: the float32 path on bfloat16 inputs).
+template <typename T, typename TG, typename TI = T>
 struct PrepArgs {
-  const T *q, *k, *v, *w, *b;
+  const TI *q, *k, *v, *w, *b;
   const TG* g;
   int T_len, H, N;
   long long NC;   // number of chunks, B*H*N
@@ -103,9 +105,9 @@ constexpr int prep_min_blocks(int esize, int BT, int D) {
   return esize == 2 && BT == 64 && D == 128 ? 3 : 1;
 }
 
-template <typename T, typename TG, int BT, int D>
+template <typename T, typename TG, int BT, int D, typename TI>
 __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T), BT, D))
-    fwd_prep(PrepArgs<T, TG> a) {
+    fwd_prep(PrepArgs<T, TG, TI> a) {
   using Op = typename Tr<T>::Op;
   constexpr int KC = Tr<T>::KC, KS = Tr<T>::KS;
   constexpr int NB = BT / 16;             // 16-token row blocks
@@ -190,8 +192,8 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
         for (int pn = 0; pn < NPN; ++pn)
 #pragma unroll
           for (int j = 0; j < NKD; ++j) {
-            const Op qv = op_load<T>(a.q + off + pn * DP + j * KS + lg * KC);
-            const Op kv = op_load<T>(a.k + off + pn * DP + j * KS + lg * KC);
+            const Op qv = op_in<T>(a.q + off + pn * DP + j * KS + lg * KC);
+            const Op kv = op_in<T>(a.k + off + pn * DP + j * KS + lg * KC);
 #pragma unroll
             for (int e = 0; e < KC; ++e) {
               sq += to_f(qv[e]) * to_f(qv[e]);
@@ -238,9 +240,9 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       for (int j = 0; j < NKD; ++j) load_f<KC>(a.g + off + j * KS + lg * KC, &loc[i][j * KC]);
 #pragma unroll
       for (int j = 0; j < NKD; ++j) {
-        qo[i][j] = op_load<T>(a.q + off + j * KS + lg * KC);
-        ko[i][j] = op_load<T>(a.k + off + j * KS + lg * KC);
-        bo[i][j] = op_load<T>(a.b + off + j * KS + lg * KC);
+        qo[i][j] = op_in<T>(a.q + off + j * KS + lg * KC);
+        ko[i][j] = op_in<T>(a.k + off + j * KS + lg * KC);
+        bo[i][j] = op_in<T>(a.b + off + j * KS + lg * KC);
       }
     }
     if (pn == 0) {
@@ -454,8 +456,8 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       const size_t off = load_row(i) + d0;
 #pragma unroll
       for (int j = 0; j < NKD; ++j) {
-        wo[i][j] = op_load<T>(a.w + off + j * KS + lg * KC);
-        vo[i][j] = op_load<T>(a.v + off + j * KS + lg * KC);
+        wo[i][j] = op_in<T>(a.w + off + j * KS + lg * KC);
+        vo[i][j] = op_in<T>(a.v + off + j * KS + lg * KC);
       }
     }
   };
@@ -1548,7 +1550,7 @@ __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
 
 // ---------------------------------------------------------------------------
 // Host launchers (called from gdn2_api.cpp).
-template <typename T, typename TG, int BT, int D>
+template <typename T, typename TG, int BT, int D, typename TI>
 hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
                       const void* v, const void* w, const void* b, const void* g,
                       const float* h0, float scale, float* out, float* h_final, char* ws,
@@ -1577,12 +1579,12 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   const bool fuse = fuse_ws && !a_dbg;
   launch_mark(st);
   if (NC > 0) {
-    PrepArgs<T, TG> pa{(const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b,
+    PrepArgs<T, TG, TI> pa{(const TI*)q, (const TI*)k, (const TI*)v, (const TI*)w, (const TI*)b,
                        (const TG*)g, T_len, H, N, (long long)NC, scale, W, UT, KgT, Qg, Aqk, GL,
                        a_dbg ? a_dbg : ((flags & 1) ? reinterpret_cast<float*>(ws + L.A)
                                                     : nullptr),
                        (flags & 2) ? 1 : 0, vl ? vl->cstart : nullptr, fuse ? 1 : 0};
-    hipLaunchKernelGGL((fwd_prep<T, TG, BT, D>), dim3(NC), dim3(64 * prep_waves(BT)), 0, st,
+    hipLaunchKernelGGL((fwd_prep<T, TG, BT, D, TI>), dim3(NC), dim3(64 * prep_waves(BT)), 0, st,
                        pa);
   }
   launch_mark(st);
@@ -1651,25 +1653,32 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   return hipGetLastError();
 }
 
-#define GDN2_INST_FWD(T, TG, BT, D)                                                          \
-  template hipError_t launch_fwd<T, TG, BT, D>(hipStream_t, int, int, int, const void*,     \
-                                               const void*, const void*, const void*,       \
-                                               const void*, const void*, const float*,      \
-                                               float, float*, float*, char*, float*, int,   \
-                                               const Varlen*);
+#define GDN2_INST_FWD(T, TG, BT, D, TI)                                                      \
+  template hipError_t launch_fwd<T, TG, BT, D, TI>(hipStream_t, int, int, int, const void*, \
+                                                   const void*, const void*, const void*,   \
+                                                   const void*, const void*, const float*,  \
+                                                   float, float*, float*, char*, float*, int, \
+                                                   const Varlen*);
 
-GDN2_INST_FWD(float, float, 64, 64)
-GDN2_INST_FWD(float, float, 64, 128)
-GDN2_INST_FWD(bf16_t, float, 64, 64)
-GDN2_INST_FWD(bf16_t, float, 64, 128)
-GDN2_INST_FWD(bf16_t, float, 128, 64)
-GDN2_INST_FWD(bf16_t, float, 128, 128)
-GDN2_INST_FWD(bf16_t, bf16_t, 64, 64)
-GDN2_INST_FWD(bf16_t, bf16_t, 64, 128)
-GDN2_INST_FWD(bf16_t, bf16_t, 128, 64)
-GDN2_INST_FWD(bf16_t, bf16_t, 128, 128)
-GDN2_INST_FWD(float, float, 64, 256)
-GDN2_INST_FWD(bf16_t, float, 64, 256)
-GDN2_INST_FWD(bf16_t, bf16_t, 64, 256)
+GDN2_INST_FWD(float, float, 64, 64, float)
+GDN2_INST_FWD(float, float, 64, 128, float)
+GDN2_INST_FWD(bf16_t, float, 64, 64, bf16_t)
+GDN2_INST_FWD(bf16_t, float, 64, 128, bf16_t)
+GDN2_INST_FWD(bf16_t, float, 128, 64, bf16_t)
+GDN2_INST_FWD(bf16_t, float, 128, 128, bf16_t)
+GDN2_INST_FWD(bf16_t, bf16_t, 64, 64, bf16_t)
+GDN2_INST_FWD(bf16_t, bf16_t, 64, 128, bf16_t)
+GDN2_INST_FWD(bf16_t, bf16_t, 128, 64, bf16_t)
+GDN2_INST_FWD(bf16_t, bf16_t, 128, 128, bf16_t)
+GDN2_INST_FWD(float, float, 64, 256, float)
+GDN2_INST_FWD(bf16_t, float, 64, 256, bf16_t)
+GDN2_INST_FWD(bf16_t, bf16_t, 64, 256, bf16_t)
+// float32 arithmetic on bfloat16 inputs (GDN2_BF16_F32)
+GDN2_INST_FWD(float, float, 64, 64, bf16_t)
+GDN2_INST_FWD(float, float, 64, 128, bf16_t)
+GDN2_INST_FWD(float, float, 64, 256, bf16_t)
+GDN2_INST_FWD(float, bf16_t, 64, 64, bf16_t)
+GDN2_INST_FWD(float, bf16_t, 64, 128, bf16_t)
+GDN2_INST_FWD(float, bf16_t, 64, 256, bf16_t)
 
 }  // namespace gdn2

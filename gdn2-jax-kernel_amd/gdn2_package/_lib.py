@@ -18,6 +18,7 @@ LIB_PATH = Path(os.environ.get("GDN2_LIB", _HERE / "libgdn2_hip.so"))
 
 GDN2_F32 = 0
 GDN2_BF16 = 1
+GDN2_BF16_F32 = 2   # bfloat16 inputs and gradients, float32 arithmetic and residuals
 FWD_SAVE_A = 1
 FWD_RAW_INPUTS = 2
 FWD_PARTIAL_CHUNK = 4

@@ -134,12 +134,20 @@ class _Prepared:
         g_dt = torch.float32
         if in_dt == torch.bfloat16 and g.dtype == torch.bfloat16:
             g_dt = torch.bfloat16
+        code = _dtype_code(in_dt)
         if compute_dtype == torch.float32:
-            in_dt = g_dt = torch.float32
+            if in_dt == torch.bfloat16:
+                # float32 arithmetic and residuals on the bfloat16 inputs as they are
+                # (GDN2_BF16_F32): no float32 copies of the inputs or gradients
+                code = _lib.GDN2_BF16_F32
+            else:
+                in_dt = g_dt = torch.float32
         self.B, self.T, self.H, self.D = q.shape
         self.BT = chunk_size_for(in_dt, chunk_size, self.D)
-        self.args = (self.B, self.T, self.H, self.D, self.BT, _dtype_code(in_dt),
-                     _dtype_code(g_dt))
+        # dtype code of the library calls; tile_dt is the workspace / MFMA operand type
+        self.code = code
+        self.tile_dt = torch.bfloat16 if code == _lib.GDN2_BF16 else torch.float32
+        self.args = (self.B, self.T, self.H, self.D, self.BT, code, _dtype_code(g_dt))
         # T % BT != 0: the last chunk is short (GDN2_FWD_PARTIAL_CHUNK); the
         # reference asserts instead (gdn2_fwd.py:146)
         self.N = -(-self.T // self.BT) if self.BT > 0 else 0
@@ -228,14 +236,14 @@ def _diag_kernel_d(tag: str, out, h_final):
 def _residual_views(p: _Prepared, ws: torch.Tensor):
     """Workspace tensors as (B,H,N,...) views in the reference's layouts."""
     B, H, D, BT, N = p.B, p.H, p.D, p.BT, p.N
-    es = 4 if p.in_dt == torch.float32 else 2
+    es = 4 if p.tile_dt == torch.float32 else 2
     NC = B * H * N
     sizes = [("W", NC * BT * D * es), ("UT", NC * D * BT * es), ("KgT", NC * D * BT * es),
              ("Qg", NC * BT * D * es), ("Aqk", NC * BT * BT * es), ("GL", NC * D * 4),
              ("HT", NC * D * D * es), ("VnT", NC * D * BT * es)]
     off, views = 0, {}
     for name, nb in sizes:
-        dt = torch.float32 if name == "GL" else p.in_dt
+        dt = torch.float32 if name == "GL" else p.tile_dt
         views[name] = ws[off:off + nb].view(dt)
         off = (off + nb + 255) // 256 * 256
     f = lambda x: x.float()
@@ -244,7 +252,7 @@ def _residual_views(p: _Prepared, ws: torch.Tensor):
     causal = (idx[:, None] >= idx[None, :])
     # bfloat16 W, UT, KgT, HT, VnT keep their last dimension in chained order
     # (gdn2_common.h kpos): undo it for the views
-    chained = p.in_dt == torch.bfloat16
+    chained = p.tile_dt == torch.bfloat16
     nat = lambda x, n: x[..., _kpos_index(n, x.device)] if chained else x
     return {
         "w_pseudo": f(nat(views["W"].view(*shp, BT, D), D)),

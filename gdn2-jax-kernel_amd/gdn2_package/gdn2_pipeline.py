@@ -7,11 +7,13 @@ A ``torch.autograd.Function`` plays the role of the reference's
 the cotangents are (d out, d h_final), and the gradients of
 (q, k, v, w, b, g, h0) come back in each input's dtype (:129-135).
 
-Arithmetic.  The trainable path computes in float32 whatever the input dtype:
-bfloat16 inputs are widened before the forward, as the reference upcasts every
-input before any arithmetic (gdn2_fwd.py:100-103,266-272; gdn2_bwd.py:130-142),
-so the residuals the backward contracts against the state cotangent are
-float32.  Gradients are cast back to each input's dtype.
+Arithmetic.  The trainable path computes in float32 whatever the input dtype,
+as the reference upcasts every input before any arithmetic
+(gdn2_fwd.py:100-103,266-272; gdn2_bwd.py:130-142), so the residuals the
+backward contracts against the state cotangent are float32.  bfloat16 inputs
+are read as they are by the float32 kernels (GDN2_BF16_F32), which write the
+gradients of q, k, v, w, b in bfloat16; inputs of mixed dtypes are widened to
+float32 first.  Gradients come back in each input's dtype.
 
 Residuals.  By default the forward keeps its per-chunk workspace (WY factors,
 chunk states, v_new) for the backward.  ``recompute=True`` keeps only the
@@ -23,7 +25,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .gdn2_fwd import GDN2ShapeError, _dtype_code, _Prepared, _raise, _run_forward
+from .gdn2_fwd import GDN2ShapeError, _Prepared, _raise, _run_forward
 
 # Chunk size of the trainable path (the backward kernels are written for 64).
 TRAIN_CHUNK = 64
@@ -118,7 +120,7 @@ class _GDN2VarlenCore(torch.autograd.Function):
         cs_d = (torch.arange(total + 1, device=dev, dtype=torch.int32) * p.BT)
         h0c = None if h0 is None else h0.to(device=dev, dtype=torch.float32).contiguous()
         L = _lib.lib()
-        nbytes = L.gdn2_fwd_varlen_workspace_bytes(total, p.H, p.D, p.BT, _dtype_code(p.in_dt))
+        nbytes = L.gdn2_fwd_varlen_workspace_bytes(total, p.H, p.D, p.BT, p.code)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
         out = torch.empty((1, p.T, p.H, p.D), dtype=torch.float32, device=dev)
         h_final = torch.empty((S, p.H, p.D, p.D), dtype=torch.float32, device=dev)
@@ -139,7 +141,7 @@ class _GDN2VarlenCore(torch.autograd.Function):
         p, S = ctx.prep, ctx.S
         total = p.T // p.BT
         L = _lib.lib()
-        bbytes = L.gdn2_bwd_varlen_workspace_bytes(total, p.H, p.D, p.BT, _dtype_code(p.in_dt))
+        bbytes = L.gdn2_bwd_varlen_workspace_bytes(total, p.H, p.D, p.BT, p.code)
         bws = torch.empty(max(bbytes, 1), dtype=torch.uint8, device=p.device)
         if dout is None:
             dout = torch.zeros((1, p.T, p.H, p.D), dtype=torch.float32, device=p.device)

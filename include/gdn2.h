@@ -35,14 +35,20 @@ extern "C" {
 
 /* Element types (in_dtype applies to q,k,v,w,b and the gradients). */
 #define GDN2_F32  0
-#define GDN2_BF16 1
+#define GDN2_BF16 1  /* bfloat16 data and bfloat16 MFMA operands (inference) */
+/* bfloat16 q,k,v,w,b and gradients, float32 arithmetic, residuals and MFMA
+ * operands: the float32 path on bfloat16 inputs, as the reference's training
+ * path upcasts every input before any arithmetic (gdn2_fwd.py:100-103,
+ * gdn2_bwd.py:130-142) -- without float32 copies of the inputs or gradients.
+ * Chunk 64 only; the workspace is sized as for GDN2_F32. */
+#define GDN2_BF16_F32 2
 
 /* Error codes. */
 #define GDN2_OK                0
 #define GDN2_ERR_HEAD_DIM     -1  /* D not in {64,128,256};
                                      ref asserts D==128, gdn2_fwd.py:145, gdn2_bwd.py:348 */
 #define GDN2_ERR_SEQ_LEN      -2  /* T % BT != 0; ref asserts, gdn2_fwd.py:146 */
-#define GDN2_ERR_CHUNK        -3  /* BT not in {64,128}, or BT=128 with float32 inputs or D=256 */
+#define GDN2_ERR_CHUNK        -3  /* BT not in {64,128}, or BT=128 with float32 arithmetic or D=256 */
 #define GDN2_ERR_DTYPE        -4  /* unknown dtype code */
 #define GDN2_ERR_NULL         -5  /* required pointer is NULL */
 #define GDN2_ERR_ALIGN        -6  /* pointer not 16-byte aligned */
@@ -137,8 +143,9 @@ size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
  * in_dtype = GDN2_BF16 they are bfloat16-rounded (h_c, v_new, W, kg, qg, Aqk)
  * and gradients contracted against a large dh_final lose accuracy.  The
  * reference upcasts every input to float32 first (gdn2_fwd.py:100-103,
- * gdn2_bwd.py:130-142); the Python trainable path does the same, running
- * bfloat16 inputs through the float32 forward and backward.
+ * gdn2_bwd.py:130-142); GDN2_BF16_F32 does the same for bfloat16 inputs
+ * (float32 residuals, bfloat16 gradients), and is what the Python trainable
+ * path uses for them.
  * Launches 4 kernels at D <= 128 (see gdn2_set_launch_events); at D = 256 the
  * per-chunk products run as separate launches (the launch marks still bracket
  * the same four stages). */

@@ -35,7 +35,7 @@ def test_version_and_strerror():
     assert L.gdn2_strerror(-1234) == b"unknown error"
 
 
-F32, BF16 = _lib.GDN2_F32, _lib.GDN2_BF16
+F32, BF16, BF16F32 = _lib.GDN2_F32, _lib.GDN2_BF16, _lib.GDN2_BF16_F32
 
 
 @pytest.mark.parametrize("args,code", [
@@ -53,6 +53,9 @@ F32, BF16 = _lib.GDN2_F32, _lib.GDN2_BF16
     ((1, 512, 2, 64, 128, F32, F32), _lib.ERR_CHUNK),       # fp32 needs BT=64
     ((1, 512, 2, 64, 64, 7, F32), _lib.ERR_DTYPE),
     ((1, 512, 2, 64, 64, F32, BF16), _lib.ERR_DTYPE),
+    ((8, 8192, 6, 128, 64, BF16F32, F32), _lib.OK),       # bf16 data, float32 arithmetic
+    ((1, 512, 2, 256, 64, BF16F32, BF16), _lib.OK),
+    ((1, 512, 2, 128, 128, BF16F32, F32), _lib.ERR_CHUNK), # float32 tiles need BT=64
     ((0, 512, 2, 64, 64, F32, F32), _lib.ERR_SHAPE),
     ((1, 512, 0, 64, 64, F32, F32), _lib.ERR_SHAPE),
     ((1, -64, 2, 64, 64, F32, F32), _lib.ERR_SHAPE),
@@ -72,6 +75,11 @@ def test_workspace_bytes():
                               nc * BT * D * s, nc * BT * BT * s, nc * D * 4,
                               nc * D * D * s, nc * D * BT * s, nc * BT * BT * 4])
     assert L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, F32) == exp
+    # bfloat16 data with float32 arithmetic keeps float32 tiles
+    assert L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, BF16F32) == exp
+    assert L.gdn2_bwd_workspace_bytes(B, T, H, D, BT, BF16F32) == \
+        L.gdn2_bwd_workspace_bytes(B, T, H, D, BT, F32)
+    assert L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, BF16) < exp
     assert L.gdn2_fwd_workspace_bytes(1, 1024, 2, 64, 64, F32) > exp
     assert L.gdn2_fwd_workspace_bytes(1, 512, 2, 96, 64, F32) == 0
     assert L.gdn2_fwd_workspace_bytes(1, 0, 2, 64, 64, F32) == 0

@@ -113,6 +113,40 @@ def test_bwd_bf16_inputs(dev):
     check(grads, ref, 2e-2)
 
 
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_bf16_storage_float32_arithmetic_equals_widened(dev, D):
+    """GDN2_BF16_F32 (bfloat16 q,k,v,w,b read as they are, float32 arithmetic and
+    residuals, bfloat16 gradients) against the same float32 kernels on the
+    inputs widened to float32 first, the gradients rounded to bfloat16
+    afterwards: the arithmetic is the same, so out, h_final and every gradient
+    agree bit for bit; g in float32 and in bfloat16."""
+    from gdn2_package import _lib
+    from gdn2_package.gdn2_fwd import _Prepared, _run_forward
+    from gdn2_package.gdn2_pipeline import _run_backward
+    B, T, H = 1, 256, 2
+    xs = O.make_inputs(B, T, H, D, seed=31)
+    rng = np.random.default_rng(5)
+    do = torch.tensor(rng.standard_normal(xs[0].shape).astype(np.float32), device=dev)
+    dh = torch.tensor(rng.standard_normal((B, H, D, D)).astype(np.float32), device=dev)
+    h0 = torch.tensor(rng.standard_normal((B, H, D, D)).astype(np.float32), device=dev)
+    for g_dt in (torch.float32, torch.bfloat16):
+        xb = [torch.tensor(x, device=dev).to(torch.bfloat16) for x in xs[:5]] + \
+            [torch.tensor(xs[5], device=dev).to(g_dt)]
+        pm = _Prepared(*xb, D ** -0.5, h0, 64, compute_dtype=torch.float32)
+        assert pm.code == _lib.GDN2_BF16_F32 and pm.q.dtype == torch.bfloat16
+        pw = _Prepared(*[x.float() for x in xb], D ** -0.5, h0, 64, compute_dtype=torch.float32)
+        assert pw.code == _lib.GDN2_F32
+        om, hm, wsm, _ = _run_forward(pm, flags=_lib.FWD_SAVE_A)
+        ow, hw, wsw, _ = _run_forward(pw, flags=_lib.FWD_SAVE_A)
+        assert torch.equal(om, ow) and torch.equal(hm, hw)
+        gm = _run_backward(pm, wsm, do, dh)
+        gw = _run_backward(pw, wsw, do, dh)
+        for i, (a, b) in enumerate(zip(gm, gw)):
+            want = b if i == 6 else b.to(xb[i].dtype)
+            assert a.dtype == want.dtype, (NAMES[i], a.dtype, want.dtype)
+            assert torch.equal(a, want), (NAMES[i], float((a.float() - want.float()).abs().max()))
+
+
 def test_config4_training_path_bf16(dev):
     """The training path at BASELINE configs[3]'s shape (8,8192,6,128) with
     bfloat16 q,k,v,w,b, float32 g, an N(0,1) cotangent on out and a unit N(0,1)
