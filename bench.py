@@ -82,11 +82,11 @@ def kernel_table(dtype_bytes, chunk):
 
 
 # Inference forwards whose state scan forms the outputs itself (no fwd_out
-# launch): bfloat16 at D = 128 (chunk 64 or 128) and float32 at D = 64 -- the
-# scan variants whose LDS holds the staged h / v_new tiles (state_out_waves in
-# gdn2_fwd.hip).  Their third launch interval is empty.
+# launch): bfloat16 at D = 128 (chunk 64 or 128) and D = 256 (chunk 64), float32
+# at D = 64 -- the scan variants whose LDS holds the staged h / v_new tiles
+# (state_out_waves_of in gdn2_layout.h).  Their third launch interval is empty.
 def fused_out(dtype_bytes, d):
-    return (dtype_bytes == 2 and d == 128) or (dtype_bytes == 4 and d == 64)
+    return (dtype_bytes == 2 and d >= 128) or (dtype_bytes == 4 and d == 64)
 
 
 def name_kernels(kms, fused):

@@ -134,7 +134,7 @@ constexpr int state_ksplit_of(int esize, int BT, int D) {
 // Output waves of the inference scan (32 value columns per workgroup), which
 // then forms the outputs itself, or 0 where a separate output pass runs: no
 // K-split (bfloat16 at D = 64), a single tile buffer, or more LDS than 160 KB
-// (float32 at D = 128, D = 256).  The LDS count mirrors fwd_state's arrays.
+// (float32 at D >= 128).  The LDS count mirrors fwd_state's arrays.
 constexpr int state_out_waves_of(int esize, int BT, int D) {
   const int NW = 2, PADT = 16 / esize;
   const int tiles = 2 * 2 * BT * D * esize;                          // W, kg^T x 2
@@ -142,7 +142,7 @@ constexpr int state_out_waves_of(int esize, int BT, int D) {
   const int xs = esize == 4 ? 2 * NW * (BT / 16) * 1024 : 0;        // K-split partials
   const int fo = 16 * NW * (D + BT + 2 * PADT) * esize;             // staged h, v_new
   const int lds = tiles + ub + xs + fo + 2 * D * 4 + 256;
-  return (state_ksplit_of(esize, BT, D) == 2 && state_bufs_of(esize, BT, D) == 2 && D <= 128 &&
+  return (state_ksplit_of(esize, BT, D) == 2 && state_bufs_of(esize, BT, D) == 2 &&
           lds <= 160 * 1024) ? BT / 32 : 0;
 }
 

@@ -106,8 +106,8 @@ size_t gdn2_fwd_workspace_bytes_ex(int B, int T, int H, int D, int BT, int in_dt
  * h0 may be NULL (zero initial state, gdn2_fwd.py:403-404).  out (B,T,H,D)
  * and h_final (B,H,D,D) are float32.  flags: 0 for inference, GDN2_FWD_SAVE_A
  * when gdn2_bwd will consume ws (the trainable forward, gdn2_pipeline.py:64-67).
- * Inference at D = 128 with bfloat16 inputs (and float32 at D = 64) runs two
- * kernels: the state scan forms the outputs itself. */
+ * Inference with bfloat16 inputs at D = 128 and 256 (and float32 at D = 64)
+ * runs two kernels: the state scan forms the outputs itself. */
 int gdn2_fwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int g_dtype,
              const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, const float* h0, float scale, float* out, float* h_final,
