@@ -1014,6 +1014,102 @@ __global__ void __launch_bounds__(256, 2) bwd_wy(WyArgs<T, TG, TI> a) {
   }
 }
 
+// Diagonal-block gradients of one row block, summed exactly for strong decay
+// (when more than kMaxDiagExp of log-decay lies between a token and the block's
+// 8th, the factors e^{lc - lm}, e^{lm - lc} of gram_bwd's factorisation would
+// overflow).  As in the forward's diag_block_exact: for groups of G = 16, 8, 4, 2
+// tokens the pairs (i in the upper, j in the lower half of one group) are
+// factorised around the group's boundary token b, where both e^{lc_i - lc_b}
+// and e^{lc_b - lc_j} are <= 1 for g <= 0, then the diagonal i = j (factor 1).
+// Returns, in gram_bwd's token layout (lane li = token I*16 + li, channel
+// dt*16 + 4 lg + r of the panel), the diagonal parts of the score gradients wrt
+// q (unscaled), b k and k with their factors applied.  Each level's factored
+// q, b k, k go into this wave's own rows of the LDS tiles (the caller's rows,
+// free at this point; every write is waited for before other lanes read it);
+// the operands are loaded again from `rowo` (this lane's token row plus the
+// panel's first channel) and the levels run in a loop the compiler keeps
+// rolled, so that this rarely taken path adds few registers to gram_bwd.
+template <int NDT>
+struct DiagGrads {
+  f32x4 q[NDT], b[NDT], k[NDT];
+};
+template <typename TI, typename TG, int NDT>
+__device__ __forceinline__ DiagGrads<NDT> diag_grads_exact(
+    const TI* __restrict__ q, const TI* __restrict__ k, const TI* __restrict__ b,
+    const TG* __restrict__ g, size_t rowo, float scale, int I, float* sAQ, float* sABK,
+    float* sKH, int LD1, const float* sDQK, const float* sDKK, int LD2) {
+  constexpr int DQ = 4 * NDT;
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const int t = I * 16 + li, dblk = I * 16 * LD2 + I * 16;
+  DiagGrads<NDT> d;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) d.q[dt] = d.b[dt] = d.k[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int L = 0; L < 5; ++L) {   // L < 4: groups of 16 >> L tokens; L = 4: i = j
+    const int G = 16 >> L, half = G / 2;
+    const bool upper = (li % G) >= half;
+    const int bnd = (li / G) * G + half - 1;   // boundary token of li's group
+    float f[DQ];
+#pragma unroll
+    for (int j = 0; j < NDT; ++j) {   // (NDT = 2: f stays in registers)
+      float lc[4], qv[4], kv[4], bv[4];
+      load_f<4>(g + rowo + j * 16 + lg * 4, lc);
+      load_f<4>(q + rowo + j * 16 + lg * 4, qv);
+      load_f<4>(k + rowo + j * 16 + lg * 4, kv);
+      load_f<4>(b + rowo + j * 16 + lg * 4, bv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float c = row_scan16(lc[e]), cb = __shfl(c, bnd, 16);
+        // (g > 0 lies outside the domain: the exponent is held below overflow)
+        const float fx = L == 4 ? 1.f : __expf(fminf(upper ? c - cb : cb - c, kMaxDiagExp));
+        f[4 * j + e] = fx;
+        const int o = t * LD1 + j * 16 + lg * 4 + e;
+        sAQ[o] = scale * qv[e] * fx;
+        sABK[o] = bv[e] * kv[e] * fx;
+        sKH[o] = kv[e] * fx;
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    f32x4 mq, mk, cq, ck;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s = 4 * lg + e;
+      // pair (i = li, j = s) and pair (i = s, j = li) of this level
+      const bool pq = L < 4 ? (li / G == s / G) && upper && (s % G < half) : s == li;
+      const bool pk = L < 4 ? (li / G == s / G) && (s % G >= half) && !upper : s == li;
+      mq[e] = pq ? sDQK[dblk + li * LD2 + s] : 0.f;
+      mk[e] = (pq && L < 4) ? sDKK[dblk + li * LD2 + s] : 0.f;
+      cq[e] = pk ? sDQK[dblk + s * LD2 + li] : 0.f;
+      ck[e] = (pk && L < 4) ? sDKK[dblk + s * LD2 + li] : 0.f;
+    }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      f32x4 ke, qe, be;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int o = (I * 16 + 4 * lg + e) * LD1 + dt * 16 + li;
+        ke[e] = sKH[o];
+        qe[e] = sAQ[o];
+        be[e] = sABK[o];
+      }
+      f32x4 tq = {0.f, 0.f, 0.f, 0.f}, tb = {0.f, 0.f, 0.f, 0.f}, tk = {0.f, 0.f, 0.f, 0.f};
+      mma(tq, ke, mq);
+      mma(tb, ke, mk);
+      mma(tk, qe, cq);
+      mma(tk, be, ck);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float fx = f[4 * dt + r];   // this lane's token, channel dt*16 + 4lg + r
+        d.q[dt][r] += fx * tq[r];
+        d.b[dt][r] += fx * tb[r];
+        d.k[dt][r] += fx * tk[r];
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  }
+  return d;
+}
+
 // ============================================================================
 // gram_bwd (B4, with the B3 elementwise tail and B5): gradients of the
 // intra-chunk scores
@@ -1097,6 +1193,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
   const int t = I * 16 + li;
   const size_t rowo = tok0 + (size_t)t * HD;
   f32x4 dqd[NDT], dbd[NDT], dkd[NDT];   // diagonal-block sums, token t, channels chan()
+  bool hier = false;   // the diagonal sums come from diag_grads_exact (factors applied)
   // this lane's in-block cumsum of g and q, k, b (token t, channels chan(x)), kept
   // for the chain rule
   float loc[DQ], qv[DQ], kv[DQ], bv[DQ];
@@ -1143,10 +1240,12 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
     // transposed (channel x token), so that lane li holds token li, channels
     // dt*16 + 4lg + r: the layout of the chain rule below, where the row factors
     // are applied.
+    bool wide = false;   // a channel's decay across the block exceeds the factors' range
 #pragma unroll
     for (int x = 0; x < DQ; ++x) {
       const int ch = chan(x);
       const float lm = sLm[I * GP + ch];
+      wide = wide || !(fabsf(loc[x] - lm) <= kMaxDiagExp);
       const float fl = __expf(loc[x] - lm), fr = __expf(lm - loc[x]);
       sAQ[t * LD1 + ch] = a.scale * qv[x] * fl;
       sABK[t * LD1 + ch] = bv[x] * kv[x] * fl;
@@ -1180,6 +1279,19 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
         mma(dbd[dt], ke, mk);   // sum_{j < i}  dAkk[i][j] KE_j
         mma(dkd[dt], qe, cq);   // sum_{i >= j} dAqk[i][j] QE_i
         mma(dkd[dt], be, ck);   //  + sum_{i > j} dAkk[i][j] BE_i
+      }
+    }
+    // strong decay: the diagonal parts again, exactly and with their factors
+    // applied (the chain rule below then takes them as they are)
+    hier = __ballot(wide) != 0;
+    if (hier) {
+      const DiagGrads<NDT> dg = diag_grads_exact<TI, TG, NDT>(
+          a.q, a.k, a.b, a.g, rowo, a.scale, I, sAQ, sABK, sKH, LD1, sDQK, sDKK, LD2);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        dqd[dt] = dg.q[dt];
+        dbd[dt] = dg.b[dt];
+        dkd[dt] = dg.k[dt];
       }
     }
     // then the off-diagonal operands in the same rows (in order within the wave)
@@ -1285,9 +1397,9 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
     for (int e = 0; e < 4; ++e) {
       const float fl = __expf(lc[e] - lm[e]), fr = __expf(lm[e] - lc[e]);
       const float el = __expf(lc[e]), ek = __expf(totI[e] - lc[e]);
-      gq[e] = a.scale * (el * rq[e] + fl * dqd[j][e]);
-      gbk[e] = el * rbk[e] + fl * dbd[j][e];
-      gk[e] = ek * rk[e] + fr * dkd[j][e];
+      gq[e] = a.scale * (el * rq[e] + (hier ? dqd[j][e] : fl * dqd[j][e]));
+      gbk[e] = el * rbk[e] + (hier ? dbd[j][e] : fl * dbd[j][e]);
+      gk[e] = ek * rk[e] + (hier ? dkd[j][e] : fr * dkd[j][e]);
     }
     f32x4 odq, odk, odb, suf;
 #pragma unroll

@@ -13,7 +13,8 @@
 // so both factors, x_i exp(gc_i - P_J) and k_j exp(P_J - gc_j), are <= 1 for
 // g <= 0 and the 16x16 block is an MFMA product.  Diagonal blocks are
 // factorised around their 8th token (|exponent| <= 8 tokens of decay) and
-// masked.  All exponents are formed from in-block partial sums, so they never
+// masked; a block with more than kMaxDiagExp of decay on either side of that
+// token takes the exact hierarchical sums of diag_block_exact.  All exponents are formed from in-block partial sums, so they never
 // subtract two large prefix sums.  This is exact math; the reference's +-20
 // clip of gc_i - gc_j (gdn2_fwd.py:125) is not applied (it changes results by
 // < exp(-20) * |q||k| in the documented input domain).
@@ -83,6 +84,83 @@ __device__ __forceinline__ int own_block(int wv, int i) {
   return i == 0 ? wv : NB - 1 - wv;
 }
 
+
+// Diagonal 16 x 16 score block of one row block, summed exactly for strong
+// decay: when more than kMaxDiagExp of log-decay lies between a token and the
+// block's 8th, the factors e^{lc - lm}, e^{lm - lc} of fwd_prep's
+// factorisation would overflow.  For groups of G = 16, 8, 4, 2 tokens the pairs
+// (i in the upper, j in the lower half of one group) are factorised around the
+// group's boundary token b instead, where both e^{lc_i - lc_b} and
+// e^{lc_b - lc_j} are <= 1 for g <= 0, then the diagonal i = j is added (factor
+// 1; Aqk only, Akk is strictly lower).  Lane (li, lg) of the caller's wave
+// gets [i = li][j = 4 lg + r] of sum_d q_i k_j e^{lc_i - lc_j} (d.q, unscaled)
+// and of sum_d (b k)_i k_j e^{..} (d.k), unmasked above the diagonal.  The
+// operands are loaded again from `off` (the row of token li plus the panel's
+// first channel; the panel's NKD k-groups) and rounded as fwd_prep rounds them;
+// `raw` applies the input activations with the caller's norms iq, ik; `real`
+// false makes the token neutral.  The operands are loaded again (from L2) and
+// the levels run in a loop the compiler keeps rolled, so that this rarely
+// taken path adds few registers to fwd_prep.
+struct DiagSums {
+  f32x4 q, k;
+};
+template <typename T, typename TI, typename TG, int NKD>
+__device__ __forceinline__ DiagSums diag_block_exact(
+    const TI* __restrict__ q, const TI* __restrict__ k, const TI* __restrict__ b,
+    const TG* __restrict__ g, size_t off, bool raw, bool real, float iq, float ik) {
+  using Op = typename Tr<T>::Op;
+  constexpr int KC = Tr<T>::KC, KS = Tr<T>::KS;
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  DiagSums d;
+  d.q = f32x4{0.f, 0.f, 0.f, 0.f};
+  d.k = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int L = 0; L < 5; ++L) {   // L < 4: groups of 16 >> L tokens; L = 4: i = j
+    const int G = 16 >> L, half = G / 2;
+    const bool upper = (li % G) >= half;
+    const int bnd = (li / G) * G + half - 1;   // boundary token of li's group
+    f32x4 tq = {0.f, 0.f, 0.f, 0.f}, tk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int j = 0; j < NKD; ++j) {
+      float lc[KC], qv[KC], kv[KC], bv[KC];
+      load_f<KC>(g + off + j * KS + lg * KC, lc);
+      load_f<KC>(q + off + j * KS + lg * KC, qv);
+      load_f<KC>(k + off + j * KS + lg * KC, kv);
+      load_f<KC>(b + off + j * KS + lg * KC, bv);
+#pragma unroll
+      for (int e = 0; e < KC; ++e) {
+        if (raw) {
+          lc[e] = neg_softplus(lc[e]);
+          qv[e] *= iq;
+          kv[e] *= ik;
+          bv[e] = sigmoidf(bv[e]);
+        }
+        qv[e] = real ? to_f(from_f<T>(qv[e])) : 0.f;
+        kv[e] = real ? to_f(from_f<T>(kv[e])) : 0.f;
+        bv[e] = real ? to_f(from_f<T>(bv[e])) : 0.f;
+        lc[e] = row_scan16(real ? lc[e] : 0.f);
+        const float lb = __shfl(lc[e], bnd, 16);
+        // (g > 0 lies outside the domain: the exponent is held below overflow)
+        const float f = L == 4 ? 1.f
+                      : __expf(fminf(upper ? lc[e] - lb : lb - lc[e], kMaxDiagExp));
+        qv[e] *= f;
+        bv[e] *= kv[e] * f;
+        kv[e] *= f;
+      }
+      const Op xo = op_from<T>(kv);
+      mma(tq, xo, op_from<T>(qv));
+      mma(tk, xo, op_from<T>(bv));
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int jj = 4 * lg + r;
+      const bool cross = L < 4 && (li / G == jj / G) && (li % G >= half) && (jj % G < half);
+      d.q[r] += (cross || (L == 4 && jj == li)) ? tq[r] : 0.f;
+      d.k[r] += cross ? tk[r] : 0.f;
+    }
+  }
+  return d;
+}
 
 // One workgroup per chunk with prep_waves(BT) waves.  A wave owns one 16-token
 // row block (8 waves at BT = 128), or the pair {wv, NB-1-wv} when there are
@@ -308,8 +386,8 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       // raw inputs: q,k <- q,k / max(|.|_2, 1e-12) over D (F.normalize) and
       // b <- sigmoid(b), in place in the loaded registers; a token's channels sit
       // in the four lanes li, li+16, li+32, li+48
+      float iq = 1.f, ik = 1.f;
       if (raw) {
-        float iq, ik;
         if constexpr (one) {
           float sq = 0.f, sk = 0.f;
 #pragma unroll
@@ -339,6 +417,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
             bo[i][j][e] = from_f<T>(sigmoidf(to_f(bo[i][j][e])));
           }
       }
+      bool wide = false;   // a channel's decay across the block exceeds the factors' range
 #pragma unroll
       for (int j = 0; j < NKD; ++j) {
         float qg[KC], kh[KC], dq[KC], dk[KC], db[KC];
@@ -361,6 +440,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
           // the diagonal-block factors keep their own exponentials: e^{loc} or
           // e^{T_I-loc} may underflow where e^{loc-loc_m} e^{loc_m-loc'} does not
           const float lm = row_bcast<7>(lc);
+          wide = wide || !(fabsf(lc - lm) <= kMaxDiagExp);
           const float edq = __expf(lc - lm), edk = __expf(lm - lc);
           dq[e] = qv * edq;
           db[e] = bk * edq;
@@ -374,6 +454,13 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
         const Op xo = op_from<T>(dk);
         mma(accq, xo, op_from<T>(dq));
         mma(acck, xo, op_from<T>(db));
+      }
+      if (__ballot(wide) != 0) {
+        const DiagSums d = diag_block_exact<T, TI, TG, NKD>(a.q, a.k, a.b, a.g,
+                                                             load_row(i) + d0, raw, real(i),
+                                                             iq, ik);
+        accq = d.q;
+        acck = d.k;
       }
       f32x4 sq, sk;
 #pragma unroll

@@ -78,6 +78,28 @@ def test_bwd_matches_oracle_fp32(dev, B, T, H, D, h0, dh, gs):
     check(grads, ref, 1e-4)
 
 
+@pytest.mark.parametrize("D,dtype", [(64, torch.float32), (128, torch.float32),
+                                     (128, torch.bfloat16)])
+def test_bwd_strong_decay_diagonal_blocks(dev, D, dtype):
+    """Channels 0..7 at about -20 of log-decay per token (past the single-center
+    factorisation of the diagonal score blocks, which take the exact
+    hierarchical sums in the forward and in gram_bwd): all gradients against
+    torch.autograd of the float64 recurrence (oracle.recurrent_grads)."""
+    B, T, H = 1, 128, 2
+    xs = O.make_inputs(B, T, H, D, seed=D + 3)
+    g = np.array(xs[5])
+    g[..., :8] *= 30.0
+    xs = list(xs[:5]) + [g]
+    rng = np.random.default_rng(13)
+    h0n = (0.2 * rng.standard_normal((B, H, D, D))).astype(np.float32)
+    do = rng.standard_normal((B, T, H, D)).astype(np.float32)
+    dhn = rng.standard_normal((B, H, D, D)).astype(np.float32)
+    _, grads, xt = run_grads(xs, D ** -0.5, do, dhn, h0=h0n, dtype=dtype, dev=dev)
+    xin = [x.detach().float().cpu().numpy() for x in xt]
+    ref = O.recurrent_grads(*xin, D ** -0.5, do, dhn, h0=h0n)
+    check(grads, ref, 1e-4 if dtype == torch.float32 else 2e-2)
+
+
 @pytest.mark.parametrize("T,h0", [(200, True), (37, False)])
 def test_bwd_partial_last_chunk(dev, T, h0):
     """T % 64 != 0 in the trainable path (zero tokens pad the inputs to whole
