@@ -36,10 +36,11 @@ typedef __bf16 bf16_t;
 constexpr float kClip = 1e4f;
 
 // Largest log-decay the single-center factorisation of a diagonal 16 x 16 score
-// block takes (e^80 and e^-80 stay finite and normal in float32 and bfloat16);
-// blocks with more decay between a token and the block's 8th are summed by the
-// hierarchical fallback instead.
-constexpr float kMaxDiagExp = 80.f;
+// block takes: a factor e^{+-60} times an operand keeps the product finite and,
+// for operands down to 2e-12, normal in float32 and bfloat16 (MFMA may flush
+// denormals).  Blocks with more decay between a token and the block's 8th are
+// summed by the hierarchical fallback instead.
+constexpr float kMaxDiagExp = 60.f;
 
 // nan -> 0, +-inf -> +-kClip, clip to [-kClip, kClip]: gdn2_fwd.py:42-44.
 // max(x, 0) + min(x, 0) is x, or 0 for NaN (IEEE maxNum / minNum return the

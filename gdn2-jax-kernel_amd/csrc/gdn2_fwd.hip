@@ -14,10 +14,11 @@
 // g <= 0 and the 16x16 block is an MFMA product.  Diagonal blocks are
 // factorised around their 8th token (|exponent| <= 8 tokens of decay) and
 // masked; a block with more than kMaxDiagExp of decay on either side of that
-// token takes the exact hierarchical sums of diag_block_exact.  All exponents are formed from in-block partial sums, so they never
-// subtract two large prefix sums.  This is exact math; the reference's +-20
-// clip of gc_i - gc_j (gdn2_fwd.py:125) is not applied (it changes results by
-// < exp(-20) * |q||k| in the documented input domain).
+// token takes the exact hierarchical sums of diag_block_exact.  All exponents
+// are formed from in-block partial sums, so they never subtract two large
+// prefix sums.  This is exact math; the reference's +-20 clip of gc_i - gc_j
+// (gdn2_fwd.py:125) is not applied (it changes results by < exp(-20) * |q||k|
+// in the documented input domain).
 //
 // Saturation.  Every stage output the reference sanitizes (clip to +-1e4,
 // nan -> 0) is sanitized here too before it is stored: the score blocks Aqk,
