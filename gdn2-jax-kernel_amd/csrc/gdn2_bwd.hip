@@ -1167,18 +1167,8 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
   __shared__ __align__(16) float sB3L[GP];         // B3's dgc at the chunk's last token
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  int cid, pn;
-  {
-    const int id = blockIdx.x, nwg = gridDim.x;
-    if (nwg % (8 * NPN) == 0) {   // block id mod 8 = XCD: a chunk's panels on one XCD
-      const int xcd = id % 8, slot = id / 8;
-      pn = slot % NPN;
-      cid = (slot / NPN) * 8 + xcd;
-    } else {
-      cid = id / NPN;
-      pn = id % NPN;
-    }
-  }
+  const UnitPart up = xcd_split(blockIdx.x, gridDim.x, NPN);   // a chunk's panels on one XCD
+  const int cid = up.unit, pn = up.part;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
   const size_t HD = (size_t)a.H * D;
   const int ch0 = pn * GP;   // first channel of the panel

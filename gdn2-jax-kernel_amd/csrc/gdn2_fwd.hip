@@ -85,6 +85,17 @@ __device__ __forceinline__ int own_block(int wv, int i) {
   return i == 0 ? wv : NB - 1 - wv;
 }
 
+// Own row block(s) of wave `wv` in fwd_prep (PW waves).  With two blocks per
+// wave as own_block.  With one block per wave and 8 waves, waves w and w + 4
+// share a SIMD (a workgroup's waves are placed on the 4 SIMDs in turn): they
+// take blocks w and 7 - w, so every SIMD runs 7 of the 28 triangular block
+// pairs (block I has I of them) instead of 4, 6, 8, 10.
+template <int NB, int PW>
+__device__ __forceinline__ int prep_block(int wv, int i) {
+  if constexpr (NB == PW && PW == 8) return wv < 4 ? wv : NB + 3 - wv;
+  return own_block<NB>(wv, i);
+}
+
 
 // Diagonal 16 x 16 score block of one row block, summed exactly for strong
 // decay: when more than kMaxDiagExp of log-decay lies between a token and the
@@ -243,9 +254,9 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
   // around the loads) and are zeroed once the values are first needed, only in
   // chunks that have padding.
   const bool padded = cr.valid < BT;
-  auto real = [&](int i) { return own_block<NB>(wv, i) * 16 + li < cr.valid; };
+  auto real = [&](int i) { return prep_block<NB, PW>(wv, i) * 16 + li < cr.valid; };
   auto load_row = [&](int i) {
-    const int t = own_block<NB>(wv, i) * 16 + li, last = cr.valid > 0 ? cr.valid - 1 : 0;
+    const int t = prep_block<NB, PW>(wv, i) * 16 + li, last = cr.valid > 0 ? cr.valid - 1 : 0;
     return rowp(t < last ? t : last);
   };
   const bool raw = a.raw != 0;
@@ -347,7 +358,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     }
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
-      const int I = own_block<NB>(wv, i);
+      const int I = prep_block<NB, PW>(wv, i);
       if (raw) {
         const bool rv = real(i);
 #pragma unroll
@@ -379,7 +390,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     float aq[NBW][DQ], ak[NBW][DQ];
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
-      const int I = own_block<NB>(wv, i);
+      const int I = prep_block<NB, PW>(wv, i);
       const int t = I * 16 + li;
       T* qgp = a.Qg + (size_t)cid * BT * D + (size_t)t * D + d0;
       T* qgf = a.Qg + (size_t)cid * BT * D;
@@ -489,7 +500,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     // ---- 3. off-diagonal score blocks (I > J) on MFMA ------------------------
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
-      const int I = own_block<NB>(wv, i);
+      const int I = prep_block<NB, PW>(wv, i);
       const int t = I * 16 + li;
       // block pair (I, J), J < I, in descending J; after each pair aq and ak
       // take the decay e^{T_J} of block J in place (they are not needed after
@@ -559,7 +570,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
   // the transposed matrix), so each factor is carried with its transpose.
 #pragma unroll
   for (int i = 0; i < NBW; ++i) {
-    const int I = own_block<NB>(wv, i);
+    const int I = prep_block<NB, PW>(wv, i);
     float* blk = &sA[(I * 16) * A_LD + I * 16];
     f32x4 L, E;
 #pragma unroll
@@ -691,7 +702,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     }
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
-      const int t = own_block<NB>(wv, i) * 16 + li;
+      const int t = prep_block<NB, PW>(wv, i) * 16 + li;
 #pragma unroll
       for (int x = 0; x < DQ; ++x)
         sWVT[chan(x) * TT_LD + t] =
@@ -1552,7 +1563,9 @@ __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
   __shared__ __align__(16) T sV[DVS * V_LD];
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  const int cid = blockIdx.x / NSL, sl = blockIdx.x % NSL;
+  // a chunk's column slices on one XCD: its q_g and Aqk are fetched once into that L2
+  const UnitPart up = xcd_split(blockIdx.x, gridDim.x, NSL);
+  const int cid = up.unit, sl = up.part;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
 
   // All global loads are issued before the first LDS store: the qg / Aqk

@@ -76,6 +76,21 @@ struct Varlen {
   int total_chunks;
 };
 
+// Workgroup id -> (unit, part) for kernels that run NS workgroups per unit (a
+// chunk's column slices or channel panels), so that a unit's workgroups share an
+// XCD and its L2: workgroups are dealt to the 8 XCDs in turn (id mod 8), so ids
+// x, x + 8, ..., x + 8 (NS - 1) take the NS parts of one unit.  Whole groups of
+// 8 NS ids are mapped that way, the ids past them unit-major.  A bijection from
+// [0, nwg) onto [0, nwg / NS) x [0, NS) for nwg a multiple of NS.
+struct UnitPart {
+  int unit, part;
+};
+constexpr UnitPart xcd_split(int id, int nwg, int NS) {
+  const int full = nwg / (8 * NS) * (8 * NS);
+  if (id < full) return UnitPart{(id / 8 / NS) * 8 + id % 8, (id / 8) % NS};
+  return UnitPart{id / NS, id % NS};
+}
+
 // Table clamps of a variable-length batch.  The kernels read their chunk
 // tables through these two functions only, so a malformed table can give wrong
 // numbers but never an access outside the buffers.  They are constexpr, which

@@ -1,6 +1,6 @@
 // Host check of the chunk-table clamps in gdn2_layout.h (chunk_rows,
 // seq_chunks): the functions the kernels read their variable-length tables
-// through.  For random and adversarial tables, every token row a kernel can
+// through; and of xcd_split, the kernels' workgroup-to-(chunk, part) map.  For random and adversarial tables, every token row a kernel can
 // touch must lie inside the packed (B*T) rows and every chunk range inside
 // [0, N).  Built with g++ by tests/test_clamps_cpu.py; prints "ok <cases>".
 #include <climits>
@@ -66,6 +66,29 @@ int main() {
           return fail("equal rows", bb, c, cr.valid);
         ++cases;
       }
+  }
+  // xcd_split: a bijection of workgroup ids onto (unit, part), and in whole
+  // groups of 8 NS ids every part of a unit on the same XCD (id mod 8)
+  for (int NS : {1, 2, 4, 8}) {
+    for (int n = 1; n <= 300; ++n) {
+      const int nwg = NS * n;
+      const int full = nwg / (8 * NS) * (8 * NS);
+      std::vector<int> seen((size_t)nwg, -1);
+      for (int id = 0; id < nwg; ++id) {
+        const gdn2::UnitPart up = gdn2::xcd_split(id, nwg, NS);
+        if (up.unit < 0 || up.unit >= n || up.part < 0 || up.part >= NS)
+          return fail("xcd_split range", NS, nwg, id);
+        int& s = seen[(size_t)up.unit * NS + up.part];
+        if (s >= 0) return fail("xcd_split twice", NS, nwg, id);
+        s = id;
+        ++cases;
+      }
+      for (int u = 0; u < n; ++u)
+        for (int p = 1; p < NS; ++p) {
+          const int a = seen[(size_t)u * NS], b = seen[(size_t)u * NS + p];
+          if (a < full && b < full && a % 8 != b % 8) return fail("xcd_split xcd", NS, nwg, u);
+        }
+    }
   }
   std::printf("ok %lld\n", cases);
   return 0;

@@ -2,8 +2,10 @@
 (chunk_rows, seq_chunks in csrc/gdn2_layout.h), pinned on the CPU: the header
 is compiled with g++ into tests/clamp_check.cpp, which feeds random and
 adversarial tables (negative, past-the-end, INT_MIN/INT_MAX entries) and checks
-that every touched token row and chunk range stays inside its buffer.  The GPU
-test test_varlen_bad_tables_stay_in_bounds exercises the same functions on the
+that every touched token row and chunk range stays inside its buffer; and
+xcd_split (same header), the workgroup-to-(chunk, part) map of fwd_out and
+gram_bwd, for being a bijection that keeps a chunk's parts on one XCD.  The
+GPU test test_varlen_bad_tables_stay_in_bounds exercises the clamps on the
 device."""
 import shutil
 import subprocess
