@@ -519,13 +519,13 @@ COPY_BYTES = 1 << 30           # calibration copy: reads and writes this many by
 KERNELS = {"fwd_prep": "fwd_prep", "fwd_state": "fwd_state_out"}
 
 
-def pmc_run(steps):
+def pmc_run(steps, chunk=CHUNK):
     """Forward steps plus one plain copy kernel of COPY_BYTES, for counter runs."""
     import torch
     import gdn2_package as gp
     xs = make_inputs(torch.bfloat16)
     for _ in range(steps):
-        gp.gdn2_pallas_forward(*xs, D ** -0.5, chunk_size=CHUNK)
+        gp.gdn2_pallas_forward(*xs, D ** -0.5, chunk_size=chunk)
     src = torch.ones(COPY_BYTES // 4, device="cuda")
     dst = torch.empty_like(src)
     torch.abs(src, out=dst)             # one elementwise kernel: reads and writes 1 GiB
@@ -558,26 +558,27 @@ def _counter_means(run_dir, counter):
     return {name: sum(v) / len(v) for name, v in by_kernel.items()}, last
 
 
-def traffic_from(fetch_dir, write_dir):
+def traffic_from(fetch_dir, write_dir, chunk=CHUNK):
     """Copy-calibrated HBM bytes per launch of each forward kernel from the
     FETCH_SIZE and WRITE_SIZE runs (counters in KiB per dispatch).  The
-    calibration copy is the last dispatch of a --pmc-run."""
+    calibration copy is the last dispatch of a --pmc-run (at the same chunk)."""
     fetch, f_copy = _counter_means(fetch_dir, "FETCH_SIZE")
     write, w_copy = _counter_means(write_dir, "WRITE_SIZE")
     f_scale = COPY_BYTES / (f_copy * 1024)
     w_scale = COPY_BYTES / (w_copy * 1024)
-    tab = kernel_table(2, CHUNK)
+    tab = kernel_table(2, chunk)
     pick = lambda t, k: next(v for n, v in t.items() if k in n)
+    sfx = "" if chunk == CHUNK else f"_c{chunk}"   # the headline's files carry no suffix
     out = {}
     for k, row in KERNELS.items():
         fb = pick(fetch, k) * 1024 * f_scale
         wb = pick(write, k) * 1024 * w_scale
-        rec = {"kernel": row, "workload": "B8 T8192 H6 D128 bf16 chunk 128",
+        rec = {"kernel": row, "workload": f"B8 T8192 H6 D128 bf16 chunk {chunk}",
                "fetch_bytes": fb, "write_bytes": wb, "bytes_per_launch": fb + wb,
                "algorithmic_bytes": tab[row]["bytes"] * B * T * H,
                "fetch_scale": f_scale, "write_scale": w_scale,
                "calibration": f"copy kernel reading and writing {COPY_BYTES} bytes"}
-        (ROOT / "profiles" / f"traffic_{row}_b8t8192h6d128_bf16.json").write_text(
+        (ROOT / "profiles" / f"traffic_{row}_b8t8192h6d128_bf16{sfx}.json").write_text(
             json.dumps(rec, indent=1) + "\n")
         out[k] = rec
     print(json.dumps(out, indent=1))
@@ -596,6 +597,8 @@ def main():
                     help="forward steps plus the calibration copy, for rocprofv3 --pmc")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="reduce two rocprofv3 counter runs to profiles/traffic_*.json")
+    ap.add_argument("--chunk", type=int, default=CHUNK,
+                    help="chunk size of --pmc-run / --traffic-from (default: the headline's)")
     ap.add_argument("--pmc-train-run", action="store_true",
                     help="one float32 training step and one headline forward, for MFMA counters")
     ap.add_argument("--mfma-from", metavar="DIR",
@@ -608,7 +611,7 @@ def main():
         pmc_train_run()
         return
     if args.traffic_from:
-        traffic_from(*args.traffic_from)
+        traffic_from(*args.traffic_from, chunk=args.chunk)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the op shards over (batch, head) "
@@ -616,7 +619,7 @@ def main():
         sys.exit(2)
 
     if args.pmc_run:
-        pmc_run(max(1, min(args.steps, 5)))
+        pmc_run(max(1, min(args.steps, 5)), chunk=args.chunk)
         return
 
     import torch
