@@ -195,6 +195,17 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
   }
   // step i works on chunk c0 + n-1-i
   auto chunk_id = [&](int i) { return (size_t)bh * a.N + c0 + (n - 1 - i); };
+  // float32 tiles up to D = 128 are stored transposed in LDS (W^T [d][t], kg
+  // [t][d]), so that every MFMA operand of the compute waves is one 16-byte LDS
+  // read; bfloat16 tiles keep the stored layout (DMA, chained columns), and so does
+  // D = 256, whose staging registers (four blocks per lane and tile) would spill
+  constexpr bool TR = sizeof(T) == 4 && D <= 128;
+  // element offset of logical (row r, element e) in a float32 tile with `re`
+  // elements per row, its 16-byte chunks XOR-swizzled by the row
+  auto swz = [](int r, int e, int re) {
+    const int nchunk = re / 4, m = (nchunk < 16 ? nchunk : 16) - 1;
+    return r * re + (((e / 4) ^ (r & m)) * 4) + (e % 4);
+  };
 
   if (wv >= NCW) {
     // ---- producers ----------------------------------------------------------
@@ -204,12 +215,54 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
     static_assert(PIECES % NP == 0 && (NW * NB) % NP == 0 && (NW * NDT) % NP == 0,
                   "work must split evenly");
     const int p = wv - NCW;
+    // TR: W and kg^T through registers in 4 x 4 blocks, four 16-byte global loads
+    // (rows of the stored tile, consecutive lanes on consecutive columns) and four
+    // 16-byte LDS stores (rows of the transposed tile) per block
+    constexpr int NBLK = (BT / 4) * (D / 4);                // blocks per tile
+    constexpr int BPL = TR ? NBLK / (64 * NP) : 1;          // blocks per producer lane
+    static_assert(!TR || NBLK % (64 * NP) == 0, "blocks must split over the producers");
+    f32x4 stW[BPL][4], stK[BPL][4];
+    auto tr_load = [&](int i) __attribute__((always_inline)) {
+      const size_t cid = chunk_id(i);
+      const float* w = reinterpret_cast<const float*>(a.W) + cid * BT * D;     // [t][d]
+      const float* k = reinterpret_cast<const float*>(a.KgT) + cid * D * BT;   // [d][t]
+#pragma unroll
+      for (int q = 0; q < BPL; ++q) {
+        const int b = (q * NP + p) * 64 + lane;
+        const int wt4 = b / (D / 4), wd4 = b % (D / 4);     // W rows 4 wt4 + r, columns 4 wd4
+        const int kd4 = b / (BT / 4), kt4 = b % (BT / 4);   // kg^T rows 4 kd4 + r, columns 4 kt4
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          stW[q][r] = load4f(w + (size_t)(4 * wt4 + r) * D + 4 * wd4);
+          stK[q][r] = load4f(k + (size_t)(4 * kd4 + r) * BT + 4 * kt4);
+        }
+      }
+    };
+    auto tr_store = [&](char* base) __attribute__((always_inline)) {
+      float* wt = reinterpret_cast<float*>(base);            // W^T [d][t]
+      float* kt = reinterpret_cast<float*>(base + WBYTES);   // kg [t][d]
+#pragma unroll
+      for (int q = 0; q < BPL; ++q) {
+        const int b = (q * NP + p) * 64 + lane;
+        const int wt4 = b / (D / 4), wd4 = b % (D / 4);
+        const int kd4 = b / (BT / 4), kt4 = b % (BT / 4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          store4(&wt[swz(4 * wd4 + c, 4 * wt4, BT)],
+                 f32x4{stW[q][0][c], stW[q][1][c], stW[q][2][c], stW[q][3][c]});
+          store4(&kt[swz(4 * kt4 + c, 4 * kd4, D)],
+                 f32x4{stK[q][0][c], stK[q][1][c], stK[q][2][c], stK[q][3][c]});
+        }
+      }
+    };
+    // loads of chunk i: the tiles (DMA, or TR: into registers) and the gathers
     auto issue = [&](int i, char* base, float* gl) __attribute__((always_inline)) {
       const size_t cid = chunk_id(i);
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
       const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
+      if constexpr (TR) tr_load(i);
 #pragma unroll
-      for (int j = 0; j < PP; ++j) {
+      for (int j = 0; j < (TR ? 0 : PP); ++j) {
         const int piece = p * PP + j;
         char* dst = base + piece * 1024;
         if (piece < WPIECES) {
@@ -295,6 +348,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
     if constexpr (NBUF == 1) {
       for (int i = 0; i < n; ++i) {
         wait_step(i);
+        if constexpr (TR) tr_store(sbuf0);
         exp_gl(sGL0);
         barrier();  // A(i)
         barrier();  // B(i)
@@ -309,6 +363,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
     }
     for (int i = 0; i < n; i += 2) {
       wait_step(i);
+      if constexpr (TR) tr_store(sbuf0);
       exp_gl(sGL0);
       barrier();  // A(i)
       barrier();  // B(i)
@@ -317,6 +372,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         if (i + 2 < n) touch(i + 2);
         if constexpr (KS > 1) barrier();  // X(i)
         wait_step(i + 1);
+        if constexpr (TR) tr_store(sbuf1);
         exp_gl(sGL1);
         barrier();  // A(i+1)
         barrier();  // B(i+1)
@@ -385,6 +441,16 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
     if constexpr (QG) lds_barrier(); else __syncthreads();  // B(i)
     const T* sW = reinterpret_cast<const T*>(cur);
     const T* sK = reinterpret_cast<const T*>(cur + WBYTES);
+    // MFMA row operands: kg[t][d] for rows d = 16 at + 4 lg + e, column t = 16 it + li
+    // (dv_new), W[t][d] for rows t = 16 it + 4 lg + e, column d = 16 at + li (dh)
+    // (TR: one 16-byte read from the transposed tiles; otherwise four reads below)
+    auto xk = [&](int at, int it) __attribute__((always_inline)) {
+      return load4f(reinterpret_cast<const float*>(cur + WBYTES) +
+                    swz(it * 16 + li, at * 16 + 4 * lg, D));
+    };
+    auto xw = [&](int it, int at) __attribute__((always_inline)) {
+      return load4f(reinterpret_cast<const float*>(cur) + swz(at * 16 + li, it * 16 + 4 * lg, BT));
+    };
 
     float* dht = a.DHT + cid * D * D + (size_t)col * D;
 #pragma unroll
@@ -401,10 +467,14 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         const int at = ks * NDH + j;
 #pragma unroll
         for (int it = 0; it < NB; ++it) {
-          f32x4 x;
+          if constexpr (TR) {
+            mma(part[it], xk(at, it), dh[j]);
+          } else {
+            f32x4 x;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
-          mma(part[it], x, dh[j]);
+            for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
+            mma(part[it], x, dh[j]);
+          }
         }
       }
       // exchange the halves; both waves form dv_new in the same order
@@ -424,10 +494,14 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       for (int it = 0; it < NB; ++it) {
 #pragma unroll
         for (int at = 0; at < NDT; ++at) {
-          f32x4 x;
+          if constexpr (TR) {
+            mma(dvn[it], xk(at, it), dh[at]);
+          } else {
+            f32x4 x;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
-          mma(dvn[it], x, dh[at]);
+            for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
+            mma(dvn[it], x, dh[at]);
+          }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) dvn[it][r] = sanitize(dvn[it][r]);
@@ -448,10 +522,14 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int it = 0; it < NB; ++it) {
-        f32x4 x;
+        if constexpr (TR) {
+          mma(acc, xw(it, at), dvn[it]);
+        } else {
+          f32x4 x;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = elem(sW, it * 16 + 4 * lg + e, at * 16 + li, D);
-        mma(acc, x, dvn[it]);
+          for (int e = 0; e < 4; ++e) x[e] = elem(sW, it * 16 + 4 * lg + e, at * 16 + li, D);
+          mma(acc, x, dvn[it]);
+        }
       }
       const f32x4 egl = load4f(eglc + at * 16 + 4 * lg);
 #pragma unroll
