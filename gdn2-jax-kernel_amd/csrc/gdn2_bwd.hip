@@ -123,9 +123,12 @@ struct BStateArgs {
 // other half of an LDS double buffer with global_load_lds_dwordx4 and gather the
 // workgroup's dvp and qg^T do rows into the compute lanes' order (one buffer,
 // freed by barrier B once copied to registers); the compute waves issue no
-// global loads.  Both products read their tile transposed: one 4-byte (2-byte
-// for bfloat16 residuals, chained column order) LDS read per element, which
-// the XOR swizzle of the 16-byte chunks keeps free of bank conflicts.
+// global loads.  Both products read their tile transposed.  Float32 tiles up to
+// D = 128 are staged by the producers through registers and stored transposed
+// (W^T, kg), so each MFMA operand is one 16-byte LDS read; otherwise (DMA) one
+// 4-byte (2-byte for bfloat16 residuals, chained column order) LDS read per
+// element.  The XOR swizzle of the 16-byte chunks keeps either free of bank
+// conflicts.
 //
 // K-split (KS = 2; bfloat16 residuals only up to D = 128, where its registers
 // fit), as in fwd_state: two compute waves per
