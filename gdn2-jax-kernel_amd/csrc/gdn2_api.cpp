@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "gdn2.h"
 #include "gdn2_common.h"
 #include "gdn2_layout.h"
@@ -128,7 +130,9 @@ struct BwdRun {
                  float scale, const float* dout, const float* dh_final, void* dq, void* dk,
                  void* dv, void* dw, void* db, void* dg, float* dh0, const char* fws,
                  char* ws, const int* cu_chunks, int nseq) {
-    if constexpr (D > 128 && BT != 64) {
+    if constexpr (std::is_same_v<T, bf16_t>) {
+      return GDN2_ERR_DTYPE;  // bfloat16 residuals: rejected by the entry points
+    } else if constexpr (D > 128 && BT != 64) {
       return GDN2_ERR_CHUNK;  // D = 256 runs at chunk 64 only
     } else {
       hipError_t e = launch_bwd<typename Tile<T>::type, TG, BT, D, typename Stor<T>::type>(
@@ -179,7 +183,7 @@ const char* gdn2_strerror(int code) {
     case GDN2_ERR_SEQ_LEN: return "sequence length T must be divisible by the chunk size BT";
     case GDN2_ERR_CHUNK:
       return "chunk size BT must be 64 or 128 (128 needs GDN2_BF16 inputs and D <= 128)";
-    case GDN2_ERR_DTYPE: return "unsupported dtype (inputs: GDN2_F32, GDN2_BF16 or GDN2_BF16_F32; g: float32, or bfloat16 with bfloat16 inputs)";
+    case GDN2_ERR_DTYPE: return "unsupported dtype (inputs: GDN2_F32, GDN2_BF16 or GDN2_BF16_F32, the backward GDN2_F32 or GDN2_BF16_F32; g: float32, or bfloat16 with bfloat16 inputs)";
     case GDN2_ERR_NULL: return "required pointer is NULL";
     case GDN2_ERR_ALIGN: return "pointer is not 16-byte aligned";
     case GDN2_ERR_WORKSPACE: return "workspace too small";
@@ -282,6 +286,7 @@ int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtyp
 }
 
 size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype) {
+  if (in_dtype == GDN2_BF16) return 0;
   if (gdn2_validate(B, T, H, D, BT, in_dtype, in_dtype) != GDN2_OK &&
       gdn2_validate(B, T, H, D, BT, in_dtype, GDN2_F32) != GDN2_OK)
     return 0;
@@ -297,6 +302,7 @@ int gdn2_bwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
   EventScope scope;
   int rc = gdn2_validate(B, T, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
+  if (in_dtype == GDN2_BF16) return GDN2_ERR_DTYPE;  // bfloat16 residuals: see gdn2.h
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, dout, dq, dk, dv, dw, db, dg}))) return rc;
   if ((rc = check_ptrs({dh0}))) return rc;
   if ((rc = check_opt({h0, dh_final}))) return rc;
@@ -329,6 +335,7 @@ int gdn2_bwd_varlen(void* stream, int num_seqs, const int* cu_chunks, int total_
   const int T = total_chunks * BT;
   int rc = gdn2_validate(1, T, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
+  if (in_dtype == GDN2_BF16) return GDN2_ERR_DTYPE;  // bfloat16 residuals: see gdn2.h
   if (BT != 64) return GDN2_ERR_CHUNK;
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, dout, dq, dk, dv, dw, db, dg}))) return rc;
   if ((rc = check_ptrs({dh0, cu_chunks}))) return rc;

@@ -414,6 +414,21 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
 #pragma unroll
     for (int j = 0; j < NDH; ++j) dh[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  // The last chunk's dh' is dh_final as given: B3 takes it raw (gdn2_pipeline.py:
+  // 52-56,105) while the carry above starts from its sanitized value (gdn2_bwd.py:53)
+  if (n > 0) {
+    float* dht = a.DHT + chunk_id(0) * D * D + (size_t)col * D;
+#pragma unroll
+    for (int j = 0; j < NDH; ++j) {
+      f32x4 raw = {0.f, 0.f, 0.f, 0.f};
+      if (a.dh_final) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          raw[r] = a.dh_final[(st_idx * D + (ks * NDH + j) * 16 + 4 * lg + r) * D + col];
+      }
+      store4(dht + (ks * NDH + j) * 16 + 4 * lg, raw);
+    }
+  }
   // this wave's qdot pieces from global memory (QG), loaded ahead
   f32x4 qnext[QG && QAHEAD ? NDH : 1], qd[NDH];
   auto load_qd = [&](int i, f32x4* dst) __attribute__((always_inline)) {
@@ -455,9 +470,11 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       return load4f(reinterpret_cast<const float*>(cur) + swz(at * 16 + li, it * 16 + 4 * lg, BT));
     };
 
-    float* dht = a.DHT + cid * D * D + (size_t)col * D;
+    if (i > 0) {   // dh_{c+1} (chunk n-1's was stored raw before the scan)
+      float* dht = a.DHT + cid * D * D + (size_t)col * D;
 #pragma unroll
-    for (int j = 0; j < NDH; ++j) store4(dht + (ks * NDH + j) * 16 + 4 * lg, dh[j]);
+      for (int j = 0; j < NDH; ++j) store4(dht + (ks * NDH + j) * 16 + 4 * lg, dh[j]);
+    }
 
     // dv_new = dvp + kg dh: X[t][d] = kg^T[d][t]
     if constexpr (KS > 1) {
@@ -1390,11 +1407,21 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
   lds_barrier();
 
   // ---- off-diagonal pairs on MFMA --------------------------------------------
+  // The reference accumulates B4 over pairs of two 32-token sub-blocks S0 = {blocks
+  // 0, 1}, S1 = {2, 3}, in the order (S0,S0), (S1,S0), (S1,S1), clipping every
+  // accumulator after each pair (_clip_acc, gdn2_bwd.py:287-328).  The sums that
+  // cross the sub-blocks are therefore kept apart: the rows of S1 against J in S0
+  // (cq, cb) and the columns of S0 against I' in S1 (ck); the rest of each sum
+  // belongs to the row block's own sub-block pair.
+  constexpr int SB = NB / 2;   // row blocks per sub-block
+  const bool rowx = I >= SB;   // this block's rows have a (S1,S0) part, its columns none
+  f32x4 cq[NDT], cb[NDT];      // (S1,S0) row sums of block I in S1; ck in cq for S0
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) {
     const int dcol = dt * 16 + li;
     // rows of block I against J < I
     f32x4 aq = {0.f, 0.f, 0.f, 0.f}, ab = {0.f, 0.f, 0.f, 0.f};
+    cq[dt] = cb[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float F = 1.f;
     for (int J = I - 1; J >= 0; --J) {
       f32x4 y, tq = {0.f, 0.f, 0.f, 0.f}, tk = {0.f, 0.f, 0.f, 0.f};
@@ -1402,8 +1429,13 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       for (int e = 0; e < 4; ++e) y[e] = sKH[(J * 16 + 4 * lg + e) * LD1 + dcol];
       mma(tq, load4f(&sDQK[(I * 16 + li) * LD2 + J * 16 + 4 * lg]), y);
       mma(tk, load4f(&sDKK[(I * 16 + li) * LD2 + J * 16 + 4 * lg]), y);
+      if (rowx && J < SB) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) { aq[r] += F * tq[r]; ab[r] += F * tk[r]; }
+        for (int r = 0; r < 4; ++r) { cq[dt][r] += F * tq[r]; cb[dt][r] += F * tk[r]; }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { aq[r] += F * tq[r]; ab[r] += F * tk[r]; }
+      }
       F *= sETot[J * GP + dcol];
     }
     // rows of block I (as the column block) against I' > I
@@ -1421,8 +1453,13 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       }
       mma(t1, xq, yq);
       mma(t2, xk, yk);
+      if (!rowx && Ip >= SB) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) akk[r] += F * (a.scale * t1[r] + t2[r]);
+        for (int r = 0; r < 4; ++r) cq[dt][r] += F * (a.scale * t1[r] + t2[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) akk[r] += F * (a.scale * t1[r] + t2[r]);
+      }
       F *= sETot[Ip * GP + dcol];
     }
     lds_barrier();  // every wave is done with channel slice dt of sAQ, sABK, sKH, sETot
@@ -1434,6 +1471,19 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       sKH[o] = akk[r];
     }
   }
+  // The score-gradient tiles are no longer read (the last barrier above): the
+  // cross sums go into their space, in the same [token][channel] layout, rows of
+  // this wave's own block only
+  float* const sXQ = sDQK;   // cq: (S1,S0) rows of dAqk (S1) / (S1,S0) columns (S0)
+  float* const sXB = sDKK;   // cb: (S1,S0) rows of dAkk (S1)
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = (I * 16 + 4 * lg + r) * LD1 + dt * 16 + li;
+      sXQ[o] = cq[dt][r];
+      sXB[o] = cb[dt][r];
+    }
 
   // ---- chain rule, lane = token t of block I, channels chan(x) -----------------
   // (gdn2_bwd.py:186-210; dqg, dkg, dkbd come from bwd_wy).  First the score
@@ -1447,6 +1497,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
     const f32x4 dqg = pdqg[j], dkg = pdkg[j], dkbd = pdkbd[j];
     const f32x4 rq = load4f(&sAQ[t * LD1 + c0]), rbk = load4f(&sABK[t * LD1 + c0]),
                 rk = load4f(&sKH[t * LD1 + c0]), lm = load4f(&sLm[I * GP + c0]);
+    const f32x4 xrq = load4f(&sXQ[t * LD1 + c0]), xrb = load4f(&sXB[t * LD1 + c0]);
     // channel c0 + e is x = 4j + e of the start's registers
     const float* const lc = &loc[4 * j];
     const float* const xq = &qv[4 * j];
@@ -1463,7 +1514,9 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
         pre[e] += m < I ? tm[e] : 0.f;
       }
     }
-    f32x4 gq, gbk, gk;
+    // B4's gradients wrt q, b k, k of this token: gq, gbk, gk from its own sub-block
+    // pair, xq, xbk (rows of S1) or xk (columns of S0) from the (S1,S0) pair
+    f32x4 gq, gbk, gk, xgq, xgb;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float fl = __expf(lc[e] - lm[e]), fr = __expf(lm[e] - lc[e]);
@@ -1471,6 +1524,8 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       gq[e] = a.scale * (el * rq[e] + (hier ? dqd[j][e] : fl * dqd[j][e]));
       gbk[e] = el * rbk[e] + (hier ? dbd[j][e] : fl * dbd[j][e]);
       gk[e] = ek * rk[e] + (hier ? dkd[j][e] : fr * dkd[j][e]);
+      xgq[e] = (rowx ? a.scale * el : ek) * xrq[e];
+      xgb[e] = el * xrb[e];
     }
     f32x4 odq, odk, odb, suf;
 #pragma unroll
@@ -1478,14 +1533,32 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       const float gc = pre[e] + lc[e];
       const float eg = __expf(gc), ekg = __expf(gl[e] - gc);
       const float kgv = xk[e] * ekg;
-      // B3's and B4's parts are sanitized as each kernel's output, then their
-      // sum (gdn2_bwd.py:212-218, 333-338; gdn2_pipeline.py:121-133)
-      odq[e] = sanitize(sanitize(dqg[e] * eg) + sanitize(gq[e]));
+      // B4's accumulators in the pair order of gdn2_bwd.py:287-328, each clipped
+      // after its pair: rows of S1 take (S1,S0) then (S1,S1); columns of S0 take
+      // (S0,S0) then (S1,S0); dgc takes a pair's row terms, then its column terms
+      float aq4, ab4, ak4, ag4;
+      if (rowx) {
+        aq4 = sanitize(sanitize(xgq[e]) + gq[e]);
+        ab4 = sanitize(sanitize(xgb[e]) + gbk[e]);
+        ak4 = sanitize(gk[e]);
+        const float gi0 = xq[e] * xgq[e] + xb[e] * xk[e] * xgb[e];
+        const float gi1 = xq[e] * gq[e] + xb[e] * xk[e] * gbk[e];
+        ag4 = sanitize(sanitize(sanitize(gi0) + gi1) - xk[e] * gk[e]);
+      } else {
+        aq4 = sanitize(gq[e]);
+        ab4 = sanitize(gbk[e]);
+        ak4 = sanitize(sanitize(gk[e]) + xgq[e]);
+        const float gi0 = xq[e] * gq[e] + xb[e] * xk[e] * gbk[e];
+        ag4 = sanitize(sanitize(sanitize(gi0) - xk[e] * gk[e]) - xk[e] * xgq[e]);
+      }
+      // B3's and B4's outputs are sanitized as each kernel's output, then their
+      // sum (gdn2_bwd.py:212-218, 330-339; gdn2_pipeline.py:121-133)
+      odq[e] = sanitize(sanitize(dqg[e] * eg) + aq4);
       odk[e] = sanitize(sanitize(dkbd[e] * xb[e] * eg + dkg[e] * ekg) +
-                        sanitize(gk[e] + gbk[e] * xb[e]));
-      odb[e] = sanitize(sanitize(dkbd[e] * xk[e] * eg) + sanitize(gbk[e] * xk[e]));
+                        sanitize(ak4 + ab4 * xb[e]));
+      odb[e] = sanitize(sanitize(dkbd[e] * xk[e] * eg) + sanitize(ab4 * xk[e]));
       const float dgc3 = dkbd[e] * xb[e] * xk[e] * eg + dqg[e] * xq[e] * eg - dkg[e] * kgv;
-      const float dgc4 = xq[e] * gq[e] + xb[e] * xk[e] * gbk[e] - xk[e] * gk[e];
+      const float dgc4 = ag4;
       // the last token's B3 part still lacks the g_last terms: kept for the end
       if (I == NB - 1 && li == 15) sB3L[c0 + e] = dgc3;
       suf[e] = row_suffix16(sanitize(dgc3) + sanitize(dgc4));
@@ -1998,17 +2071,7 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
       void*, void*, void*, void*, void*, float*, const char*, char*, const int*, int);
 GDN2_INST_BWD(float, float, 64, 64, float)
 GDN2_INST_BWD(float, float, 64, 128, float)
-GDN2_INST_BWD(bf16_t, float, 64, 64, bf16_t)
-GDN2_INST_BWD(bf16_t, float, 64, 128, bf16_t)
-GDN2_INST_BWD(bf16_t, float, 128, 64, bf16_t)
-GDN2_INST_BWD(bf16_t, float, 128, 128, bf16_t)
-GDN2_INST_BWD(bf16_t, bf16_t, 64, 64, bf16_t)
-GDN2_INST_BWD(bf16_t, bf16_t, 64, 128, bf16_t)
-GDN2_INST_BWD(bf16_t, bf16_t, 128, 64, bf16_t)
-GDN2_INST_BWD(bf16_t, bf16_t, 128, 128, bf16_t)
 GDN2_INST_BWD(float, float, 64, 256, float)
-GDN2_INST_BWD(bf16_t, float, 64, 256, bf16_t)
-GDN2_INST_BWD(bf16_t, bf16_t, 64, 256, bf16_t)
 // float32 arithmetic on bfloat16 inputs and gradients (GDN2_BF16_F32)
 GDN2_INST_BWD(float, float, 64, 64, bf16_t)
 GDN2_INST_BWD(float, float, 64, 128, bf16_t)

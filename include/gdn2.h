@@ -49,7 +49,7 @@ extern "C" {
                                      ref asserts D==128, gdn2_fwd.py:145, gdn2_bwd.py:348 */
 #define GDN2_ERR_SEQ_LEN      -2  /* T % BT != 0; ref asserts, gdn2_fwd.py:146 */
 #define GDN2_ERR_CHUNK        -3  /* BT not in {64,128}, or BT=128 with float32 arithmetic or D=256 */
-#define GDN2_ERR_DTYPE        -4  /* unknown dtype code */
+#define GDN2_ERR_DTYPE        -4  /* unknown dtype code; GDN2_BF16 in the backward */
 #define GDN2_ERR_NULL         -5  /* required pointer is NULL */
 #define GDN2_ERR_ALIGN        -6  /* pointer not 16-byte aligned */
 #define GDN2_ERR_WORKSPACE    -7  /* workspace smaller than *_workspace_bytes() */
@@ -138,14 +138,14 @@ size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
  * gdn2_pipeline.py:77-83; a caller that kept no residuals re-runs gdn2_fwd
  * first).  BT must be 64.  dh_final and h0 may be NULL (zero).  dq,dk,dv,dw,db
  * are in_dtype, dg is g_dtype, dh0 is float32 (B,H,D,D); all gradients are
- * sanitized as gdn2_pipeline.py:129-135.  The arithmetic is float32; the
- * residuals it reads from fwd_ws are in the forward's operand type, so with
- * in_dtype = GDN2_BF16 they are bfloat16-rounded (h_c, v_new, W, kg, qg, Aqk)
- * and gradients contracted against a large dh_final lose accuracy.  The
- * reference upcasts every input to float32 first (gdn2_fwd.py:100-103,
- * gdn2_bwd.py:130-142); GDN2_BF16_F32 does the same for bfloat16 inputs
- * (float32 residuals, bfloat16 gradients), and is what the Python trainable
- * path uses for them.
+ * sanitized as gdn2_pipeline.py:129-135.  in_dtype is GDN2_F32 or GDN2_BF16_F32:
+ * the arithmetic and the residuals in fwd_ws are float32, as the reference
+ * upcasts every input before any arithmetic (gdn2_fwd.py:100-103,
+ * gdn2_bwd.py:130-142; gdn2_pipeline.py:129-135); GDN2_BF16_F32 reads bfloat16
+ * inputs and writes bfloat16 gradients.  in_dtype = GDN2_BF16 (bfloat16
+ * residuals, whose rounding puts gradients contracted against a unit dh_final
+ * outside the bfloat16 tolerance) is GDN2_ERR_DTYPE, and
+ * gdn2_bwd_workspace_bytes returns 0 for it.
  * Launches 4 kernels at D <= 128 (see gdn2_set_launch_events); at D = 256 the
  * per-chunk products run as separate launches (the launch marks still bracket
  * the same four stages). */

@@ -445,14 +445,24 @@ def _wy_dqkg_backward(q, k, b, w, v, gc, A, h_pre, v_new, do, dv, dh_next, scale
                 dv_raw=sanitize(dv_raw), dgc=sanitize(dgc), dAkk=sanitize(dakk))
 
 
-def _intra_backward(daqk, dakk, q, k, b, gc, scale, clip=True):
-    """B4, gdn2_bwd.py:248-339 (full-chunk form of the sub-block pair loop)."""
+def _intra_backward(daqk, dakk, q, k, b, gc, scale, clip=True, n_sub=2):
+    """B4, gdn2_bwd.py:248-339.
+
+    ``n_sub`` sub-blocks of BC = BT / n_sub tokens (the reference's N_SUB = 2,
+    BT = N_SUB * BC, gdn2_fwd.py:29-31), visited as the pair loop of
+    gdn2_bwd.py:287-328 does -- (si, sj) for si in range(n_sub), sj <= si -- with
+    ``_clip_acc`` (gdn2_bwd.py:26-28) on every accumulator after each pair: dq and
+    d(bk) of the row block, dk of the column block, then dgc of the row block and
+    dgc of the column block (the same rows when si == sj).  The final
+    dk + d(bk) b, d(bk) k and the outputs are sanitized (gdn2_bwd.py:330-339).
+    ``n_sub=None`` sums every pair first and clips each output once (equal to the
+    pair loop wherever no partial sum passes the clip)."""
     BT = q.shape[-2]
     idx = np.arange(BT)
     causal = idx[:, None] >= idx[None, :]
     strict = idx[:, None] > idx[None, :]
 
-    def one(daqk, dakk, q, k, b, gc):
+    def whole(daqk, dakk, q, k, b, gc):
         E, mask = _decay(gc, clip)
         bk = b * k
         dqk = daqk * causal
@@ -467,8 +477,42 @@ def _intra_backward(daqk, dakk, q, k, b, gc, scale, clip=True):
         dgc = wq.sum(axis=-2) - wq.sum(axis=-3) + wk.sum(axis=-2) - wk.sum(axis=-3)
         return (sanitize(dq), sanitize(dk + dbk * b), sanitize(dbk * k), sanitize(dgc))
 
+    def pairs(daqk, dakk, q, k, b, gc):
+        E, mask = _decay(gc, clip)
+        bk = b * k
+        BC = BT // n_sub
+        sidx = np.arange(BC)
+        s_causal = sidx[:, None] >= sidx[None, :]
+        s_strict = sidx[:, None] > sidx[None, :]
+        dq, dk, dbk, dgc = (np.zeros_like(q) for _ in range(4))
+        for si in range(n_sub):
+            for sj in range(si + 1):
+                I = slice(si * BC, (si + 1) * BC)
+                J = slice(sj * BC, (sj + 1) * BC)
+                Ep, mp = E[..., I, J, :], mask[..., I, J, :]
+                dmq, dmk = daqk[..., I, J], dakk[..., I, J]
+                if si == sj:
+                    dmq, dmk = dmq * s_causal, dmk * s_strict
+                terms = []
+                for dm, L, R in ((dmq, scale * q[..., I, :], k[..., J, :]),
+                                 (dmk, bk[..., I, :], k[..., J, :])):
+                    wgt = dm[..., None] * Ep                      # _dL/_dR/_dgc_pair_sum
+                    terms.append((np.einsum("...ijd,...jd->...id", wgt, R),
+                                   np.einsum("...ijd,...id->...jd", wgt, L),
+                                   (wgt * L[..., :, None, :] * R[..., None, :, :] * mp)))
+                (dLq, dRq, wq), (dLk, dRk, wk) = terms
+                dq[..., I, :] = sanitize(dq[..., I, :] + dLq * scale)
+                dbk[..., I, :] = sanitize(dbk[..., I, :] + dLk)
+                dk[..., J, :] = sanitize(dk[..., J, :] + dRq + dRk)
+                dgc[..., I, :] = sanitize(dgc[..., I, :] + wq.sum(axis=-2) + wk.sum(axis=-2))
+                dgc[..., J, :] = sanitize(dgc[..., J, :] - wq.sum(axis=-3) - wk.sum(axis=-3))
+        return (sanitize(dq), sanitize(dk + dbk * b), sanitize(dbk * k), sanitize(dgc))
+
+    if n_sub is not None:
+        assert BT % n_sub == 0, f"BT={BT} must split into {n_sub} sub-blocks"
+    fn = whole if n_sub is None else pairs
     # _tiled flattens on the shape of its first tensor: pass a (...,BT,D) one first.
-    return _tiled(lambda q, k, b, gc, daqk, dakk: one(daqk, dakk, q, k, b, gc),
+    return _tiled(lambda q, k, b, gc, daqk, dakk: fn(daqk, dakk, q, k, b, gc),
                   (q, k, b, gc, daqk, dakk), 4)
 
 
@@ -478,12 +522,15 @@ def _reverse_cumsum(dgc):
 
 
 def chunked_bwd(q, k, v, w, b, g, scale, do, dh_final=None, h0=None, BT=64, BC=None,
-                clip=True, dtype=np.float64):
+                clip=True, dtype=np.float64, n_sub=2):
     """Gradients (dq,dk,dv,dw,db,dg,dh0) of chunked_fwd, as gdn2_pipeline.py:70-137.
 
     Recomputes the forward (gdn2_pipeline.py:77-83), then B2 -> B1 -> B3 -> B4
     -> B5, sums and applies the final clip (:121-135).  Inputs (B,T,H,D),
-    ``do`` (B,T,H,D), ``dh_final`` (B,H,D,D) or None (zero).
+    ``do`` (B,T,H,D), ``dh_final`` (B,H,D,D) or None (zero).  B1 carries the
+    sanitized dh_final (gdn2_bwd.py:53) while B3 receives it raw as the last
+    chunk's dh' (gdn2_pipeline.py:52-56,105).  ``n_sub``: B4's sub-blocks per
+    chunk (see ``_intra_backward``).
     """
     B, L, H, D = q.shape
     Dv = v.shape[-1]
@@ -499,11 +546,13 @@ def chunked_bwd(q, k, v, w, b, g, scale, do, dh_final=None, h0=None, BT=64, BC=N
     daqk, dv_partial = _dav_backward(res["Aqk"], res["v_new_all"], dos)
     dh_all, dh0, dv_all = _dhu_backward(dos, dv_partial, res["w_pseudo"], res["qg"],
                                         res["kg"], res["gc_last"], scale, dh_final)
-    # gdn2_pipeline.py:52-56: dh_next[c] = dh entering chunk c from the right
-    dh_next = np.concatenate([dh_all[:, :, 1:], sanitize(dh_final)[:, :, None]], axis=2)
+    # gdn2_pipeline.py:52-56: dh_next[c] = dh entering chunk c from the right; the
+    # last chunk's is dh_final as given (B1 alone sanitizes it, gdn2_bwd.py:53)
+    dh_next = np.concatenate([dh_all[:, :, 1:], dh_final[:, :, None]], axis=2)
     b3 = _wy_dqkg_backward(qs, ks, bs, ws, vs, gc, res["A"], res["h_pre_all"],
                            res["v_new_all"], dos, dv_all, dh_next, scale)
-    dq4, dk4, db4, dgc4 = _intra_backward(daqk, b3["dAkk"], qs, ks, bs, gc, scale, clip=clip)
+    dq4, dk4, db4, dgc4 = _intra_backward(daqk, b3["dAkk"], qs, ks, bs, gc, scale, clip=clip,
+                                          n_sub=n_sub)
     dg = _reverse_cumsum(b3["dgc"] + dgc4)
     grads = (b3["dq"] + dq4, b3["dk"] + dk4, b3["dv_raw"], b3["dw"], b3["db"] + db4, dg)
     dq, dk, dv, dw, db, dg = (sanitize(from_chunks(x)) for x in grads)

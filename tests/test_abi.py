@@ -137,6 +137,25 @@ def test_bwd_rejects_before_launch():
     assert call(dims, 0x4000, fws - 1) == _lib.ERR_WORKSPACE
 
 
+def test_bwd_rejects_bf16_residuals():
+    """The backward runs on float32 residuals only (GDN2_F32, GDN2_BF16_F32), as
+    the reference upcasts before any arithmetic (ref gdn2_bwd.py:130-142,
+    gdn2_pipeline.py:129-135): GDN2_BF16 is refused by the sizing function and
+    by both backward entry points, before any pointer is looked at."""
+    L = _lib.lib()
+    fake = [0x100000 * (i + 1) for i in range(6)]
+    grads = [0x900000 * (i + 1) for i in range(6)]
+    assert L.gdn2_bwd_workspace_bytes(1, 512, 2, 64, 64, BF16) == 0
+    assert L.gdn2_bwd_varlen_workspace_bytes(4, 2, 64, 64, BF16) == 0
+    assert L.gdn2_bwd_workspace_bytes(1, 512, 2, 64, 64, BF16F32) > 0
+    for gdt in (F32, BF16):
+        assert L.gdn2_bwd(None, 1, 512, 2, 64, 64, BF16, gdt, *fake, None, 0.125, 0x4000, None,
+                          *grads, 0x5000, 0x6000, 1 << 40, 0x7000, 1 << 40) == _lib.ERR_DTYPE
+        assert L.gdn2_bwd_varlen(None, 2, 0x7000, 4, 2, 64, 64, BF16, gdt, *fake, None, 0.125,
+                                 0x4000, None, *grads, 0x6000, 0x5000, 1 << 40, 0x7100,
+                                 1 << 40) == _lib.ERR_DTYPE
+
+
 def test_launch_events_hook_is_host_only():
     L = _lib.lib()
     arr = (ctypes.c_void_p * 4)()

@@ -79,7 +79,8 @@ def test_bwd_matches_oracle_fp32(dev, B, T, H, D, h0, dh, gs):
 
 
 @pytest.mark.parametrize("D,dtype", [(64, torch.float32), (128, torch.float32),
-                                     (128, torch.bfloat16)])
+                                     (128, torch.bfloat16), (256, torch.float32),
+                                     (256, torch.bfloat16)])
 def test_bwd_strong_decay_diagonal_blocks(dev, D, dtype):
     """Channels 0..7 at about -20 of log-decay per token (past the single-center
     factorisation of the diagonal score blocks, which take the exact
@@ -267,3 +268,38 @@ def test_bwd_d256_matches_oracle(dev, T, H, h0, dh, dtype):
     xin = [x.detach().float().cpu().numpy() for x in xt]
     ref = O.chunked_bwd(*xin, D ** -0.5, do, dhn, h0=h0n, BT=64, clip=False)
     check(grads, ref, 1e-4 if dtype == torch.float32 else 2e-2)
+
+
+# ----------------------------------------------------------------------------- saturation
+@pytest.mark.parametrize("D,dos,dhs", [(64, 1e4, 0.0), (64, 3e3, 3e4), (128, 3e3, 3e4)])
+def test_bwd_saturation_matches_reference_clipping(dev, D, dos, dhs):
+    """Cotangents past the reference's clip (do x 1e4, or do x 3e3 with dh_final x
+    3e4; slow decay, unit v and scale): B2's dAqk / dv_partial, B1's dv_new and
+    dh carry (and its sanitized dh_final), B3's dA, dA A^T and outputs, B4's
+    accumulators in the sub-block pair order and B5 all clip somewhere, and
+    4-20 % of the gradients saturate.  The float32 trainable path matches the
+    oracle's restatement with the same clip points (oracle.chunked_bwd,
+    clip=True: B4's pair loop with _clip_acc, gdn2_bwd.py:287-339, and the raw
+    dh_final as B3's last dh', gdn2_pipeline.py:52-56).  The test first checks
+    on the oracle that both of those change the result here, so a kernel that
+    clipped B4 once per output or fed B3 the sanitized dh_final would fail.
+    Tolerance on the saturation scale: |got - ref| <= 1e-4 * 1e4 + 1e-4 * |ref|."""
+    B, T, H, scale = 1, 256, 2, 1.0
+    xs = O.make_inputs(B, T, H, D, seed=40, g_scale=0.05)
+    rng = np.random.default_rng(3)
+    do = (rng.standard_normal((B, T, H, D)) * dos).astype(np.float32)
+    dhn = (rng.standard_normal((B, H, D, D)) * dhs).astype(np.float32)
+    h0n = rng.standard_normal((B, H, D, D)).astype(np.float32)
+    _, grads, _ = run_grads(xs, scale, do, dhn, h0=h0n, dev=dev)
+    ref = O.chunked_bwd(*xs, scale, do, dhn, h0=h0n, BT=64, clip=True)
+    whole = O.chunked_bwd(*xs, scale, do, dhn, h0=h0n, BT=64, clip=True, n_sub=None)
+    # B4's pair order matters here (in dq, dk or db)
+    assert max(np.abs(ref[i] - whole[i]).max() for i in (0, 1, 4)) > 100.0
+    if dhs:
+        san = O.chunked_bwd(*xs, scale, do, O.sanitize(dhn), h0=h0n, BT=64, clip=True)
+        assert np.abs(ref[1] - san[1]).max() > 100.0        # and so does the raw dh_final
+    assert 0.01 < np.mean(np.abs(ref[0]) == 1e4) < 0.5
+    for n, g, r in zip(NAMES, grads, ref):
+        assert np.isfinite(g).all() and np.abs(g).max() <= 1e4, n
+        ok, e = close(g * 1e-4, r * 1e-4, 1e-4)
+        assert ok, (n, e * 1e4)

@@ -218,7 +218,7 @@ def strong_decay_inputs(B, T, H, D, seed):
 
 @pytest.mark.parametrize("dtype,BT,D", [
     (torch.float32, 64, 64), (torch.float32, 64, 128), (torch.bfloat16, 128, 128),
-    (torch.bfloat16, 64, 128), (torch.bfloat16, 64, 256),
+    (torch.bfloat16, 64, 128), (torch.bfloat16, 64, 256), (torch.float32, 64, 256),
 ])
 def test_strong_decay_diagonal_blocks(dev, dtype, BT, D):
     """Strong decay in some channels: out and h_final (inference path, and the

@@ -342,3 +342,71 @@ def test_mutation_missing_last_row_dgl_is_caught(monkeypatch):
     (o * torch.tensor(do)).sum().backward()
     got = O.chunked_bwd(q, k, v, w, b, g, 0.5, do, BT=32, clip=False)
     assert maxerr(got[5], ts[5].grad.numpy()) > 1e-6
+
+
+# --------------------------------------------------------------------------- saturation order
+def test_b4_pair_loop_equals_whole_sums_in_domain():
+    """B4's sub-block pair loop (ref gdn2_bwd.py:287-328) sums the same terms as
+    the whole-chunk form: with every partial sum inside the clip, 1, 2 and 4
+    sub-blocks and the unclipped whole sums agree (the whole sums are pinned to
+    torch.autograd through chunked_bwd above)."""
+    q, k, v, w, b, g = inputs(B=1, T=64, H=2, D=8, seed=21)
+    rng = np.random.default_rng(5)
+    qs, ks, bs = (O.to_chunks(x, 32) for x in (q, k, b))
+    gc = np.cumsum(O.to_chunks(g, 32), axis=-2)
+    daqk = rng.standard_normal(qs.shape[:-1] + (32,))
+    dakk = rng.standard_normal(qs.shape[:-1] + (32,))
+    ref = O._intra_backward(daqk, dakk, qs, ks, bs, gc, 0.4, clip=False, n_sub=None)
+    for ns in (1, 2, 4):
+        got = O._intra_backward(daqk, dakk, qs, ks, bs, gc, 0.4, clip=False, n_sub=ns)
+        for gv, rv in zip(got, ref):
+            assert maxerr(gv, rv) < 1e-12, ns
+
+
+def test_b4_pair_loop_clip_order_known_answer():
+    """Known answer, worked by hand from ref gdn2_bwd.py:287-339 with two
+    one-token sub-blocks (BT = 2, D = 1, gc = 0, scale = 1): q = (2, 1),
+    k = (1, 2), b = (0.5, 0.5), dAqk = [[1.5e4, .], [-4e3, 7e3]], dAkk[1][0] = 2e3.
+      pair (0,0): dq0 = c(1.5e4) = 1e4, dk0 = c(3e4) = 1e4, dgc0 = c(c(3e4) - 3e4) = -1e4
+      pair (1,0): dq1 = -4e3, dbk1 = 2e3, dk0 = c(1e4 - 4e3 + 2e3) = 8e3,
+                  dgc1 = c(-4e3 + 2e3) = -2e3, dgc0 = c(-1e4 + 4e3 - 2e3) = -8e3
+      pair (1,1): dq1 = c(-4e3 + 1.4e4) = 1e4, dk1 = 7e3,
+                  dgc1 = c(c(-2e3 + 1.4e4) - 1.4e4) = -4e3
+      outputs:    dk = (8e3, 7e3 + 2e3 * 0.5), db = (0, 2e3 * 2)
+    Clipping each output once instead (the whole sums) gives dk0 = 1e4,
+    dgc = (2e3, -2e3): the known answer catches a dropped accumulator clip."""
+    q = np.array([[[2.0], [1.0]]])
+    k = np.array([[[1.0], [2.0]]])
+    b = np.full((1, 2, 1), 0.5)
+    gc = np.zeros((1, 2, 1))
+    daqk = np.array([[[1.5e4, 9e9], [-4e3, 7e3]]])     # 9e9: masked (right of the diagonal)
+    dakk = np.array([[[9e9, 9e9], [2e3, 9e9]]])
+    want = ([1e4, 1e4], [8e3, 8e3], [0.0, 4e3], [-8e3, -4e3])
+    got = O._intra_backward(daqk, dakk, q, k, b, gc, 1.0, clip=True, n_sub=2)
+    for gv, wv in zip(got, want):
+        np.testing.assert_array_equal(gv.ravel(), wv)
+    whole = O._intra_backward(daqk, dakk, q, k, b, gc, 1.0, clip=True, n_sub=None)
+    assert whole[1].ravel()[0] == 1e4 and list(whole[3].ravel()) == [2e3, -2e3]
+
+
+def test_raw_dh_final_reaches_b3_known_answer():
+    """B1 carries sanitize(dh_final) (ref gdn2_bwd.py:53) but B3 receives the raw
+    dh_final as the last chunk's dh' (gdn2_pipeline.py:52-56,105).  One live
+    token (the last of a 16-token chunk; the others have k = q = 0 and g = 0, so
+    they leave the state and the gradients alone), D = 1, k = v = 1, w = 0.1,
+    b = 0.5, do = 0, h0 = 0, dh_final = 5e4.  By hand: v_new = w v = 0.1, W = 0.5;
+    B1: dh = 1e4, dv_new = kg dh = 1e4, dh0 = c(1e4 - W dv_new) = 5e3;
+    B3: dkg = v_new dh' = 5e3 (5e4 raw; 1e3 from the sanitized value), so
+    dk = 5e3, dv = w d(wv) = 1e3, dw = v d(wv) = 1e4, and dg = 0 (the last
+    token's -dkg kg cancels against its g_last term)."""
+    x = [np.zeros((1, 16, 1, 1)) for _ in range(6)]
+    x[1][:, 15] = 1.0
+    x[2][:, 15] = 1.0
+    x[3][:, 15] = 0.1
+    x[4][:, 15] = 0.5
+    got = O.chunked_bwd(*x, 1.0, np.zeros((1, 16, 1, 1)),
+                        dh_final=np.full((1, 1, 1, 1), 5e4), BT=16)
+    want = [0.0, 5e3, 1e3, 1e4, 0.0, 0.0]
+    for i, wv in enumerate(want):
+        assert abs(got[i][0, 15, 0, 0] - wv) < 1e-9 and np.all(got[i][0, :15] == 0), i
+    assert abs(got[6].item() - 5e3) < 1e-9
