@@ -211,15 +211,19 @@ int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype)
 }
 
 // Forward workspace for the segment count that `flags` selects (automatic
-// when its segment field is 0).
-static size_t fwd_ws_need(int B, int T, int H, int D, int BT, int in_dtype, int flags) {
+// when its segment field is 0).  An inference call whose scan forms the outputs
+// itself writes no h^T / v_new^T tiles, and its workspace has none, unless the
+// call is the debug path (`debug`: the residual tiles are kept for inspection).
+static size_t fwd_ws_need(int B, int T, int H, int D, int BT, int in_dtype, int flags,
+                          bool debug = false) {
   const int N = chunks_per_seq(T, BT);
   const int es = (int)elem_size(in_dtype);
   const bool fused = state_out_waves_of(es, BT, D) > 0 && !(flags & GDN2_FWD_SAVE_A);
   const int S = state_segments((long long)B * H, N, D, es, (flags >> 8) & 0xff,
                                fused ? 32 : seg_pass_cols(es, D));
   return fwd_layout(nchunks(B, T, H, BT), BT, D, elem_size(in_dtype),
-                    S > 1 ? (size_t)B * H * S : 0, !(flags & kFwdNoARegion)).total;
+                    S > 1 ? (size_t)B * H * S : 0, !(flags & kFwdNoARegion),
+                    !fused || debug).total;
 }
 
 size_t gdn2_fwd_workspace_bytes_ex(int B, int T, int H, int D, int BT, int in_dtype, int flags) {
@@ -249,7 +253,7 @@ int fwd_entry(void* stream, int B, int T, int H, int D, int BT, int in_dtype, in
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, out}))) return rc;
   if ((rc = check_ptrs({h_final}))) return rc;
   if ((rc = check_opt({h0, a_dbg}))) return rc;
-  const size_t need = fwd_ws_need(B, T, H, D, BT, in_dtype, flags);
+  const size_t need = fwd_ws_need(B, T, H, D, BT, in_dtype, flags, a_dbg != nullptr);
   if (need > 0 && (rc = check_ptrs({ws}))) return rc;
   if (ws_bytes < need) return GDN2_ERR_WORKSPACE;
   return dispatch<FwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, B, T, H, q, k, v, w,

@@ -53,6 +53,8 @@ struct PrepArgs {
                       // ([N+1], B = 1); rows past cstart[c+1] are neutral padding
   int frag;           // Qg and Aqk in operand-fragment order (qg_frag / aqk_frag):
                       // for the scan's output waves, which then read 1 KB per load
+  int* sat_clear;     // segmented scan: its saturation flag, cleared here (the first
+                      // launch of the call)
 };
 
 // Operand-fragment order of a chunk's q_g [BT][D] tile: the 16-byte operand
@@ -233,6 +235,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
   float* const sF1 = sSmall + 3 * NB * DP;     // e^{S_{I+1}}
 
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  if (a.sat_clear && blockIdx.x == 0 && tid == 0) *a.sat_clear = 0;
   // Chunk order (the grid is (b,h) pairs x N chunks).  bfloat16: dealt last-first
   // across all (b,h), so the state scan's first chunks are the most recently
   // written (still in the last-level cache): the latency-bound bf16 scan gains 5 %.
@@ -776,6 +779,12 @@ struct StateArgs {
   float scale;
   int T_len;
   const int* cstart;  // variable-length chunk table (see PrepArgs)
+  // Segmented scan (S > 1): `sat` is set to 1 when a clip of the carried state
+  // binds in a segmented pass (the segments' affine combination is exact only
+  // while none does); a pass with `gate` runs only if *gate is nonzero -- the
+  // serial scan that then replaces the segmented result
+  int* sat;
+  const int* gate;
 };
 
 // One workgroup = one (b,h) and 16*NW value columns: NW compute waves (16
@@ -797,7 +806,8 @@ struct StateArgs {
 // from the identity with u = 0 and no clipping, its transition M_seg; the
 // combine kernel chains the segment entry states; the final pass reruns every
 // segment from its entry state, writing h^T / v_new^T.  The combine is exact
-// while the +-1e4 clip of h stays inactive.
+// while the +-1e4 clip of h does not bind; all three launches flag a binding
+// clip (StateArgs::sat), and a flagged call is finished by the serial scan.
 //
 // W / kg^T tiles are stored unpadded with the 16-byte chunks of row r
 // XOR-permuted by (r mod 16), so the 16 rows an MFMA operand read touches land
@@ -883,6 +893,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
   static_assert(NO == 0 || (NXB > 0 && NBUF == 2 && NO == NB / 2),
                 "output waves need an X barrier per chunk, two tile buffers and NB/2 waves");
 
+  if (a.gate && *a.gate == 0) return;   // whole workgroups, before any barrier
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   // A unit is one (b,h) segment; it has NVS column slices (2 NVS in the summary
@@ -1204,6 +1215,9 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
     for (int i = 0; i < NDH; ++i) h[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const bool write_tiles = !a.summary;
+  // segmented passes: whether a clip of the state bound (NaN included)
+  const bool track = a.sat != nullptr && !mslice;
+  bool bound = false;
 
   // One chunk: v_new = u - W h, h <- e^{gl} h + kg^T v_new, with chunk c in `cur`.
   // output waves: the pieces of chunk c-1's h^T / v_new^T this wave puts into
@@ -1429,6 +1443,12 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
       }
       }
       if (!mslice) {
+        if (track) {
+#pragma unroll
+          for (int at = 0; at < NDH; ++at)
+#pragma unroll
+            for (int r2 = 0; r2 < 4; ++r2) bound = bound || !(fabsf(h[at][r2]) <= kClip);
+        }
 #pragma unroll
         for (int at = 0; at < NDH; ++at)
 #pragma unroll
@@ -1453,6 +1473,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
     if (n > 0) put_tiles();
     __syncthreads();  // B(n)
   }
+  if (track && __ballot(bound) != 0 && lane == 0) *a.sat = 1;
   float* hout = a.cu ? a.h_final + ((size_t)sg * a.H + bh) * D * D
               : a.summary ? a.seg + ((size_t)unit * 2 + (mslice ? 1 : 0)) * D * D
               : (sg == a.S - 1) ? a.h_final + (size_t)bh * D * D : nullptr;
@@ -1474,7 +1495,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
 // state sits transposed in LDS as the chained operand of the next product.
 template <int D>
 __global__ void __launch_bounds__(256) seg_combine(const float* seg, const float* h0, float* hin,
-                                                   int S) {
+                                                   int S, int* sat) {
   constexpr int NDT = D / 16;
   __shared__ __align__(16) float sHT[16 * (D + 4)];   // current state, [col][row]
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
@@ -1492,6 +1513,7 @@ __global__ void __launch_bounds__(256) seg_combine(const float* seg, const float
     sHT[cc * (D + 4) + r] = e0;
   }
   __syncthreads();
+  bool bound = false;   // a clip of an entry state bound (see StateArgs::sat)
   for (int s = 1; s + 1 < S; ++s) {
     const float* M = segb + ((size_t)s * 2 + 1) * DD;
     const float* e = segb + (size_t)s * 2 * DD;
@@ -1517,7 +1539,9 @@ __global__ void __launch_bounds__(256) seg_combine(const float* seg, const float
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const size_t o = (size_t)(at * 16 + 4 * lg + r) * D + c0 + li;
-          nh[r] = sanitize(acc[j][r] + e[o]);
+          const float x = acc[j][r] + e[o];
+          bound = bound || !(fabsf(x) <= kClip);
+          nh[r] = sanitize(x);
           hinb[(size_t)(s + 1) * DD + o] = nh[r];
         }
         store4(&sHT[li * (D + 4) + at * 16 + 4 * lg], nh);
@@ -1525,6 +1549,7 @@ __global__ void __launch_bounds__(256) seg_combine(const float* seg, const float
     }
     __syncthreads();
   }
+  if (__ballot(bound) != 0 && lane == 0) *sat = 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -1665,8 +1690,14 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   const int S_ws = vl ? 1
                       : state_segments((long long)B * H, N, D, (int)sizeof(T), (flags >> 8) & 0xff,
                                        fuse_ws ? 32 : seg_pass_cols(sizeof(T), D));
-  const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), S_ws > 1 ? (size_t)B * H * S_ws : 0,
-                                 !(flags & kFwdNoARegion));
+  // Inference (no residuals kept): the scan forms the outputs itself where its
+  // variant has output waves (state_out_waves), fwd_out is not launched and the
+  // h^T / v_new^T tiles have no region (a variable-length workspace keeps them:
+  // its size does not depend on flags)
+  const bool fuse = fuse_ws && !a_dbg;
+  const size_t seg_units = S_ws > 1 ? (size_t)B * H * S_ws : 0;
+  const FwdLayout L = fwd_layout(NC, BT, D, sizeof(T), seg_units, !(flags & kFwdNoARegion),
+                                 !fuse || vl != nullptr);
   T* W = reinterpret_cast<T*>(ws + L.W);
   T* UT = reinterpret_cast<T*>(ws + L.UT);
   T* KgT = reinterpret_cast<T*>(ws + L.KgT);
@@ -1675,16 +1706,16 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   float* GL = reinterpret_cast<float*>(ws + L.GL);
   T* HT = reinterpret_cast<T*>(ws + L.HT);
   T* VnT = reinterpret_cast<T*>(ws + L.VnT);
-  // Inference (no residuals kept): the scan forms the outputs itself where its
-  // variant has output waves (state_out_waves), and fwd_out is not launched.
-  const bool fuse = fuse_ws && !a_dbg;
+  // segmented scan: its saturation flag, in the last slot of SEG
+  int* sat = seg_units ? reinterpret_cast<int*>(ws + L.SEG + seg_flag_offset(seg_units, D))
+                       : nullptr;
   launch_mark(st);
   if (NC > 0) {
     PrepArgs<T, TG, TI> pa{(const TI*)q, (const TI*)k, (const TI*)v, (const TI*)w, (const TI*)b,
                        (const TG*)g, T_len, H, N, (long long)NC, scale, W, UT, KgT, Qg, Aqk, GL,
                        a_dbg ? a_dbg : ((flags & 1) ? reinterpret_cast<float*>(ws + L.A)
                                                     : nullptr),
-                       (flags & 2) ? 1 : 0, vl ? vl->cstart : nullptr, fuse ? 1 : 0};
+                       (flags & 2) ? 1 : 0, vl ? vl->cstart : nullptr, fuse ? 1 : 0, sat};
     hipLaunchKernelGGL((fwd_prep<T, TG, BT, D, TI>), dim3(NC), dim3(64 * prep_waves(BT)), 0, st,
                        pa);
   }
@@ -1721,19 +1752,31 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     float* seg = reinterpret_cast<float*>(ws + L.SEG);          // [bh][S][2][D][D]
     float* hin = seg + BH * S * 2 * (size_t)D * D;               // [bh][S][D][D]
     StateArgs<T> sum{W, UT, KgT, GL, h0, N, S, Lseg, 1, nullptr, seg, HT, VnT, h_final,
-                     nullptr, H};
+                     nullptr, H, Qg, Aqk, out, scale, T_len, nullptr, sat, nullptr};
     hipLaunchKernelGGL((fwd_state<T, BT, D, GW, SP, GK>), dim3(BH * S * 2 * GVS),
                        dim3(64 * (GW * GK + SP)), 0, st, sum);
     hipLaunchKernelGGL((seg_combine<D>), dim3(BH * (D / 16)), dim3(256), 0, st, seg, h0, hin,
-                       S);
+                       S, sat);
     StateArgs<T> fin{W, UT, KgT, GL, h0, N, S, Lseg, 0, hin, nullptr, HT, VnT, h_final,
-                     nullptr, H, Qg, Aqk, out, scale, T_len, nullptr};
+                     nullptr, H, Qg, Aqk, out, scale, T_len, nullptr, sat, nullptr};
     if (fuse)   // final pass with output waves: 32-column workgroups
       hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK, NO>), dim3(BH * S * NVS), dim3(NTHO),
                          0, st, fin);
     else
       hipLaunchKernelGGL((fwd_state<T, BT, D, GW, SP, GK>), dim3(BH * S * GVS),
                          dim3(64 * (GW * GK + SP)), 0, st, fin);
+    // A clip of the state bound somewhere in the segmented passes: the segments'
+    // affine combination does not hold, and the serial scan (the plain pass below)
+    // recomputes everything the final pass wrote; otherwise its workgroups return
+    // at once
+    StateArgs<T> ser{W, UT, KgT, GL, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT, h_final,
+                     nullptr, H, Qg, Aqk, out, scale, T_len, nullptr, nullptr, sat};
+    if (fuse)
+      hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK, NO>), dim3(BH * NVS), dim3(NTHO), 0,
+                         st, ser);
+    else
+      hipLaunchKernelGGL((fwd_state<T, BT, D, SW, SP, SK>), dim3(BH * NVS), dim3(NTH), 0, st,
+                         ser);
   } else {
     StateArgs<T> sa{W, UT, KgT, GL, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT, h_final,
                     nullptr, H, Qg, Aqk, out, scale, T_len, nullptr};

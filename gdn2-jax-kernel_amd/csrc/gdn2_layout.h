@@ -43,11 +43,17 @@ constexpr int kFwdNoARegion = 1 << 24;
 
 // SEG (only with a segmented state scan, S > 1): per (b,h) and segment the end
 // state from h = 0 and the transition M_seg ([bh][S][2][D][D] f32), then the
-// segment entry states ([bh][S][D][D] f32).  It comes last, so the offsets the
-// backward reads do not depend on S.  Without `a_region` the A tiles take no
-// space (SEG moves up accordingly).
+// segment entry states ([bh][S][D][D] f32), then the saturation flag (one int32
+// in a 256-byte slot, the last of the workspace: set when a clip of the state
+// bound in the segmented passes, see seg_flag_offset).  SEG comes last, so the
+// offsets the backward reads do not depend on S.  Without `a_region` the A
+// tiles take no space, without `states` the HT / VnT tiles (the inference scan
+// that forms the outputs itself writes neither); later regions move up.
+inline size_t seg_bytes(size_t seg_units, int D) {
+  return seg_units ? seg_units * 3 * (size_t)D * D * 4 + 256 : 0;
+}
 inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem, size_t seg_units = 0,
-                            bool a_region = true) {
+                            bool a_region = true, bool states = true) {
   FwdLayout L;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
@@ -57,12 +63,16 @@ inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem, size_t s
   L.Qg = take(nchunks * BT * D * elem);
   L.Aqk = take(nchunks * BT * BT * elem);
   L.GL = take(nchunks * D * 4);
-  L.HT = take(nchunks * D * D * elem);
-  L.VnT = take(nchunks * D * BT * elem);
+  L.HT = take(states ? nchunks * D * D * elem : 0);
+  L.VnT = take(states ? nchunks * D * BT * elem : 0);
   L.A = take(a_region ? nchunks * BT * BT * 4 : 0);
-  L.SEG = take(seg_units * 3 * (size_t)D * D * 4);
+  L.SEG = take(seg_bytes(seg_units, D));
   L.total = off;
   return L;
+}
+// Byte offset of the saturation flag inside SEG (S > 1).
+inline size_t seg_flag_offset(size_t seg_units, int D) {
+  return seg_units * 3 * (size_t)D * D * 4;
 }
 
 // A variable-length batch (B = 1, sequences packed along T): sequence s owns

@@ -8,12 +8,17 @@
 // is a host-side stand-in, not a device address, so the device address is looked
 // up once per device with hipGetSymbolAddress (on the entry point's first call
 // on that device, with that device current) and kept per device; every launch
-// uses that address.  Each GPU the library runs on holds its own copy of the
-// array (GDN2_NOALLOC_SCRATCH_BYTES) until the process ends.  Calls on one GPU
-// share its array: calls that overlap on one GPU (different streams, or threads
-// without ordering) race on it and must be serialised by the caller.  Nothing in
-// the array needs to start at zero -- the forward writes every workspace tile
-// before reading it -- so the previous call's contents are harmless.
+// uses that address.  The device is the stream's (the kernels run there), which
+// need not be the caller's current device: the lookup then makes the stream's
+// device current for its duration and restores the caller's.  Each GPU the
+// library runs on holds its own copy of the array (GDN2_NOALLOC_SCRATCH_BYTES,
+// in every process that loads the library, whether or not it calls this entry
+// point) until the process ends.  Calls on one GPU share its array: calls that
+// overlap on one GPU (different streams, or threads without ordering) race on
+// it and must be serialised by the caller.  Nothing in the array needs to start
+// at zero -- the forward writes every workspace tile (and clears the segmented
+// scan's saturation flag) before reading it -- so the previous call's contents
+// are harmless.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -41,14 +46,21 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 // Device address of `scratch` per device, resolved on first use.
 std::atomic<void*> g_scratch[kMaxDevices];
 
-// The current device's scratch address, or nullptr if it cannot be resolved.
-void* scratch_ptr() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+// The scratch address on the device `stream` belongs to (the current device for
+// the null stream), or nullptr if it cannot be resolved.
+void* scratch_ptr(hipStream_t stream) {
+  int cur = 0, dev = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+  dev = cur;
+  if (stream && hipStreamGetDevice(stream, &dev) != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
   void* p = g_scratch[dev].load(std::memory_order_acquire);
   if (!p) {
     // idempotent: concurrent first calls store the same address
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) return nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) hipSetDevice(cur);
+    if (e != hipSuccess || !p) return nullptr;
     g_scratch[dev].store(p, std::memory_order_release);
   }
   return p;
@@ -69,7 +81,7 @@ extern "C" int gdn2_fwd_noalloc(void* stream, int B, int T, int H, int D, int BT
   if (need > kScratchBytes) return GDN2_ERR_SCRATCH;
   // need == 0: invalid shapes, which fwd_entry reports with their own code, or
   // an empty sequence, which launches no kernel that reads the workspace
-  void* ws = need > 0 ? scratch_ptr() : nullptr;
+  void* ws = need > 0 ? scratch_ptr((hipStream_t)stream) : nullptr;
   if (need > 0 && !ws) return GDN2_ERR_LAUNCH;
   return fwd_entry(stream, B, T, H, D, BT, in_dtype, g_dtype, q, k, v, w, b, g, h0, scale, out,
                    h_final, ws, need > 0 ? kScratchBytes : 0, nullptr, flags);

@@ -184,8 +184,9 @@ def _run_forward(p: _Prepared, debug_a: bool = False, flags: int = 0):
     L = _lib.lib()
     if p.partial:
         flags |= _lib.FWD_PARTIAL_CHUNK
-    nbytes = L.gdn2_fwd_workspace_bytes_ex(*p.args[:6], _lib.FWD_PARTIAL_CHUNK if debug_a
-                                           else flags)
+    # the debug path keeps every residual tile: sized as the residual-keeping forward
+    nbytes = L.gdn2_fwd_workspace_bytes_ex(
+        *p.args[:6], (_lib.FWD_PARTIAL_CHUNK | _lib.FWD_SAVE_A) if debug_a else flags)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=p.device)
     out = torch.empty((p.B, p.T, p.H, p.D), dtype=torch.float32, device=p.device)
     h_final = torch.empty((p.B, p.H, p.D, p.D), dtype=torch.float32, device=p.device)

@@ -33,7 +33,7 @@ TRAIN_CHUNK = 64
 
 def _run_backward(p: _Prepared, ws: torch.Tensor, dout, dh_final):
     L = _lib.lib()
-    fbytes = L.gdn2_fwd_workspace_bytes(*p.args[:6])
+    fbytes = ws.numel()   # the residual-keeping forward's workspace (GDN2_FWD_SAVE_A)
     bbytes = L.gdn2_bwd_workspace_bytes(*p.args[:6])
     bws = torch.empty(max(bbytes, 1), dtype=torch.uint8, device=p.device)
     dout = dout.to(device=p.device, dtype=torch.float32).contiguous()

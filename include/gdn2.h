@@ -68,11 +68,13 @@ const char* gdn2_strerror(int code);
  * trace-time assertions gdn2_fwd.py:145-146 and gdn2_bwd.py:348-349. */
 int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype);
 
-/* Bytes of workspace gdn2_fwd needs.  After a call with GDN2_FWD_SAVE_A the
- * workspace holds the per-chunk residuals (WY factors, chunk states, v_new)
- * that gdn2_bwd reads; after an inference call its contents are unspecified
- * (where the state scan forms the outputs itself, the chunk states and v_new
- * never leave the GPU's on-chip memory). */
+/* Bytes of workspace gdn2_fwd needs for an inference call (flags 0).  With
+ * GDN2_FWD_SAVE_A (gdn2_fwd_workspace_bytes_ex) the workspace holds the
+ * per-chunk residuals (WY factors, chunk states, v_new) that gdn2_bwd reads;
+ * after an inference call its contents are unspecified.  Where the state scan
+ * forms the outputs itself (bfloat16 inputs at D = 128 and 256, float32 at
+ * D = 64), the chunk states and v_new never leave the GPU's on-chip memory and
+ * the inference workspace has no room for them. */
 size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype);
 
 /* gdn2_fwd flags. */
@@ -86,8 +88,12 @@ size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
 /* Segments of the state scan (bits 8-15; 0 = automatic).  Long sequences with
  * few (b,h) pairs split the serial chunk recurrence into S segments scanned in
  * parallel and chained by their affine transitions (the sequence-parallel
- * design of the reference's kernel D, gdn2_fwd.py:338-366).  n is clamped to
- * [1, T/BT]; a forced count needs gdn2_fwd_workspace_bytes_ex's workspace. */
+ * design of the reference's kernel D, gdn2_fwd.py:338-366).  The chaining is
+ * exact while the +-1e4 clip of the carried state (gdn2_fwd.py:358) does not
+ * bind; the segmented passes flag any state clip that binds, and a flagged call
+ * reruns the scan serially on the device (no host round trip), so the result
+ * is the serial one either way.  n is clamped to [1, T/BT]; a forced count
+ * needs gdn2_fwd_workspace_bytes_ex's workspace. */
 #define GDN2_FWD_SEGMENTS(n) (((n) & 0xff) << 8)
 /* Accept T % BT != 0: the last chunk of each sequence holds T % BT tokens and
  * is padded inside the kernels with neutral tokens (k = q = 0, g = 0; the state
@@ -114,7 +120,10 @@ int gdn2_fwd(void* stream, int B, int T, int H, int D, int BT, int in_dtype, int
              void* ws, size_t ws_bytes, int flags);
 
 /* Test hook: as gdn2_fwd, and additionally writes A = (I + Akk)^{-1}
- * (kernel B's output, gdn2_fwd.py:246-260) as float32 (B,H,N,BT,BT) to a_out. */
+ * (kernel B's output, gdn2_fwd.py:246-260) as float32 (B,H,N,BT,BT) to a_out.
+ * The workspace keeps every residual tile (h_c and v_new included), so it
+ * takes gdn2_fwd_workspace_bytes_ex(..., GDN2_FWD_SAVE_A) bytes (or
+ * GDN2_FWD_SAVE_A | GDN2_FWD_PARTIAL_CHUNK when T % BT != 0). */
 int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
                    int g_dtype, const void* q, const void* k, const void* v,
                    const void* w, const void* b, const void* g, const float* h0,
@@ -198,9 +207,9 @@ int gdn2_bwd_varlen(void* stream, int num_seqs, const int* cu_chunks, int total_
  * without ws / ws_bytes; flags: GDN2_FWD_RAW_INPUTS, GDN2_FWD_PARTIAL_CHUNK,
  * GDN2_FWD_SEGMENTS(n) -- GDN2_FWD_SAVE_A is GDN2_ERR_FLAGS (the residuals would
  * not survive the next call).  A workload whose inference workspace exceeds the
- * scratch returns GDN2_ERR_SCRATCH before any launch (128 MiB: about 74 k
+ * scratch returns GDN2_ERR_SCRATCH before any launch (128 MiB: about 97 k
  * token-heads B*T*H for bfloat16 inputs at chunk 128 and D = 128, e.g.
- * B = 1, T = 8192, H = 8).
+ * B = 1, T = 8192, H = 11).
  * All calls on one GPU share its scratch: calls that overlap on one GPU (other
  * streams, other threads) race and must be serialised by the caller. */
 #define GDN2_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)

@@ -66,21 +66,34 @@ def test_validate(args, code):
 
 def test_workspace_bytes():
     L = _lib.lib()
-    # layout: 9 per-chunk tensors (the last is A, float32), each region 256-byte aligned
+    # layout: 9 per-chunk tensors W, UT, KgT, Qg, Aqk, GL, HT, VnT, A (float32), each
+    # region 256-byte aligned; the residual-keeping forward (GDN2_FWD_SAVE_A) takes all
     B, T, H, D, BT = 1, 512, 2, 64, 64
     nc = B * H * (T // BT)
     al = lambda x: (x + 255) // 256 * 256
     s = 4
-    exp = sum(al(x) for x in [nc * BT * D * s, nc * D * BT * 4, nc * D * BT * s,
-                              nc * BT * D * s, nc * BT * BT * s, nc * D * 4,
-                              nc * D * D * s, nc * D * BT * s, nc * BT * BT * 4])
-    assert L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, F32) == exp
+    head = [nc * BT * D * s, nc * D * BT * s, nc * D * BT * s, nc * BT * D * s,
+            nc * BT * BT * s, nc * D * 4]
+    states = [nc * D * D * s, nc * D * BT * s]
+    a_tiles = [nc * BT * BT * 4]
+    exp = sum(al(x) for x in head + states + a_tiles)
+    assert L.gdn2_fwd_workspace_bytes_ex(B, T, H, D, BT, F32, _lib.FWD_SAVE_A) == exp
+    # float32 at D = 64: the inference scan forms the outputs itself and writes no
+    # h^T / v_new^T tiles, which then take no space
+    assert L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, F32) == \
+        sum(al(x) for x in head + a_tiles)
+    # float32 at D = 128 has a separate output pass, which reads those tiles
+    nc2, D2 = nc, 128
+    assert L.gdn2_fwd_workspace_bytes(B, T, H, D2, BT, F32) == sum(al(x) for x in [
+        nc2 * BT * D2 * s, nc2 * D2 * BT * s, nc2 * D2 * BT * s, nc2 * BT * D2 * s,
+        nc2 * BT * BT * s, nc2 * D2 * 4, nc2 * D2 * D2 * s, nc2 * D2 * BT * s, nc2 * BT * BT * 4])
     # bfloat16 data with float32 arithmetic keeps float32 tiles
-    assert L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, BF16F32) == exp
+    assert L.gdn2_fwd_workspace_bytes_ex(B, T, H, D, BT, BF16F32, _lib.FWD_SAVE_A) == exp
     assert L.gdn2_bwd_workspace_bytes(B, T, H, D, BT, BF16F32) == \
         L.gdn2_bwd_workspace_bytes(B, T, H, D, BT, F32)
-    assert L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, BF16) < exp
-    assert L.gdn2_fwd_workspace_bytes(1, 1024, 2, 64, 64, F32) > exp
+    assert L.gdn2_fwd_workspace_bytes_ex(B, T, H, D, BT, BF16, _lib.FWD_SAVE_A) < exp
+    assert L.gdn2_fwd_workspace_bytes(1, 1024, 2, 64, 64, F32) > \
+        L.gdn2_fwd_workspace_bytes(B, T, H, D, BT, F32)
     assert L.gdn2_fwd_workspace_bytes(1, 512, 2, 96, 64, F32) == 0
     assert L.gdn2_fwd_workspace_bytes(1, 0, 2, 64, 64, F32) == 0
 
@@ -167,26 +180,26 @@ def test_launch_events_hook_is_host_only():
 
 def test_segment_workspace():
     """Forward workspace with a segmented state scan: S segments add
-    B*H*S*3*D*D floats (end states, transitions, entry states) after the
-    per-chunk tensors.  The automatic choice fills 256 workgroups in the final
-    pass: for config 5 (1 x 131072 x 8 heads, D = 128) with bfloat16 tiles S = 8
-    for inference (the final pass is the 32-column scan with output waves) and
-    S = 16 when the residuals are kept (64-column final pass), S = 8 with
-    float32 tiles (32 columns per workgroup), and none for the headline shape."""
+    B*H*S*3*D*D floats (end states, transitions, entry states) and a 256-byte
+    slot for the saturation flag after the per-chunk tensors.  The automatic
+    choice fills 256 workgroups in the final pass: for config 5 (1 x 131072 x 8
+    heads, D = 128) with bfloat16 tiles S = 8 for inference (the final pass is
+    the 32-column scan with output waves) and S = 16 when the residuals are kept
+    (64-column final pass), S = 8 with float32 tiles (32 columns per
+    workgroup), and none for the headline shape."""
     L = _lib.lib()
     al = lambda x: (x + 255) // 256 * 256
+    seg = lambda units, D: al(units * 3 * D * D * 4 + 256)
     plain = L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 128, BF16, _lib.FWD_SEGMENTS(1))
-    assert L.gdn2_fwd_workspace_bytes(1, 131072, 8, 128, 128, BF16) == \
-        plain + al(8 * 8 * 3 * 128 * 128 * 4)
+    assert L.gdn2_fwd_workspace_bytes(1, 131072, 8, 128, 128, BF16) == plain + seg(8 * 8, 128)
     saved = L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 128, BF16,
                                           _lib.FWD_SEGMENTS(1) | _lib.FWD_SAVE_A)
     assert L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 128, BF16, _lib.FWD_SAVE_A) == \
-        saved + al(8 * 16 * 3 * 128 * 128 * 4)
+        saved + seg(8 * 16, 128)
     plain32 = L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 64, F32, _lib.FWD_SEGMENTS(1))
-    assert L.gdn2_fwd_workspace_bytes(1, 131072, 8, 128, 64, F32) == \
-        plain32 + al(8 * 8 * 3 * 128 * 128 * 4)
+    assert L.gdn2_fwd_workspace_bytes(1, 131072, 8, 128, 64, F32) == plain32 + seg(8 * 8, 128)
     assert L.gdn2_fwd_workspace_bytes_ex(1, 131072, 8, 128, 128, BF16, _lib.FWD_SEGMENTS(3)) == \
-        plain + al(8 * 3 * 3 * 128 * 128 * 4)
+        plain + seg(8 * 3, 128)
     head = L.gdn2_fwd_workspace_bytes(8, 8192, 6, 128, 128, BF16)
     assert head == L.gdn2_fwd_workspace_bytes_ex(8, 8192, 6, 128, 128, BF16, _lib.FWD_SEGMENTS(1))
     # a count above the chunk count is clamped; uneven splits leave no empty segment
@@ -195,10 +208,10 @@ def test_segment_workspace():
     base = L.gdn2_fwd_workspace_bytes_ex(1, 640, 1, 64, 64, F32, _lib.FWD_SEGMENTS(1))
     # N = 10, asked for 4: segments of 3 -> 4 segments (3, 3, 3, 1)
     assert L.gdn2_fwd_workspace_bytes_ex(1, 640, 1, 64, 64, F32, _lib.FWD_SEGMENTS(4)) == \
-        base + al(4 * 3 * 64 * 64 * 4)
+        base + seg(4, 64)
     # N = 10, asked for 6: segments of 2 -> 5 segments
     assert L.gdn2_fwd_workspace_bytes_ex(1, 640, 1, 64, 64, F32, _lib.FWD_SEGMENTS(6)) == \
-        base + al(5 * 3 * 64 * 64 * 4)
+        base + seg(5, 64)
 
 
 def test_decode_rejects_before_launch():
@@ -228,8 +241,9 @@ def test_varlen_rejects_before_launch():
     assert call(2, 2, 100, _lib.FWD_SAVE_A | _lib.FWD_RAW_INPUTS) == _lib.ERR_FLAGS
     assert call(2, 2, 100, cu=None) == _lib.ERR_NULL
     assert call(2, 2, 100, hf=None) == _lib.ERR_NULL
+    # sized for either use (inference, or the residuals of GDN2_FWD_SAVE_A)
     assert L.gdn2_fwd_varlen_workspace_bytes(5, 2, 64, 64, F32) == \
-        L.gdn2_fwd_workspace_bytes(1, 5 * 64, 2, 64, 64, F32)
+        L.gdn2_fwd_workspace_bytes_ex(1, 5 * 64, 2, 64, 64, F32, _lib.FWD_SAVE_A)
 
 
 def test_bwd_varlen_rejects_before_launch():

@@ -347,6 +347,51 @@ def test_segmented_scan_matches_serial_and_oracle(dev, B, T, H, D, dtype, BT, S,
     assert ok_o and ok_h, ("vs oracle", e_o, e_h)
 
 
+@pytest.mark.parametrize("dtype,BT,D,save", [
+    (torch.bfloat16, 128, 128, False), (torch.float32, 64, 128, False),
+    (torch.float32, 64, 64, False), (torch.float32, 64, 128, True),
+])
+def test_segmented_scan_under_saturation(dev, dtype, BT, D, save):
+    """The segments' affine combination holds only while the +-1e4 clip of the
+    carried state (gdn2_fwd.py:358) does not bind.  The segmented passes flag a
+    binding clip in the workspace's last slot; a flagged call reruns the scan
+    serially.  In the domain the flag stays clear (the segmented result is
+    used); on saturating inputs (v x 1e5, slow decay: states reach the clip) it
+    is set, and out, h_final -- and with GDN2_FWD_SAVE_A the residual tiles the
+    backward reads -- equal the serial scan's bit for bit and the oracle's
+    clipped recurrence (oracle.chunked_fwd, clip=True) on the saturation scale."""
+    from gdn2_package import _lib
+    from gdn2_package.gdn2_fwd import _Prepared, _residual_views, _run_forward
+    B, T, H, S = 1, 2048, 2, 4
+    scale = 1.0 if dtype == torch.bfloat16 else 20.0
+    extra = _lib.FWD_SAVE_A if save else 0
+    flag = lambda ws: ws[-256:-252].view(torch.int32).item()
+    for vmul, want in ((1.0, 0), (1e5, 1)):
+        xs = list(O.make_inputs(B, T, H, D, seed=41, g_scale=0.05))
+        xs[2] = xs[2] * vmul
+        xt = to_dev(xs, dev, dtype)
+        p = _Prepared(*xt, scale, None, BT)
+        out_s, hf_s, ws_s, _ = _run_forward(p, flags=_lib.FWD_SEGMENTS(S) | extra)
+        out_1, hf_1, ws_1, _ = _run_forward(p, flags=_lib.FWD_SEGMENTS(1) | extra)
+        assert flag(ws_s) == want, (vmul, flag(ws_s))
+        if want:
+            assert torch.equal(out_s, out_1) and torch.equal(hf_s, hf_1)
+            if save:   # every residual tile the backward reads (Aqk masked as it reads it)
+                rs, r1 = _residual_views(p, ws_s), _residual_views(p, ws_1)
+                for key in rs:
+                    assert torch.equal(rs[key], r1[key]), key
+            ro, rh = O.chunked_fwd(*host(xt), scale, BT=BT, clip=True)
+            assert np.abs(rh).max() == 1e4          # the state clip binds
+            tol = 1e-4 if dtype == torch.float32 else 2e-2
+            ok_o, e_o = close(out_s.cpu().numpy() * 1e-4, ro * 1e-4, tol)
+            ok_h, e_h = close(hf_s.cpu().numpy() * 1e-4, rh * 1e-4, tol)
+            assert ok_o and ok_h, (e_o * 1e4, e_h * 1e4)
+        else:
+            tol = 1e-5 if dtype == torch.float32 else 2e-3
+            assert close(out_s.cpu().numpy(), out_1.cpu().numpy(), tol)[0]
+            assert close(hf_s.cpu().numpy(), hf_1.cpu().numpy(), tol)[0]
+
+
 def test_segmented_scan_is_automatic_for_long_few_heads(dev):
     """One head of 128 chunks picks S = 8 by itself; it matches the forced
     serial pass and the recurrence."""

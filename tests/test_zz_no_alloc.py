@@ -37,14 +37,19 @@ def _inputs(B, T, H, D, dtype, dev, seed):
     return [x.to(dtype).contiguous() for x in t[:5]] + [t[5].contiguous()]
 
 
-@pytest.mark.parametrize("dtype,BT,D", [(torch.bfloat16, 128, 128), (torch.float32, 64, 64)])
-def test_noalloc_matches_gdn2_fwd(dev, dtype, BT, D):
+@pytest.mark.parametrize("dtype,BT,D,segs", [
+    (torch.bfloat16, 128, 128, 0),      # the scan forms the outputs
+    (torch.float32, 64, 64, 0),         # idem, float32
+    (torch.bfloat16, 64, 64, 0),        # a separate output pass (h^T / v_new^T tiles)
+    (torch.bfloat16, 64, 128, 4),       # segmented scan (the SEG region, its flag slot)
+])
+def test_noalloc_matches_gdn2_fwd(dev, dtype, BT, D, segs):
     from gdn2_package import _lib
     L = _lib.lib()
     for (B, T, H), seed in (((2, 1024, 4), 1), ((1, 200, 2), 2)):   # second call smaller
         xs = _inputs(B, T, H, D, dtype, dev, seed)
         h0 = 0.1 * torch.randn((B, H, D, D), device=dev)
-        flags = _lib.FWD_PARTIAL_CHUNK
+        flags = _lib.FWD_PARTIAL_CHUNK | (_lib.FWD_SEGMENTS(segs) if segs else 0)
         rc1, o1, h1 = _run(L, dev, xs, h0, D ** -0.5, BT, dtype, True, flags)
         rc2, o2, h2 = _run(L, dev, xs, h0, D ** -0.5, BT, dtype, False, flags)
         assert rc1 == 0 and rc2 == 0, (rc1, rc2)
