@@ -24,6 +24,9 @@ that calibrates the counters), reduced on any host by ``--traffic-from``:
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d <F> -- python bench.py --pmc-run
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d <W> -- python bench.py --pmc-run
     python bench.py --traffic-from <F> <W>      # writes profiles/traffic_*.json
+
+The float32 training step's traffic (``train.roofline.traffic``) the same way
+over ``--pmc-train-run``, reduced by ``--train-traffic-from <F> <W>``.
 """
 from __future__ import annotations
 
@@ -135,12 +138,19 @@ def roofline(per, ms):
     return roof
 
 
+TRAIN_TRAFFIC = ROOT / "profiles" / "traffic_train_b8t8192h6d128_fp32.json"
+
+
 def train_roofline(tms):
     """configs[3] (float32 fwd+bwd): algorithmic flops per token-head (forward
     5CD + 6D^2 + C^2/3, backward twice that) on the float32 MFMA peak, against
     compulsory bytes (80 D per token-head) on HBM; the larger time is the bound.
-    `frac` uses C = 128 (the published lower bound, 219 GFLOP -> 1.392 ms);
-    `at_chunk_64` the same formula at the chunk this path runs (166 GFLOP)."""
+    `frac` is the published bound's (C = 128: 219 GFLOP -> 1.392 ms) over the
+    step; `executed` the same at the chunk this path runs (C = 64: 166 GFLOP),
+    and `achieved_tflops` is that executed algorithmic work per second.
+    `traffic` is the counter-measured HBM bytes of one step (the sum over its
+    seven launches, profiles/traffic_train_*.json) and `hbm_floor_ms` the time
+    those bytes take at 8 TB/s."""
     th = B * T * H
     nbytes = 80 * D * th
 
@@ -152,8 +162,14 @@ def train_roofline(tms):
                 "lower_bound_ms": lb * 1e3, "frac": lb / (tms * 1e-3)}
 
     r = at(128)
-    r.update({"bytes": nbytes, "achieved_tflops": r["flops"] / (tms * 1e-3) / 1e12,
-              "peak_tflops": FP32_MFMA_PEAK, "at_chunk_64": at(TRAIN_CHUNK)})
+    exe = at(TRAIN_CHUNK)
+    exe["chunk"] = TRAIN_CHUNK
+    r.update({"bytes": nbytes, "peak_tflops": FP32_MFMA_PEAK,
+              "achieved_tflops": exe["flops"] / (tms * 1e-3) / 1e12, "executed": exe,
+              "traffic": None, "hbm_floor_ms": None})
+    if TRAIN_TRAFFIC.exists():
+        tb = json.loads(TRAIN_TRAFFIC.read_text())["bytes_per_step"]
+        r.update({"traffic": tb, "hbm_floor_ms": tb / HBM_PEAK * 1e3})
     return r
 
 
@@ -271,7 +287,10 @@ def train_kernels(gp, xs):
 
 
 def pmc_train_run():
-    """One float32 training step and one headline forward, for MFMA counters."""
+    """Float32 training steps (train_kernels: the forward with residuals and the
+    backward, each twice), one headline forward and, last, the calibration copy
+    of --pmc-run: for the MFMA counters (--mfma-from) and the training step's
+    HBM traffic (FETCH_SIZE / WRITE_SIZE runs, --train-traffic-from)."""
     import torch
     import gdn2_package as gp
     xs = make_inputs(torch.float32)
@@ -279,7 +298,46 @@ def pmc_train_run():
     del xs
     xb = make_inputs(torch.bfloat16)
     gp.gdn2_pallas_forward(*xb, D ** -0.5, chunk_size=CHUNK)
+    del xb
+    src = torch.ones(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.abs(src, out=dst)             # one elementwise kernel: reads and writes 1 GiB
     torch.cuda.synchronize()
+    print(json.dumps({"pmc_train_run": 1, "copy_bytes": COPY_BYTES}), flush=True)
+
+
+TRAIN_KERNELS = ("fwd_prep", "fwd_state", "fwd_out", "bwd_b2", "bwd_state", "bwd_wy",
+                 "gram_bwd")
+
+
+def train_traffic_from(fetch_dir, write_dir):
+    """Copy-calibrated HBM bytes of each float32 training kernel (chunk 64) from
+    the FETCH_SIZE and WRITE_SIZE runs of --pmc-train-run, their sum per step
+    against the step's algorithmic bytes, written to profiles/traffic_train_*."""
+    fetch, f_copy = _counter_means(fetch_dir, "FETCH_SIZE")
+    write, w_copy = _counter_means(write_dir, "WRITE_SIZE")
+    f_scale = COPY_BYTES / (f_copy * 1024)
+    w_scale = COPY_BYTES / (w_copy * 1024)
+    bf16 = lambda n: "DF16b" in n or "__bf16" in n or "bfloat16" in n
+    rows = {}
+    for k in TRAIN_KERNELS:
+        names = [n for n in fetch if k in n and "gdn2" in n and not bf16(n)
+                 and not (k == "fwd_state" and "seg_" in n)]
+        if len(names) != 1:
+            raise SystemExit(f"{k}: expected one float32 kernel, found {names}")
+        n = names[0]
+        rows[k] = {"fetch_bytes": fetch[n] * 1024 * f_scale,
+                   "write_bytes": write[n] * 1024 * w_scale}
+        rows[k]["bytes"] = rows[k]["fetch_bytes"] + rows[k]["write_bytes"]
+    total = sum(r["bytes"] for r in rows.values())
+    rec = {"workload": "B8 T8192 H6 D128 float32 training step (forward with residuals + "
+                       f"backward), chunk {TRAIN_CHUNK}",
+           "kernels": rows, "bytes_per_step": total,
+           "compulsory_bytes": 80 * D * B * T * H,
+           "fetch_scale": f_scale, "write_scale": w_scale,
+           "calibration": f"copy kernel reading and writing {COPY_BYTES} bytes"}
+    TRAIN_TRAFFIC.write_text(json.dumps(rec, indent=1) + "\n")
+    print(json.dumps(rec, indent=1))
 
 
 def mfma_from(run_dir):
@@ -603,9 +661,14 @@ def main():
                     help="one float32 training step and one headline forward, for MFMA counters")
     ap.add_argument("--mfma-from", metavar="DIR",
                     help="reduce a --pmc-train-run MFMA counter run (per-kernel flops, utilisation)")
+    ap.add_argument("--train-traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="reduce two --pmc-train-run counter runs to profiles/traffic_train_*")
     args = ap.parse_args()
     if args.mfma_from:
         mfma_from(args.mfma_from)
+        return
+    if args.train_traffic_from:
+        train_traffic_from(*args.train_traffic_from)
         return
     if args.pmc_train_run:
         pmc_train_run()
@@ -638,7 +701,7 @@ def main():
 
     del xs
     torch.cuda.empty_cache()
-    train = None
+    train, failed = None, None
     if not args.no_train:
         try:
             xs32 = make_inputs(torch.float32)
@@ -651,8 +714,9 @@ def main():
                      "ms_per_step": tms, "tokens_per_s": tokens / (tms * 1e-3),
                      "kernels_ms": kms, "mfma": mfma, "roofline": train_roofline(tms)}
             del xs32
-        except Exception as e:  # backward entry point not available in this build
-            train = {"error": f"{type(e).__name__}: {e}"[:200]}
+        except Exception as e:   # reported in the line, and the run fails
+            failed = f"{type(e).__name__}: {e}"[:300]
+            train = {"error": failed}
 
     line = {
         "metric": "fwd & fwd+bwd ms, tokens/s at B8 T8192 H6 D128; % MFMA/HBM roofline",
@@ -676,6 +740,9 @@ def main():
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
+    if failed:
+        print(f"bench.py: the training step failed: {failed}", file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

@@ -1423,25 +1423,26 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
     f32x4 aq = {0.f, 0.f, 0.f, 0.f}, ab = {0.f, 0.f, 0.f, 0.f};
     cq[dt] = cb[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float F = 1.f;
-    for (int J = I - 1; J >= 0; --J) {
+    // J from I-1 down: first the blocks of I's own sub-block, then (rows of S1) S0's
+    auto rowpair = [&](int J, f32x4& sq, f32x4& sb) __attribute__((always_inline)) {
       f32x4 y, tq = {0.f, 0.f, 0.f, 0.f}, tk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) y[e] = sKH[(J * 16 + 4 * lg + e) * LD1 + dcol];
       mma(tq, load4f(&sDQK[(I * 16 + li) * LD2 + J * 16 + 4 * lg]), y);
       mma(tk, load4f(&sDKK[(I * 16 + li) * LD2 + J * 16 + 4 * lg]), y);
-      if (rowx && J < SB) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) { cq[dt][r] += F * tq[r]; cb[dt][r] += F * tk[r]; }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) { aq[r] += F * tq[r]; ab[r] += F * tk[r]; }
-      }
+      for (int r = 0; r < 4; ++r) { sq[r] += F * tq[r]; sb[r] += F * tk[r]; }
       F *= sETot[J * GP + dcol];
+    };
+    for (int J = I - 1; J >= (rowx ? SB : 0); --J) rowpair(J, aq, ab);
+    if (rowx) {
+      for (int J = SB - 1; J >= 0; --J) rowpair(J, cq[dt], cb[dt]);
     }
-    // rows of block I (as the column block) against I' > I
+    // rows of block I (as the column block) against I' > I: first I's own
+    // sub-block, then (columns of S0) S1's
     f32x4 akk = {0.f, 0.f, 0.f, 0.f};
     F = 1.f;
-    for (int Ip = I + 1; Ip < NB; ++Ip) {
+    auto colpair = [&](int Ip, f32x4& sk) __attribute__((always_inline)) {
       f32x4 xq, xk, yq, yk, t1 = {0.f, 0.f, 0.f, 0.f}, t2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -1453,14 +1454,13 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       }
       mma(t1, xq, yq);
       mma(t2, xk, yk);
-      if (!rowx && Ip >= SB) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) cq[dt][r] += F * (a.scale * t1[r] + t2[r]);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) akk[r] += F * (a.scale * t1[r] + t2[r]);
-      }
+      for (int r = 0; r < 4; ++r) sk[r] += F * (a.scale * t1[r] + t2[r]);
       F *= sETot[Ip * GP + dcol];
+    };
+    for (int Ip = I + 1; Ip < (rowx ? NB : SB); ++Ip) colpair(Ip, akk);
+    if (!rowx) {
+      for (int Ip = SB; Ip < NB; ++Ip) colpair(Ip, cq[dt]);
     }
     lds_barrier();  // every wave is done with channel slice dt of sAQ, sABK, sKH, sETot
 #pragma unroll
@@ -1482,7 +1482,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
     for (int r = 0; r < 4; ++r) {
       const int o = (I * 16 + 4 * lg + r) * LD1 + dt * 16 + li;
       sXQ[o] = cq[dt][r];
-      sXB[o] = cb[dt][r];
+      if (rowx) sXB[o] = cb[dt][r];
     }
 
   // ---- chain rule, lane = token t of block I, channels chan(x) -----------------
@@ -1497,7 +1497,8 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
     const f32x4 dqg = pdqg[j], dkg = pdkg[j], dkbd = pdkbd[j];
     const f32x4 rq = load4f(&sAQ[t * LD1 + c0]), rbk = load4f(&sABK[t * LD1 + c0]),
                 rk = load4f(&sKH[t * LD1 + c0]), lm = load4f(&sLm[I * GP + c0]);
-    const f32x4 xrq = load4f(&sXQ[t * LD1 + c0]), xrb = load4f(&sXB[t * LD1 + c0]);
+    const f32x4 xrq = load4f(&sXQ[t * LD1 + c0]);
+    const f32x4 xrb = rowx ? load4f(&sXB[t * LD1 + c0]) : f32x4{0.f, 0.f, 0.f, 0.f};
     // channel c0 + e is x = 4j + e of the start's registers
     const float* const lc = &loc[4 * j];
     const float* const xq = &qv[4 * j];
