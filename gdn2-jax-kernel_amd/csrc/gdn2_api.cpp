@@ -57,8 +57,10 @@ static int check_opt(std::initializer_list<const void*> ps) {
   return GDN2_OK;
 }
 
-// Chunks per sequence, a short last chunk included.
-static int chunks_per_seq(int T, int BT) { return BT > 0 ? (T + BT - 1) / BT : 0; }
+// Chunks per sequence, a short last chunk included (64-bit sum: T may be INT_MAX).
+static int chunks_per_seq(int T, int BT) {
+  return BT > 0 ? (int)(((long long)T + BT - 1) / BT) : 0;
+}
 static size_t nchunks(int B, int T, int H, int BT) {
   return (size_t)B * H * (size_t)chunks_per_seq(T, BT);
 }
@@ -207,6 +209,9 @@ int gdn2_validate(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype)
   if (BT == 128 && (in_dtype != GDN2_BF16 || D == 256)) return GDN2_ERR_CHUNK;
   if (T % BT != 0) return GDN2_ERR_SEQ_LEN;
   if ((double)B * T * H * D > 9.0e15) return GDN2_ERR_SHAPE;
+  // launch grids: up to 8 workgroups per chunk (or per (b,h) and 16 columns of
+  // the state), counted in 31 bits
+  if ((double)B * H * ((double)T / BT + 1.0) * (D / 16) > 2147483647.0) return GDN2_ERR_SHAPE;
   return GDN2_OK;
 }
 
@@ -334,7 +339,8 @@ int gdn2_bwd_varlen(void* stream, int num_seqs, const int* cu_chunks, int total_
                     void* dv, void* dw, void* db, void* dg, float* dh0, const void* fwd_ws,
                     size_t fwd_ws_bytes, void* ws, size_t ws_bytes) {
   EventScope scope;
-  if (num_seqs < 1 || total_chunks < 0 || (double)total_chunks * BT > 2.0e9)
+  if (num_seqs < 1 || total_chunks < 0 || (double)total_chunks * BT > 2.0e9 ||
+      (double)num_seqs * H * (D / 16) > 2147483647.0)
     return GDN2_ERR_SHAPE;
   const int T = total_chunks * BT;
   int rc = gdn2_validate(1, T, H, D, BT, in_dtype, g_dtype);
@@ -367,10 +373,11 @@ int gdn2_fwd_varlen(void* stream, int num_seqs, const int* cu_chunks, const int*
                     const void* g, const float* h0, float scale, float* out, float* h_final,
                     void* ws, size_t ws_bytes, int flags) {
   EventScope scope;
-  if (num_seqs < 1 || total_chunks < 0 || T < 0 || T > total_chunks * (long long)BT)
+  if (num_seqs < 1 || total_chunks < 0 || T < 0 || T > total_chunks * (long long)BT ||
+      (double)total_chunks * BT > 2.0e9 || (double)num_seqs * H * (D / 16) > 2147483647.0)
     return GDN2_ERR_SHAPE;
   if (T < total_chunks) return GDN2_ERR_SEQ_LEN;  // every chunk holds at least one token
-  int rc = gdn2_validate(1, 0, H, D, BT, in_dtype, g_dtype);
+  int rc = gdn2_validate(1, BT > 0 ? total_chunks * BT : 0, H, D, BT, in_dtype, g_dtype);
   if (rc) return rc;
   if ((flags & GDN2_FWD_SAVE_A) && (flags & GDN2_FWD_RAW_INPUTS)) return GDN2_ERR_FLAGS;
   if (T > 0 && (rc = check_ptrs({q, k, v, w, b, g, out}))) return rc;

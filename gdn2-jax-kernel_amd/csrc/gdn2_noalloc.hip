@@ -59,7 +59,7 @@ void* scratch_ptr(hipStream_t stream) {
     // idempotent: concurrent first calls store the same address
     if (dev != cur && hipSetDevice(dev) != hipSuccess) return nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (dev != cur) hipSetDevice(cur);
+    if (dev != cur) (void)hipSetDevice(cur);
     if (e != hipSuccess || !p) return nullptr;
     g_scratch[dev].store(p, std::memory_order_release);
   }

@@ -11,8 +11,9 @@ is no CPU fallback: without the library every call raises.
 
 Chunk size.  ``BT`` below plays the role of gdn2_fwd.py:29 but is read at call
 time, so overriding it also reaches the backward (the reference binds it by
-value at import, gdn2_bwd.py:23).  ``None`` picks 128 for bfloat16 inputs and
-64 for float32; 64 and 128 are accepted (128 only with bfloat16 inputs).
+value at import, gdn2_bwd.py:23).  ``None`` picks 128 for bfloat16 inputs at
+D = 64 and 64 otherwise (see ``chunk_size_for``); 64 and 128 are accepted (128
+only with bfloat16 inputs at D <= 128), the reference's 256 is refused.
 Results do not depend on the chunk size beyond rounding.
 """
 from __future__ import annotations

@@ -53,7 +53,8 @@ extern "C" {
 #define GDN2_ERR_NULL         -5  /* required pointer is NULL */
 #define GDN2_ERR_ALIGN        -6  /* pointer not 16-byte aligned */
 #define GDN2_ERR_WORKSPACE    -7  /* workspace smaller than *_workspace_bytes() */
-#define GDN2_ERR_SHAPE        -8  /* B<1, H<1, T<0, or sizes overflow */
+#define GDN2_ERR_SHAPE        -8  /* B<1, H<1, T<0, or sizes overflow (elements,
+                                     or workgroups of a launch past 2^31) */
 #define GDN2_ERR_LAUNCH       -9  /* HIP launch failure */
 #define GDN2_ERR_FLAGS       -10  /* invalid flag combination */
 #define GDN2_ERR_SCRATCH     -11  /* gdn2_fwd_noalloc: workload needs more than its scratch */

@@ -35,6 +35,54 @@ def test_shape_errors_are_assertion_errors(shape):
         gp.gdn2_pallas_forward(*_inputs(shape), 0.1)
 
 
+def test_clip_override_is_refused(monkeypatch):
+    """The kernels clip stage outputs at the reference's 1e4 (gdn2_fwd.py:33); a
+    changed module constant CLIP (the reference README's fwd.CLIP = 1e3) raises
+    before anything runs, rather than being ignored."""
+    import gdn2_package as gp
+    from gdn2_package import gdn2_fwd
+    monkeypatch.setattr(gdn2_fwd, "CLIP", 1e3)
+    with pytest.raises(gp.GDN2Error, match="CLIP"):
+        gp.gdn2_pallas_forward(*_inputs((1, 128, 2, 64)), 0.1)
+    with pytest.raises(gp.GDN2Error, match="CLIP"):
+        gp.gdn2_pallas_forward_trainable(*_inputs((1, 128, 2, 64)), 0.1)
+
+
+@pytest.mark.parametrize("how", ["module", "argument"])
+def test_chunk_256_is_refused(monkeypatch, how):
+    """The reference's default BT = 256 (gdn2_fwd.py:29) does not fit a gfx950
+    workgroup (its 256 x 256 float32 inverse alone is 256 KB of LDS): set as the
+    module constant (the reference README's fwd.BT = ...) or passed as
+    chunk_size it raises the package's shape error (an AssertionError, as the
+    reference's trace-time asserts) naming the supported sizes."""
+    import gdn2_package as gp
+    from gdn2_package import gdn2_fwd
+    kw = {}
+    if how == "module":
+        monkeypatch.setattr(gdn2_fwd, "BT", 256)
+    else:
+        kw["chunk_size"] = 256
+    with pytest.raises(AssertionError, match="chunk size 256"):
+        gp.gdn2_pallas_forward(*_inputs((1, 512, 2, 64)), 0.1, **kw)
+
+
+def test_chunk_size_choice():
+    """None picks 128 for bfloat16 inputs at D = 64 and 64 otherwise; the
+    module constant BT, when set, wins over that choice (64 and 128 accepted)."""
+    from gdn2_package import gdn2_fwd
+    assert gdn2_fwd.chunk_size_for(torch.bfloat16, None, 64) == 128
+    assert gdn2_fwd.chunk_size_for(torch.bfloat16, None, 128) == 64
+    assert gdn2_fwd.chunk_size_for(torch.bfloat16, None, 256) == 64
+    assert gdn2_fwd.chunk_size_for(torch.float32, None, 64) == 64
+    assert gdn2_fwd.chunk_size_for(torch.bfloat16, 128, 128) == 128
+    old = gdn2_fwd.BT
+    try:
+        gdn2_fwd.BT = 128
+        assert gdn2_fwd.chunk_size_for(torch.bfloat16, None, 128) == 128
+    finally:
+        gdn2_fwd.BT = old
+
+
 def test_mismatched_input_shapes_rejected():
     import gdn2_package as gp
     xs = _inputs((1, 128, 2, 64))

@@ -21,8 +21,11 @@ def test_chunk_table_clamps_stay_in_bounds(tmp_path):
     if gxx is None:
         pytest.skip("g++ not available")
     exe = tmp_path / "clamp_check"
-    subprocess.run([gxx, "-std=c++17", "-O1", "-Wall", "-Werror",
+    # under AddressSanitizer and UndefinedBehaviorSanitizer: an out-of-range index
+    # or an overflowing clamp computation aborts the run
+    subprocess.run([gxx, "-std=c++17", "-O1", "-g", "-Wall", "-Werror",
+                    "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
                     f"-I{ROOT / 'gdn2-jax-kernel_amd' / 'csrc'}",
                     str(ROOT / "tests" / "clamp_check.cpp"), "-o", str(exe)], check=True)
-    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert res.returncode == 0 and res.stdout.startswith("ok"), res.stdout + res.stderr
