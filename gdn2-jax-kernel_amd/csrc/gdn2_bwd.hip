@@ -1416,60 +1416,70 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
   constexpr int SB = NB / 2;   // row blocks per sub-block
   const bool rowx = I >= SB;   // this block's rows have a (S1,S0) part, its columns none
   f32x4 cq[NDT], cb[NDT];      // (S1,S0) row sums of block I in S1; ck in cq for S0
+  // Compiled once per row block (the wave's block is fixed), so every pair loop
+  // has constant bounds, unrolls, and picks its accumulator at compile time.
+  auto offdiag = [&](auto Ic) __attribute__((always_inline)) {
+    constexpr int IC = decltype(Ic)::value;
+    constexpr bool RX = IC >= SB;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
-    const int dcol = dt * 16 + li;
-    // rows of block I against J < I
-    f32x4 aq = {0.f, 0.f, 0.f, 0.f}, ab = {0.f, 0.f, 0.f, 0.f};
-    cq[dt] = cb[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float F = 1.f;
-    // J from I-1 down: first the blocks of I's own sub-block, then (rows of S1) S0's
-    auto rowpair = [&](int J, f32x4& sq, f32x4& sb) __attribute__((always_inline)) {
-      f32x4 y, tq = {0.f, 0.f, 0.f, 0.f}, tk = {0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < NDT; ++dt) {
+      const int dcol = dt * 16 + li;
+      // rows of block IC against J < IC (J from IC-1 down): the blocks of IC's own
+      // sub-block, then (rows of S1) those of S0
+      f32x4 aq = {0.f, 0.f, 0.f, 0.f}, ab = {0.f, 0.f, 0.f, 0.f};
+      cq[dt] = cb[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      float F = 1.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = sKH[(J * 16 + 4 * lg + e) * LD1 + dcol];
-      mma(tq, load4f(&sDQK[(I * 16 + li) * LD2 + J * 16 + 4 * lg]), y);
-      mma(tk, load4f(&sDKK[(I * 16 + li) * LD2 + J * 16 + 4 * lg]), y);
+      for (int J = IC - 1; J >= 0; --J) {
+        f32x4 y, tq = {0.f, 0.f, 0.f, 0.f}, tk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) { sq[r] += F * tq[r]; sb[r] += F * tk[r]; }
-      F *= sETot[J * GP + dcol];
-    };
-    for (int J = I - 1; J >= (rowx ? SB : 0); --J) rowpair(J, aq, ab);
-    if (rowx) {
-      for (int J = SB - 1; J >= 0; --J) rowpair(J, cq[dt], cb[dt]);
-    }
-    // rows of block I (as the column block) against I' > I: first I's own
-    // sub-block, then (columns of S0) S1's
-    f32x4 akk = {0.f, 0.f, 0.f, 0.f};
-    F = 1.f;
-    auto colpair = [&](int Ip, f32x4& sk) __attribute__((always_inline)) {
-      f32x4 xq, xk, yq, yk, t1 = {0.f, 0.f, 0.f, 0.f}, t2 = {0.f, 0.f, 0.f, 0.f};
+        for (int e = 0; e < 4; ++e) y[e] = sKH[(J * 16 + 4 * lg + e) * LD1 + dcol];
+        mma(tq, load4f(&sDQK[(IC * 16 + li) * LD2 + J * 16 + 4 * lg]), y);
+        mma(tk, load4f(&sDKK[(IC * 16 + li) * LD2 + J * 16 + 4 * lg]), y);
+        f32x4& sq = (RX && J < SB) ? cq[dt] : aq;
+        f32x4& sb = (RX && J < SB) ? cb[dt] : ab;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = Ip * 16 + 4 * lg + e;
-        xq[e] = sDQK[i * LD2 + I * 16 + li];
-        xk[e] = sDKK[i * LD2 + I * 16 + li];
-        yq[e] = sAQ[i * LD1 + dcol];
-        yk[e] = sABK[i * LD1 + dcol];
+        for (int r = 0; r < 4; ++r) { sq[r] += F * tq[r]; sb[r] += F * tk[r]; }
+        if (J > 0) F *= sETot[J * GP + dcol];
       }
-      mma(t1, xq, yq);
-      mma(t2, xk, yk);
+      // rows of block IC (as the column block) against I' > IC: IC's own
+      // sub-block, then (columns of S0) S1's
+      f32x4 akk = {0.f, 0.f, 0.f, 0.f};
+      F = 1.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sk[r] += F * (a.scale * t1[r] + t2[r]);
-      F *= sETot[Ip * GP + dcol];
-    };
-    for (int Ip = I + 1; Ip < (rowx ? NB : SB); ++Ip) colpair(Ip, akk);
-    if (!rowx) {
-      for (int Ip = SB; Ip < NB; ++Ip) colpair(Ip, cq[dt]);
-    }
-    lds_barrier();  // every wave is done with channel slice dt of sAQ, sABK, sKH, sETot
+      for (int Ip = IC + 1; Ip < NB; ++Ip) {
+        f32x4 xq, xk, yq, yk, t1 = {0.f, 0.f, 0.f, 0.f}, t2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int o = (I * 16 + 4 * lg + r) * LD1 + dcol;
-      sAQ[o] = aq[r];
-      sABK[o] = ab[r];
-      sKH[o] = akk[r];
+        for (int e = 0; e < 4; ++e) {
+          const int i = Ip * 16 + 4 * lg + e;
+          xq[e] = sDQK[i * LD2 + IC * 16 + li];
+          xk[e] = sDKK[i * LD2 + IC * 16 + li];
+          yq[e] = sAQ[i * LD1 + dcol];
+          yk[e] = sABK[i * LD1 + dcol];
+        }
+        mma(t1, xq, yq);
+        mma(t2, xk, yk);
+        f32x4& sk = (!RX && Ip >= SB) ? cq[dt] : akk;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sk[r] += F * (a.scale * t1[r] + t2[r]);
+        if (Ip + 1 < NB) F *= sETot[Ip * GP + dcol];
+      }
+      lds_barrier();  // every wave is done with channel slice dt of sAQ, sABK, sKH, sETot
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = (IC * 16 + 4 * lg + r) * LD1 + dcol;
+        sAQ[o] = aq[r];
+        sABK[o] = ab[r];
+        sKH[o] = akk[r];
+      }
     }
+  };
+  static_assert(NB == 4, "one specialisation per row block");
+  switch (I) {   // wave-uniform
+    case 0: offdiag(std::integral_constant<int, 0>{}); break;
+    case 1: offdiag(std::integral_constant<int, 1>{}); break;
+    case 2: offdiag(std::integral_constant<int, 2>{}); break;
+    default: offdiag(std::integral_constant<int, 3>{}); break;
   }
   // The score-gradient tiles are no longer read (the last barrier above): the
   // cross sums go into their space, in the same [token][channel] layout, rows of
@@ -1528,38 +1538,64 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       xgq[e] = (rowx ? a.scale * el : ek) * xrq[e];
       xgb[e] = el * xrb[e];
     }
+    // B4's accumulators in the pair order of gdn2_bwd.py:287-328, each clipped
+    // after its pair: rows of S1 take (S1,S0) then (S1,S1); columns of S0 take
+    // (S0,S0) then (S1,S0); dgc takes a pair's row terms, then its column terms.
+    // Those intermediate clips change nothing unless a partial sum reaches the
+    // clip: a wave whose partial sums all stay inside (the input domain) takes the
+    // totals directly.
+    f32x4 aq4, ab4, ak4, ag4;
+    bool inside = true;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float bk = xb[e] * xk[e];
+      const float tq = rowx ? gq[e] + xgq[e] : gq[e];
+      const float tb = rowx ? gbk[e] + xgb[e] : gbk[e];
+      const float tk = rowx ? gk[e] : gk[e] + xgq[e];
+      const float gi = xq[e] * tq + bk * tb;           // all row terms of dgc
+      const float in = !rowx ? gi : xq[e] * xgq[e] + bk * xgb[e];
+      const float p1 = rowx ? xgq[e] : gk[e] + xgq[e], p2 = rowx ? xgb[e] : gi - xk[e] * gk[e];
+      inside = inside && fabsf(p1) <= kClip && fabsf(p2) <= kClip && fabsf(in) <= kClip &&
+               fabsf(gi) <= kClip && fabsf(tb) <= kClip && fabsf(gk[e]) <= kClip;
+      aq4[e] = tq;
+      ab4[e] = tb;
+      ak4[e] = tk;
+      ag4[e] = gi - xk[e] * tk;
+    }
+    if (__ballot(!inside) != 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float bk = xb[e] * xk[e];
+        if (rowx) {
+          aq4[e] = sanitize(sanitize(xgq[e]) + gq[e]);
+          ab4[e] = sanitize(sanitize(xgb[e]) + gbk[e]);
+          ak4[e] = sanitize(gk[e]);
+          const float gi0 = xq[e] * xgq[e] + bk * xgb[e];
+          const float gi1 = xq[e] * gq[e] + bk * gbk[e];
+          ag4[e] = sanitize(sanitize(sanitize(gi0) + gi1) - xk[e] * gk[e]);
+        } else {
+          aq4[e] = sanitize(gq[e]);
+          ab4[e] = sanitize(gbk[e]);
+          ak4[e] = sanitize(sanitize(gk[e]) + xgq[e]);
+          const float gi0 = xq[e] * gq[e] + bk * gbk[e];
+          ag4[e] = sanitize(sanitize(sanitize(gi0) - xk[e] * gk[e]) - xk[e] * xgq[e]);
+        }
+      }
+    }
     f32x4 odq, odk, odb, suf;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float gc = pre[e] + lc[e];
       const float eg = __expf(gc), ekg = __expf(gl[e] - gc);
       const float kgv = xk[e] * ekg;
-      // B4's accumulators in the pair order of gdn2_bwd.py:287-328, each clipped
-      // after its pair: rows of S1 take (S1,S0) then (S1,S1); columns of S0 take
-      // (S0,S0) then (S1,S0); dgc takes a pair's row terms, then its column terms
-      float aq4, ab4, ak4, ag4;
-      if (rowx) {
-        aq4 = sanitize(sanitize(xgq[e]) + gq[e]);
-        ab4 = sanitize(sanitize(xgb[e]) + gbk[e]);
-        ak4 = sanitize(gk[e]);
-        const float gi0 = xq[e] * xgq[e] + xb[e] * xk[e] * xgb[e];
-        const float gi1 = xq[e] * gq[e] + xb[e] * xk[e] * gbk[e];
-        ag4 = sanitize(sanitize(sanitize(gi0) + gi1) - xk[e] * gk[e]);
-      } else {
-        aq4 = sanitize(gq[e]);
-        ab4 = sanitize(gbk[e]);
-        ak4 = sanitize(sanitize(gk[e]) + xgq[e]);
-        const float gi0 = xq[e] * gq[e] + xb[e] * xk[e] * gbk[e];
-        ag4 = sanitize(sanitize(sanitize(gi0) - xk[e] * gk[e]) - xk[e] * xgq[e]);
-      }
       // B3's and B4's outputs are sanitized as each kernel's output, then their
       // sum (gdn2_bwd.py:212-218, 330-339; gdn2_pipeline.py:121-133)
-      odq[e] = sanitize(sanitize(dqg[e] * eg) + aq4);
+      odq[e] = sanitize(sanitize(dqg[e] * eg) + sanitize(aq4[e]));
       odk[e] = sanitize(sanitize(dkbd[e] * xb[e] * eg + dkg[e] * ekg) +
-                        sanitize(ak4 + ab4 * xb[e]));
-      odb[e] = sanitize(sanitize(dkbd[e] * xk[e] * eg) + sanitize(ab4 * xk[e]));
+                        sanitize(ak4[e] + ab4[e] * xb[e]));
+      odb[e] = sanitize(sanitize(dkbd[e] * xk[e] * eg) + sanitize(ab4[e] * xk[e]));
       const float dgc3 = dkbd[e] * xb[e] * xk[e] * eg + dqg[e] * xq[e] * eg - dkg[e] * kgv;
-      const float dgc4 = ag4;
+      const float dgc4 = ag4[e];
       // the last token's B3 part still lacks the g_last terms: kept for the end
       if (I == NB - 1 && li == 15) sB3L[c0 + e] = dgc3;
       suf[e] = row_suffix16(sanitize(dgc3) + sanitize(dgc4));
