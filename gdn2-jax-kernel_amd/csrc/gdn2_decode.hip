@@ -6,18 +6,28 @@
 // are sanitized like every chunk state and output, gdn2_fwd.py:355-356).  The
 // state layout is h0 / h_final's: S[b][h][dk][dv] (gdn2_fwd.py:342).
 //
-// One 256-thread workgroup per (b,h) and slice of 32 state columns (B H D / 32
+// One 256-thread workgroup per (b,h) and slice of 16 state columns (B H D / 16
 // workgroups: enough to spread one decode step over the chip): thread (column
-// e, row group rg) keeps D / 8 state rows of column e in registers.  Both
-// column reductions (pred and o) run over the rows, so the columns split
-// freely; they are summed over the 8 row groups in LDS.  The state is read and
-// written once (memory-bound); h_out may alias h_in.
+// quad c4, row group rg) keeps D / 64 state rows of four columns in registers,
+// read and written with 16-byte accesses.  Both column reductions (pred and o)
+// run over the rows, so the columns split freely; they are summed over the row
+// groups of a wave by lane shuffles, then over the four waves in LDS.  The state
+// is read and written once (memory-bound); h_out may alias h_in.
 #include "gdn2_common.h"
 
 namespace gdn2 {
 
 template <int D>
-constexpr int decode_cols() { return 32; }
+constexpr int decode_cols() { return 16; }
+
+// Sum of x over the lanes of a wave that hold the same column quad (lane & 3).
+__device__ __forceinline__ f32x4 rowgroup_sum(f32x4 x) {
+#pragma unroll
+  for (int m = 4; m < 64; m *= 2)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) x[c] += __shfl_xor(x[c], m);
+  return x;
+}
 
 template <typename T, typename TG, int D>
 __global__ void __launch_bounds__(256) decode_step(const T* q, const T* k, const T* v,
@@ -25,13 +35,25 @@ __global__ void __launch_bounds__(256) decode_step(const T* q, const T* k, const
                                                    float scale, const float* h_in,
                                                    float* h_out, float* out) {
   constexpr int CS = decode_cols<D>(), NSL = D / CS;
-  constexpr int RG = 256 / CS, RPT = D / RG;   // row groups, rows per thread
+  constexpr int C4 = CS / 4, RG = 256 / C4, RPT = D / RG;   // row groups, rows per thread
+  static_assert(RPT >= 1 && D % RG == 0, "rows must split over the row groups");
   __shared__ float sQ[D], sK[D], sBK[D], sEG[D];
-  __shared__ float sRed[RG][CS];
-  const int tid = threadIdx.x, e = tid % CS, rg = tid / CS;
+  __shared__ f32x4 sRed[4][C4];   // per wave and column quad
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c4 = tid % C4, rg = tid / C4;
   const size_t bh = blockIdx.x / NSL;
-  const int col = (blockIdx.x % NSL) * CS + e;
+  const int col = (blockIdx.x % NSL) * CS + 4 * c4;   // first of this thread's four columns
   const size_t vo = bh * D;                  // token vectors are (B,H,D) contiguous
+  // the state rows and this thread's w, v first: their loads are in flight while
+  // the token vectors are gathered into LDS (the step is latency-bound)
+  const float* src = h_in ? h_in + bh * D * D : nullptr;
+  f32x4 s[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
+    s[i] = src ? load4f(src + (size_t)(rg * RPT + i) * D + col) : f32x4{0.f, 0.f, 0.f, 0.f};
+  float wv4[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) wv4[c] = to_f(w[vo + col + c]) * to_f(v[vo + col + c]);
   for (int i = tid; i < D; i += 256) {
     const float kv = to_f(k[vo + i]);
     sQ[i] = to_f(q[vo + i]);
@@ -40,38 +62,43 @@ __global__ void __launch_bounds__(256) decode_step(const T* q, const T* k, const
     sEG[i] = __expf(to_f(g[vo + i]));
   }
   __syncthreads();
-  const float* src = h_in ? h_in + bh * D * D : nullptr;
-  float s[RPT];
-  float pred = 0.f;
+  f32x4 pred = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
     const int d = rg * RPT + i;
-    s[i] = (src ? sanitize(src[(size_t)d * D + col]) : 0.f) * sEG[d];
-    pred += sBK[d] * s[i];
-  }
-  sRed[rg][e] = pred;
-  __syncthreads();
-  pred = 0.f;
 #pragma unroll
-  for (int r = 0; r < RG; ++r) pred += sRed[r][e];
-  const float delta = to_f(w[vo + col]) * to_f(v[vo + col]) - pred;
+    for (int c = 0; c < 4; ++c) {
+      s[i][c] = sanitize(s[i][c]) * sEG[d];
+      pred[c] += sBK[d] * s[i][c];
+    }
+  }
+  pred = rowgroup_sum(pred);
+  if (lane < C4) sRed[wave][lane] = pred;
+  __syncthreads();
+  pred = sRed[0][c4] + sRed[1][c4] + sRed[2][c4] + sRed[3][c4];
+  f32x4 delta;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) delta[c] = wv4[c] - pred[c];
   __syncthreads();  // every thread has read sRed
-  float o = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
   float* dst = h_out + bh * D * D;
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
     const int d = rg * RPT + i;
-    const float nv = sanitize(s[i] + sK[d] * delta);
-    dst[(size_t)d * D + col] = nv;
-    o += sQ[d] * nv;
-  }
-  sRed[rg][e] = o;
-  __syncthreads();
-  if (rg == 0) {
-    o = 0.f;
+    f32x4 nv;
 #pragma unroll
-    for (int r = 0; r < RG; ++r) o += sRed[r][e];
-    out[vo + col] = sanitize(scale * o);
+    for (int c = 0; c < 4; ++c) {
+      nv[c] = sanitize(s[i][c] + sK[d] * delta[c]);
+      o[c] += sQ[d] * nv[c];
+    }
+    store4(dst + (size_t)d * D + col, nv);
+  }
+  o = rowgroup_sum(o);
+  if (lane < C4) sRed[wave][lane] = o;
+  __syncthreads();
+  if (tid < C4) {
+    const f32x4 t = sRed[0][tid] + sRed[1][tid] + sRed[2][tid] + sRed[3][tid];
+    store4(out + vo + (blockIdx.x % NSL) * CS + 4 * tid, sanitize4(scale * t));
   }
 }
 
