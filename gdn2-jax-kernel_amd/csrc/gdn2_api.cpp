@@ -25,6 +25,22 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       const char* fws, char* ws, const int* cu_chunks, int nseq);
 
 size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t elem);
+template <typename TG, int D, typename TI>
+hipError_t launch_stage_scores(hipStream_t st, int B, int T_len, int H, const void* q,
+                               const void* k, const void* b, const void* g, float scale,
+                               float* aqk, float* akk);
+hipError_t launch_stage_solve(hipStream_t st, size_t nchunks, const float* akk, float* a_out);
+template <typename TG, int D, typename TI>
+hipError_t launch_stage_wy(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
+                           const void* v, const void* w, const void* b, const void* g,
+                           const float* A, float* w_pseudo, float* u, float* kg, float* qg,
+                           float* gc_last);
+template <int D>
+hipError_t launch_stage_combine(hipStream_t st, int B, int N, int H, const float* aqk,
+                                const float* w_pseudo, const float* u, const float* kg,
+                                const float* qg, const float* gc_last, const float* h0,
+                                float scale, float* out, float* h_final, float* h_pre_all,
+                                float* v_new_all, char* ws);
 
 template <typename T, typename TG, int D>
 hipError_t launch_decode(hipStream_t st, int B, int H, const void* q, const void* k,
@@ -142,6 +158,56 @@ struct BwdRun {
           dh0, fws, ws, cu_chunks, nseq);
       return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
     }
+  }
+};
+
+// The stage entry points (the reference's kernels A-D one at a time): float32
+// tiles at chunk 64; bfloat16 inputs are computed in float32 (GDN2_BF16_F32).
+static int validate_stage(int B, int T, int H, int D, int BT, int in_dtype, int g_dtype) {
+  if (BT != 64) return GDN2_ERR_CHUNK;
+  return gdn2_validate(B, T, H, D, BT, in_dtype == GDN2_BF16 ? GDN2_BF16_F32 : in_dtype,
+                       g_dtype);
+}
+
+// Dispatch of a stage launcher on (g storage type, D, input storage type).
+template <template <typename, int, typename> class F, typename... A>
+static int dispatch_stage(int in_dtype, int g_dtype, int D, A... args) {
+#define GDN2_SCASE(TG, D_, TI) \
+  if (D == D_) return F<TG, D_, TI>::run(args...);
+  if (in_dtype == GDN2_F32) {
+    GDN2_SCASE(float, 64, float)
+    GDN2_SCASE(float, 128, float)
+    GDN2_SCASE(float, 256, float)
+  } else if (g_dtype == GDN2_F32) {
+    GDN2_SCASE(float, 64, bf16_t)
+    GDN2_SCASE(float, 128, bf16_t)
+    GDN2_SCASE(float, 256, bf16_t)
+  } else {
+    GDN2_SCASE(bf16_t, 64, bf16_t)
+    GDN2_SCASE(bf16_t, 128, bf16_t)
+    GDN2_SCASE(bf16_t, 256, bf16_t)
+  }
+#undef GDN2_SCASE
+  return GDN2_ERR_HEAD_DIM;
+}
+
+template <typename TG, int D, typename TI>
+struct ScoresRun {
+  static int run(hipStream_t st, int B, int T, int H, const void* q, const void* k,
+                 const void* b, const void* g, float scale, float* aqk, float* akk) {
+    hipError_t e = launch_stage_scores<TG, D, TI>(st, B, T, H, q, k, b, g, scale, aqk, akk);
+    return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+  }
+};
+
+template <typename TG, int D, typename TI>
+struct WyRun {
+  static int run(hipStream_t st, int B, int T, int H, const void* q, const void* k,
+                 const void* v, const void* w, const void* b, const void* g, const float* A,
+                 float* w_pseudo, float* u, float* kg, float* qg, float* gc_last) {
+    hipError_t e = launch_stage_wy<TG, D, TI>(st, B, T, H, q, k, v, w, b, g, A, w_pseudo, u, kg,
+                                              qg, gc_last);
+    return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
   }
 };
 
@@ -391,6 +457,86 @@ int gdn2_fwd_varlen(void* stream, int num_seqs, const int* cu_chunks, const int*
   return dispatch<FwdRun>(in_dtype, g_dtype, BT, D, (hipStream_t)stream, 1, T, H, q, k, v, w,
                           b, g, h0, scale, out, h_final, (char*)ws, (float*)nullptr,
                           flags & (GDN2_FWD_RAW_INPUTS | GDN2_FWD_SAVE_A), &vl);
+}
+
+int gdn2_chunk_scores(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
+                      int g_dtype, const void* q, const void* k, const void* b,
+                      const void* g, float scale, float* aqk, float* akk) {
+  EventScope scope;
+  int rc = validate_stage(B, T, H, D, BT, in_dtype, g_dtype);
+  if (rc) return rc;
+  if (T == 0) return GDN2_OK;   // no chunks
+  if ((rc = check_ptrs({q, k, b, g, aqk, akk}))) return rc;
+  return dispatch_stage<ScoresRun>(in_dtype, g_dtype, D, (hipStream_t)stream, B, T, H, q, k, b,
+                                   g, scale, aqk, akk);
+}
+
+int gdn2_wy_solve(void* stream, long long nchunks, int BT, const float* akk, float* a) {
+  EventScope scope;
+  if (BT != 64) return GDN2_ERR_CHUNK;
+  if (nchunks < 0 || nchunks > 0x7fffffffLL) return GDN2_ERR_SHAPE;
+  if (nchunks == 0) return GDN2_OK;
+  int rc = check_ptrs({akk, a});
+  if (rc) return rc;
+  return launch_stage_solve((hipStream_t)stream, (size_t)nchunks, akk, a) == hipSuccess
+             ? GDN2_OK
+             : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_recompute_wy(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
+                      int g_dtype, const void* q, const void* k, const void* v,
+                      const void* w, const void* b, const void* g, const float* a,
+                      float* w_pseudo, float* u, float* kg, float* qg, float* gc_last) {
+  EventScope scope;
+  int rc = validate_stage(B, T, H, D, BT, in_dtype, g_dtype);
+  if (rc) return rc;
+  if (T == 0) return GDN2_OK;   // no chunks
+  if ((rc = check_ptrs({q, k, v, w, b, g, a, w_pseudo, u, kg, qg, gc_last}))) return rc;
+  return dispatch_stage<WyRun>(in_dtype, g_dtype, D, (hipStream_t)stream, B, T, H, q, k, v, w,
+                               b, g, a, w_pseudo, u, kg, qg, gc_last);
+}
+
+// gdn2_chunk_combine's shape checks: N chunks of 64 tokens, and the transposes
+// of the D x D state tiles (one workgroup per 32 x 32 tile) within a 31-bit grid.
+static int validate_combine(int B, int N, int H, int D, int BT) {
+  if (N < 0 || (long long)N * 64 > 0x7fffffffLL) return GDN2_ERR_SHAPE;
+  const int rc = validate_stage(B, N * 64, H, D, BT, GDN2_F32, GDN2_F32);
+  if (rc) return rc;
+  if ((double)B * H * N * (D / 32) * (D / 32) > 2147483647.0) return GDN2_ERR_SHAPE;
+  return GDN2_OK;
+}
+
+size_t gdn2_chunk_combine_workspace_bytes(int B, int N, int H, int D, int BT) {
+  if (validate_combine(B, N, H, D, BT) != GDN2_OK) return 0;
+  return combine_layout(nchunks(B, N * 64, H, 64), 64, D).total;
+}
+
+int gdn2_chunk_combine(void* stream, int B, int N, int H, int D, int BT, const float* aqk,
+                       const float* w_pseudo, const float* u, const float* kg,
+                       const float* qg, const float* gc_last, const float* h0, float scale,
+                       float* out, float* h_final, float* h_pre_all, float* v_new_all,
+                       void* ws, size_t ws_bytes) {
+  EventScope scope;
+  int rc = validate_combine(B, N, H, D, BT);
+  if (rc) return rc;
+  if (N > 0 && (rc = check_ptrs({aqk, w_pseudo, u, kg, qg, gc_last, out}))) return rc;
+  if ((rc = check_ptrs({h_final}))) return rc;
+  if ((rc = check_opt({h0, h_pre_all, v_new_all}))) return rc;
+  const size_t need = combine_layout(nchunks(B, N * 64, H, 64), 64, D).total;
+  if (need > 0 && (rc = check_ptrs({ws}))) return rc;
+  if (ws_bytes < need) return GDN2_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (D == 64)
+    e = launch_stage_combine<64>(st, B, N, H, aqk, w_pseudo, u, kg, qg, gc_last, h0, scale, out,
+                                 h_final, h_pre_all, v_new_all, (char*)ws);
+  else if (D == 128)
+    e = launch_stage_combine<128>(st, B, N, H, aqk, w_pseudo, u, kg, qg, gc_last, h0, scale, out,
+                                  h_final, h_pre_all, v_new_all, (char*)ws);
+  else
+    e = launch_stage_combine<256>(st, B, N, H, aqk, w_pseudo, u, kg, qg, gc_last, h0, scale, out,
+                                  h_final, h_pre_all, v_new_all, (char*)ws);
+  return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
 int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, const void* q,

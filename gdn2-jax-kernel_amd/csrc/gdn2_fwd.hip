@@ -55,7 +55,19 @@ struct PrepArgs {
                       // for the scan's output waves, which then read 1 KB per load
   int* sat_clear;     // segmented scan: its saturation flag, cleared here (the first
                       // launch of the call)
+  // Stage modes (PrepMode): Akk output of kPrepScores, the given A of kPrepWy,
+  // the given Akk of kPrepSolve ([cid][BT][BT] float32 each)
+  float* akk_out;
+  const float* a_in;
 };
+
+// What one fwd_prep launch computes.  kPrepFull: the forward's per-chunk tiles
+// (kernels A-C fused).  The reference's stages one at a time, float32 tiles in
+// the reference's (B,H,N,BT,.) layout: kPrepScores Aqk and Akk
+// (build_chunk_scores_pallas, gdn2_fwd.py:142-170); kPrepSolve A = (I + Akk)^{-1}
+// from a given Akk (wy_solve_pallas, :246-260); kPrepWy w_pseudo, u, kg, qg,
+// gc_last from a given A (recompute_wy_pallas, :298-330).
+enum PrepMode { kPrepFull = 0, kPrepScores = 1, kPrepSolve = 2, kPrepWy = 3 };
 
 // Operand-fragment order of a chunk's q_g [BT][D] tile: the 16-byte operand
 // run a lane (li, lg) feeds a 16 x 16 MFMA for row block I and k-group j
@@ -197,9 +209,11 @@ constexpr int prep_min_blocks(int esize, int BT, int D) {
   return esize == 2 && BT == 64 && D == 128 ? 3 : 1;
 }
 
-template <typename T, typename TG, int BT, int D, typename TI>
+template <typename T, typename TG, int BT, int D, typename TI, int MODE = kPrepFull>
 __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T), BT, D))
     fwd_prep(PrepArgs<T, TG, TI> a) {
+  static_assert(MODE == kPrepFull || (sizeof(T) == 4 && BT == 64),
+                "the stage modes run float32 tiles at chunk 64");
   using Op = typename Tr<T>::Op;
   constexpr int KC = Tr<T>::KC, KS = Tr<T>::KS;
   constexpr int NB = BT / 16;             // 16-token row blocks
@@ -314,6 +328,20 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     for (int J = 0; J < NB; ++J) qoff[i][J] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // kPrepSolve: the strictly lower part of the given Akk into sA; no input is read
+  if constexpr (MODE == kPrepSolve) {
+    const float* src = a.a_in + (size_t)cid * BT * BT;
+    for (int i = tid; i < BT * BT / 4; i += NT) {
+      const int r = i / (BT / 4), c4 = (i % (BT / 4)) * 4;
+      f32x4 x = load4f(src + (size_t)r * BT + c4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = c4 + e < r ? x[e] : 0.f;
+      store4(&sA[r * A_LD + c4], x);
+    }
+    lds_barrier();
+  }
+
+  if constexpr (MODE != kPrepSolve) {
 #pragma unroll
   for (int pn = 0; pn < NPN; ++pn) {
     const int d0 = pn * DP;               // first channel of the panel
@@ -382,7 +410,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       float run = 0.f;
 #pragma unroll
       for (int m = 0; m < NB; ++m) { sF0[m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
-      a.GL[(size_t)cid * D + d0 + tid] = sanitize(run);
+      if constexpr (MODE != kPrepScores) a.GL[(size_t)cid * D + d0 + tid] = sanitize(run);
       run = 0.f;
 #pragma unroll
       for (int m = NB - 1; m >= 0; --m) { sF1[m * DP + tid] = __expf(run); run += sTot[m * DP + tid]; }
@@ -435,7 +463,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       bool wide = false;   // a channel's decay across the block exceeds the factors' range
 #pragma unroll
       for (int j = 0; j < NKD; ++j) {
-        float qg[KC], kh[KC], dq[KC], dk[KC], db[KC];
+        float qg[KC], kh[KC], dq[KC], dk[KC], db[KC], kgr[KC];
 #pragma unroll
         for (int e = 0; e < KC; ++e) {
           const int x = j * KC + e, ch = chan(x);
@@ -446,9 +474,10 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
           const float egc = eloc * sF0[I * DP + ch];
           const float bk = bv * kv;
           qg[e] = sanitize(qv * egc);
-          sKbdT[(d0 + ch) * TT_LD + t] = from_f<T>(bk * egc);
-          kgT[(size_t)(d0 + ch) * BT + kpos<T>(t)] =
-              from_f<T>(sanitize(kv * ekh * sF1[I * DP + ch]));
+          if constexpr (MODE != kPrepScores) sKbdT[(d0 + ch) * TT_LD + t] = from_f<T>(bk * egc);
+          const float kgv = sanitize(kv * ekh * sF1[I * DP + ch]);
+          if constexpr (MODE == kPrepFull) kgT[(size_t)(d0 + ch) * BT + kpos<T>(t)] = from_f<T>(kgv);
+          kgr[e] = kgv;
           kh[e] = kv * ekh;
           aq[i][x] = qv * eloc;
           ak[i][x] = bk * eloc;
@@ -461,8 +490,14 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
           db[e] = bk * edq;
           dk[e] = kv * edk;
         }
-        *reinterpret_cast<Op*>(a.frag ? qgf + qg_frag<T, BT, D>(I, d0 / KS + j, lane)
-                                      : qgp + j * KS + lg * KC) = op_from<T>(qg);
+        if constexpr (MODE != kPrepScores)
+          *reinterpret_cast<Op*>(a.frag ? qgf + qg_frag<T, BT, D>(I, d0 / KS + j, lane)
+                                        : qgp + j * KS + lg * KC) = op_from<T>(qg);
+        if constexpr (MODE == kPrepWy) {   // kg [t][d]
+          *reinterpret_cast<Op*>(a.KgT + (size_t)cid * BT * D + (size_t)t * D + d0 + j * KS +
+                                 lg * KC) = op_from<T>(kgr);
+          continue;                        // no scores
+        }
         *reinterpret_cast<Op*>(&sR0[t * KH_LD + j * KS + lg * KC]) = op_from<T>(kh);
         // diagonal block, factorised around its 8th token: X = k rows (j),
         // Y = q / bk rows (i) -> lane holds [i=li][j=4lg+r]
@@ -470,6 +505,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
         mma(accq, xo, op_from<T>(dq));
         mma(acck, xo, op_from<T>(db));
       }
+      if constexpr (MODE == kPrepWy) continue;
       if (__ballot(wide) != 0) {
         const DiagSums d = diag_block_exact<T, TI, TG, NKD>(a.q, a.k, a.b, a.g,
                                                              load_row(i) + d0, raw, real(i),
@@ -502,7 +538,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
 
     // ---- 3. off-diagonal score blocks (I > J) on MFMA ------------------------
 #pragma unroll
-    for (int i = 0; i < NBW; ++i) {
+    for (int i = 0; i < (MODE == kPrepWy ? 0 : NBW); ++i) {
       const int I = prep_block<NB, PW>(wv, i);
       const int t = I * 16 + li;
       // block pair (I, J), J < I, in descending J; after each pair aq and ak
@@ -547,6 +583,20 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     }
   }
   lds_barrier();
+  }  // MODE != kPrepSolve
+
+  // kPrepScores: Akk (sA, zero above the strict lower part) out, Aqk's blocks
+  // above the diagonal zeroed (the steps above wrote the others)
+  if constexpr (MODE == kPrepScores) {
+    float* dst = a.akk_out + (size_t)cid * BT * BT;
+    float* aq = reinterpret_cast<float*>(aqk);
+    for (int i = tid; i < BT * BT / 4; i += NT) {
+      const int r = i / (BT / 4), c4 = (i % (BT / 4)) * 4;
+      store4(dst + (size_t)r * BT + c4, load4f(&sA[r * A_LD + c4]));
+      if (c4 / 16 > r / 16) store4(aq + (size_t)r * BT + c4, f32x4{0.f, 0.f, 0.f, 0.f});
+    }
+    return;
+  }
 
 
   // w, v of the first panel: in flight during the inverse (issued earlier they
@@ -563,8 +613,17 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       }
     }
   };
-  load_wv(0);
+  if constexpr (MODE != kPrepSolve) load_wv(0);
 
+  if constexpr (MODE == kPrepWy) {
+    // the given A into sA
+    const float* src = a.a_in + (size_t)cid * BT * BT;
+    for (int i = tid; i < BT * BT / 4; i += NT) {
+      const int r = i / (BT / 4), c4 = (i % (BT / 4)) * 4;
+      store4(&sA[r * A_LD + c4], load4f(src + (size_t)r * BT + c4));
+    }
+    lds_barrier();
+  } else {
   // ---- 4. A = (I + Akk)^{-1}: diagonal blocks ---------------------------------
   // The diagonal block L of Akk is strictly lower 16 x 16, so L^16 = 0 and
   // (I + L)^{-1} = (I - L)(I + L^2)(I + L^4)(I + L^8): ten 16 x 16 products in
@@ -678,6 +737,17 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     if constexpr (NB >= 8) level(std::integral_constant<int, 4>{});
     static_assert(NB <= 8, "doubling steps up to h = 4");
   }
+  }  // MODE != kPrepWy
+
+  if constexpr (MODE == kPrepSolve) {
+    // A out (the inverse of a lower-triangular matrix: zero above the diagonal)
+    float* dst = a.a_dbg + (size_t)cid * BT * BT;
+    for (int i = tid; i < BT * BT / 4; i += NT) {
+      const int r = i / (BT / 4), c4 = (i % (BT / 4)) * 4;
+      store4(dst + (size_t)r * BT + c4, load4f(&sA[r * A_LD + c4]));
+    }
+    return;
+  }
   T* sWVT = sR0;
 #pragma unroll
   for (int pn = 0; pn < NPN; ++pn) {
@@ -734,7 +804,7 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
       f32x4 accw = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kg = 0; kg < NKT; ++kg) {
-        if (kg <= kgmax) {
+        if (MODE == kPrepWy || kg <= kgmax) {   // kPrepWy: all of the given A
           float tmp[KC];
 #pragma unroll
           for (int e = 0; e < KC; e += 4) {
@@ -747,7 +817,13 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
         }
       }
       store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dg + 4 * lg), sanitize4(accw));
-      store4(Uc + (size_t)(dg + li) * BT + kpos<T>(I * 16 + 4 * lg), sanitize4(accu));
+      if constexpr (MODE == kPrepWy) {   // u [t][d]
+        T* uc = a.UT + (size_t)cid * BT * D;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) uc[(size_t)(I * 16 + 4 * lg + r) * D + dg + li] = sanitize(accu[r]);
+      } else {
+        store4(Uc + (size_t)(dg + li) * BT + kpos<T>(I * 16 + 4 * lg), sanitize4(accu));
+      }
     }
   }
 }
@@ -1796,6 +1872,172 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
   launch_mark(st);
   return hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// The reference's forward stages one at a time: float32 tiles at chunk 64, the
+// reference's (B,H,N,BT,.) layouts.
+
+// dst[m][c][r] = src[m][r][c] for matrices of R x C float32 (R, C multiples of
+// 32), one 32 x 32 tile per workgroup; the grid covers the tiles of all matrices.
+__global__ void __launch_bounds__(256) tile_transpose(const float* __restrict__ src,
+                                                      float* __restrict__ dst, int R, int C) {
+  __shared__ float t[32][33];
+  const int tr = R / 32, tc = C / 32;
+  const size_t m = blockIdx.x / (size_t)(tr * tc);
+  const int rem = (int)(blockIdx.x % (size_t)(tr * tc));
+  const int r0 = rem / tc * 32, c0 = rem % tc * 32;
+  const float* s = src + m * R * C;
+  float* d = dst + m * R * C;
+  const int x = threadIdx.x & 31, y = threadIdx.x >> 5;
+  for (int j = y; j < 32; j += 8) t[j][x] = s[(size_t)(r0 + j) * C + c0 + x];
+  __syncthreads();
+  for (int j = y; j < 32; j += 8) d[(size_t)(c0 + j) * R + r0 + x] = t[x][j];
+}
+
+static void transpose_all(hipStream_t st, const float* src, float* dst, size_t n, int R, int C) {
+  if (n > 0)
+    hipLaunchKernelGGL(tile_transpose, dim3(n * (R / 32) * (C / 32)), dim3(256), 0, st, src, dst,
+                       R, C);
+}
+
+// Kernel A (build_chunk_scores_pallas): Aqk, Akk [cid][64][64].
+template <typename TG, int D, typename TI>
+hipError_t launch_stage_scores(hipStream_t st, int B, int T_len, int H, const void* q,
+                               const void* k, const void* b, const void* g, float scale,
+                               float* aqk, float* akk) {
+  const int N = T_len / 64;
+  const size_t NC = (size_t)B * H * N;
+  if (NC > 0) {
+    PrepArgs<float, TG, TI> pa{};
+    pa.q = (const TI*)q;
+    pa.k = (const TI*)k;
+    pa.b = (const TI*)b;
+    pa.g = (const TG*)g;
+    pa.T_len = T_len;
+    pa.H = H;
+    pa.N = N;
+    pa.NC = (long long)NC;
+    pa.scale = scale;
+    pa.Aqk = aqk;
+    pa.akk_out = akk;
+    hipLaunchKernelGGL((fwd_prep<float, TG, 64, D, TI, kPrepScores>), dim3(NC),
+                       dim3(64 * prep_waves(64)), 0, st, pa);
+  }
+  return hipGetLastError();
+}
+
+// Kernel B (wy_solve_pallas): A = (I + Akk)^{-1} per [64][64] chunk tile, from
+// the strictly lower part of Akk.
+hipError_t launch_stage_solve(hipStream_t st, size_t nchunks, const float* akk, float* a_out) {
+  if (nchunks > 0) {
+    PrepArgs<float, float, float> pa{};
+    pa.T_len = 64;
+    pa.H = 1;
+    pa.N = 1;
+    pa.NC = (long long)nchunks;
+    pa.a_in = akk;
+    pa.a_dbg = a_out;
+    hipLaunchKernelGGL((fwd_prep<float, float, 64, 64, float, kPrepSolve>), dim3(nchunks),
+                       dim3(64 * prep_waves(64)), 0, st, pa);
+  }
+  return hipGetLastError();
+}
+
+// Kernel C (recompute_wy_pallas): w_pseudo, u, kg, qg [cid][64][D] and gc_last
+// [cid][D] from the inputs and a given A [cid][64][64].
+template <typename TG, int D, typename TI>
+hipError_t launch_stage_wy(hipStream_t st, int B, int T_len, int H, const void* q, const void* k,
+                           const void* v, const void* w, const void* b, const void* g,
+                           const float* A, float* w_pseudo, float* u, float* kg, float* qg,
+                           float* gc_last) {
+  const int N = T_len / 64;
+  const size_t NC = (size_t)B * H * N;
+  if (NC > 0) {
+    PrepArgs<float, TG, TI> pa{};
+    pa.q = (const TI*)q;
+    pa.k = (const TI*)k;
+    pa.v = (const TI*)v;
+    pa.w = (const TI*)w;
+    pa.b = (const TI*)b;
+    pa.g = (const TG*)g;
+    pa.T_len = T_len;
+    pa.H = H;
+    pa.N = N;
+    pa.NC = (long long)NC;
+    pa.W = w_pseudo;
+    pa.UT = u;
+    pa.KgT = kg;
+    pa.Qg = qg;
+    pa.GL = gc_last;
+    pa.a_in = A;
+    hipLaunchKernelGGL((fwd_prep<float, TG, 64, D, TI, kPrepWy>), dim3(NC),
+                       dim3(64 * prep_waves(64)), 0, st, pa);
+  }
+  return hipGetLastError();
+}
+
+// Kernel D (gdn2_inter_chunk_combine(_with_state)): the serial state scan and the
+// outputs over given per-chunk tiles.  u and kg are transposed into the scan's
+// [D][BT] layout in `ws` (combine_layout); out is (B, N*64, H, D); h_pre_all
+// [cid][D][D] (h entering the chunk, [dk][dv]) and v_new_all [cid][64][D] are
+// written when not null.
+template <int D>
+hipError_t launch_stage_combine(hipStream_t st, int B, int N, int H, const float* aqk,
+                                const float* w_pseudo, const float* u, const float* kg,
+                                const float* qg, const float* gc_last, const float* h0,
+                                float scale, float* out, float* h_final, float* h_pre_all,
+                                float* v_new_all, char* ws) {
+  constexpr int BT = 64;
+  const size_t NC = (size_t)B * H * N;
+  const CombineLayout L = combine_layout(NC, BT, D);
+  float* UT = reinterpret_cast<float*>(ws + L.UT);
+  float* KgT = reinterpret_cast<float*>(ws + L.KgT);
+  float* HT = reinterpret_cast<float*>(ws + L.HT);
+  float* VnT = reinterpret_cast<float*>(ws + L.VnT);
+  const int T_len = N * BT;
+  transpose_all(st, u, UT, NC, BT, D);
+  transpose_all(st, kg, KgT, NC, BT, D);
+  constexpr int SW = 2, SP = 4, SK = state_ksplit<float, BT, D>();
+  constexpr int NVS = D / (16 * SW);
+  StateArgs<float> sa{w_pseudo, UT, KgT, gc_last, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT,
+                      h_final, nullptr, H, qg, aqk, out, scale, T_len, nullptr};
+  hipLaunchKernelGGL((fwd_state<float, BT, D, SW, SP, SK>), dim3((size_t)B * H * NVS),
+                     dim3(64 * (SW * SK + SP)), 0, st, sa);
+  if (NC > 0) {
+    OutArgs<float> oa{qg, aqk, HT, VnT, T_len, H, N, scale, out, nullptr};
+    hipLaunchKernelGGL((fwd_out<float, BT, D>), dim3(NC * (D / out_cols<float, D>())),
+                       dim3(256), 0, st, oa);
+  }
+  if (h_pre_all) transpose_all(st, HT, h_pre_all, NC, D, D);
+  if (v_new_all) transpose_all(st, VnT, v_new_all, NC, D, BT);
+  return hipGetLastError();
+}
+
+#define GDN2_INST_STAGE(TG, D, TI)                                                            \
+  template hipError_t launch_stage_scores<TG, D, TI>(hipStream_t, int, int, int, const void*,  \
+                                                     const void*, const void*, const void*,    \
+                                                     float, float*, float*);                   \
+  template hipError_t launch_stage_wy<TG, D, TI>(hipStream_t, int, int, int, const void*,      \
+                                                 const void*, const void*, const void*,        \
+                                                 const void*, const void*, const float*,       \
+                                                 float*, float*, float*, float*, float*);
+GDN2_INST_STAGE(float, 64, float)
+GDN2_INST_STAGE(float, 128, float)
+GDN2_INST_STAGE(float, 256, float)
+GDN2_INST_STAGE(float, 64, bf16_t)
+GDN2_INST_STAGE(float, 128, bf16_t)
+GDN2_INST_STAGE(float, 256, bf16_t)
+GDN2_INST_STAGE(bf16_t, 64, bf16_t)
+GDN2_INST_STAGE(bf16_t, 128, bf16_t)
+GDN2_INST_STAGE(bf16_t, 256, bf16_t)
+#define GDN2_INST_COMBINE(D)                                                                   \
+  template hipError_t launch_stage_combine<D>(hipStream_t, int, int, int, const float*,        \
+                                              const float*, const float*, const float*,        \
+                                              const float*, const float*, const float*, float, \
+                                              float*, float*, float*, float*, char*);
+GDN2_INST_COMBINE(64)
+GDN2_INST_COMBINE(128)
+GDN2_INST_COMBINE(256)
 
 #define GDN2_INST_FWD(T, TG, BT, D, TI)                                                      \
   template hipError_t launch_fwd<T, TG, BT, D, TI>(hipStream_t, int, int, int, const void*, \

@@ -5,7 +5,10 @@ Drop-in for the reference package's exports (tests/test_imports.py:5,12):
 beyond them ``gdn2_pallas_forward_raw`` (input activations fused into the
 forward), ``gdn2_pallas_forward_varlen`` (variable-length packed batches; trainable as
 ``gdn2_pallas_forward_varlen_trainable``) and
-``gdn2_decode_step`` (one-token recurrent step on the state).
+``gdn2_decode_step`` (one-token recurrent step on the state).  The reference's
+per-kernel forward functions (``build_chunk_scores_pallas``, ``wy_solve_pallas``,
+``recompute_wy_pallas``, ``gdn2_inter_chunk_combine(_with_state)``) are in
+``gdn2_fwd``, as in the reference.
 Compute runs in libgdn2_hip.so (hand-written gfx950 HIP kernels, C ABI in
 include/gdn2.h); torch supplies device memory and streams.
 """

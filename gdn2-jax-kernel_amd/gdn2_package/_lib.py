@@ -68,6 +68,12 @@ SIGNATURES = {
     "gdn2_bwd_varlen_workspace_bytes": (_c_size, [_c_int] * 5),
     "gdn2_bwd_varlen": (_c_int, [_vp, _c_int, _vp] + [_c_int] * 6 + [_vp] * 7
                         + [_c_float, _vp, _vp] + [_vp] * 7 + [_vp, _c_size, _vp, _c_size]),
+    "gdn2_chunk_scores": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 4 + [_c_float, _vp, _vp]),
+    "gdn2_wy_solve": (_c_int, [_vp, ctypes.c_longlong, _c_int, _vp, _vp]),
+    "gdn2_recompute_wy": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7 + [_vp] * 5),
+    "gdn2_chunk_combine_workspace_bytes": (_c_size, [_c_int] * 5),
+    "gdn2_chunk_combine": (_c_int, [_vp] + [_c_int] * 5 + [_vp] * 7
+                           + [_c_float, _vp, _vp, _vp, _vp, _vp, _c_size]),
 }
 
 

@@ -366,3 +366,153 @@ def _forward_with_residuals(p: _Prepared):
     eye = torch.eye(p.BT, device=p.device, dtype=torch.float64)
     res["Akk"] = torch.tril(torch.linalg.inv(a_out.double()) - eye, -1).float()
     return out, h_final, res
+
+
+# ---------------------------------------------------------------------------
+# The forward's stages one at a time (the reference's module-level kernels).
+# Each runs a HIP kernel of libgdn2_hip.so in float32 at chunk 64 and returns
+# float32 tensors in the reference's (B,H,N,BT,...) layouts.
+_STAGE_BT = 64
+
+
+def _stage_chunk(D: int) -> int:
+    """The stage functions run at chunk 64 (float32 tiles); a module BT
+    override to another size is refused, as the reference asserts its
+    shapes against BT (gdn2_fwd.py:144,249)."""
+    bt = chunk_size_for(torch.float32, None, D)
+    if bt != _STAGE_BT:
+        raise GDN2ShapeError(f"gdn2: the per-kernel stage functions run at chunk "
+                             f"{_STAGE_BT}; BT = {bt} is not supported for them")
+    return _STAGE_BT
+
+
+def _stage_inputs(q, k, v, w, b, g, scale):
+    D = q.shape[-1] if isinstance(q, torch.Tensor) and q.dim() == 4 else 0
+    p = _Prepared(q, k, v, w, b, g, scale, None, _stage_chunk(D),
+                  compute_dtype=torch.float32)
+    if p.partial:
+        raise GDN2ShapeError(f"gdn2: L={p.T} must be divisible by BT={p.BT} "
+                             f"(gdn2_fwd.py:145,301)")
+    return p
+
+
+def _chunk_tensor(x, name, shape, device):
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"gdn2: {name} must be a torch tensor on the ROCm device")
+    if tuple(x.shape) != tuple(shape):
+        raise GDN2ShapeError(f"gdn2: {name} must have shape {tuple(shape)}; got "
+                             f"{tuple(x.shape)}")
+    if x.device != device:
+        raise GDN2Error(f"gdn2: {name} must live on {device}")
+    return x.to(torch.float32).contiguous()
+
+
+def build_chunk_scores_pallas(q, k, b, g, scale):
+    """Kernel A, gdn2_fwd.py:142-170: per chunk, Aqk = scale * causal
+    sum_d q_i k_j e^{gc_i - gc_j} and Akk = strictly lower sum_d (b k)_i k_j
+    e^{gc_i - gc_j}, each (B,H,N,BT,BT) float32 and sanitized.  The HIP kernel
+    is the forward's fwd_prep run to its score blocks (stage kPrepScores).
+    D may be 64, 128 or 256 (the reference asserts 128)."""
+    p = _stage_inputs(q, k, k, k, b, g, scale)
+    aqk = torch.empty((p.B, p.H, p.N, p.BT, p.BT), dtype=torch.float32, device=p.device)
+    akk = torch.empty_like(aqk)
+    rc = _lib.lib().gdn2_chunk_scores(p.stream(), *p.args, p.ptr(p.q), p.ptr(p.k), p.ptr(p.b),
+                                      p.ptr(p.g), p.scale, aqk.data_ptr(), akk.data_ptr())
+    if rc:
+        _raise(rc, "gdn2_chunk_scores")
+    return aqk, akk
+
+
+def wy_solve_pallas(Akk):
+    """Kernel B, gdn2_fwd.py:246-260: A = (I + Akk)^{-1} per chunk, for Akk of
+    shape (..., BT, BT) (only its strictly lower part is read), float32."""
+    if not isinstance(Akk, torch.Tensor):
+        raise TypeError("gdn2: Akk must be a torch tensor on the ROCm device")
+    BT = _stage_chunk(128)
+    if Akk.dim() < 2 or tuple(Akk.shape[-2:]) != (BT, BT):
+        raise GDN2ShapeError(f"gdn2: Akk must end in ({BT},{BT}); got {tuple(Akk.shape)}")
+    if Akk.device.type != "cuda":
+        raise GDN2Error("gdn2: Akk must live on the ROCm device (torch 'cuda')")
+    akk = Akk.to(torch.float32).contiguous()
+    a = torch.empty_like(akk)
+    n = akk.numel() // (BT * BT)
+    rc = _lib.lib().gdn2_wy_solve(torch.cuda.current_stream(akk.device).cuda_stream, n, BT,
+                                  akk.data_ptr(), a.data_ptr())
+    if rc:
+        _raise(rc, "gdn2_wy_solve")
+    return a
+
+
+def recompute_wy_pallas(q, k, v, w, b, g, A):
+    """Kernel C, gdn2_fwd.py:298-330: w_pseudo = A (b k e^gc), u = A (w v),
+    kg = k e^{gc_last - gc}, qg = q e^gc (each (B,H,N,BT,D)) and gc_last
+    (B,H,N,D), float32 and sanitized, from the inputs and the given A
+    (B,H,N,BT,BT)."""
+    p = _stage_inputs(q, k, v, w, b, g, 1.0)
+    a = _chunk_tensor(A, "A", (p.B, p.H, p.N, p.BT, p.BT), p.device)
+    shp = (p.B, p.H, p.N, p.BT, p.D)
+    w_pseudo, u, kg, qg = (torch.empty(shp, dtype=torch.float32, device=p.device)
+                           for _ in range(4))
+    gc_last = torch.empty((p.B, p.H, p.N, p.D), dtype=torch.float32, device=p.device)
+    rc = _lib.lib().gdn2_recompute_wy(p.stream(), *p.args, p.ptr(p.q), p.ptr(p.k), p.ptr(p.v),
+                                      p.ptr(p.w), p.ptr(p.b), p.ptr(p.g), a.data_ptr(),
+                                      w_pseudo.data_ptr(), u.data_ptr(), kg.data_ptr(),
+                                      qg.data_ptr(), gc_last.data_ptr())
+    if rc:
+        _raise(rc, "gdn2_recompute_wy")
+    return w_pseudo, u, kg, qg, gc_last
+
+
+def _combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0, debug_tag, with_state):
+    if not isinstance(w_pseudo, torch.Tensor) or w_pseudo.dim() != 5:
+        raise GDN2ShapeError("gdn2: w_pseudo must be a (B,H,N,BT,D) tensor")
+    B, H, N, BT, D = w_pseudo.shape
+    if BT != _stage_chunk(D):
+        raise GDN2ShapeError(f"gdn2: chunk tiles of {BT} tokens; the stage functions take "
+                             f"{_STAGE_BT}")
+    dev = w_pseudo.device
+    if dev.type != "cuda":
+        raise GDN2Error("gdn2: the chunk tiles must live on the ROCm device (torch 'cuda')")
+    aqk = _chunk_tensor(Aqk, "Aqk", (B, H, N, BT, BT), dev)
+    wp, uu, kk, qq = (_chunk_tensor(x, n, (B, H, N, BT, D), dev) for x, n in
+                      ((w_pseudo, "w_pseudo"), (u, "u"), (kg, "kg"), (qg, "qg")))
+    gl = _chunk_tensor(gc_last, "gc_last", (B, H, N, D), dev)
+    h0c = None if h0 is None else _chunk_tensor(h0, "h0", (B, H, D, D), dev)
+    L = _lib.lib()
+    nbytes = L.gdn2_chunk_combine_workspace_bytes(B, N, H, D, BT)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    out = torch.empty((B, N * BT, H, D), dtype=torch.float32, device=dev)
+    h_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    h_pre = v_new = None
+    if with_state:
+        h_pre = torch.empty((B, H, N, D, D), dtype=torch.float32, device=dev)
+        v_new = torch.empty((B, H, N, BT, D), dtype=torch.float32, device=dev)
+    ptr = lambda x: None if x is None else x.data_ptr()
+    rc = L.gdn2_chunk_combine(torch.cuda.current_stream(dev).cuda_stream, B, N, H, D, BT,
+                              aqk.data_ptr(), wp.data_ptr(), uu.data_ptr(), kk.data_ptr(),
+                              qq.data_ptr(), gl.data_ptr(), ptr(h0c), float(scale),
+                              out.data_ptr(), h_final.data_ptr(), ptr(h_pre), ptr(v_new),
+                              ws.data_ptr(), nbytes)
+    if rc:
+        _raise(rc, "gdn2_chunk_combine")
+    # the reference returns o per chunk: (B,L,H,D) -> (B,H,N,BT,D)
+    o = out.view(B, N, BT, H, D).permute(0, 3, 1, 2, 4).contiguous()
+    h_final = _stage_diag(f"{debug_tag}:kernel_D_h_final", h_final)
+    o = _stage_diag(f"{debug_tag}:kernel_D_o", o)
+    return (o, h_final, h_pre, v_new) if with_state else (o, h_final)
+
+
+def gdn2_inter_chunk_combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0=None, debug_tag=""):
+    """Kernel D, gdn2_fwd.py:338-366: the serial state scan over the chunks
+    and the outputs, from the per-chunk tiles of kernels A and C.  Returns o
+    (B,H,N,BT,D) and h_final (B,H,D,D), float32.  h0 is sanitized first."""
+    return _combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0, debug_tag, False)
+
+
+def gdn2_inter_chunk_combine_with_state(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0=None,
+                                        debug_tag=""):
+    """gdn2_fwd.py:369-397: as gdn2_inter_chunk_combine, plus h_pre_all
+    (B,H,N,D,D), the state entering each chunk, and v_new_all (B,H,N,BT,D).
+    These two come in the (B,H,N,...) layout the backward consumes; the
+    reference's lax.scan stacks them chunk-first, (N,B,H,...)."""
+    return _combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0, debug_tag, True)

@@ -230,6 +230,50 @@ int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, co
                 const void* k, const void* v, const void* w, const void* b, const void* g,
                 float scale, const float* h_in, float* h_out, float* out);
 
+/* ---- The forward's stages one at a time ------------------------------------
+ * The reference's module-level kernels, for callers that run or inspect them
+ * separately.  Float32 arithmetic and float32 outputs in the reference's
+ * (B,H,N,BT,.) layouts; chunk 64 only (GDN2_ERR_CHUNK otherwise); in_dtype
+ * GDN2_F32, or GDN2_BF16 / GDN2_BF16_F32 for bfloat16 inputs (computed in float32,
+ * as the reference upcasts, gdn2_fwd.py:100-103,266-272); T % 64 == 0.
+ * gdn2_fwd runs the same mathematics fused. */
+
+/* Kernel A: replaces build_chunk_scores_pallas (gdn2_fwd.py:142-170).  q,k,b,g
+ * (B,T,H,D); aqk = scale * causal scores, akk = strictly lower (b k) k scores,
+ * each (B,H,N,64,64) float32, zero above the diagonal. */
+int gdn2_chunk_scores(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
+                      int g_dtype, const void* q, const void* k, const void* b,
+                      const void* g, float scale, float* aqk, float* akk);
+
+/* Kernel B: replaces wy_solve_pallas (gdn2_fwd.py:246-260).  a = (I + akk)^{-1}
+ * for nchunks tiles of 64 x 64 float32 ([nchunks][64][64]); only the strictly
+ * lower part of akk is read. */
+int gdn2_wy_solve(void* stream, long long nchunks, int BT, const float* akk, float* a);
+
+/* Kernel C: replaces recompute_wy_pallas (gdn2_fwd.py:298-330).  Inputs
+ * (B,T,H,D) and a given a (B,H,N,64,64); w_pseudo = a (b k e^gc), u = a (w v),
+ * kg, qg (B,H,N,64,D) and gc_last (B,H,N,D), float32. */
+int gdn2_recompute_wy(void* stream, int B, int T, int H, int D, int BT, int in_dtype,
+                      int g_dtype, const void* q, const void* k, const void* v,
+                      const void* w, const void* b, const void* g, const float* a,
+                      float* w_pseudo, float* u, float* kg, float* qg, float* gc_last);
+
+/* Workspace bytes of gdn2_chunk_combine (N chunks per sequence). */
+size_t gdn2_chunk_combine_workspace_bytes(int B, int N, int H, int D, int BT);
+
+/* Kernel D: replaces gdn2_inter_chunk_combine and
+ * gdn2_inter_chunk_combine_with_state (gdn2_fwd.py:338-397).  Per-chunk float32
+ * tiles as kernels A and C give them: aqk (B,H,N,64,64), w_pseudo, u, kg, qg
+ * (B,H,N,64,D), gc_last (B,H,N,D); h0 may be NULL.  out is (B, N*64, H, D) (the
+ * token layout of gdn2_fwd; the reference returns it per chunk), h_final
+ * (B,H,D,D).  h_pre_all (B,H,N,D,D), the state entering each chunk, and
+ * v_new_all (B,H,N,64,D) are written when not NULL. */
+int gdn2_chunk_combine(void* stream, int B, int N, int H, int D, int BT, const float* aqk,
+                       const float* w_pseudo, const float* u, const float* kg,
+                       const float* qg, const float* gc_last, const float* h0, float scale,
+                       float* out, float* h_final, float* h_pre_all, float* v_new_all,
+                       void* ws, size_t ws_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -265,3 +265,45 @@ def test_bwd_varlen_rejects_before_launch():
     assert call(2, 4, dh0=None) == _lib.ERR_NULL
     assert call(2, 4, fws=need_f - 1) == _lib.ERR_WORKSPACE
     assert call(2, 4, bws=need_b - 1) == _lib.ERR_WORKSPACE
+
+
+def test_stage_entry_points_reject_before_launch():
+    """gdn2_chunk_scores / gdn2_wy_solve / gdn2_recompute_wy / gdn2_chunk_combine
+    (the reference's kernels A-D one at a time): chunk 64 only, the forward's
+    shape and dtype rules, then pointers and workspace, all before a launch."""
+    L = _lib.lib()
+    fake = [0x100000 * (i + 1) for i in range(6)]
+    outs = [0x900000 * (i + 1) for i in range(5)]
+    sc = lambda d, p=fake, o=outs: L.gdn2_chunk_scores(None, *d, p[0], p[1], p[4], p[5], 0.125,
+                                                       o[0], o[1])
+    assert sc((1, 512, 2, 64, 128, BF16, F32)) == _lib.ERR_CHUNK     # chunk 64 only
+    assert sc((1, 512, 2, 96, 64, F32, F32)) == _lib.ERR_HEAD_DIM
+    assert sc((1, 500, 2, 64, 64, F32, F32)) == _lib.ERR_SEQ_LEN
+    assert sc((1, 512, 2, 64, 64, F32, BF16)) == _lib.ERR_DTYPE
+    assert sc((1, 512, 2, 64, 64, F32, F32), o=[None] + outs[1:]) == _lib.ERR_NULL
+    assert sc((1, 512, 2, 64, 64, BF16, F32), p=[0x100002] + fake[1:]) == _lib.ERR_ALIGN
+    assert sc((1, 0, 2, 64, 64, F32, F32), p=[None] * 6, o=[None] * 5) == _lib.OK  # nothing to do
+    assert L.gdn2_wy_solve(None, 4, 128, 0x1000, 0x2000) == _lib.ERR_CHUNK
+    assert L.gdn2_wy_solve(None, -1, 64, 0x1000, 0x2000) == _lib.ERR_SHAPE
+    assert L.gdn2_wy_solve(None, 1 << 31, 64, 0x1000, 0x2000) == _lib.ERR_SHAPE
+    assert L.gdn2_wy_solve(None, 4, 64, None, 0x2000) == _lib.ERR_NULL
+    assert L.gdn2_wy_solve(None, 0, 64, None, None) == _lib.OK
+    wy = lambda d, a=0x3000: L.gdn2_recompute_wy(None, *d, *fake, a, *outs)
+    assert wy((1, 512, 2, 64, 128, BF16, F32)) == _lib.ERR_CHUNK
+    assert wy((1, 512, 2, 64, 64, F32, F32), a=None) == _lib.ERR_NULL
+    # combine: N chunks of 64; workspace = u^T, kg^T, h^T, v_new^T float32 tiles
+    nc, D = 2 * 2 * 8, 64
+    need = L.gdn2_chunk_combine_workspace_bytes(2, 8, 2, D, 64)
+    assert need == 3 * nc * D * 64 * 4 + nc * D * D * 4
+    assert L.gdn2_chunk_combine_workspace_bytes(2, 8, 2, D, 128) == 0
+    assert L.gdn2_chunk_combine_workspace_bytes(2, -1, 2, D, 64) == 0
+    tiles = [0x100000 * (i + 1) for i in range(6)]
+    cb = lambda dims, t=tiles, hf=0x8000, wsb=need, ws=0x9000: L.gdn2_chunk_combine(
+        None, *dims, *t, None, 0.125, 0x7000, hf, None, None, ws, wsb)
+    assert cb((2, 8, 2, 96, 64)) == _lib.ERR_HEAD_DIM
+    assert cb((2, 8, 2, D, 128)) == _lib.ERR_CHUNK
+    assert cb((2, 1 << 26, 2, D, 64)) == _lib.ERR_SHAPE              # N * 64 past 31 bits
+    assert cb((2, 8, 2, D, 64), t=[None] + tiles[1:]) == _lib.ERR_NULL
+    assert cb((2, 8, 2, D, 64), hf=None) == _lib.ERR_NULL
+    assert cb((2, 8, 2, D, 64), wsb=need - 1) == _lib.ERR_WORKSPACE
+    assert cb((2, 8, 2, D, 64), ws=None) == _lib.ERR_NULL

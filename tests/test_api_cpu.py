@@ -179,3 +179,22 @@ def test_stage_diag_reports(monkeypatch, capsys):
     assert "t:kernel_C_u" in out and "2.000e+06" in out and "non-finite" not in out
     F._stage_diag("t:kernel_C_qg", ok)
     assert capsys.readouterr().out == ""
+
+
+def test_stage_functions_exist_and_refuse_other_chunks(monkeypatch):
+    """The reference's per-kernel forward functions (gdn2_fwd.py:142-397) are in
+    gdn2_package.gdn2_fwd; they run at chunk 64, and a module BT override to
+    128 or a wrongly shaped Akk raises the shape error before anything runs."""
+    import torch
+    from gdn2_package import gdn2_fwd as F
+    for n in ("build_chunk_scores_pallas", "wy_solve_pallas", "recompute_wy_pallas",
+              "gdn2_inter_chunk_combine", "gdn2_inter_chunk_combine_with_state"):
+        assert callable(getattr(F, n)), n
+    with pytest.raises(AssertionError, match="ends? in|end in"):
+        F.wy_solve_pallas(torch.zeros(2, 32, 32))
+    monkeypatch.setattr(F, "BT", 128)
+    q = _inputs((1, 128, 2, 64))
+    with pytest.raises(AssertionError, match="chunk 64"):
+        F.build_chunk_scores_pallas(q[0], q[1], q[4], q[5], 0.1)
+    with pytest.raises(AssertionError, match="chunk 64"):
+        F.wy_solve_pallas(torch.zeros(2, 64, 64))
