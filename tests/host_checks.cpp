@@ -151,6 +151,40 @@ int main() {
                          GDN2_FWD_SAVE_A) == GDN2_ERR_FLAGS);
   CHECK(gdn2_fwd_noalloc(nullptr, 2, 32768, 16, 128, 128, GDN2_BF16, GDN2_F32, x[0], x[1], x[2],
                          x[3], x[4], x[5], nullptr, 0.1f, fo, fh, 0) == GDN2_ERR_SCRATCH);
+  // the stage entry points (kernels A-D one at a time): chunk 64 only, shape and
+  // dtype rules of the forward, 31-bit grids, then pointers and workspace
+  float* fa = static_cast<float*>(P(0x600000));
+  for (int B : Bs)
+    for (int T : Ts)
+      for (int D : Ds)
+        for (int BT : {0, 64, 128}) {
+          const int rs = gdn2_chunk_scores(nullptr, B, T, 3, D, BT, GDN2_BF16, GDN2_F32, x[0],
+                                           x[1], x[4], x[5], 0.1f, fo, fh);
+          CHECK(known(rs));
+          if (BT != 64) CHECK(rs == GDN2_ERR_CHUNK);
+          const int rw = gdn2_recompute_wy(nullptr, B, T, 3, D, BT, GDN2_F32, GDN2_F32, x[0],
+                                           x[1], x[2], x[3], x[4], x[5], fa, fo, fo, fo, fo,
+                                           fh);
+          CHECK(known(rw));
+          if (rs == GDN2_OK || rw == GDN2_OK) CHECK(BT == 64 && T % 64 == 0 && B >= 1);
+          const int N = T / 64;
+          if (N <= 0) continue;   // no chunks: the scan would launch for h_final
+          const size_t cws = gdn2_chunk_combine_workspace_bytes(B, N, 3, D, BT);
+          const int rc = gdn2_chunk_combine(nullptr, B, N, 3, D, BT, fa, fa, fa, fa, fa, fa,
+                                            nullptr, 0.1f, fo, fh, nullptr, nullptr,
+                                            P(0xb00000), cws ? cws - 1 : 0);
+          CHECK(known(rc) && rc != GDN2_OK);
+          if (cws > 0) CHECK(rc == GDN2_ERR_WORKSPACE);
+        }
+  for (long long nc : {LLONG_MIN, -1LL, 0LL, 5LL, (long long)INT_MAX, (long long)INT_MAX + 1,
+                       LLONG_MAX}) {
+    const int rc = gdn2_wy_solve(nullptr, nc, 64, fa, fo);
+    CHECK(known(rc));
+    if (nc < 0 || nc > INT_MAX) CHECK(rc == GDN2_ERR_SHAPE);
+    if (nc == 0) CHECK(rc == GDN2_OK);
+  }
+  CHECK(gdn2_wy_solve(nullptr, 5, 128, fa, fo) == GDN2_ERR_CHUNK);
+  CHECK(gdn2_wy_solve(nullptr, 5, 64, nullptr, fo) == GDN2_ERR_NULL);
   for (int c = -20; c <= 5; ++c) CHECK(gdn2_strerror(c) != nullptr);
   CHECK(gdn2_set_launch_events(nullptr, -5) == 0);
   std::printf("host checks: %ld shape combinations, %d failures\n", n, g_fail);
