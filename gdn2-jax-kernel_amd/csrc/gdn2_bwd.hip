@@ -198,11 +198,12 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
   }
   // step i works on chunk c0 + n-1-i
   auto chunk_id = [&](int i) { return (size_t)bh * a.N + c0 + (n - 1 - i); };
-  // float32 tiles up to D = 128 are stored transposed in LDS (W^T [d][t], kg
-  // [t][d]), so that every MFMA operand of the compute waves is one 16-byte LDS
-  // read; bfloat16 tiles keep the stored layout (DMA, chained columns), and so does
-  // D = 256, whose staging registers (four blocks per lane and tile) would spill
-  constexpr bool TR = sizeof(T) == 4 && D <= 128;
+  // float32 tiles are stored transposed in LDS (W^T [d][t], kg [t][d]), so that
+  // every MFMA operand of the compute waves is one 16-byte LDS read; bfloat16 tiles
+  // keep the stored layout (DMA, chained columns).  With one tile buffer (D = 256)
+  // the producers stage one tile at a time (four blocks per lane and tile: both
+  // at once would spill)
+  constexpr bool TR = sizeof(T) == 4;
   // element offset of logical (row r, element e) in a float32 tile with `re`
   // elements per row, its 16-byte chunks XOR-swizzled by the row
   auto swz = [](int r, int e, int re) {
@@ -225,37 +226,78 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
     constexpr int BPL = TR ? NBLK / (64 * NP) : 1;          // blocks per producer lane
     static_assert(!TR || NBLK % (64 * NP) == 0, "blocks must split over the producers");
     f32x4 stW[BPL][4], stK[BPL][4];
-    auto tr_load = [&](int i) __attribute__((always_inline)) {
-      const size_t cid = chunk_id(i);
-      const float* w = reinterpret_cast<const float*>(a.W) + cid * BT * D;     // [t][d]
-      const float* k = reinterpret_cast<const float*>(a.KgT) + cid * D * BT;   // [d][t]
+    auto tr_load_w = [&](int i) __attribute__((always_inline)) {
+      const float* w = reinterpret_cast<const float*>(a.W) + chunk_id(i) * BT * D;  // [t][d]
+      int ln = lane;   // one tile buffer: the block offsets are recomputed per
+      if constexpr (NBUF == 1) asm volatile("" : "+v"(ln));   // staging, not kept live
 #pragma unroll
       for (int q = 0; q < BPL; ++q) {
-        const int b = (q * NP + p) * 64 + lane;
+        const int b = (q * NP + p) * 64 + ln;
         const int wt4 = b / (D / 4), wd4 = b % (D / 4);     // W rows 4 wt4 + r, columns 4 wd4
-        const int kd4 = b / (BT / 4), kt4 = b % (BT / 4);   // kg^T rows 4 kd4 + r, columns 4 kt4
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          stW[q][r] = load4f(w + (size_t)(4 * wt4 + r) * D + 4 * wd4);
-          stK[q][r] = load4f(k + (size_t)(4 * kd4 + r) * BT + 4 * kt4);
-        }
+        for (int r = 0; r < 4; ++r) stW[q][r] = load4f(w + (size_t)(4 * wt4 + r) * D + 4 * wd4);
       }
     };
-    auto tr_store = [&](char* base) __attribute__((always_inline)) {
-      float* wt = reinterpret_cast<float*>(base);            // W^T [d][t]
-      float* kt = reinterpret_cast<float*>(base + WBYTES);   // kg [t][d]
+    auto tr_load_k = [&](int i) __attribute__((always_inline)) {
+      const float* k = reinterpret_cast<const float*>(a.KgT) + chunk_id(i) * D * BT;  // [d][t]
+      int ln = lane;   // one tile buffer: the block offsets are recomputed per
+      if constexpr (NBUF == 1) asm volatile("" : "+v"(ln));   // staging, not kept live
 #pragma unroll
       for (int q = 0; q < BPL; ++q) {
-        const int b = (q * NP + p) * 64 + lane;
-        const int wt4 = b / (D / 4), wd4 = b % (D / 4);
-        const int kd4 = b / (BT / 4), kt4 = b % (BT / 4);
+        const int b = (q * NP + p) * 64 + ln;
+        const int kd4 = b / (BT / 4), kt4 = b % (BT / 4);   // kg^T rows 4 kd4 + r, columns 4 kt4
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int r = 0; r < 4; ++r) stK[q][r] = load4f(k + (size_t)(4 * kd4 + r) * BT + 4 * kt4);
+      }
+    };
+    auto tr_store_w = [&](char* base) __attribute__((always_inline)) {
+      float* wt = reinterpret_cast<float*>(base);            // W^T [d][t]
+      int ln = lane;   // one tile buffer: the block offsets are recomputed per
+      if constexpr (NBUF == 1) asm volatile("" : "+v"(ln));   // staging, not kept live
+#pragma unroll
+      for (int q = 0; q < BPL; ++q) {
+        const int b = (q * NP + p) * 64 + ln;
+        const int wt4 = b / (D / 4), wd4 = b % (D / 4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
           store4(&wt[swz(4 * wd4 + c, 4 * wt4, BT)],
                  f32x4{stW[q][0][c], stW[q][1][c], stW[q][2][c], stW[q][3][c]});
+      }
+    };
+    auto tr_store_k = [&](char* base) __attribute__((always_inline)) {
+      float* kt = reinterpret_cast<float*>(base + WBYTES);   // kg [t][d]
+      int ln = lane;   // one tile buffer: the block offsets are recomputed per
+      if constexpr (NBUF == 1) asm volatile("" : "+v"(ln));   // staging, not kept live
+#pragma unroll
+      for (int q = 0; q < BPL; ++q) {
+        const int b = (q * NP + p) * 64 + ln;
+        const int kd4 = b / (BT / 4), kt4 = b % (BT / 4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
           store4(&kt[swz(4 * kt4 + c, 4 * kd4, D)],
                  f32x4{stK[q][0][c], stK[q][1][c], stK[q][2][c], stK[q][3][c]});
-        }
+      }
+    };
+    auto tr_load = [&](int i) __attribute__((always_inline)) {
+      tr_load_w(i);
+      tr_load_k(i);
+    };
+    auto tr_store = [&](char* base) __attribute__((always_inline)) {
+      tr_store_w(base);
+      tr_store_k(base);
+    };
+    // g_last of chunk i into `gl`
+    auto gl_dma = [&](int i, float* gl) __attribute__((always_inline)) {
+      if (p == NP - 1 && lane < D / 4) lds_dma16(a.GL + chunk_id(i) * D + lane * 4, gl);
+    };
+    // dvp^T[col][t] of chunk i: compute wave w, row block it -> sDV[(w NB + it) 64 + lane]
+    auto gather_dv = [&](int i) __attribute__((always_inline)) {
+      const float* dsrc =
+          a.DVPT + chunk_id(i) * D * BT + (size_t)(vs * 16 * NW + li) * BT + 4 * lg;
+#pragma unroll
+      for (int j = 0; j < NW * NB / NP; ++j) {
+        const int q = j * NP + p, w = q / NB, it = q % NB;
+        lds_dma16(dsrc + (size_t)w * 16 * BT + it * 16, &sDV[q * 64]);
       }
     };
     // loads of chunk i: the tiles (DMA, or TR: into registers) and the gathers
@@ -280,14 +322,8 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
           lds_dma16(ksrc + (size_t)r * ROWB_K + ((pch ^ (r & M)) * 16), dst);
         }
       }
-      if (p == NP - 1 && lane < D / 4) lds_dma16(a.GL + cid * D + lane * 4, gl);
-      // dvp^T[col][t]: compute wave w, row block it -> sDV[(w NB + it) 64 + lane]
-      const float* dsrc = a.DVPT + cid * D * BT + (size_t)(vs * 16 * NW + li) * BT + 4 * lg;
-#pragma unroll
-      for (int j = 0; j < NW * NB / NP; ++j) {
-        const int q = j * NP + p, w = q / NB, it = q % NB;
-        lds_dma16(dsrc + (size_t)w * 16 * BT + it * 16, &sDV[q * 64]);
-      }
+      gl_dma(i, gl);
+      gather_dv(i);
       // (scale qg^T do)^T[col][d]: wave w, tile at -> sQD[(w NDT + at) 64 + lane]
       if constexpr (!QG) {
         const float* qsrc = a.QDOT + cid * D * D + (size_t)(vs * 16 * NW + li) * D + 4 * lg;
@@ -345,6 +381,50 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
           if (j * 64 + lane < D) gl[j * 64 + lane] = __expf(gl[j * 64 + lane]);
       }
     };
+    if constexpr (NBUF == 1 && TR) {
+      // One tile buffer, tiles through registers one at a time.  Chunk i+1's
+      // dvp gather and kg^T loads go out after B(i) (dvp(i) is in registers), its
+      // kg is stored after X(i) (the first product has read kg(i)) and its W loads
+      // issued; g_last after E(i) (the dh update has read e^{g_last}(i)); W and
+      // e^{g_last} are stored after A(i+1), before X(i+1) where the dh update
+      // starts reading them.  Register results are waited for by the compiler; the
+      // LDS-DMA gathers before the barrier that publishes them.
+      if (n > 0) {
+        gather_dv(0);
+        gl_dma(0, sGL0);
+        tr_load_k(0);
+        tr_store_k(sbuf0);
+        __builtin_amdgcn_sched_barrier(0);
+        tr_load_w(0);
+      }
+      if (n > 1) touch(1);
+      for (int i = 0; i < n; ++i) {
+        if (i == 0) wait_vmcnt<0>();   // chunk 0's gather, g_last and W
+        barrier();  // A(i)
+        if (i > 0) wait_step(i);       // g_last(i): only the touches may be outstanding
+        tr_store_w(sbuf0);
+        exp_gl(sGL0);
+        barrier();  // B(i)
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < n) {
+          gather_dv(i + 1);
+          tr_load_k(i + 1);
+        }
+        barrier();  // X(i)
+        if (i + 1 < n) {
+          tr_store_k(sbuf0);   // waits for the kg loads and so for the gather issued before
+          // one tile's registers at a time: the W loads stay behind the kg stores
+          __builtin_amdgcn_sched_barrier(0);
+          tr_load_w(i + 1);
+        }
+        barrier();  // E(i): chunk i's W and e^{g_last} are no longer read
+        if (i + 1 < n) {
+          gl_dma(i + 1, sGL0);
+          if (i + 2 < n) touch(i + 2);
+        }
+      }
+      return;
+    }
     // The dvp / qdot buffer is single: the next chunk's gather goes out after B.
     if (n > 0) issue(0, sbuf0, sGL0);
     if (n > 1) touch(1);
