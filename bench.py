@@ -505,10 +505,31 @@ def extras(gp, steps=10, warmup=3):
     state = torch.zeros((B, H, D, D), device="cuda")
     ms_d = _time(lambda: gp.gdn2_decode_step(*tok, D ** -0.5, state=state, inplace=True),
                  100, 10)
+    # the same step captured in a HIP graph (static token buffers, state updated in
+    # place): one step per replay, and 16 steps per replay (time per token)
+    st_g = torch.zeros_like(state)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        gp.gdn2_decode_step(*tok, D ** -0.5, state=st_g, inplace=True)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g1, g16 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        gp.gdn2_decode_step(*tok, D ** -0.5, state=st_g, inplace=True)
+    with torch.cuda.graph(g16):
+        for _ in range(16):
+            gp.gdn2_decode_step(*tok, D ** -0.5, state=st_g, inplace=True)
+    us_g1 = _time(g1.replay, 200, 20) * 1e3
+    us_g16 = _time(g16.replay, 50, 5) * 1e3 / 16
     res["decode_step"] = {"shape": "B8 H6 D128, one token", "call_us": ms_d * 1e3,
-                          "note": "per call, Python wrapper and launch included (host-bound); "
-                                  "the kernel (decode_step, 6.3 MB of fp32 state read and "
-                                  "written) is timed by rocprofv3 in profiles/"}
+                          "graph_replay_us": us_g1, "graph_16_steps_us_per_token": us_g16,
+                          "note": "call_us per eager call, Python wrapper and launch included "
+                                  "(host-bound); graph_*: the step captured in a HIP graph, "
+                                  "one or 16 steps per replay; the kernel (decode_step, 6.3 MB "
+                                  "of fp32 state read and written) is timed by rocprofv3 in "
+                                  "profiles/"}
+    del g1, g16
     return res
 
 
