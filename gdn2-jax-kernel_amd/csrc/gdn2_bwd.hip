@@ -950,19 +950,19 @@ __global__ void __launch_bounds__(256, 2) bwd_wy(WyArgs<T, TG, TI> a) {
       for (int kg = 0; kg < NDT; ++kg) {
 #pragma unroll
         for (int nt = 0; nt < NDH; ++nt) {
-          const f32x4 y = colop(sR1, LDH, kg * 16, nt * 16);   // h[d][e] as (n = d, k = e)
-          mma(aq[nt], xdo[kg], y);
-          mma(aw[nt], xdv[kg], y);
+          // h[d][e] as the row operand (rows d, k = e): the lane's sums are 4
+          // consecutive channels d of its own token t, stored as one 16-byte run
+          const f32x4 y = colop(sR1, LDH, kg * 16, nt * 16);
+          mma(aq[nt], y, xdo[kg]);
+          mma(aw[nt], y, xdv[kg]);
         }
       }
       float* dqg = a.DQG + (size_t)cid * BT * D + d0;
 #pragma unroll
-      for (int nt = 0; nt < NDH; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          dqg[orow(r) * D + nt * 16 + li] = a.scale * aq[nt][r];
-          sW[orow(r) * LDH + nt * 16 + li] = -aw[nt][r];
-        }
+      for (int nt = 0; nt < NDH; ++nt) {
+        store4(dqg + (size_t)t * D + nt * 16 + 4 * lg, a.scale * aq[nt]);
+        store4(&sW[t * LDH + nt * 16 + 4 * lg], -aw[nt]);
+      }
     }
 
     // ---- 2. dkg = v_new dh'^T, sum_e dh'[d][e] h[d][e] (columns d of the half) --
@@ -1000,13 +1000,11 @@ __global__ void __launch_bounds__(256, 2) bwd_wy(WyArgs<T, TG, TI> a) {
       for (int kg = 0; kg < NDT; ++kg) {
 #pragma unroll
         for (int nt = 0; nt < NDH; ++nt)
-          mma(ak[nt], xvn[kg], colop(sR1, LDH, kg * 16, nt * 16));
+          mma(ak[nt], colop(sR1, LDH, kg * 16, nt * 16), xvn[kg]);   // token t, 4 channels
       }
       float* dkg = a.DKG + (size_t)cid * BT * D + d0;
 #pragma unroll
-      for (int nt = 0; nt < NDH; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dkg[orow(r) * D + nt * 16 + li] = ak[nt][r];
+      for (int nt = 0; nt < NDH; ++nt) store4(dkg + (size_t)t * D + nt * 16 + 4 * lg, ak[nt]);
     }
     // step 3's inputs (channels of the half)
     constexpr int NJ = NDH;
@@ -1112,32 +1110,30 @@ __global__ void __launch_bounds__(256, 2) bwd_wy(WyArgs<T, TG, TI> a) {
           const f32x4 x = colop(sA, LD4, kt * 16, wv * 16);   // A^T rows m, k = t
 #pragma unroll
           for (int nt = 0; nt < NDH; ++nt) {
-            mma(akb[nt], x, colop(sW, LDH, kt * 16, nt * 16));   // dW[t][d] as (n = d, k = t)
-            mma(awv[nt], x, rowop(sDV, LD4, nt * 16, kt * 16));  // dv_new^T[e][t]
+            // the channel operand as the rows: the lane's sums are 4 consecutive
+            // channels of token m = 16 w + li
+            mma(akb[nt], colop(sW, LDH, kt * 16, nt * 16), x);   // dW[t][d] as (rows d, k = t)
+            mma(awv[nt], rowop(sDV, LD4, nt * 16, kt * 16), x);  // dv_new^T[e][t]
           }
         }
       }
       // dv = d(wv) w, dw = d(wv) v: w and v re-read in this layout (L2: step 3
       // read them), so the element-wise pass does not need them
       float* dkbd = a.DKBD + (size_t)cid * BT * D + d0;
-      float wl[NDH][4], vl[NDH][4];
+      f32x4 wl[NDH], vl[NDH];
 #pragma unroll
-      for (int nt = 0; nt < NDH; ++nt)
+      for (int nt = 0; nt < NDH; ++nt) {
+        const size_t o = tok0 + (size_t)t * HD + d0 + nt * 16 + 4 * lg;
+        wl[nt] = load4f(a.w + o);
+        vl[nt] = load4f(a.v + o);
+      }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const size_t o = tok0 + (size_t)orow(r) * HD + d0 + nt * 16 + li;
-          wl[nt][r] = to_f(a.w[o]);
-          vl[nt][r] = to_f(a.v[o]);
-        }
-#pragma unroll
-      for (int nt = 0; nt < NDH; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const size_t o = tok0 + (size_t)orow(r) * HD + d0 + nt * 16 + li;
-          dkbd[orow(r) * D + nt * 16 + li] = akb[nt][r];
-          a.dv[o] = from_f<TI>(sanitize(awv[nt][r] * wl[nt][r]));
-          a.dw[o] = from_f<TI>(sanitize(awv[nt][r] * vl[nt][r]));
-        }
+      for (int nt = 0; nt < NDH; ++nt) {
+        const size_t o = tok0 + (size_t)t * HD + d0 + nt * 16 + 4 * lg;
+        store4(dkbd + (size_t)t * D + nt * 16 + 4 * lg, akb[nt]);
+        store4(a.dv + o, sanitize4(awv[nt] * wl[nt]));
+        store4(a.dw + o, sanitize4(awv[nt] * vl[nt]));
+      }
     }
   }
 
