@@ -19,7 +19,8 @@ ROOT = HERE.parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 OUT = HERE / "gdn2_package" / "libgdn2_hip.so"
-SOURCES = ["gdn2_api.cpp", "gdn2_fwd.hip", "gdn2_bwd.hip", "gdn2_decode.hip", "gdn2_noalloc.hip"]
+SOURCES = ["gdn2_api.cpp", "gdn2_fwd.hip", "gdn2_bwd.hip", "gdn2_decode.hip", "gdn2_noalloc.hip",
+           "gdn2_stage.hip"]
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are kept out of the generated code on purpose.

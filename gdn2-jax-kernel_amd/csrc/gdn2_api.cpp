@@ -8,6 +8,7 @@
 #include "gdn2.h"
 #include "gdn2_common.h"
 #include "gdn2_layout.h"
+#include "gdn2_stage.h"
 
 namespace gdn2 {
 
@@ -25,6 +26,29 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       const char* fws, char* ws, const int* cu_chunks, int nseq);
 
 size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t elem);
+template <int D>
+hipError_t launch_stage_dav(hipStream_t st, int B, int N, int H, const float* aqk,
+                            const float* v_new, const float* dout, float* daqk, float* dv_new,
+                            char* ws, size_t* need);
+template <int D>
+hipError_t launch_stage_dhu(hipStream_t st, int B, int N, int H, const float* dout,
+                            const float* dv_partial, const float* w_pseudo, const float* qg,
+                            const float* kg, const float* gc_last, float scale,
+                            const float* dht, float* dh_all, float* dh0, float* dv_all,
+                            char* ws, size_t* need);
+template <int D>
+hipError_t launch_stage_wy_dqkg(hipStream_t st, int B, int N, int H, const float* q,
+                                const float* k, const float* b, const float* w, const float* v,
+                                const float* gc, const float* A, const float* h_pre,
+                                const float* v_new, const float* dout, const float* dv,
+                                const float* dh_next, float scale, float* dq, float* dk,
+                                float* db, float* dw, float* dv_raw, float* dgc, float* dakk,
+                                char* ws, size_t* need);
+template <int D>
+hipError_t launch_stage_intra(hipStream_t st, int B, int T_len, int H, const float* daqk,
+                              const float* dakk, const float* q, const float* k, const float* b,
+                              const float* g, float scale, float* dq, float* dk, float* db,
+                              float* dgc, char* ws, size_t* need);
 template <typename TG, int D, typename TI>
 hipError_t launch_stage_scores(hipStream_t st, int B, int T_len, int H, const void* q,
                                const void* k, const void* b, const void* g, float scale,
@@ -538,6 +562,149 @@ int gdn2_chunk_combine(void* stream, int B, int N, int H, int D, int BT, const f
                                   h_final, h_pre_all, v_new_all, (char*)ws);
   return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
+
+// ---- backward stages ------------------------------------------------------------
+// Shapes of the backward stage entry points: those of gdn2_chunk_combine (float32,
+// chunk 64, N chunks of 64 tokens per sequence, the D x D tile transposes within
+// a 31-bit grid, the largest of their grids).
+static int validate_bstage(int B, int N, int H, int D, int BT) {
+  return validate_combine(B, N, H, D, BT);
+}
+
+// Dispatch of a backward stage launcher on D.
+#define GDN2_BSTAGE_CALL(fn, ...)                                   \
+  (D == 64 ? fn<64>(__VA_ARGS__) : D == 128 ? fn<128>(__VA_ARGS__) \
+                                            : fn<256>(__VA_ARGS__))
+
+size_t gdn2_bwd_stage_workspace_bytes(int stage, int B, int N, int H, int D, int BT) {
+  if (validate_bstage(B, N, H, D, BT) != GDN2_OK) return 0;
+  size_t need = 0;
+  hipStream_t st = nullptr;
+  switch (stage) {
+    case GDN2_STAGE_DHU:
+      GDN2_BSTAGE_CALL(launch_stage_dhu, st, B, N, H, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, nullptr, 1.f, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       &need);
+      break;
+    case GDN2_STAGE_DAV:
+      GDN2_BSTAGE_CALL(launch_stage_dav, st, B, N, H, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, nullptr, &need);
+      break;
+    case GDN2_STAGE_WY:
+      GDN2_BSTAGE_CALL(launch_stage_wy_dqkg, st, B, N, H, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       1.f, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, &need);
+      break;
+    case GDN2_STAGE_INTRA:
+      GDN2_BSTAGE_CALL(launch_stage_intra, st, B, N * 64, H, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, nullptr, 1.f, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       &need);
+      break;
+    default:
+      return 0;
+  }
+  return need;
+}
+
+// The workspace check shared by the backward stage entry points.
+static int check_bstage_ws(int stage, int B, int N, int H, int D, int BT, const void* ws,
+                           size_t ws_bytes) {
+  const size_t need = gdn2_bwd_stage_workspace_bytes(stage, B, N, H, D, BT);
+  if (need > 0 && !ws) return GDN2_ERR_NULL;
+  if (need > 0 && ((uintptr_t)ws & 15u)) return GDN2_ERR_ALIGN;
+  return ws_bytes < need ? GDN2_ERR_WORKSPACE : GDN2_OK;
+}
+
+int gdn2_bwd_dhu(void* stream, int B, int N, int H, int D, int BT, const float* dout,
+                 const float* dv_partial, const float* w_pseudo, const float* qg,
+                 const float* kg, const float* gc_last, float scale, const float* dht,
+                 float* dh_all, float* dh0, float* dv_all, void* ws, size_t ws_bytes) {
+  EventScope scope;
+  int rc = validate_bstage(B, N, H, D, BT);
+  if (rc) return rc;
+  if (N > 0 && (rc = check_ptrs({dout, dv_partial, w_pseudo, qg, kg, gc_last, dh_all, dv_all})))
+    return rc;
+  if ((rc = check_ptrs({dh0}))) return rc;
+  if ((rc = check_opt({dht}))) return rc;
+  if ((rc = check_bstage_ws(GDN2_STAGE_DHU, B, N, H, D, BT, ws, ws_bytes))) return rc;
+  size_t unused = 0;
+  const hipError_t e = GDN2_BSTAGE_CALL(launch_stage_dhu, (hipStream_t)stream, B, N, H, dout,
+                                        dv_partial, w_pseudo, qg, kg, gc_last, scale, dht,
+                                        dh_all, dh0, dv_all, (char*)ws, &unused);
+  return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_bwd_dav(void* stream, int B, int N, int H, int D, int BT, const float* aqk,
+                 const float* v_new, const float* dout, float* daqk, float* dv_new, void* ws,
+                 size_t ws_bytes) {
+  EventScope scope;
+  int rc = validate_bstage(B, N, H, D, BT);
+  if (rc) return rc;
+  if (N == 0) return GDN2_OK;
+  if ((rc = check_ptrs({aqk, v_new, dout, daqk, dv_new}))) return rc;
+  if ((rc = check_bstage_ws(GDN2_STAGE_DAV, B, N, H, D, BT, ws, ws_bytes))) return rc;
+  size_t unused = 0;
+  const hipError_t e = GDN2_BSTAGE_CALL(launch_stage_dav, (hipStream_t)stream, B, N, H, aqk,
+                                        v_new, dout, daqk, dv_new, (char*)ws, &unused);
+  return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_bwd_wy_dqkg(void* stream, int B, int N, int H, int D, int BT, const float* q,
+                     const float* k, const float* b, const float* w, const float* v,
+                     const float* gc, const float* a, const float* h_pre_all,
+                     const float* v_new_all, const float* dout, const float* dv,
+                     const float* dh_next_all, float scale, float* dq, float* dk, float* db,
+                     float* dw, float* dv_raw, float* dgc, float* dakk, void* ws,
+                     size_t ws_bytes) {
+  EventScope scope;
+  int rc = validate_bstage(B, N, H, D, BT);
+  if (rc) return rc;
+  if (N == 0) return GDN2_OK;
+  if ((rc = check_ptrs({q, k, b, w, v, gc, a, h_pre_all, v_new_all, dout, dv, dh_next_all})))
+    return rc;
+  if ((rc = check_ptrs({dq, dk, db, dw, dv_raw, dgc, dakk}))) return rc;
+  if ((rc = check_bstage_ws(GDN2_STAGE_WY, B, N, H, D, BT, ws, ws_bytes))) return rc;
+  size_t unused = 0;
+  const hipError_t e = GDN2_BSTAGE_CALL(
+      launch_stage_wy_dqkg, (hipStream_t)stream, B, N, H, q, k, b, w, v, gc, a, h_pre_all,
+      v_new_all, dout, dv, dh_next_all, scale, dq, dk, db, dw, dv_raw, dgc, dakk, (char*)ws,
+      &unused);
+  return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_bwd_intra(void* stream, int B, int T, int H, int D, int BT, const float* daqk,
+                   const float* dakk, const float* q, const float* k, const float* b,
+                   const float* g, float scale, float* dq, float* dk, float* db, float* dgc,
+                   void* ws, size_t ws_bytes) {
+  EventScope scope;
+  if (T < 0 || BT != 64) return BT != 64 ? GDN2_ERR_CHUNK : GDN2_ERR_SHAPE;
+  if (T % 64 != 0) return GDN2_ERR_SEQ_LEN;
+  const int N = T / 64;
+  int rc = validate_bstage(B, N, H, D, BT);
+  if (rc) return rc;
+  if (N == 0) return GDN2_OK;
+  if ((rc = check_ptrs({daqk, dakk, q, k, b, g, dq, dk, db, dgc}))) return rc;
+  if ((rc = check_bstage_ws(GDN2_STAGE_INTRA, B, N, H, D, BT, ws, ws_bytes))) return rc;
+  size_t unused = 0;
+  const hipError_t e = GDN2_BSTAGE_CALL(launch_stage_intra, (hipStream_t)stream, B, T, H, daqk,
+                                        dakk, q, k, b, g, scale, dq, dk, db, dgc, (char*)ws,
+                                        &unused);
+  return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_bwd_reverse_cumsum(void* stream, long long tiles, int BT, int D, const float* dgc,
+                            float* dg) {
+  EventScope scope;
+  if (tiles < 0 || BT < 1 || D < 1 || BT > 4096 || D > 65536) return GDN2_ERR_SHAPE;
+  if ((double)tiles * BT * D > 9.0e15) return GDN2_ERR_SHAPE;
+  if (tiles == 0) return GDN2_OK;
+  if (!dgc || !dg) return GDN2_ERR_NULL;
+  if (((uintptr_t)dgc & 3u) || ((uintptr_t)dg & 3u)) return GDN2_ERR_ALIGN;
+  reverse_cumsum((hipStream_t)stream, dgc, dg, (size_t)tiles, BT, D);
+  return hipGetLastError() == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+#undef GDN2_BSTAGE_CALL
 
 int gdn2_decode(void* stream, int B, int H, int D, int in_dtype, int g_dtype, const void* q,
                 const void* k, const void* v, const void* w, const void* b, const void* g,

@@ -15,6 +15,7 @@
 
 #include "gdn2_common.h"
 #include "gdn2_layout.h"
+#include "gdn2_stage.h"
 
 namespace gdn2 {
 
@@ -683,7 +684,12 @@ struct B2Args {
   float *DAQK, *DVPT, *QDOT;
 };
 
-template <typename T, int D>
+// What one bwd_b2 launch forms: all three products (the fused backward), or for
+// the stage entry points only B2's dAqk and Aqk^T do (dav_backward_pallas) or only
+// B1's scale qg^T do (gdn2_dhu_backward).
+enum B2Mode { kB2All = 0, kB2Dav = 1, kB2Qdot = 2 };
+
+template <typename T, int D, int B2M = kB2All>
 __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
   constexpr int BT = 64, NDT = D / 16, NKT = BT / 16;
   constexpr int LDO = D + 4, LDV = BT + 4, LDA = BT + 4, LDQ = D + 4;
@@ -721,15 +727,16 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
     // Aqk: blocks right of the diagonal block are unwritten; causal mask on load
     const GMat mA{a.Aqk, BF, BT, 1, 0};
     stage_load(s1, mDo, tok0, BT, D, tid);
-    stage_load(s2, mV, (size_t)cid * D * BT, D, BT, tid);
+    if constexpr (B2M != kB2Qdot) stage_load(s2, mV, (size_t)cid * D * BT, D, BT, tid);
     stage_store(sDo, LDO, s1, mDo, BT, D, 0, 0, false, tid);
-    stage_store(sV, LDV, s2, mV, D, BT, 0, 0, false, tid);
+    if constexpr (B2M != kB2Qdot) stage_store(sV, LDV, s2, mV, D, BT, 0, 0, false, tid);
     // qg and Aqk are in flight while dAqk is formed (LDS-only barriers); at
     // D = 256 qg (64 KB) is loaded after the Aqk^T do product instead, which
     // would otherwise spill the registers that hold it
-    if constexpr (D <= 128) stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
-    stage_load(s2, mA, (size_t)cid * BT * BT, BT, BT, tid);
+    if constexpr (D <= 128 && B2M != kB2Dav) stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
+    if constexpr (B2M != kB2Qdot) stage_load(s2, mA, (size_t)cid * BT * BT, BT, BT, tid);
     lds_barrier();
+    if constexpr (B2M != kB2Qdot) {
     // dAqk[t][s] = sum_e do[t][e] v_new[s][e], s <= t: column blocks right of
     // the own row block are zero and not formed
     {
@@ -754,8 +761,10 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
     }
     lds_barrier();  // every wave is done with v_new^T
     stage_store(sA, LDA, s2, mA, BT, BT, 0, 0, false, tid);
+    }  // B2M != kB2Qdot
   }
   lds_barrier();
+  if constexpr (B2M != kB2Qdot) {
   // dvp^T[e][s] = sum_t Aqk[t][s] do[t][e]: rows s of the own block, stored as
   // [e][s]; Aqk[t][s] = 0 for t < s, so token blocks before the own one add nothing
   // (with dAqk's skipped blocks: 5 of 8 block-products per wave, on every wave)
@@ -775,6 +784,8 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
     for (int nt = 0; nt < NDT; ++nt)
       store4(o + (size_t)(nt * 16 + li) * BT + wv * 16 + 4 * lg, sanitize4(acc[nt]));  // :96
   }
+  }  // B2M != kB2Qdot
+  if constexpr (B2M == kB2Dav) return;
   if constexpr (D > 128) stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
   lds_barrier();  // every wave is done with Aqk
   stage_store(sQ, LDQ, s1, mQ, BT, D, 0, 0, false, tid);
@@ -1324,7 +1335,14 @@ struct GramArgs {
 // sharing the chunk's dAqk / dAkk tiles in its L2.
 constexpr int gram_panel() { return 32; }
 
-template <typename T, typename TG, int D, typename TI>
+// What one gram_bwd launch forms: the fused B4 + B3 tail + B5 (kGramAll), or for
+// the stage entry points B3's element-wise tail alone (kGramB3: the score
+// gradients taken as zero; wy_dqkg_backward_pallas's dq, dk, db, dgc) or B4 alone
+// (kGramB4: the B3 partials taken as zero; intra_backward_pallas), both writing
+// dgc per token (no B5) into `dg`.
+enum GramMode { kGramAll = 0, kGramB3 = 1, kGramB4 = 2 };
+
+template <typename T, typename TG, int D, typename TI, int GM = kGramAll>
 __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
   constexpr int BT = 64, NB = 4, GP = gram_panel(), NPN = D / GP, NDT = GP / 16, DQ = GP / 4;
   constexpr int LD1 = GP + 4, LD2 = BT + 4;
@@ -1368,8 +1386,12 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
 #pragma unroll
     for (int u = 0; u < SU; ++u) {
       const int i = tid + 256 * u, r = i / (BT / 4), cc = (i % (BT / 4)) * 4;
-      sq[u] = load4f(dq + r * BT + cc);
-      sk[u] = load4f(dk + r * BT + cc);
+      if constexpr (GM == kGramB3) {
+        sq[u] = sk[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      } else {
+        sq[u] = load4f(dq + r * BT + cc);
+        sk[u] = load4f(dk + r * BT + cc);
+      }
     }
 #pragma unroll
     for (int j = 0; j < NDT; ++j) load_f<4>(a.g + rowo + j * 16 + lg * 4, &loc[j * 4]);
@@ -1475,10 +1497,14 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
 #pragma unroll
   for (int j = 0; j < NDT; ++j) {
     const int c0 = j * 16 + lg * 4;
-    pdqg[j] = load4f(a.DQG + wrow_t + c0);
-    pdkg[j] = load4f(a.DKG + wrow_t + c0);
-    pdkbd[j] = load4f(a.DKBD + wrow_t + c0);
-    psdh[j] = load4f(a.SDH + (size_t)cid * D + ch0 + c0);
+    if constexpr (GM == kGramB4) {
+      pdqg[j] = pdkg[j] = pdkbd[j] = psdh[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      pdqg[j] = load4f(a.DQG + wrow_t + c0);
+      pdkg[j] = load4f(a.DKG + wrow_t + c0);
+      pdkbd[j] = load4f(a.DKBD + wrow_t + c0);
+      psdh[j] = load4f(a.SDH + (size_t)cid * D + ch0 + c0);
+    }
   }
   lds_barrier();
 
@@ -1674,13 +1700,18 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       const float dgc4 = ag4[e];
       // the last token's B3 part still lacks the g_last terms: kept for the end
       if (I == NB - 1 && li == 15) sB3L[c0 + e] = dgc3;
-      suf[e] = row_suffix16(sanitize(dgc3) + sanitize(dgc4));
+      if constexpr (GM == kGramAll) {
+        suf[e] = row_suffix16(sanitize(dgc3) + sanitize(dgc4));
+      } else {   // dgc per token (one of the two parts is zero)
+        suf[e] = sanitize(dgc3) + sanitize(dgc4);
+      }
       const float skg = row_suffix16(dkg[e] * kgv);   // lane 0: the block's sum
       if (li == 0) {
         sETot[I * GP + c0 + e] = suf[e];
         sSkg[I * GP + c0 + e] = skg;
       }
     }
+    if constexpr (GM != kGramAll) store4(a.dg + rowo + c0, suf);
     store4(&sAQ[t * LD1 + c0], suf);   // in place of gq, read by this lane only
     store4(a.dq + rowo + c0, odq);
     store4(a.dk + rowo + c0, odk);
@@ -1713,11 +1744,16 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
     for (int e = 0; e < 4; ++e) {
       const float dgl = skg[e] + __expf(gl[e]) * sdh[e];
       const float b3 = b3l[e], b3g = b3 + dgl;
-      const float corr = (fabsf(b3) < kClip && fabsf(b3g) < kClip)
-                             ? dgl : sanitize(b3g) - sanitize(b3);
-      odg[e] = sanitize(suf[e] + later[e] + corr);
+      if constexpr (GM == kGramAll) {
+        const float corr = (fabsf(b3) < kClip && fabsf(b3g) < kClip)
+                               ? dgl : sanitize(b3g) - sanitize(b3);
+        odg[e] = sanitize(suf[e] + later[e] + corr);
+      } else {   // the last token: B3's dgc with the g_last terms (gdn2_bwd.py:199-201)
+        odg[e] = sanitize(b3g) + (suf[e] - sanitize(b3));
+      }
     }
-    store4(a.dg + rowo + c0, odg);
+    if constexpr (GM == kGramAll) store4(a.dg + rowo + c0, odg);
+    else if (t == BT - 1) store4(a.dg + rowo + c0, odg);
   }
 }
 
@@ -2176,6 +2212,195 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     return hipGetLastError();
   }
 }
+
+// ---------------------------------------------------------------------------
+// The reference's backward kernels one at a time (gdn2_bwd.py:32-342): float32,
+// chunk 64, the reference's (B,H,N,BT,.) chunk layouts.  The kernels read token
+// rows and transposed tiles, so each launcher copies its operands into `ws`
+// (chunk_rows_permute, transpose_all) and its results back.  With ws == nullptr a
+// launcher only reports the workspace it needs in *need.
+namespace {
+struct Bump {
+  char* base;
+  size_t off = 0;
+  float* take(size_t floats) {
+    const size_t o = off;
+    off = align256(off + floats * 4);
+    return base ? reinterpret_cast<float*>(base + o) : nullptr;
+  }
+};
+constexpr int SBT = 64;   // chunk of the stage entry points
+}  // namespace
+
+// B2, dav_backward_pallas: dAqk = (do v_new^T) . causal, dv_new = Aqk^T do (the causal
+// Aqk, as kernel A gives it).
+template <int D>
+hipError_t launch_stage_dav(hipStream_t st, int B, int N, int H, const float* aqk,
+                            const float* v_new, const float* dout, float* daqk, float* dv_new,
+                            char* ws, size_t* need) {
+  const size_t NC = (size_t)B * H * N;
+  Bump m{ws};
+  float* dtok = m.take(NC * SBT * D);
+  float* VnT = m.take(NC * D * SBT);
+  float* DVPT = m.take(NC * D * SBT);
+  if (!ws) { *need = m.off; return hipSuccess; }
+  if (NC == 0) return hipSuccess;
+  chunk_rows_permute(st, dout, dtok, B, H, N, SBT, D, true, false);
+  transpose_all(st, v_new, VnT, NC, SBT, D);
+  B2Args<float> ba{dtok, VnT, aqk, nullptr, N * SBT, H, N, 1.f, daqk, DVPT, nullptr};
+  hipLaunchKernelGGL((bwd_b2<float, D, kB2Dav>), dim3(NC), dim3(256), 0, st, ba);
+  transpose_all(st, DVPT, dv_new, NC, D, SBT);
+  return hipGetLastError();
+}
+
+// B1, gdn2_dhu_backward: the reverse state scan; dh_all[c] is the gradient of the
+// state entering chunk c (dh_all[0] = dh0), dv_all the chunks' dv_new.
+template <int D>
+hipError_t launch_stage_dhu(hipStream_t st, int B, int N, int H, const float* dout,
+                            const float* dv_partial, const float* w_pseudo, const float* qg,
+                            const float* kg, const float* gc_last, float scale,
+                            const float* dht, float* dh_all, float* dh0, float* dv_all,
+                            char* ws, size_t* need) {
+  const size_t NC = (size_t)B * H * N, BH = (size_t)B * H;
+  Bump m{ws};
+  float* dtok = m.take(NC * SBT * D);
+  float* QDOT = m.take(NC * D * D);
+  float* DVPT = m.take(NC * D * SBT);
+  float* KgT = m.take(NC * D * SBT);
+  float* DHT = m.take(NC * D * D);
+  float* DVNT = m.take(NC * D * SBT);
+  if (!ws) { *need = m.off; return hipSuccess; }
+  if (N == 0) {   // no chunk: dh0 = sanitize(dht) (the scan's initial carry)
+    sanitized_copy(st, dht, dh0, BH * D * D);
+    return hipGetLastError();
+  }
+  if (NC > 0) {
+    chunk_rows_permute(st, dout, dtok, B, H, N, SBT, D, true, false);
+    B2Args<float> ba{dtok, nullptr, nullptr, qg, N * SBT, H, N, scale, nullptr, nullptr, QDOT};
+    hipLaunchKernelGGL((bwd_b2<float, D, kB2Qdot>), dim3(NC), dim3(256), 0, st, ba);
+    transpose_all(st, dv_partial, DVPT, NC, SBT, D);
+    transpose_all(st, kg, KgT, NC, SBT, D);
+  }
+  BStateArgs<float> sa{w_pseudo, KgT, gc_last, DVPT, QDOT, dht, N, DHT, DVNT, dh0, nullptr, 1, H};
+  constexpr int BW = 2, BK = bstate_ksplit<float, D>(), BP = BK > 1 ? 4 : 2;
+  hipLaunchKernelGGL((bwd_state<float, SBT, D, BW, BP, BK>), dim3(BH * (D / (16 * BW))),
+                     dim3(64 * (BW * BK + BP)), 0, st, sa);
+  if (NC > 0) {
+    // DHT[c] = dh_{c+1}^T: dh_all[c+1] = DHT[c]^T, and dh_all[0] = dh0
+    transpose_shift(st, DHT, dh_all, BH, N, D, D);
+    (void)hipMemcpy2DAsync(dh_all, (size_t)N * D * D * 4, dh0, (size_t)D * D * 4,
+                           (size_t)D * D * 4, BH, hipMemcpyDeviceToDevice, st);
+    transpose_all(st, DVNT, dv_all, NC, D, SBT);
+  }
+  return hipGetLastError();
+}
+
+// B3, wy_dqkg_backward_pallas: the gradients through the WY factors, kg and qg;
+// dgc per token (the g_last terms on each chunk's last token), dAkk.
+template <int D>
+hipError_t launch_stage_wy_dqkg(hipStream_t st, int B, int N, int H, const float* q,
+                                const float* k, const float* b, const float* w, const float* v,
+                                const float* gc, const float* A, const float* h_pre,
+                                const float* v_new, const float* dout, const float* dv,
+                                const float* dh_next, float scale, float* dq, float* dk,
+                                float* db, float* dw, float* dv_raw, float* dgc, float* dakk,
+                                char* ws, size_t* need) {
+  const size_t NC = (size_t)B * H * N, rows = NC * SBT * D;
+  Bump m{ws};
+  float* tq = m.take(rows);
+  float* tk = m.take(rows);
+  float* tb = m.take(rows);
+  float* tw = m.take(rows);
+  float* tv = m.take(rows);
+  float* tg = m.take(rows);
+  float* tdo = m.take(rows);
+  float* HT = m.take(NC * D * D);
+  float* VnT = m.take(NC * D * SBT);
+  float* DHT = m.take(NC * D * D);
+  float* DVNT = m.take(NC * D * SBT);
+  float* DQG = m.take(rows);
+  float* DKG = m.take(rows);
+  float* DKBD = m.take(rows);
+  float* SDH = m.take(NC * D);
+  float* oq = m.take(rows);
+  float* ok = m.take(rows);
+  float* ob = m.take(rows);
+  float* ow = m.take(rows);
+  float* ov = m.take(rows);
+  float* og = m.take(rows);
+  if (!ws) { *need = m.off; return hipSuccess; }
+  if (NC == 0) return hipSuccess;
+  const float* in[] = {q, k, b, w, v, dout};
+  float* tok[] = {tq, tk, tb, tw, tv, tdo};
+  for (int i = 0; i < 6; ++i) chunk_rows_permute(st, in[i], tok[i], B, H, N, SBT, D, true, false);
+  chunk_rows_permute(st, gc, tg, B, H, N, SBT, D, true, true);   // g from the cumsum
+  transpose_all(st, h_pre, HT, NC, D, D);
+  transpose_all(st, v_new, VnT, NC, SBT, D);
+  transpose_all(st, dh_next, DHT, NC, D, D);
+  transpose_all(st, dv, DVNT, NC, SBT, D);
+  const int T_len = N * SBT;
+  WyArgs<float, float, float> wa{tk,  tw,  tv,  tb,  tg,  tdo, HT,  VnT, A,  DHT, DVNT, T_len,
+                                 H,   N,   scale, DQG, DKG, DKBD, dakk, SDH, ov, ow};
+  if constexpr (D > 128)
+    hipLaunchKernelGGL((bwd_wy_wide<float, float, float>), dim3(NC), dim3(512), 0, st, wa);
+  else
+    hipLaunchKernelGGL((bwd_wy<float, float, D, float>), dim3(NC), dim3(256), 0, st, wa);
+  GramArgs<float, float, float> gr{tq,  tk,    tb, tg, nullptr, nullptr, SDH, DQG, DKG, DKBD,
+                                   T_len, H,   N,  scale, oq, ok, ob, og};
+  hipLaunchKernelGGL((gram_bwd<float, float, D, float, kGramB3>), dim3(NC * (D / gram_panel())),
+                     dim3(256), 0, st, gr);
+  const float* res[] = {oq, ok, ob, ow, ov, og};
+  float* outs[] = {dq, dk, db, dw, dv_raw, dgc};
+  for (int i = 0; i < 6; ++i) chunk_rows_permute(st, res[i], outs[i], B, H, N, SBT, D, false, false);
+  return hipGetLastError();
+}
+
+// B4, intra_backward_pallas: the gradients through the score blocks; q, k, b, g in
+// (B,T,H,D) as the reference takes them, dq, dk, db, dgc per chunk.
+template <int D>
+hipError_t launch_stage_intra(hipStream_t st, int B, int T_len, int H, const float* daqk,
+                              const float* dakk, const float* q, const float* k, const float* b,
+                              const float* g, float scale, float* dq, float* dk, float* db,
+                              float* dgc, char* ws, size_t* need) {
+  const int N = T_len / SBT;
+  const size_t NC = (size_t)B * H * N, rows = NC * SBT * D;
+  Bump m{ws};
+  float* oq = m.take(rows);
+  float* ok = m.take(rows);
+  float* ob = m.take(rows);
+  float* og = m.take(rows);
+  if (!ws) { *need = m.off; return hipSuccess; }
+  if (NC == 0) return hipSuccess;
+  GramArgs<float, float, float> gr{q,  k,     b,  g,  daqk, dakk, nullptr, nullptr, nullptr,
+                                   nullptr, T_len, H, N, scale, oq, ok, ob, og};
+  hipLaunchKernelGGL((gram_bwd<float, float, D, float, kGramB4>), dim3(NC * (D / gram_panel())),
+                     dim3(256), 0, st, gr);
+  const float* res[] = {oq, ok, ob, og};
+  float* outs[] = {dq, dk, db, dgc};
+  for (int i = 0; i < 4; ++i) chunk_rows_permute(st, res[i], outs[i], B, H, N, SBT, D, false, false);
+  return hipGetLastError();
+}
+
+#define GDN2_INST_BSTAGE(D)                                                                   \
+  template hipError_t launch_stage_dav<D>(hipStream_t, int, int, int, const float*,           \
+                                          const float*, const float*, float*, float*, char*,  \
+                                          size_t*);                                           \
+  template hipError_t launch_stage_dhu<D>(hipStream_t, int, int, int, const float*,           \
+                                          const float*, const float*, const float*,           \
+                                          const float*, const float*, float, const float*,    \
+                                          float*, float*, float*, char*, size_t*);             \
+  template hipError_t launch_stage_wy_dqkg<D>(                                                \
+      hipStream_t, int, int, int, const float*, const float*, const float*, const float*,     \
+      const float*, const float*, const float*, const float*, const float*, const float*,     \
+      const float*, const float*, float, float*, float*, float*, float*, float*, float*,      \
+      float*, char*, size_t*);                                                                \
+  template hipError_t launch_stage_intra<D>(hipStream_t, int, int, int, const float*,         \
+                                            const float*, const float*, const float*,         \
+                                            const float*, const float*, float, float*,        \
+                                            float*, float*, float*, char*, size_t*);
+GDN2_INST_BSTAGE(64)
+GDN2_INST_BSTAGE(128)
+GDN2_INST_BSTAGE(256)
 
 #define GDN2_INST_BWD(T, TG, BT, D, TI)                                                    \
   template hipError_t launch_bwd<T, TG, BT, D, TI>(                                        \

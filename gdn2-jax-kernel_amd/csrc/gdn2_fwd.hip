@@ -28,6 +28,7 @@
 
 #include "gdn2_common.h"
 #include "gdn2_layout.h"
+#include "gdn2_stage.h"
 
 namespace gdn2 {
 
@@ -1876,29 +1877,6 @@ hipError_t launch_fwd(hipStream_t st, int B, int T_len, int H, const void* q, co
 // ---------------------------------------------------------------------------
 // The reference's forward stages one at a time: float32 tiles at chunk 64, the
 // reference's (B,H,N,BT,.) layouts.
-
-// dst[m][c][r] = src[m][r][c] for matrices of R x C float32 (R, C multiples of
-// 32), one 32 x 32 tile per workgroup; the grid covers the tiles of all matrices.
-__global__ void __launch_bounds__(256) tile_transpose(const float* __restrict__ src,
-                                                      float* __restrict__ dst, int R, int C) {
-  __shared__ float t[32][33];
-  const int tr = R / 32, tc = C / 32;
-  const size_t m = blockIdx.x / (size_t)(tr * tc);
-  const int rem = (int)(blockIdx.x % (size_t)(tr * tc));
-  const int r0 = rem / tc * 32, c0 = rem % tc * 32;
-  const float* s = src + m * R * C;
-  float* d = dst + m * R * C;
-  const int x = threadIdx.x & 31, y = threadIdx.x >> 5;
-  for (int j = y; j < 32; j += 8) t[j][x] = s[(size_t)(r0 + j) * C + c0 + x];
-  __syncthreads();
-  for (int j = y; j < 32; j += 8) d[(size_t)(c0 + j) * R + r0 + x] = t[x][j];
-}
-
-static void transpose_all(hipStream_t st, const float* src, float* dst, size_t n, int R, int C) {
-  if (n > 0)
-    hipLaunchKernelGGL(tile_transpose, dim3(n * (R / 32) * (C / 32)), dim3(256), 0, st, src, dst,
-                       R, C);
-}
 
 // Kernel A (build_chunk_scores_pallas): Aqk, Akk [cid][64][64].
 template <typename TG, int D, typename TI>

@@ -22,6 +22,11 @@ GDN2_BF16_F32 = 2   # bfloat16 inputs and gradients, float32 arithmetic and resi
 FWD_SAVE_A = 1
 FWD_RAW_INPUTS = 2
 FWD_PARTIAL_CHUNK = 4
+# gdn2_bwd_stage_workspace_bytes: which backward stage
+STAGE_DHU = 1
+STAGE_DAV = 2
+STAGE_WY = 3
+STAGE_INTRA = 4
 
 
 def FWD_SEGMENTS(n: int) -> int:
@@ -74,6 +79,15 @@ SIGNATURES = {
     "gdn2_chunk_combine_workspace_bytes": (_c_size, [_c_int] * 5),
     "gdn2_chunk_combine": (_c_int, [_vp] + [_c_int] * 5 + [_vp] * 7
                            + [_c_float, _vp, _vp, _vp, _vp, _vp, _c_size]),
+    "gdn2_bwd_stage_workspace_bytes": (_c_size, [_c_int] * 6),
+    "gdn2_bwd_dhu": (_c_int, [_vp] + [_c_int] * 5 + [_vp] * 6
+                     + [_c_float, _vp, _vp, _vp, _vp, _vp, _c_size]),
+    "gdn2_bwd_dav": (_c_int, [_vp] + [_c_int] * 5 + [_vp] * 6 + [_c_size]),
+    "gdn2_bwd_wy_dqkg": (_c_int, [_vp] + [_c_int] * 5 + [_vp] * 12 + [_c_float]
+                         + [_vp] * 8 + [_c_size]),
+    "gdn2_bwd_intra": (_c_int, [_vp] + [_c_int] * 5 + [_vp] * 6 + [_c_float]
+                       + [_vp] * 5 + [_c_size]),
+    "gdn2_bwd_reverse_cumsum": (_c_int, [_vp, ctypes.c_longlong, _c_int, _c_int, _vp, _vp]),
 }
 
 

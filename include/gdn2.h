@@ -274,6 +274,59 @@ int gdn2_chunk_combine(void* stream, int B, int N, int H, int D, int BT, const f
                        float* out, float* h_final, float* h_pre_all, float* v_new_all,
                        void* ws, size_t ws_bytes);
 
+/* ---- The backward's stages one at a time -----------------------------------
+ * The reference's backward module functions (gdn2_bwd.py:32-342), float32 on
+ * the reference's chunk layouts (B,H,N,64,.), chunk 64 (GDN2_ERR_CHUNK
+ * otherwise), D in {64, 128, 256}.  Each takes a device workspace of
+ * gdn2_bwd_stage_workspace_bytes(stage, ...) bytes for its layout copies (none
+ * for the reverse cumsum).  gdn2_bwd runs the same mathematics fused. */
+#define GDN2_STAGE_DHU 1   /* gdn2_bwd_dhu */
+#define GDN2_STAGE_DAV 2   /* gdn2_bwd_dav */
+#define GDN2_STAGE_WY 3    /* gdn2_bwd_wy_dqkg */
+#define GDN2_STAGE_INTRA 4 /* gdn2_bwd_intra */
+size_t gdn2_bwd_stage_workspace_bytes(int stage, int B, int N, int H, int D, int BT);
+
+/* B1: replaces gdn2_dhu_backward (gdn2_bwd.py:45-80).  do, dv_partial,
+ * w_pseudo, qg, kg (B,H,N,64,D), gc_last (B,H,N,D), dht (B,H,D,D) or NULL.
+ * dh_all (B,H,N,D,D): the gradient of the state entering each chunk (dh_all[0]
+ * = dh0); dh0 (B,H,D,D); dv_all (B,H,N,64,D). */
+int gdn2_bwd_dhu(void* stream, int B, int N, int H, int D, int BT, const float* dout,
+                 const float* dv_partial, const float* w_pseudo, const float* qg,
+                 const float* kg, const float* gc_last, float scale, const float* dht,
+                 float* dh_all, float* dh0, float* dv_all, void* ws, size_t ws_bytes);
+
+/* B2: replaces dav_backward_pallas (gdn2_bwd.py:99-122).  aqk (B,H,N,64,64),
+ * taken as causal (kernel A's output); v_new, do (B,H,N,64,D).  daqk (B,H,N,64,64),
+ * dv_new = aqk^T do (B,H,N,64,D). */
+int gdn2_bwd_dav(void* stream, int B, int N, int H, int D, int BT, const float* aqk,
+                 const float* v_new, const float* dout, float* daqk, float* dv_new, void* ws,
+                 size_t ws_bytes);
+
+/* B3: replaces wy_dqkg_backward_pallas (gdn2_bwd.py:213-244).  q, k, b, w, v,
+ * gc (the in-chunk cumsum of g), v_new_all, do, dv (B,H,N,64,D); a (B,H,N,64,64);
+ * h_pre_all, dh_next_all (B,H,N,D,D).  dq, dk, db, dw, dv_raw, dgc (B,H,N,64,D),
+ * dakk (B,H,N,64,64). */
+int gdn2_bwd_wy_dqkg(void* stream, int B, int N, int H, int D, int BT, const float* q,
+                     const float* k, const float* b, const float* w, const float* v,
+                     const float* gc, const float* a, const float* h_pre_all,
+                     const float* v_new_all, const float* dout, const float* dv,
+                     const float* dh_next_all, float scale, float* dq, float* dk, float* db,
+                     float* dw, float* dv_raw, float* dgc, float* dakk, void* ws,
+                     size_t ws_bytes);
+
+/* B4: replaces intra_backward_pallas (gdn2_bwd.py:342-375).  daqk, dakk
+ * (B,H,N,64,64); q, k, b, g (B,T,H,D) as the reference takes them.  dq, dk, db,
+ * dgc (B,H,N,64,D), the sub-block pair clipping of gdn2_bwd.py:287-328 included. */
+int gdn2_bwd_intra(void* stream, int B, int T, int H, int D, int BT, const float* daqk,
+                   const float* dakk, const float* q, const float* k, const float* b,
+                   const float* g, float scale, float* dq, float* dk, float* db, float* dgc,
+                   void* ws, size_t ws_bytes);
+
+/* B5: replaces reverse_cumsum_bwd (gdn2_bwd.py:32-41).  For `tiles` tiles of BT
+ * rows by D columns: dg[i] = sanitize(sum_{j >= i} dgc[j]), row-wise. */
+int gdn2_bwd_reverse_cumsum(void* stream, long long tiles, int BT, int D, const float* dgc,
+                            float* dg);
+
 #ifdef __cplusplus
 }
 #endif

@@ -185,6 +185,44 @@ int main() {
   }
   CHECK(gdn2_wy_solve(nullptr, 5, 128, fa, fo) == GDN2_ERR_CHUNK);
   CHECK(gdn2_wy_solve(nullptr, 5, 64, nullptr, fo) == GDN2_ERR_NULL);
+  // the backward stage entry points (kernels B1-B5 one at a time): workspace sizes
+  // stay finite and a workspace one byte short is refused before any launch
+  void* wsp = P(0xc00000);
+  for (int B : Bs)
+    for (int T : Ts)
+      for (int D : Ds)
+        for (int BT : {0, 64, 128}) {
+          const int N = T / 64;
+          for (int stage = 0; stage <= 5; ++stage) {
+            const size_t need = gdn2_bwd_stage_workspace_bytes(stage, B, N, 3, D, BT);
+            CHECK(need < ((size_t)1 << 50));
+            if (need > 0) CHECK(stage >= 1 && stage <= 4 && BT == 64 && N >= 1 && B >= 1);
+          }
+          if (N <= 0) continue;   // B1 with no chunk writes dh0 = sanitize(dht)
+          const size_t w1 = gdn2_bwd_stage_workspace_bytes(GDN2_STAGE_DHU, B, N, 3, D, BT);
+          int rc = gdn2_bwd_dhu(nullptr, B, N, 3, D, BT, fa, fa, fa, fa, fa, fa, 0.1f, nullptr,
+                                fo, fh, fo, wsp, w1 ? w1 - 1 : 0);
+          CHECK(known(rc) && rc != GDN2_OK);
+          const size_t w2 = gdn2_bwd_stage_workspace_bytes(GDN2_STAGE_DAV, B, N, 3, D, BT);
+          rc = gdn2_bwd_dav(nullptr, B, N, 3, D, BT, fa, fa, fa, fo, fo, wsp, w2 ? w2 - 1 : 0);
+          CHECK(known(rc) && rc != GDN2_OK);
+          const size_t w3 = gdn2_bwd_stage_workspace_bytes(GDN2_STAGE_WY, B, N, 3, D, BT);
+          rc = gdn2_bwd_wy_dqkg(nullptr, B, N, 3, D, BT, fa, fa, fa, fa, fa, fa, fa, fa, fa, fa,
+                                fa, fa, 0.1f, fo, fo, fo, fo, fo, fo, fo, wsp, w3 ? w3 - 1 : 0);
+          CHECK(known(rc) && rc != GDN2_OK);
+          const size_t w4 = gdn2_bwd_stage_workspace_bytes(GDN2_STAGE_INTRA, B, N, 3, D, BT);
+          rc = gdn2_bwd_intra(nullptr, B, T, 3, D, BT, fa, fa, fa, fa, fa, fa, 0.1f, fo, fo, fo,
+                              fo, wsp, w4 ? w4 - 1 : 0);
+          CHECK(known(rc) && rc != GDN2_OK);
+        }
+  for (long long tiles : {LLONG_MIN, -1LL, (long long)INT_MAX, LLONG_MAX})
+    for (int bt : {-1, 0, 64, 4097})
+      for (int d : {0, 128, INT_MAX}) {
+        const int rc = gdn2_bwd_reverse_cumsum(nullptr, tiles, bt, d, fa, fo);
+        CHECK(known(rc));
+        if (rc == GDN2_OK || rc == GDN2_ERR_LAUNCH)   // only in-range shapes reach a launch
+          CHECK(tiles >= 0 && bt >= 1 && bt <= 4096 && d >= 1 && d <= 65536);
+      }
   for (int c = -20; c <= 5; ++c) CHECK(gdn2_strerror(c) != nullptr);
   CHECK(gdn2_set_launch_events(nullptr, -5) == 0);
   std::printf("host checks: %ld shape combinations, %d failures\n", n, g_fail);

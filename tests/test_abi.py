@@ -307,3 +307,60 @@ def test_stage_entry_points_reject_before_launch():
     assert cb((2, 8, 2, D, 64), hf=None) == _lib.ERR_NULL
     assert cb((2, 8, 2, D, 64), wsb=need - 1) == _lib.ERR_WORKSPACE
     assert cb((2, 8, 2, D, 64), ws=None) == _lib.ERR_NULL
+
+
+def test_backward_stage_entry_points_reject_before_launch():
+    """gdn2_bwd_dhu / _dav / _wy_dqkg / _intra / _reverse_cumsum (the reference's
+    kernels B1-B5 one at a time): chunk 64, D in {64, 128, 256}, then pointers and
+    the workspace (its size: the layout copies each stage makes), all before a
+    launch; zero chunks return at once, except B1 whose dh0 = sanitize(dht)."""
+    L = _lib.lib()
+    B, N, H, D = 2, 8, 2, 64
+    nc = B * H * N
+    rows, sq = nc * 64 * D * 4, nc * D * D * 4
+    ws = L.gdn2_bwd_stage_workspace_bytes
+    assert ws(_lib.STAGE_DAV, B, N, H, D, 64) == 3 * rows
+    assert ws(_lib.STAGE_DHU, B, N, H, D, 64) == 4 * rows + 2 * sq
+    assert ws(_lib.STAGE_WY, B, N, H, D, 64) == 18 * rows + 2 * sq + nc * D * 4
+    assert ws(_lib.STAGE_INTRA, B, N, H, D, 64) == 4 * rows
+    assert ws(9, B, N, H, D, 64) == 0 and ws(_lib.STAGE_DAV, B, N, H, D, 128) == 0
+    assert ws(_lib.STAGE_DAV, B, N, H, 96, 64) == 0
+    p = [0x100000 * (i + 1) for i in range(12)]
+    o = [0x900000 * (i + 1) for i in range(7)]
+    need = ws(_lib.STAGE_DAV, B, N, H, D, 64)
+    dav = lambda dims, a=p[0], w=0x7000000, wb=need: L.gdn2_bwd_dav(None, *dims, a, p[1], p[2],
+                                                                 o[0], o[1], w, wb)
+    assert dav((B, N, H, D, 128)) == _lib.ERR_CHUNK
+    assert dav((B, N, H, 96, 64)) == _lib.ERR_HEAD_DIM
+    assert dav((B, 1 << 26, H, D, 64)) == _lib.ERR_SHAPE
+    assert dav((B, N, H, D, 64), a=None) == _lib.ERR_NULL
+    assert dav((B, N, H, D, 64), wb=need - 1) == _lib.ERR_WORKSPACE
+    assert dav((B, N, H, D, 64), w=None) == _lib.ERR_NULL
+    assert dav((B, N, H, D, 64), w=0x7000008) == _lib.ERR_ALIGN
+    assert L.gdn2_bwd_dav(None, B, 0, H, D, 64, *[None] * 6, 0) == _lib.OK
+    need = ws(_lib.STAGE_DHU, B, N, H, D, 64)
+    dhu = lambda dims, d0=o[1], wb=need: L.gdn2_bwd_dhu(None, *dims, *p[:6], 0.125, None, o[0],
+                                                       d0, o[2], 0x7000000, wb)
+    assert dhu((B, N, H, D, 128)) == _lib.ERR_CHUNK
+    assert dhu((B, N, H, D, 64), d0=None) == _lib.ERR_NULL
+    assert dhu((B, N, H, D, 64), wb=0) == _lib.ERR_WORKSPACE
+    need = ws(_lib.STAGE_WY, B, N, H, D, 64)
+    wy = lambda dims, x=p, wb=need: L.gdn2_bwd_wy_dqkg(None, *dims, *x, 0.125, *o, 0x7000000,
+                                                       wb)
+    assert wy((B, N, H, 128, 128)) == _lib.ERR_CHUNK
+    assert wy((B, N, H, D, 64), x=p[:11] + [None]) == _lib.ERR_NULL
+    assert wy((B, N, H, D, 64), wb=need - 256) == _lib.ERR_WORKSPACE
+    assert L.gdn2_bwd_wy_dqkg(None, B, 0, H, D, 64, *[None] * 12, 0.1, *[None] * 8, 0) == _lib.OK
+    need = ws(_lib.STAGE_INTRA, B, N, H, D, 64)
+    intra = lambda T, wb=need: L.gdn2_bwd_intra(None, B, T, H, D, 64, *p[:6], 0.125, *o[:4],
+                                               0x7000000, wb)
+    assert intra(N * 64 - 1) == _lib.ERR_SEQ_LEN
+    assert intra(-64) == _lib.ERR_SHAPE
+    assert intra(N * 64, wb=need - 1) == _lib.ERR_WORKSPACE
+    assert L.gdn2_bwd_intra(None, B, 0, H, D, 64, *[None] * 6, 0.1, *[None] * 5, 0) == _lib.OK
+    rc = L.gdn2_bwd_reverse_cumsum
+    assert rc(None, -1, 64, 128, 0x1000, 0x2000) == _lib.ERR_SHAPE
+    assert rc(None, 4, 0, 128, 0x1000, 0x2000) == _lib.ERR_SHAPE
+    assert rc(None, 4, 64, 128, None, 0x2000) == _lib.ERR_NULL
+    assert rc(None, 4, 64, 128, 0x1002, 0x2000) == _lib.ERR_ALIGN
+    assert rc(None, 0, 64, 128, None, None) == _lib.OK

@@ -198,3 +198,26 @@ def test_stage_functions_exist_and_refuse_other_chunks(monkeypatch):
         F.build_chunk_scores_pallas(q[0], q[1], q[4], q[5], 0.1)
     with pytest.raises(AssertionError, match="chunk 64"):
         F.wy_solve_pallas(torch.zeros(2, 64, 64))
+
+
+def test_backward_stage_functions_exist_and_check_shapes(monkeypatch):
+    """The reference's backward module functions (gdn2_bwd.py:32-375) are in
+    gdn2_package.gdn2_bwd; wrongly shaped tiles, a module BT override and tensors
+    off the ROCm device are refused before anything runs."""
+    import torch
+    from gdn2_package import gdn2_bwd as G, gdn2_fwd as F
+    for n in ("reverse_cumsum_bwd", "gdn2_dhu_backward", "dav_backward_pallas",
+              "wy_dqkg_backward_pallas", "intra_backward_pallas"):
+        assert callable(getattr(G, n)), n
+    t = torch.zeros(1, 2, 3, 64, 64)
+    with pytest.raises(AssertionError, match="end in"):
+        G.reverse_cumsum_bwd(torch.zeros(2, 32, 8), 64)
+    with pytest.raises(AssertionError, match="shape"):
+        G.dav_backward_pallas(torch.zeros(1, 2, 3, 64, 32), t, t)
+    with pytest.raises(AssertionError, match="divisible"):
+        G.intra_backward_pallas(t, t, *[torch.zeros(1, 100, 2, 64)] * 4, 0.1)
+    with pytest.raises(G.GDN2Error, match="ROCm"):
+        G.dav_backward_pallas(torch.zeros(1, 2, 3, 64, 64), t, t)
+    monkeypatch.setattr(F, "BT", 128)
+    with pytest.raises(AssertionError, match="chunk 64"):
+        G.gdn2_dhu_backward(t, t, t, t, t, torch.zeros(1, 2, 3, 64), 0.1)

@@ -15,7 +15,8 @@ import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 CSRC = ROOT / "gdn2-jax-kernel_amd" / "csrc"
-SOURCES = ["gdn2_api.cpp", "gdn2_fwd.hip", "gdn2_bwd.hip", "gdn2_decode.hip", "gdn2_noalloc.hip"]
+SOURCES = ["gdn2_api.cpp", "gdn2_fwd.hip", "gdn2_bwd.hip", "gdn2_decode.hip", "gdn2_noalloc.hip",
+           "gdn2_stage.hip"]
 
 
 def _tool(name):
