@@ -895,9 +895,11 @@ struct StateArgs {
 // that reads of one half never alias the DMA into the other.
 //
 // Where two buffers do not fit in LDS (float32 at D = 256: 128 KB per chunk)
-// the kernel runs single-buffered: a third barrier E per chunk marks the end of
-// the compute waves' reads, after which the producers move the next chunk, by
-// then in L2 through the touch issued one chunk ahead.
+// the kernel runs single-buffered, with a third barrier E per chunk after the
+// compute waves' last reads.  The two tiles are read in different phases (W
+// before the K-split exchange X, kg^T after it), so the producers refill W and
+// u^T after X(c) and kg^T and g_last after E(c): each move hides behind the
+// other product, from L2 through the touch issued one chunk ahead.
 //
 // K-split (KS = 2): the two chained products of a chunk are the step's
 // critical path.  Each 16-column slice then has two compute waves, each
@@ -1212,23 +1214,91 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
           if (i * 64 + lane < D) gl[i * 64 + lane] = __expf(gl[i * 64 + lane]);
       }
     };
-    if (n > 0) issue(0, sbuf0, sGL0);
-    if (n > 1) touch(1);
     if constexpr (NBUF == 1) {
+      // One tile buffer: W and u^T of chunk c+1 move in once barrier X(c) has
+      // passed (the compute waves are done with W(c) and u^T(c)), kg^T and g_last
+      // once E(c) has passed, so each move hides behind the other product of the
+      // chain (kg^T v_new of chunk c, then W h of chunk c+1).  Every producer
+      // moves the same counts: its share of the W pieces and u^T blocks, then its
+      // share of the kg^T pieces and of g_last, which it exponentiates itself.
+      constexpr int PPW = WPIECES / NP, PPK = (PIECES - WPIECES) / NP, GQ = D / NP;
+      static_assert(WPIECES % NP == 0 && (PIECES - WPIECES) % NP == 0 && NXB == 1 &&
+                        GQ % 4 == 0 && GQ <= 64,
+                    "single-buffer split: equal shares per producer, one X barrier");
+      auto piece_dma = [&](const char* wsrc, const char* ksrc, int piece) __attribute__((always_inline)) {
+        char* dst = sbuf0 + piece * 1024;
+        if (piece < WPIECES) {
+          const int ib = piece * 1024 + lane * 16;
+          const int r = ib / ROWB_W, pch = (ib % ROWB_W) / 16;
+          constexpr int NCH = ROWB_W / 16, M = (NCH < 16 ? NCH : 16) - 1;
+          lds_dma16(wsrc + (size_t)r * ROWB_W + ((pch ^ (r & M)) * 16), dst);
+        } else {
+          const int ib = (piece - WPIECES) * 1024 + lane * 16;
+          const int r = ib / ROWB_K, pch = (ib % ROWB_K) / 16;
+          constexpr int NCH = ROWB_K / 16, M = (NCH < 16 ? NCH : 16) - 1;
+          lds_dma16(ksrc + (size_t)r * ROWB_K + ((pch ^ (r & M)) * 16), dst);
+        }
+      };
+      auto issue_w = [&](int c) __attribute__((always_inline)) {
+        const size_t cid = (size_t)bh * a.N + c0 + c;
+        const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
+#pragma unroll
+        for (int i = 0; i < PPW; ++i) piece_dma(wsrc, nullptr, p * PPW + i);
+        if (mslice) return;  // M columns: u = 0
+        constexpr int EPP = 16 / sizeof(T);
+        const T* usrc = a.UT + cid * D * BT + (size_t)(vs * 16 * NW + li) * BT + EPP * lg;
+#pragma unroll
+        for (int j = 0; j < NW * UB / NP; ++j) {
+          const int q = j * NP + p, w = q / UB, it = q % UB;
+          lds_dma16(usrc + (size_t)w * 16 * BT + it * 4 * EPP, &sU[q * 64]);
+        }
+      };
+      auto issue_k = [&](int c) __attribute__((always_inline)) {
+        const size_t cid = (size_t)bh * a.N + c0 + c;
+        const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
+#pragma unroll
+        for (int i = 0; i < PPK; ++i) piece_dma(nullptr, ksrc, WPIECES + p * PPK + i);
+        if (lane < GQ / 4) lds_dma16(a.GL + cid * D + p * GQ + lane * 4, sGL0 + p * GQ);
+      };
+      auto exp_q = [&]() __attribute__((always_inline)) {
+        if (lane < GQ) sGL0[p * GQ + lane] = __expf(sGL0[p * GQ + lane]);
+      };
+      if (n > 0) {
+        issue_w(0);
+        issue_k(0);
+      }
+      if (n > 1) touch(1);
       for (int c = 0; c < n; ++c) {
-        wait_chunk(c);
-        exp_gl(sGL0);
-        barrier();  // A(c)
+        // in flight here (c > 0): W / u^T of chunk c, then kg^T / g_last of chunk
+        // c (PPK + 1), then touch(c+1) if c+1 < n (NTP)
+        const bool tch = c + 1 < n;
+        if (c == 0) {
+          if (tch) wait_vmcnt<NTP>();
+          else wait_vmcnt<0>();
+          exp_q();
+        } else {
+          if (tch) wait_vmcnt<PPK + 1 + NTP>();
+          else wait_vmcnt<PPK + 1>();
+        }
+        barrier();  // A(c): W(c), u^T(c) resident
         barrier();  // B(c)
-        for (int x = 0; x < NXB; ++x) barrier();  // X(c)
-        barrier();  // E(c): chunk c's tiles are no longer read
+        if (c > 0) {
+          if (tch) wait_vmcnt<NTP>();
+          else wait_vmcnt<0>();
+          exp_q();
+        }
+        barrier();  // X(c): kg^T(c), e^{g_last(c)} resident; W(c) no longer read
+        if (c + 1 < n) issue_w(c + 1);
+        barrier();  // E(c): kg^T(c) no longer read
         if (c + 1 < n) {
-          issue(c + 1, sbuf0, sGL0);
+          issue_k(c + 1);
           if (c + 2 < n) touch(c + 2);
         }
       }
       return;
     }
+    if (n > 0) issue(0, sbuf0, sGL0);
+    if (n > 1) touch(1);
     for (int c = 0; c < n; c += 2) {
       wait_chunk(c);
       exp_gl(sGL0);
