@@ -1715,11 +1715,13 @@ struct OutArgs {
 // o = scale qg h_c + Aqk v_new per chunk (gdn2_fwd.py:349-353), computed as
 // o^T tiles so each lane stores 4 consecutive floats of an output row.  One
 // workgroup per chunk and slice of out_cols() value columns: float32 at
-// D >= 128 in 64-column slices (a 32 KB h^T slice: two workgroups per CU;
-// whole 128 columns, one per CU, took 1.5x as long), bfloat16 in slices of up
-// to 128 columns.
+// D = 128 in 64-column slices (a 32 KB h^T slice: two workgroups per CU;
+// whole 128 columns, one per CU, took 1.5x as long), at D = 256 in 32-column
+// slices (the same 32 KB), bfloat16 in slices of up to 128 columns.
 template <typename T, int D>
-constexpr int out_cols() { return sizeof(T) == 4 ? (D < 128 ? D : 64) : (D < 128 ? D : 128); }
+constexpr int out_cols() {
+  return sizeof(T) == 4 ? (D < 128 ? D : 8192 / D) : (D < 128 ? D : 128);
+}
 
 template <typename T, int BT, int D>
 __global__ void __launch_bounds__(256) fwd_out(OutArgs<T> a) {
