@@ -26,6 +26,11 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
                       const char* fws, char* ws, const int* cu_chunks, int nseq);
 
 size_t bwd_ws_bytes(size_t nchunks, int BT, int D, size_t elem);
+// The clip bound of each translation unit that launches kernels (gdn2_set_clip).
+hipError_t set_clip_fwd(float c);
+hipError_t set_clip_bwd(float c);
+hipError_t set_clip_decode(float c);
+hipError_t set_clip_stage(float c);
 template <int D>
 hipError_t launch_stage_dav(hipStream_t st, int B, int N, int H, const float* aqk,
                             const float* v_new, const float* dout, float* daqk, float* dv_new,
@@ -261,6 +266,15 @@ struct EventScope {
 extern "C" {
 
 const char* gdn2_version(void) { return "0.1.0"; }
+
+int gdn2_set_clip(float clip) {
+  if (!(clip > 0.f) || !(clip <= 3.4e38f)) return GDN2_ERR_SHAPE;   // NaN, <= 0, inf
+  const hipError_t e[] = {set_clip_fwd(clip), set_clip_bwd(clip), set_clip_decode(clip),
+                          set_clip_stage(clip)};
+  for (const hipError_t x : e)
+    if (x != hipSuccess) return GDN2_ERR_LAUNCH;
+  return GDN2_OK;
+}
 
 int gdn2_set_launch_events(void* const* events, int n) {
   g_launch_events = LaunchEvents{events, n > 0 ? n : 0, 0};

@@ -1657,8 +1657,8 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       const float gi = xq[e] * tq + bk * tb;           // all row terms of dgc
       const float in = !rowx ? gi : xq[e] * xgq[e] + bk * xgb[e];
       const float p1 = rowx ? xgq[e] : gk[e] + xgq[e], p2 = rowx ? xgb[e] : gi - xk[e] * gk[e];
-      inside = inside && fabsf(p1) <= kClip && fabsf(p2) <= kClip && fabsf(in) <= kClip &&
-               fabsf(gi) <= kClip && fabsf(tb) <= kClip && fabsf(gk[e]) <= kClip;
+      inside = inside && fabsf(p1) <= g_clip && fabsf(p2) <= g_clip && fabsf(in) <= g_clip &&
+               fabsf(gi) <= g_clip && fabsf(tb) <= g_clip && fabsf(gk[e]) <= g_clip;
       aq4[e] = tq;
       ab4[e] = tb;
       ak4[e] = tk;
@@ -1745,7 +1745,7 @@ __global__ void __launch_bounds__(256) gram_bwd(GramArgs<T, TG, TI> a) {
       const float dgl = skg[e] + __expf(gl[e]) * sdh[e];
       const float b3 = b3l[e], b3g = b3 + dgl;
       if constexpr (GM == kGramAll) {
-        const float corr = (fabsf(b3) < kClip && fabsf(b3g) < kClip)
+        const float corr = (fabsf(b3) < g_clip && fabsf(b3g) < g_clip)
                                ? dgl : sanitize(b3g) - sanitize(b3);
         odg[e] = sanitize(suf[e] + later[e] + corr);
       } else {   // the last token: B3's dgc with the g_last terms (gdn2_bwd.py:199-201)
@@ -2417,5 +2417,8 @@ GDN2_INST_BWD(float, float, 64, 256, bf16_t)
 GDN2_INST_BWD(float, bf16_t, 64, 64, bf16_t)
 GDN2_INST_BWD(float, bf16_t, 64, 128, bf16_t)
 GDN2_INST_BWD(float, bf16_t, 64, 256, bf16_t)
+
+// This translation unit's clip bound on the current device (gdn2_set_clip).
+hipError_t set_clip_bwd(float c) { return set_unit_clip(c); }
 
 }  // namespace gdn2

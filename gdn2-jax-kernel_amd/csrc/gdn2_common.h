@@ -32,8 +32,17 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16_t;
 
-// Reference saturation constant, gdn2_fwd.py:33.
+// Reference saturation constant, gdn2_fwd.py:33: the default clip bound.
 constexpr float kClip = 1e4f;
+// The clip bound in use: the reference's module constant CLIP, which its README
+// overrides after import (README.md:87-92).  Every translation unit that
+// launches kernels holds a copy in constant memory (kClip until set), which its
+// host code sets on the current device with set_unit_clip (synchronous); the C
+// ABI's gdn2_set_clip sets them all.
+[[maybe_unused]] static __constant__ float g_clip = kClip;
+[[maybe_unused]] static inline hipError_t set_unit_clip(float c) {
+  return hipMemcpyToSymbol(HIP_SYMBOL(g_clip), &c, sizeof(c), 0, hipMemcpyHostToDevice);
+}
 
 // Largest log-decay the single-center factorisation of a diagonal 16 x 16 score
 // block takes: a factor e^{+-60} times an operand keeps the product finite and,
@@ -42,14 +51,14 @@ constexpr float kClip = 1e4f;
 // summed by the hierarchical fallback instead.
 constexpr float kMaxDiagExp = 60.f;
 
-// nan -> 0, +-inf -> +-kClip, clip to [-kClip, kClip]: gdn2_fwd.py:42-44.
+// nan -> 0, +-inf -> +-CLIP, clip to [-CLIP, CLIP]: gdn2_fwd.py:42-44.
 // max(x, 0) + min(x, 0) is x, or 0 for NaN (IEEE maxNum / minNum return the
 // non-NaN operand); v_med3 then clamps (+-inf included).  Four independent
 // VALU operations per value and no compare: a NaN test through VCC would
 // serialise every element of a tile behind one register.
 __device__ __forceinline__ float sanitize(float x) {
   const float y = fmaxf(x, 0.f) + fminf(x, 0.f);
-  return __builtin_amdgcn_fmed3f(y, -kClip, kClip);
+  return __builtin_amdgcn_fmed3f(y, -g_clip, g_clip);
 }
 __device__ __forceinline__ f32x4 sanitize4(f32x4 v) {
   return f32x4{sanitize(v[0]), sanitize(v[1]), sanitize(v[2]), sanitize(v[3])};

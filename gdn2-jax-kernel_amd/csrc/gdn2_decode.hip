@@ -130,4 +130,7 @@ GDN2_INST_DEC(float, float, 256)
 GDN2_INST_DEC(bf16_t, float, 256)
 GDN2_INST_DEC(bf16_t, bf16_t, 256)
 
+// This translation unit's clip bound on the current device (gdn2_set_clip).
+hipError_t set_clip_decode(float c) { return set_unit_clip(c); }
+
 }  // namespace gdn2

@@ -1594,7 +1594,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
 #pragma unroll
           for (int at = 0; at < NDH; ++at)
 #pragma unroll
-            for (int r2 = 0; r2 < 4; ++r2) bound = bound || !(fabsf(h[at][r2]) <= kClip);
+            for (int r2 = 0; r2 < 4; ++r2) bound = bound || !(fabsf(h[at][r2]) <= g_clip);
         }
 #pragma unroll
         for (int at = 0; at < NDH; ++at)
@@ -1687,7 +1687,7 @@ __global__ void __launch_bounds__(256) seg_combine(const float* seg, const float
         for (int r = 0; r < 4; ++r) {
           const size_t o = (size_t)(at * 16 + 4 * lg + r) * D + c0 + li;
           const float x = acc[j][r] + e[o];
-          bound = bound || !(fabsf(x) <= kClip);
+          bound = bound || !(fabsf(x) <= g_clip);
           nh[r] = sanitize(x);
           hinb[(size_t)(s + 1) * DD + o] = nh[r];
         }
@@ -2116,5 +2116,8 @@ GDN2_INST_FWD(float, float, 64, 256, bf16_t)
 GDN2_INST_FWD(float, bf16_t, 64, 64, bf16_t)
 GDN2_INST_FWD(float, bf16_t, 64, 128, bf16_t)
 GDN2_INST_FWD(float, bf16_t, 64, 256, bf16_t)
+
+// This translation unit's clip bound on the current device (gdn2_set_clip).
+hipError_t set_clip_fwd(float c) { return set_unit_clip(c); }
 
 }  // namespace gdn2

@@ -131,4 +131,7 @@ void sanitized_copy(hipStream_t st, const float* src, float* dst, size_t n) {
     hipLaunchKernelGGL(sanitize_copy, dim3(grid_for(n)), dim3(256), 0, st, src, dst, n);
 }
 
+// This translation unit's clip bound on the current device (gdn2_set_clip).
+hipError_t set_clip_stage(float c) { return set_unit_clip(c); }
+
 }  // namespace gdn2

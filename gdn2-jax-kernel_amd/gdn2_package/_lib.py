@@ -62,6 +62,7 @@ SIGNATURES = {
     "gdn2_fwd_debug": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7
                        + [_c_float, _vp, _vp, _vp, _c_size, _vp]),
     "gdn2_set_launch_events": (_c_int, [_vp, _c_int]),
+    "gdn2_set_clip": (_c_int, [_c_float]),
     "gdn2_bwd": (_c_int, [_vp] + [_c_int] * 7 + [_vp] * 7
                  + [_c_float, _vp, _vp] + [_vp] * 7 + [_vp, _c_size, _vp, _c_size]),
     "gdn2_decode": (_c_int, [_vp] + [_c_int] * 5 + [_vp] * 6 + [_c_float, _vp, _vp, _vp]),

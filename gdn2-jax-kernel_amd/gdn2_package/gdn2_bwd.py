@@ -22,8 +22,8 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .gdn2_fwd import (BC, CLIP, N_SUB, GDN2Error, GDN2ShapeError, _raise, _stage_chunk,
-                       _STAGE_BT)
+from .gdn2_fwd import (BC, CLIP, N_SUB, GDN2Error, GDN2ShapeError, _apply_clip, _raise,
+                       _stage_chunk, _STAGE_BT)
 
 __all__ = ["reverse_cumsum_bwd", "gdn2_dhu_backward", "dav_backward_pallas",
            "wy_dqkg_backward_pallas", "intra_backward_pallas", "BC", "N_SUB", "CLIP"]
@@ -60,6 +60,7 @@ def _workspace(stage, B, N, H, D, BT, dev):
     be on the ROCm device."""
     if dev.type != "cuda":
         raise GDN2Error("gdn2: the stage tensors must live on the ROCm device (torch 'cuda')")
+    _apply_clip(dev)
     nbytes = _lib.lib().gdn2_bwd_stage_workspace_bytes(stage, B, N, H, D, BT)
     return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev), nbytes
 
@@ -82,6 +83,7 @@ def reverse_cumsum_bwd(dgc, chunk_size):
         raise GDN2ShapeError(f"gdn2: dgc must end in ({C}, D); got {tuple(dgc.shape)}")
     if dgc.device.type != "cuda":
         raise GDN2Error("gdn2: dgc must live on the ROCm device (torch 'cuda')")
+    _apply_clip(dgc.device)
     x = dgc.to(torch.float32).contiguous()
     out = torch.empty_like(x)
     D = x.shape[-1]

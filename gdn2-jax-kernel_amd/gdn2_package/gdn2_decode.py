@@ -18,7 +18,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .gdn2_fwd import GDN2Error, GDN2ShapeError, _dtype_code, _raise, _SUPPORTED_IN
+from .gdn2_fwd import GDN2Error, GDN2ShapeError, _apply_clip, _dtype_code, _raise, _SUPPORTED_IN
 
 
 def gdn2_decode_step(q, k, v, w, b, g, scale, state=None, inplace=False):
@@ -40,6 +40,7 @@ def gdn2_decode_step(q, k, v, w, b, g, scale, state=None, inplace=False):
     dev = q.device
     if dev.type != "cuda" or any(x.device != dev for x in xs):
         raise GDN2Error("gdn2_decode_step: inputs must live on one ROCm device; no CPU path")
+    _apply_clip(dev)
     in_dt = q.dtype if q.dtype in _SUPPORTED_IN else torch.float32
     if any(x.dtype != in_dt for x in (k, v, w, b)):
         in_dt = torch.float32

@@ -13,11 +13,17 @@ Chunk size.  ``BT`` below plays the role of gdn2_fwd.py:29 but is read at call
 time, so overriding it also reaches the backward (the reference binds it by
 value at import, gdn2_bwd.py:23).  ``None`` picks 128 for bfloat16 inputs at
 D = 64 and 64 otherwise (see ``chunk_size_for``); 64 and 128 are accepted (128
-only with bfloat16 inputs at D <= 128), the reference's 256 is refused.
-Results do not depend on the chunk size beyond rounding.
+only with bfloat16 inputs at D <= 128), and the reference's default 256 runs at
+the automatic choice.  Results do not depend on the chunk size beyond rounding.
+
+Clip bound.  ``CLIP`` (gdn2_fwd.py:33) is read at call time too: overriding it
+(the reference README's ``fwd.CLIP = 1e3``, README.md:87-92) sets the saturation
+bound of every stage sanitize in the library (``gdn2_set_clip``) before the
+next call on each device.
 """
 from __future__ import annotations
 
+import math
 import os
 
 import torch
@@ -87,27 +93,49 @@ def chunk_size_for(dtype, chunk_size=None, D=128) -> int:
     D = 128 and 256: at D = 128 the chunk-64 forward, whose state scan forms the
     outputs, takes 0.48 ms at B8 T8192 H6 against 0.56 ms at chunk 128).
 
-    The reference's default BT = 256 (gdn2_fwd.py:29) is refused with a
-    GDN2ShapeError: its 256 x 256 float32 inverse does not fit a gfx950
-    workgroup's LDS.  Results do not depend on the chunk size beyond rounding,
-    so callers that set BT = 256 lose nothing by leaving BT at None."""
+    The reference's default BT = 256 (gdn2_fwd.py:29), explicit or as the
+    module constant, runs at the automatic choice: a 256 x 256 float32 inverse
+    does not fit a gfx950 workgroup's LDS, and results do not depend on the
+    chunk size beyond rounding.  Other sizes than 64 and 128 are refused by the
+    library's shape check (GDN2ShapeError)."""
     bt = chunk_size if chunk_size is not None else BT
-    if bt is None:
+    if bt is None or int(bt) == 256:
         return 128 if dtype == torch.bfloat16 and D <= 64 else 64
-    if int(bt) == 256:
-        raise GDN2ShapeError(
-            "gdn2: chunk size 256 (the reference default, gdn2_fwd.py:29) is not supported "
-            "on gfx950; use None (automatic), 64, or 128 with bfloat16 inputs -- results do "
-            "not depend on the chunk size beyond rounding")
     return int(bt)
 
 
-def _check_clip():
-    """The kernels saturate at 1e4 (gdn2_fwd.py:33); an override of the module
-    constant CLIP (README.md:87-92) is refused instead of silently ignored."""
-    if float(CLIP) != 1e4:
-        raise GDN2Error(f"gdn2: CLIP = {CLIP!r} is not supported; the gfx950 kernels clip "
-                        f"stage outputs at the reference value 1e4 (gdn2_fwd.py:33)")
+# The clip bound set in the library on each device (device index -> value); the
+# library starts at the reference's 1e4.
+_CLIP_SET: dict = {}
+
+
+def _clip_value() -> float:
+    """The module constant CLIP (gdn2_fwd.py:33), read at call time as the
+    reference reads it when it traces; overridable as its README shows
+    (README.md:87-92).  It must be finite and positive."""
+    try:
+        c = float(CLIP)
+    except (TypeError, ValueError):
+        raise GDN2Error(f"gdn2: CLIP = {CLIP!r} is not a number") from None
+    if not (math.isfinite(c) and c > 0.0):
+        raise GDN2Error(f"gdn2: CLIP = {CLIP!r} must be finite and positive")
+    return c
+
+
+def _apply_clip(device) -> None:
+    """Make CLIP the clip bound of the library's kernels on `device` (a copy into
+    each kernel unit's constant memory, made only when CLIP changed; the device
+    is synchronised first so that no call in flight sees the change)."""
+    c = _clip_value()
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if _CLIP_SET.get(idx, 1e4) == c:
+        return
+    with torch.cuda.device(idx):
+        torch.cuda.synchronize()
+        rc = _lib.lib().gdn2_set_clip(c)
+    if rc:
+        _raise(rc, "gdn2_set_clip")
+    _CLIP_SET[idx] = c
 
 
 class _Prepared:
@@ -118,7 +146,7 @@ class _Prepared:
         float32 kernels (the trainable path: the reference upcasts every input
         before any arithmetic, gdn2_fwd.py:100-103,266-272, gdn2_bwd.py:130-142);
         ``in_dtypes`` keeps the caller's dtypes for the gradients."""
-        _check_clip()
+        _clip_value()
         xs = (q, k, v, w, b, g)
         for x in xs:
             if not isinstance(x, torch.Tensor):
@@ -163,6 +191,7 @@ class _Prepared:
         if dev.type != "cuda" or any(x.device != dev for x in xs):
             raise GDN2Error("gdn2: inputs must live on one ROCm device (torch 'cuda'); "
                             "this library has no CPU path")
+        _apply_clip(dev)
         self.in_dtypes = tuple(x.dtype for x in xs)
         self.q, self.k, self.v, self.w, self.b = (x.to(in_dt).contiguous() for x in xs[:5])
         self.g = g.to(g_dt).contiguous()
@@ -433,6 +462,7 @@ def wy_solve_pallas(Akk):
         raise GDN2ShapeError(f"gdn2: Akk must end in ({BT},{BT}); got {tuple(Akk.shape)}")
     if Akk.device.type != "cuda":
         raise GDN2Error("gdn2: Akk must live on the ROCm device (torch 'cuda')")
+    _apply_clip(Akk.device)
     akk = Akk.to(torch.float32).contiguous()
     a = torch.empty_like(akk)
     n = akk.numel() // (BT * BT)
@@ -478,6 +508,7 @@ def _combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0, debug_tag, with_state
                       ((w_pseudo, "w_pseudo"), (u, "u"), (kg, "kg"), (qg, "qg")))
     gl = _chunk_tensor(gc_last, "gc_last", (B, H, N, D), dev)
     h0c = None if h0 is None else _chunk_tensor(h0, "h0", (B, H, D, D), dev)
+    _apply_clip(dev)
     L = _lib.lib()
     nbytes = L.gdn2_chunk_combine_workspace_bytes(B, N, H, D, BT)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)

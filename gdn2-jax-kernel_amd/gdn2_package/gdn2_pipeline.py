@@ -25,13 +25,14 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .gdn2_fwd import GDN2ShapeError, _Prepared, _raise, _run_forward
+from .gdn2_fwd import GDN2ShapeError, _Prepared, _apply_clip, _raise, _run_forward
 
 # Chunk size of the trainable path (the backward kernels are written for 64).
 TRAIN_CHUNK = 64
 
 
 def _run_backward(p: _Prepared, ws: torch.Tensor, dout, dh_final):
+    _apply_clip(p.device)   # CLIP as it is when the backward runs
     L = _lib.lib()
     fbytes = ws.numel()   # the residual-keeping forward's workspace (GDN2_FWD_SAVE_A)
     bbytes = L.gdn2_bwd_workspace_bytes(*p.args[:6])
@@ -140,6 +141,7 @@ class _GDN2VarlenCore(torch.autograd.Function):
     def backward(ctx, dout, dh_final):
         p, S = ctx.prep, ctx.S
         total = p.T // p.BT
+        _apply_clip(p.device)
         L = _lib.lib()
         bbytes = L.gdn2_bwd_varlen_workspace_bytes(total, p.H, p.D, p.BT, p.code)
         bws = torch.empty(max(bbytes, 1), dtype=torch.uint8, device=p.device)

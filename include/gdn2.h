@@ -21,7 +21,7 @@
  *  - Return value 0 on success, a negative GDN2_ERR_* code otherwise;
  *    gdn2_strerror() names it.  Invalid shapes are rejected before any launch.
  *  - No mutable global state beyond the per-thread timing request of
- *    gdn2_set_launch_events: calls on different streams may run concurrently
+ *    gdn2_set_launch_events and the clip bound of gdn2_set_clip: calls on different streams may run concurrently
  *    provided their workspaces do not overlap.
  */
 #ifndef GDN2_H_
@@ -138,6 +138,15 @@ int gdn2_fwd_debug(void* stream, int B, int T, int H, int D, int BT, int in_dtyp
  * gdn2_fwd has 3 stages (fwd_prep, the state scan, fwd_out); where the scan
  * forms the outputs the third stage launches nothing.  Returns 0. */
 int gdn2_set_launch_events(void* const* events, int n);
+
+/* Saturation bound of every stage sanitize (x -> clip(nan_to_num(x)) to
+ * [-clip, clip]), the reference's module constant CLIP (gdn2_fwd.py:33, 1e4 by
+ * default), which its README overrides after import (README.md:87-92), for
+ * every kernel this library launches on the current device from now on.
+ * Synchronous (a copy into constant memory): call it with none of this
+ * library's work in flight on the device and outside graph capture.  Returns
+ * GDN2_ERR_SHAPE for a bound that is not finite and positive. */
+int gdn2_set_clip(float clip);
 
 /* Bytes of workspace gdn2_bwd needs in addition to the forward workspace. */
 size_t gdn2_bwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype);

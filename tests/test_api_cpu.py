@@ -35,35 +35,36 @@ def test_shape_errors_are_assertion_errors(shape):
         gp.gdn2_pallas_forward(*_inputs(shape), 0.1)
 
 
-def test_clip_override_is_refused(monkeypatch):
-    """The kernels clip stage outputs at the reference's 1e4 (gdn2_fwd.py:33); a
-    changed module constant CLIP (the reference README's fwd.CLIP = 1e3) raises
-    before anything runs, rather than being ignored."""
+@pytest.mark.parametrize("bad", [0.0, -1e3, float("nan"), float("inf"), "x"])
+def test_clip_override_must_be_finite_and_positive(monkeypatch, bad):
+    """CLIP (gdn2_fwd.py:33) is read at call time and may be overridden (the
+    reference README's fwd.CLIP = 1e3); a bound that is not a finite positive
+    number raises before anything runs, and the C ABI refuses it as well."""
     import gdn2_package as gp
-    from gdn2_package import gdn2_fwd
-    monkeypatch.setattr(gdn2_fwd, "CLIP", 1e3)
+    from gdn2_package import _lib, gdn2_fwd
+    monkeypatch.setattr(gdn2_fwd, "CLIP", bad)
     with pytest.raises(gp.GDN2Error, match="CLIP"):
         gp.gdn2_pallas_forward(*_inputs((1, 128, 2, 64)), 0.1)
     with pytest.raises(gp.GDN2Error, match="CLIP"):
         gp.gdn2_pallas_forward_trainable(*_inputs((1, 128, 2, 64)), 0.1)
+    if not isinstance(bad, str):
+        assert _lib.lib().gdn2_set_clip(bad) == _lib.ERR_SHAPE
 
 
-@pytest.mark.parametrize("how", ["module", "argument"])
-def test_chunk_256_is_refused(monkeypatch, how):
-    """The reference's default BT = 256 (gdn2_fwd.py:29) does not fit a gfx950
-    workgroup (its 256 x 256 float32 inverse alone is 256 KB of LDS): set as the
-    module constant (the reference README's fwd.BT = ...) or passed as
-    chunk_size it raises the package's shape error (an AssertionError, as the
-    reference's trace-time asserts) naming the supported sizes."""
+def test_chunk_256_runs_at_the_automatic_chunk(monkeypatch):
+    """The reference's default BT = 256 (gdn2_fwd.py:29), passed as chunk_size
+    or set as the module constant (the reference README's fwd.BT = ...), runs
+    at the automatic chunk (a 256 x 256 float32 inverse does not fit a gfx950
+    workgroup; results do not depend on the chunk size beyond rounding); other
+    sizes reach the library's shape check."""
     import gdn2_package as gp
     from gdn2_package import gdn2_fwd
-    kw = {}
-    if how == "module":
-        monkeypatch.setattr(gdn2_fwd, "BT", 256)
-    else:
-        kw["chunk_size"] = 256
-    with pytest.raises(AssertionError, match="chunk size 256"):
-        gp.gdn2_pallas_forward(*_inputs((1, 512, 2, 64)), 0.1, **kw)
+    for dt, D in ((torch.bfloat16, 64), (torch.bfloat16, 128), (torch.float32, 128)):
+        assert gdn2_fwd.chunk_size_for(dt, 256, D) == gdn2_fwd.chunk_size_for(dt, None, D)
+    monkeypatch.setattr(gdn2_fwd, "BT", 256)
+    assert gdn2_fwd.chunk_size_for(torch.bfloat16, None, 64) == 128
+    with pytest.raises(AssertionError):
+        gp.gdn2_pallas_forward(*_inputs((1, 512, 2, 64)), 0.1, chunk_size=32)
 
 
 def test_chunk_size_choice():
