@@ -6,6 +6,7 @@
 // fake device pointers are never dereferenced.  Exit status 0 when every check
 // holds (a sanitizer report aborts the run).
 #include <climits>
+#include <limits>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -223,6 +224,11 @@ int main() {
         if (rc == GDN2_OK || rc == GDN2_ERR_LAUNCH)   // only in-range shapes reach a launch
           CHECK(tiles >= 0 && bt >= 1 && bt <= 4096 && d >= 1 && d <= 65536);
       }
+  // the clip bound: not finite and positive -> refused before any copy
+  for (float c : {0.f, -0.f, -1e4f, std::numeric_limits<float>::quiet_NaN(),
+                  std::numeric_limits<float>::infinity(), -std::numeric_limits<float>::infinity(),
+                  -std::numeric_limits<float>::denorm_min()})
+    CHECK(gdn2_set_clip(c) == GDN2_ERR_SHAPE);
   for (int c = -20; c <= 5; ++c) CHECK(gdn2_strerror(c) != nullptr);
   CHECK(gdn2_set_launch_events(nullptr, -5) == 0);
   std::printf("host checks: %ld shape combinations, %d failures\n", n, g_fail);
