@@ -2288,8 +2288,9 @@ hipError_t launch_stage_dhu(hipStream_t st, int B, int N, int H, const float* do
   if (NC > 0) {
     // DHT[c] = dh_{c+1}^T: dh_all[c+1] = DHT[c]^T, and dh_all[0] = dh0
     transpose_shift(st, DHT, dh_all, BH, N, D, D);
-    (void)hipMemcpy2DAsync(dh_all, (size_t)N * D * D * 4, dh0, (size_t)D * D * 4,
-                           (size_t)D * D * 4, BH, hipMemcpyDeviceToDevice, st);
+    const hipError_t e = hipMemcpy2DAsync(dh_all, (size_t)N * D * D * 4, dh0, (size_t)D * D * 4,
+                                          (size_t)D * D * 4, BH, hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return e;
     transpose_all(st, DVNT, dv_all, NC, D, SBT);
   }
   return hipGetLastError();

@@ -144,8 +144,12 @@ def test_dhu_zero_chunks_and_saturated_dht(dev):
 
 
 # ----------------------------------------------------------------------------- B3
-@pytest.mark.parametrize("D,g_scale", [(64, 1.0), (128, 1.0), (128, 0.05), (256, 1.0)])
+@pytest.mark.parametrize("D,g_scale", [(64, 1.0), (128, 1.0), (128, 0.05), (256, 1.0),
+                                     (128, 30.0)])
 def test_wy_dqkg_matches_oracle(dev, D, g_scale):
+    """The kernels take g per token and form gc by their own in-chunk cumsum, so
+    the given gc is turned into g by differences first; strong decay (g_scale
+    30, |gc| up to ~1e3) checks that this round trip keeps the tolerance."""
     c = case(1, 256, 2, D, seed=D + 3, g_scale=g_scale)
     ins = [c[n] for n in ("q", "k", "b", "w", "v", "gc", "A", "Akk", "h_pre_all",
                           "v_new_all", "do", "dv_all", "dh_next")]
