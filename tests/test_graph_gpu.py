@@ -106,3 +106,53 @@ def test_forward_graph_replays_match_eager(dev, chunk):
             junk = torch.randn(4096, device=dev).sum()
             assert torch.isfinite(junk)
             assert torch.equal(out, eager[i][0]) and torch.equal(hf, eager[i][1]), (rep, i)
+
+
+def test_training_step_graph_replays_match_eager(dev):
+    """A whole float32 training step -- the trainable forward and its backward
+    (torch.autograd.grad with the output cotangent given, so that no torch
+    reduction enters the graph) -- captured once and replayed on three input
+    sets; every replay's output, final state and seven gradients equal the eager
+    step's bit for bit."""
+    B, T, H, D = 2, 512, 3, 128
+    scale = D ** -0.5
+    gen = torch.Generator(device=dev).manual_seed(11)
+    f = torch.nn.functional
+    sets = []
+    for _ in range(3):
+        r = lambda: torch.randn((B, T, H, D), generator=gen, device=dev)
+        xs = [f.normalize(r(), dim=-1), f.normalize(r(), dim=-1), r(), torch.sigmoid(r()),
+              torch.sigmoid(r()), -f.softplus(r())]
+        h0 = 0.1 * torch.randn((B, H, D, D), generator=gen, device=dev)
+        sets.append((xs, h0, r()))
+
+    def step(xs, h0, do):
+        out, hf = gp().gdn2_pallas_forward_trainable(*xs, scale, h0=h0)
+        grads = torch.autograd.grad(out, list(xs) + [h0], grad_outputs=do)
+        return out, hf, grads
+
+    eager = []
+    for xs, h0, do in sets:
+        leaves = [x.clone().requires_grad_(True) for x in xs]
+        h0l = h0.clone().requires_grad_(True)
+        out, hf, grads = step(leaves, h0l, do)
+        eager.append([out.detach().clone(), hf.detach().clone()] + [x.clone() for x in grads])
+    s_xs = [x.clone().requires_grad_(True) for x in sets[0][0]]
+    s_h0 = sets[0][1].clone().requires_grad_(True)
+    s_do = sets[0][2].clone()
+    g, res = _capture(lambda: step(s_xs, s_h0, s_do))
+    out, hf, grads = res
+    for rep in range(2):
+        for i, (xs, h0, do) in enumerate(sets):
+            with torch.no_grad():
+                for s_, x in zip(s_xs, xs):
+                    s_.copy_(x)
+                s_h0.copy_(h0)
+                s_do.copy_(do)
+            g.replay()
+            torch.cuda.synchronize()
+            junk = torch.randn(4096, device=dev).cumsum(0)   # eager work between replays
+            assert torch.isfinite(junk).all()
+            got = [out, hf] + list(grads)
+            for j, (a, b) in enumerate(zip(got, eager[i])):
+                assert torch.equal(a, b), (rep, i, j)
