@@ -689,12 +689,17 @@ struct B2Args {
 // B1's scale qg^T do (gdn2_dhu_backward).
 enum B2Mode { kB2All = 0, kB2Dav = 1, kB2Qdot = 2 };
 
+// Waves of a bwd_b2 workgroup: four (one per 16-token row block), eight at D = 256,
+// where the 136 KB of LDS leave one workgroup per CU: the row blocks' column
+// tiles are then dealt over two waves each (two waves per SIMD instead of one).
+constexpr int b2_waves(int D) { return D > 128 ? 8 : 4; }
+
 template <typename T, int D, int B2M = kB2All>
-__global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
+__global__ void __launch_bounds__(64 * b2_waves(D), 2) bwd_b2(B2Args<T> a) {
   constexpr int BT = 64, NDT = D / 16, NKT = BT / 16;
+  constexpr int NWV = b2_waves(D), NT = 64 * NWV, WPB = NWV / 4;   // waves per row block
   constexpr int LDO = D + 4, LDV = BT + 4, LDA = BT + 4, LDQ = D + 4;
   constexpr int BF = sizeof(T) == 2;
-  constexpr int QB = NDT / 4;               // qdot row blocks per wave
   constexpr int RV = D * LDV, RA = BT * LDA, RQ = BT * LDQ;
   constexpr int RS = RV > RQ ? (RV > RA ? RV : RA) : (RQ > RA ? RQ : RA);
   __shared__ __align__(16) float sDo[BT * LDO];
@@ -704,6 +709,8 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
   float* const sQ = sR;
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: MFMA under branches
+  // row block; part of its column tiles (WPB parts; a constant 0 with one wave per block)
+  const int rb = WPB == 1 ? wv : wv % 4, part = WPB == 1 ? 0 : wv / 4;
   const int cid = blockIdx.x;
   const int c = cid % a.N, bh = cid / a.N, hh = bh % a.H, bb = bh / a.H;
   const size_t HD = (size_t)a.H * D;
@@ -726,90 +733,98 @@ __global__ void __launch_bounds__(256, D <= 128 ? 2 : 1) bwd_b2(B2Args<T> a) {
     const GMat mV{a.VnT, BF, BT, 0, BF};
     // Aqk: blocks right of the diagonal block are unwritten; causal mask on load
     const GMat mA{a.Aqk, BF, BT, 1, 0};
-    stage_load(s1, mDo, tok0, BT, D, tid);
-    if constexpr (B2M != kB2Qdot) stage_load(s2, mV, (size_t)cid * D * BT, D, BT, tid);
-    stage_store(sDo, LDO, s1, mDo, BT, D, 0, 0, false, tid);
-    if constexpr (B2M != kB2Qdot) stage_store(sV, LDV, s2, mV, D, BT, 0, 0, false, tid);
-    // qg and Aqk are in flight while dAqk is formed (LDS-only barriers); at
-    // D = 256 qg (64 KB) is loaded after the Aqk^T do product instead, which
-    // would otherwise spill the registers that hold it
-    if constexpr (D <= 128 && B2M != kB2Dav) stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
-    if constexpr (B2M != kB2Qdot) stage_load(s2, mA, (size_t)cid * BT * BT, BT, BT, tid);
+    stage_load<NT>(s1, mDo, tok0, BT, D, tid);
+    if constexpr (B2M != kB2Qdot) stage_load<NT>(s2, mV, (size_t)cid * D * BT, D, BT, tid);
+    stage_store<NT>(sDo, LDO, s1, mDo, BT, D, 0, 0, false, tid);
+    if constexpr (B2M != kB2Qdot) stage_store<NT>(sV, LDV, s2, mV, D, BT, 0, 0, false, tid);
+    // qg and Aqk are in flight while dAqk is formed (LDS-only barriers)
+    if constexpr (B2M != kB2Dav) stage_load<NT>(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
+    if constexpr (B2M != kB2Qdot) stage_load<NT>(s2, mA, (size_t)cid * BT * BT, BT, BT, tid);
     lds_barrier();
     if constexpr (B2M != kB2Qdot) {
     // dAqk[t][s] = sum_e do[t][e] v_new[s][e], s <= t: column blocks right of
-    // the own row block are zero and not formed
+    // the own row block are zero and not formed; column tile st of row block rb
+    // belongs to part st mod WPB
     {
       f32x4 acc[NKT];
 #pragma unroll
       for (int st = 0; st < NKT; ++st) acc[st] = z4;
 #pragma unroll
       for (int kg = 0; kg < NDT; ++kg) {
-        const f32x4 x = rowop(sDo, LDO, wv * 16, kg * 16);
+        const f32x4 x = rowop(sDo, LDO, rb * 16, kg * 16);
 #pragma unroll
         for (int st = 0; st < NKT; ++st)
-          if (st <= wv) mma(acc[st], x, colop(sV, LDV, kg * 16, st * 16));
+          if (st <= rb && st % WPB == part) mma(acc[st], x, colop(sV, LDV, kg * 16, st * 16));
       }
       float* o = a.DAQK + (size_t)cid * BT * BT;
 #pragma unroll
-      for (int st = 0; st < NKT; ++st)
+      for (int st = 0; st < NKT; ++st) {
+        if (st % WPB != part) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = wv * 16 + 4 * lg + r, s2 = st * 16 + li;
+          const int row = rb * 16 + 4 * lg + r, s2 = st * 16 + li;
           o[row * BT + s2] = s2 <= row ? sanitize(acc[st][r]) : 0.f;   // gdn2_bwd.py:95
         }
+      }
     }
     lds_barrier();  // every wave is done with v_new^T
-    stage_store(sA, LDA, s2, mA, BT, BT, 0, 0, false, tid);
+    stage_store<NT>(sA, LDA, s2, mA, BT, BT, 0, 0, false, tid);
     }  // B2M != kB2Qdot
   }
   lds_barrier();
   if constexpr (B2M != kB2Qdot) {
   // dvp^T[e][s] = sum_t Aqk[t][s] do[t][e]: rows s of the own block, stored as
   // [e][s]; Aqk[t][s] = 0 for t < s, so token blocks before the own one add nothing
-  // (with dAqk's skipped blocks: 5 of 8 block-products per wave, on every wave)
+  // (with dAqk's skipped blocks: 5 of 8 block-products per row block); the e tiles
+  // of a row block are split over its WPB parts
   {
-    f32x4 acc[NDT];
+    constexpr int NDV = NDT / WPB;
+    f32x4 acc[NDV];
 #pragma unroll
-    for (int nt = 0; nt < NDT; ++nt) acc[nt] = z4;
+    for (int n = 0; n < NDV; ++n) acc[n] = z4;
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
-      if (kt < wv) continue;
-      const f32x4 x = colop(sA, LDA, kt * 16, wv * 16);      // Aqk^T rows s, k = t
+      if (kt < rb) continue;
+      const f32x4 x = colop(sA, LDA, kt * 16, rb * 16);      // Aqk^T rows s, k = t
 #pragma unroll
-      for (int nt = 0; nt < NDT; ++nt) mma(acc[nt], x, colop(sDo, LDO, kt * 16, nt * 16));
+      for (int n = 0; n < NDV; ++n)
+        mma(acc[n], x, colop(sDo, LDO, kt * 16, (part * NDV + n) * 16));
     }
     float* o = a.DVPT + (size_t)cid * D * BT;
 #pragma unroll
-    for (int nt = 0; nt < NDT; ++nt)
-      store4(o + (size_t)(nt * 16 + li) * BT + wv * 16 + 4 * lg, sanitize4(acc[nt]));  // :96
+    for (int n = 0; n < NDV; ++n)
+      store4(o + (size_t)((part * NDV + n) * 16 + li) * BT + rb * 16 + 4 * lg,
+             sanitize4(acc[n]));  // :96
   }
   }  // B2M != kB2Qdot
   if constexpr (B2M == kB2Dav) return;
-  if constexpr (D > 128) stage_load(s1, mQ, (size_t)cid * BT * D, BT, D, tid);
   lds_barrier();  // every wave is done with Aqk
-  stage_store(sQ, LDQ, s1, mQ, BT, D, 0, 0, false, tid);
+  stage_store<NT>(sQ, LDQ, s1, mQ, BT, D, 0, 0, false, tid);
   lds_barrier();
-  // qdot[e][d] = scale sum_t do[t][e] qg[t][d] (one row block at a time: at
-  // D = 256 a block's sixteen accumulator tiles are 64 registers)
+  // qdot[e][d] = scale sum_t do[t][e] qg[t][d], in items of one row block e and
+  // QCT column tiles d (at D = 256 half a row: eight accumulator tiles, 32
+  // registers), QI items per wave, one at a time
   {
-#pragma unroll (D <= 128 ? QB : 1)
-    for (int qb = 0; qb < QB; ++qb) {
-      const int eb = wv * QB + qb;
-      f32x4 acc[NDT];
+    constexpr int QCT = D > 128 ? NDT / 2 : NDT, NCH = NDT / QCT, QI = NDT * NCH / NWV;
+    static_assert(QI * NWV == NDT * NCH, "qdot items must split over the waves");
+#pragma unroll (D <= 128 ? QI : 1)
+    for (int qi = 0; qi < QI; ++qi) {
+      const int item = wv * QI + qi, eb = item / NCH, d0 = (item % NCH) * QCT;
+      f32x4 acc[QCT];
 #pragma unroll
-      for (int nt = 0; nt < NDT; ++nt) acc[nt] = z4;
+      for (int n = 0; n < QCT; ++n) acc[n] = z4;
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt) {
         const f32x4 x = colop(sDo, LDO, kt * 16, eb * 16);   // do^T rows e, k = t
 #pragma unroll
-        for (int nt = 0; nt < NDT; ++nt) mma(acc[nt], x, colop(sQ, LDQ, kt * 16, nt * 16));
+        for (int n = 0; n < QCT; ++n) mma(acc[n], x, colop(sQ, LDQ, kt * 16, (d0 + n) * 16));
       }
       float* o = a.QDOT + (size_t)cid * D * D;
 #pragma unroll
-      for (int nt = 0; nt < NDT; ++nt)
+      for (int n = 0; n < QCT; ++n)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[(eb * 16 + 4 * lg + r) * D + nt * 16 + li] = a.scale * acc[nt][r];
+        for (int r = 0; r < 4; ++r)
+          o[(eb * 16 + 4 * lg + r) * D + (d0 + n) * 16 + li] = a.scale * acc[n][r];
     }
   }
 }
@@ -2105,7 +2120,7 @@ hipError_t launch_bwd_wide(hipStream_t st, int B, int T_len, int H, const void* 
     // B2: dAqk = (do v_new^T) . causal, dvp^T = (Aqk^T do)^T, qdot = scale (qg^T do)^T
     B2Args<T> ba{dout, (const T*)fVnT, (const T*)(fws + F.Aqk), (const T*)(fws + F.Qg), T_len,
                  H, N, scale, buf(B_DAQK), buf(B_DVPT), buf(B_QDOT)};
-    hipLaunchKernelGGL((bwd_b2<T, D>), dim3(NC), dim3(256), 0, st, ba);
+    hipLaunchKernelGGL((bwd_b2<T, D>), dim3(NC), dim3(64 * b2_waves(D)), 0, st, ba);
     launch_mark(st);
   }
   BStateArgs<T> sa{(const T*)(fws + F.W), (const T*)(fws + F.KgT),
@@ -2173,7 +2188,7 @@ hipError_t launch_bwd(hipStream_t st, int B, int T_len, int H, const void* q, co
     if (NC > 0) {
       B2Args<T> ba{dout, (const T*)fVnT, (const T*)fAqk, (const T*)fQg, T_len, H, N, scale,
                    buf(B_DAQK), buf(B_DVPT), buf(B_QDOT)};
-      hipLaunchKernelGGL((bwd_b2<T, D>), dim3(NC), dim3(256), 0, st, ba);
+      hipLaunchKernelGGL((bwd_b2<T, D>), dim3(NC), dim3(64 * b2_waves(D)), 0, st, ba);
       launch_mark(st);
     }
     // B1: reverse state scan
@@ -2248,7 +2263,7 @@ hipError_t launch_stage_dav(hipStream_t st, int B, int N, int H, const float* aq
   chunk_rows_permute(st, dout, dtok, B, H, N, SBT, D, true, false);
   transpose_all(st, v_new, VnT, NC, SBT, D);
   B2Args<float> ba{dtok, VnT, aqk, nullptr, N * SBT, H, N, 1.f, daqk, DVPT, nullptr};
-  hipLaunchKernelGGL((bwd_b2<float, D, kB2Dav>), dim3(NC), dim3(256), 0, st, ba);
+  hipLaunchKernelGGL((bwd_b2<float, D, kB2Dav>), dim3(NC), dim3(64 * b2_waves(D)), 0, st, ba);
   transpose_all(st, DVPT, dv_new, NC, D, SBT);
   return hipGetLastError();
 }
@@ -2277,7 +2292,7 @@ hipError_t launch_stage_dhu(hipStream_t st, int B, int N, int H, const float* do
   if (NC > 0) {
     chunk_rows_permute(st, dout, dtok, B, H, N, SBT, D, true, false);
     B2Args<float> ba{dtok, nullptr, nullptr, qg, N * SBT, H, N, scale, nullptr, nullptr, QDOT};
-    hipLaunchKernelGGL((bwd_b2<float, D, kB2Qdot>), dim3(NC), dim3(256), 0, st, ba);
+    hipLaunchKernelGGL((bwd_b2<float, D, kB2Qdot>), dim3(NC), dim3(64 * b2_waves(D)), 0, st, ba);
     transpose_all(st, dv_partial, DVPT, NC, SBT, D);
     transpose_all(st, kg, KgT, NC, SBT, D);
   }
