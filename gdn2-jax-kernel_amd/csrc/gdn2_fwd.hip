@@ -1109,12 +1109,13 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
     constexpr int PP = PIECES / NP;
     static_assert(PIECES % NP == 0 && (NW * UB) % NP == 0, "work must split evenly");
     const int p = wv - NCW;
-    auto issue = [&](int c, char* base, float* gl) __attribute__((always_inline)) {
+    // parts: 1 the W / kg^T tiles and g_last, 2 the u^T blocks, 3 both
+    auto issue = [&](int c, char* base, float* gl, int parts = 3) __attribute__((always_inline)) {
       const size_t cid = (size_t)bh * a.N + c0 + c;
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
       const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
 #pragma unroll
-      for (int i = 0; i < PP; ++i) {
+      for (int i = 0; i < ((parts & 1) ? PP : 0); ++i) {
         const int piece = p * PP + i;                      // wave-uniform
         char* dst = base + piece * 1024;
         if (piece < WPIECES) {
@@ -1129,7 +1130,8 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
           lds_dma16(ksrc + (size_t)r * ROWB_K + ((pch ^ (r & M)) * 16), dst);
         }
       }
-      if (p == NP - 1 && lane < D / 4) lds_dma16(a.GL + cid * D + lane * 4, gl);
+      if ((parts & 1) && p == NP - 1 && lane < D / 4) lds_dma16(a.GL + cid * D + lane * 4, gl);
+      if (!(parts & 2)) return;
       // u^T[col][t] for compute wave w, piece q: lane (li, lg) of that wave gets
       // the 16 bytes at u^T[16 w + li][16 q + 4 lg] (float32: row block q) or
       // [32 q + 8 lg] (bfloat16: row blocks 2q, 2q+1, chained), at sU[(w UB + q) 64 + lane]
@@ -1299,20 +1301,29 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
     }
     if (n > 0) issue(0, sbuf0, sGL0);
     if (n > 1) touch(1);
+    // float32: the next chunk's W / kg^T / g_last move once A(c) has passed (their
+    // buffer was last read in chunk c-1), its u^T once B(c) has (one u^T buffer,
+    // read between A(c) and B(c)); the touch comes last, so waiting for all but
+    // the touch waits for both.  The MFMA-bound float32 step gains the head start
+    // (training scan 0.458 -> 0.437 ms); the latency-bound bfloat16 steps lost
+    // (0.210 -> 0.229 ms at chunk 128) and issue everything after B(c).
+    constexpr int EARLY = F32 ? 1 : 0;
     for (int c = 0; c < n; c += 2) {
       wait_chunk(c);
       exp_gl(sGL0);
       barrier();  // A(c)
+      if (EARLY && c + 1 < n) issue(c + 1, sbuf1, sGL1, 1);
       barrier();  // B(c)
       if (c + 1 < n) {
-        issue(c + 1, sbuf1, sGL1);
+        issue(c + 1, sbuf1, sGL1, EARLY ? 2 : 3);
         if (c + 2 < n) touch(c + 2);
         for (int x = 0; x < NXB; ++x) barrier();  // X(c)
         wait_chunk(c + 1);
         exp_gl(sGL1);
         barrier();  // A(c+1)
+        if (EARLY && c + 2 < n) issue(c + 2, sbuf0, sGL0, 1);
         barrier();  // B(c+1)
-        if (c + 2 < n) issue(c + 2, sbuf0, sGL0);
+        if (c + 2 < n) issue(c + 2, sbuf0, sGL0, EARLY ? 2 : 3);
         if (c + 3 < n) touch(c + 3);
         for (int x = 0; x < NXB; ++x) barrier();  // X(c+1)
       } else {
