@@ -301,11 +301,13 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         lds_dma16(dsrc + (size_t)w * 16 * BT + it * 16, &sDV[q * 64]);
       }
     };
-    // loads of chunk i: the tiles (DMA, or TR: into registers) and the gathers
-    auto issue = [&](int i, char* base, float* gl) __attribute__((always_inline)) {
+    // loads of chunk i: parts 1 the tiles (DMA, or TR: into registers) and g_last,
+    // 2 the gathers (dvp^T, qdot), 3 both
+    auto issue = [&](int i, char* base, float* gl, int parts = 3) __attribute__((always_inline)) {
       const size_t cid = chunk_id(i);
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
       const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
+      if (parts & 1) {
       if constexpr (TR) tr_load(i);
 #pragma unroll
       for (int j = 0; j < (TR ? 0 : PP); ++j) {
@@ -324,6 +326,8 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         }
       }
       gl_dma(i, gl);
+      }
+      if (!(parts & 2)) return;
       gather_dv(i);
       // (scale qg^T do)^T[col][d]: wave w, tile at -> sQD[(w NDT + at) 64 + lane]
       if constexpr (!QG) {
@@ -445,22 +449,28 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       }
       return;
     }
+    // The next chunk's tiles and g_last move once A(i) has passed (their buffers
+    // were last read in chunk i-1), its gathers once B(i) has (single buffers,
+    // read between A(i) and B(i)); the touch comes last, so waiting for all but
+    // the touch waits for both.
     for (int i = 0; i < n; i += 2) {
       wait_step(i);
       if constexpr (TR) tr_store(sbuf0);
       exp_gl(sGL0);
       barrier();  // A(i)
+      if (i + 1 < n) issue(i + 1, sbuf1, sGL1, 1);
       barrier();  // B(i)
       if (i + 1 < n) {
-        issue(i + 1, sbuf1, sGL1);
+        issue(i + 1, sbuf1, sGL1, 2);
         if (i + 2 < n) touch(i + 2);
         if constexpr (KS > 1) barrier();  // X(i)
         wait_step(i + 1);
         if constexpr (TR) tr_store(sbuf1);
         exp_gl(sGL1);
         barrier();  // A(i+1)
+        if (i + 2 < n) issue(i + 2, sbuf0, sGL0, 1);
         barrier();  // B(i+1)
-        if (i + 2 < n) issue(i + 2, sbuf0, sGL0);
+        if (i + 2 < n) issue(i + 2, sbuf0, sGL0, 2);
         if (i + 3 < n) touch(i + 3);
         if constexpr (KS > 1) barrier();  // X(i+1)
       } else {
