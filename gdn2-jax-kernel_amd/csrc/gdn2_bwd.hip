@@ -301,13 +301,14 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         lds_dma16(dsrc + (size_t)w * 16 * BT + it * 16, &sDV[q * 64]);
       }
     };
-    // loads of chunk i: parts 1 the tiles (DMA, or TR: into registers) and g_last,
-    // 2 the gathers (dvp^T, qdot), 3 both
-    auto issue = [&](int i, char* base, float* gl, int parts = 3) __attribute__((always_inline)) {
+    // loads of chunk i, in parts: kTiles the tiles (DMA, or TR: into registers),
+    // kGl g_last, kGather the gathers (dvp^T, qdot)
+    constexpr int kTiles = 1, kGl = 2, kGather = 4, kAll = 7;
+    auto issue = [&](int i, char* base, float* gl, int parts) __attribute__((always_inline)) {
       const size_t cid = chunk_id(i);
       const char* wsrc = reinterpret_cast<const char*>(a.W + cid * BT * D);
       const char* ksrc = reinterpret_cast<const char*>(a.KgT + cid * D * BT);
-      if (parts & 1) {
+      if (parts & kTiles) {
       if constexpr (TR) tr_load(i);
 #pragma unroll
       for (int j = 0; j < (TR ? 0 : PP); ++j) {
@@ -325,9 +326,9 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
           lds_dma16(ksrc + (size_t)r * ROWB_K + ((pch ^ (r & M)) * 16), dst);
         }
       }
-      gl_dma(i, gl);
       }
-      if (!(parts & 2)) return;
+      if (parts & kGl) gl_dma(i, gl);
+      if (!(parts & kGather)) return;
       gather_dv(i);
       // (scale qg^T do)^T[col][d]: wave w, tile at -> sQD[(w NDT + at) 64 + lane]
       if constexpr (!QG) {
@@ -431,7 +432,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       return;
     }
     // The dvp / qdot buffer is single: the next chunk's gather goes out after B.
-    if (n > 0) issue(0, sbuf0, sGL0);
+    if (n > 0) issue(0, sbuf0, sGL0, kAll);
     if (n > 1) touch(1);
     if constexpr (NBUF == 1) {
       for (int i = 0; i < n; ++i) {
@@ -443,34 +444,38 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         if constexpr (KS > 1) barrier();  // X(i)
         barrier();  // E(i): chunk i's tiles are no longer read
         if (i + 1 < n) {
-          issue(i + 1, sbuf0, sGL0);
+          issue(i + 1, sbuf0, sGL0, kAll);
           if (i + 2 < n) touch(i + 2);
         }
       }
       return;
     }
     // The next chunk's tiles and g_last move once A(i) has passed (their buffers
-    // were last read in chunk i-1), its gathers once B(i) has (single buffers,
-    // read between A(i) and B(i)); the touch comes last, so waiting for all but
-    // the touch waits for both.
+    // were last read in chunk i-1) -- with TR the tile loads, into the producers'
+    // registers, already once this chunk's tiles are stored -- its gathers once
+    // B(i) has (single buffers, read between A(i) and B(i)); the touch comes
+    // last, so waiting for all but the touch waits for all of them.
+    constexpr int kEarly = TR ? kTiles : 0, kAfterA = TR ? kGl : kTiles | kGl;
     for (int i = 0; i < n; i += 2) {
       wait_step(i);
       if constexpr (TR) tr_store(sbuf0);
+      if (kEarly && i + 1 < n) issue(i + 1, sbuf1, sGL1, kEarly);
       exp_gl(sGL0);
       barrier();  // A(i)
-      if (i + 1 < n) issue(i + 1, sbuf1, sGL1, 1);
+      if (i + 1 < n) issue(i + 1, sbuf1, sGL1, kAfterA);
       barrier();  // B(i)
       if (i + 1 < n) {
-        issue(i + 1, sbuf1, sGL1, 2);
+        issue(i + 1, sbuf1, sGL1, kGather);
         if (i + 2 < n) touch(i + 2);
         if constexpr (KS > 1) barrier();  // X(i)
         wait_step(i + 1);
         if constexpr (TR) tr_store(sbuf1);
+        if (kEarly && i + 2 < n) issue(i + 2, sbuf0, sGL0, kEarly);
         exp_gl(sGL1);
         barrier();  // A(i+1)
-        if (i + 2 < n) issue(i + 2, sbuf0, sGL0, 1);
+        if (i + 2 < n) issue(i + 2, sbuf0, sGL0, kAfterA);
         barrier();  // B(i+1)
-        if (i + 2 < n) issue(i + 2, sbuf0, sGL0, 2);
+        if (i + 2 < n) issue(i + 2, sbuf0, sGL0, kGather);
         if (i + 3 < n) touch(i + 3);
         if constexpr (KS > 1) barrier();  // X(i+1)
       } else {
