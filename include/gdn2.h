@@ -21,8 +21,9 @@
  *  - Return value 0 on success, a negative GDN2_ERR_* code otherwise;
  *    gdn2_strerror() names it.  Invalid shapes are rejected before any launch.
  *  - No mutable global state beyond the per-thread timing request of
- *    gdn2_set_launch_events and the clip bound of gdn2_set_clip: calls on different streams may run concurrently
- *    provided their workspaces do not overlap.
+ *    gdn2_set_launch_events and the clip bound of gdn2_set_clip: calls on
+ *    different streams may run concurrently provided their workspaces do not
+ *    overlap.
  */
 #ifndef GDN2_H_
 #define GDN2_H_
@@ -90,7 +91,7 @@ size_t gdn2_fwd_workspace_bytes(int B, int T, int H, int D, int BT, int in_dtype
  * few (b,h) pairs split the serial chunk recurrence into S segments scanned in
  * parallel and chained by their affine transitions (the sequence-parallel
  * design of the reference's kernel D, gdn2_fwd.py:338-366).  The chaining is
- * exact while the +-1e4 clip of the carried state (gdn2_fwd.py:358) does not
+ * exact while the +-CLIP clip of the carried state (gdn2_fwd.py:358) does not
  * bind; the segmented passes flag any state clip that binds, and a flagged call
  * reruns the scan serially on the device (no host round trip), so the result
  * is the serial one either way.  n is clamped to [1, T/BT]; a forced count
