@@ -138,6 +138,14 @@ struct BStateArgs {
 // place of the qdot gather: each compute wave then loads its own 16-byte qdot
 // pieces (four per step) straight from global memory one step ahead, hitting
 // L2 behind the producers' touch.
+// Float32 tiles: the scan's two chained products (kg dh, W^T dv_new) in the split
+// form (gdn2_common.h: three bfloat16 MFMAs per 32-deep k step instead of eight
+// float32 ones).
+#ifndef GDN2_SPLIT_SCAN
+#define GDN2_SPLIT_SCAN 1
+#endif
+constexpr bool kSplitScanB = GDN2_SPLIT_SCAN != 0;
+
 template <typename T, int D>
 constexpr int bstate_ksplit() { return sizeof(T) == 4 || D <= 128 ? 2 : 1; }
 
@@ -578,6 +586,18 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       f32x4 part[NB];
 #pragma unroll
       for (int it = 0; it < NB; ++it) part[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (TR && kSplitScanB) {
+        // split form (gdn2_common.h): dh split once per chunk, kg pairs as read
+        static_assert(NDH % 2 == 0, "pairs of k-groups");
+        Split8 dhs[NDH / 2];
+#pragma unroll
+        for (int q = 0; q < NDH / 2; ++q) dhs[q] = split8(dh[2 * q], dh[2 * q + 1]);
+#pragma unroll
+        for (int q = 0; q < NDH / 2; ++q)
+#pragma unroll
+          for (int it = 0; it < NB; ++it)
+            mma3(part[it], split8(xk(ks * NDH + 2 * q, it), xk(ks * NDH + 2 * q + 1, it)), dhs[q]);
+      } else {
 #pragma unroll
       for (int j = 0; j < NDH; ++j) {
         const int at = ks * NDH + j;
@@ -592,6 +612,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
             mma(part[it], x, dh[j]);
           }
         }
+      }
       }
       // exchange the halves; both waves form dv_new in the same order
 #pragma unroll
@@ -632,12 +653,23 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
 
     // dh <- e^{gl} dh + qdot - W^T dv_new: X[d][t] = W[t][d]
     if constexpr (QG && !QAHEAD) load_qd(i, qd);
+    // split form: dv_new split once per chunk, W^T pairs as read
+    constexpr bool SPB = TR && kSplitScanB;
+    Split8 dvs[SPB ? NB / 2 : 1];
+    if constexpr (SPB) {
+#pragma unroll
+      for (int q = 0; q < NB / 2; ++q) dvs[q] = split8(dvn[2 * q], dvn[2 * q + 1]);
+    }
 #pragma unroll
     for (int j = 0; j < NDH; ++j) {
       const int at = ks * NDH + j;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (SPB) {
 #pragma unroll
-      for (int it = 0; it < NB; ++it) {
+        for (int q = 0; q < NB / 2; ++q) mma3(acc, split8(xw(2 * q, at), xw(2 * q + 1, at)), dvs[q]);
+      }
+#pragma unroll
+      for (int it = 0; it < (SPB ? 0 : NB); ++it) {
         if constexpr (TR) {
           mma(acc, xw(it, at), dvn[it]);
         } else {

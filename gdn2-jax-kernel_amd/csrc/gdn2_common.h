@@ -86,6 +86,45 @@ __device__ __forceinline__ void mma(f32x4& acc, const bf16x8& x, const bf16x8& y
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, acc, 0, 0, 0);
 }
 
+// float32 products on the bfloat16 matrix cores ("split" form).  A float32
+// operand element x is carried as hi = bf16(x) and lo = bf16(x - hi), so that
+// x = hi + lo to about 2^-17 relative, and x y = hi_x hi_y + hi_x lo_y + lo_x hi_y
+// + lo_x lo_y; the last term (2^-18 relative) is dropped.  Three 16x16x32 bfloat16
+// MFMAs then replace the eight 16x16x4 float32 MFMAs of a 32-deep k step: the
+// bfloat16 products are exact in the float32 accumulator.  The eight k positions
+// a lane feeds are two consecutive float32 k-groups (elements e of both operands
+// pair up, as in the float32 form), so the float32 operand layouts are unchanged.
+struct Split8 {
+  bf16x8 hi, lo;
+};
+__device__ __forceinline__ Split8 split8(const f32x4& a, const f32x4& b) {
+  Split8 s;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    s.hi[e] = (bf16_t)a[e];
+    s.hi[4 + e] = (bf16_t)b[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    s.lo[e] = (bf16_t)(a[e] - (float)s.hi[e]);
+    s.lo[4 + e] = (bf16_t)(b[e] - (float)s.hi[4 + e]);
+  }
+  return s;
+}
+// Split pair layout of a float32 tile in LDS: in every 32-element run of a row
+// (eight 16-byte chunks, chunk j = elements 4j .. 4j+3) the chunks j and 4 + j
+// (j < 4) are replaced by the hi and the lo parts of their eight elements, in
+// the order of split8(chunk j, chunk 4 + j).  A lane that reads chunks j and 4 + j
+// for two consecutive k-groups of the float32 form then holds its split operand.
+__device__ __forceinline__ Split8 split_read(const f32x4& chunk_hi, const f32x4& chunk_lo) {
+  return Split8{__builtin_bit_cast(bf16x8, chunk_hi), __builtin_bit_cast(bf16x8, chunk_lo)};
+}
+__device__ __forceinline__ void mma3(f32x4& acc, const Split8& x, const Split8& y) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.lo, y.hi, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.hi, y.lo, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.hi, y.hi, acc, 0, 0, 0);
+}
+
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(bf16_t x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f(float x);

@@ -830,6 +830,14 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
 }
 
 // ---------------------------------------------------------------------------
+// Float32 scans form their two chained products (W h, kg^T v_new) in the split
+// form (gdn2_common.h: three bfloat16 MFMAs per 32-deep k step instead of eight
+// float32 ones), which shortens the serial chain per chunk.
+#ifndef GDN2_SPLIT_SCAN
+#define GDN2_SPLIT_SCAN 1
+#endif
+constexpr bool kSplitScan = GDN2_SPLIT_SCAN != 0;
+
 template <typename T>
 struct StateArgs {
   const T* W;
@@ -1450,7 +1458,20 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
         else return op_load<T>(&sW[swz(r, (ks * NKD + kk) * 32 + 8 * lg, D)]);
       };
       f32x4 acc[NB];
-      if constexpr (F32) {
+      if constexpr (F32 && kSplitScan) {
+        // split form: h split once per chunk, each W operand pair as it is read
+        static_assert(NKD % 2 == 0, "pairs of k-groups");
+        Split8 hs[NKD / 2];
+#pragma unroll
+        for (int p = 0; p < NKD / 2; ++p) hs[p] = split8(hb[2 * p], hb[2 * p + 1]);
+#pragma unroll
+        for (int it = 0; it < NB; ++it) acc[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < NKD / 2; ++p)
+#pragma unroll
+          for (int it = 0; it < NB; ++it)
+            mma3(acc[it], split8(wop(it, 2 * p), wop(it, 2 * p + 1)), hs[p]);
+      } else if constexpr (F32) {
         Op wc[NB], wn[NB];
 #pragma unroll
         for (int it = 0; it < NB; ++it) {
@@ -1555,7 +1576,18 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
         if constexpr (F32) return load4f(&sK[swz(r, kk * 16 + 4 * lg, BT)]);
         else return op_load<T>(&sK[swz(r, kk * 32 + 8 * lg, BT)]);
       };
-      if constexpr (!F32) {
+      if constexpr (F32 && kSplitScan) {
+        // split form: v_new split once per chunk, each kg^T operand pair as read
+        static_assert(NKT % 2 == 0, "pairs of k-groups");
+        Split8 vs2[NKT / 2];
+#pragma unroll
+        for (int p = 0; p < NKT / 2; ++p) vs2[p] = split8(vn[2 * p], vn[2 * p + 1]);
+#pragma unroll
+        for (int p = 0; p < NKT / 2; ++p)
+#pragma unroll
+          for (int at = 0; at < NDH; ++at)
+            mma3(h[at], split8(kop(at, 2 * p), kop(at, 2 * p + 1)), vs2[p]);
+      } else if constexpr (!F32) {
         // bfloat16: one chain per row tile of h, as for W h above
         Op vb[NKT], kc2[NKT], kn2[NKT];
 #pragma unroll
