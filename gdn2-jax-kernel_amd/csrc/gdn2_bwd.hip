@@ -124,12 +124,14 @@ struct BStateArgs {
 // other half of an LDS double buffer with global_load_lds_dwordx4 and gather the
 // workgroup's dvp and qg^T do rows into the compute lanes' order (one buffer,
 // freed by barrier B once copied to registers); the compute waves issue no
-// global loads.  Both products read their tile transposed.  Float32 tiles up to
-// D = 128 are staged by the producers through registers and stored transposed
-// (W^T, kg), so each MFMA operand is one 16-byte LDS read; otherwise (DMA) one
-// 4-byte (2-byte for bfloat16 residuals, chained column order) LDS read per
-// element.  The XOR swizzle of the 16-byte chunks keeps either free of bank
-// conflicts.
+// global loads.  Both products read their tile transposed.  Float32 tiles (in
+// the split pair layout of gdn2_common.h, as fwd_prep writes W and kg^T) are
+// staged by the producers through registers and stored transposed (W^T, kg),
+// still split, so each operand pair is two 16-byte LDS reads and each 32-deep k
+// step three bfloat16 MFMAs (the split form; dh and dv_new are split once per
+// chunk); bfloat16 tiles move by DMA, one 2-byte LDS read per element (chained
+// column order).  The XOR swizzle of the 16-byte chunks keeps either free of
+// bank conflicts.
 //
 // K-split (KS = 2; bfloat16 residuals only up to D = 128, where its registers
 // fit), as in fwd_state: two compute waves per
@@ -138,14 +140,6 @@ struct BStateArgs {
 // place of the qdot gather: each compute wave then loads its own 16-byte qdot
 // pieces (four per step) straight from global memory one step ahead, hitting
 // L2 behind the producers' touch.
-// Float32 tiles: the scan's two chained products (kg dh, W^T dv_new) in the split
-// form (gdn2_common.h: three bfloat16 MFMAs per 32-deep k step instead of eight
-// float32 ones).
-#ifndef GDN2_SPLIT_SCAN
-#define GDN2_SPLIT_SCAN 1
-#endif
-constexpr bool kSplitScanB = GDN2_SPLIT_SCAN != 0;
-
 template <typename T, int D>
 constexpr int bstate_ksplit() { return sizeof(T) == 4 || D <= 128 ? 2 : 1; }
 
@@ -154,6 +148,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
   constexpr int NB = BT / 16, NDT = D / 16;
   constexpr int NCW = NW * KS, NDH = NDT / KS;
   static_assert(KS == 1 || (NDT % KS == 0 && NB % KS == 0), "K-split must tile dh and dv_new");
+  static_assert(sizeof(T) == 2 || KS == 2, "float32 tiles (split products) run the K-split");
   constexpr int NVS = D / (16 * NW);
   constexpr int WBYTES = BT * D * (int)sizeof(T);
   constexpr int BUF = 2 * WBYTES;
@@ -214,10 +209,19 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
   // at once would spill)
   constexpr bool TR = sizeof(T) == 4;
   // element offset of logical (row r, element e) in a float32 tile with `re`
-  // elements per row, its 16-byte chunks XOR-swizzled by the row
+  // elements per row, its 16-byte chunks XOR-swizzled by the row: by r ^ (r >> 4),
+  // a permutation over any 16 consecutive rows (the MFMA operand reads), which also
+  // spreads the rows 4 w + c that the producers' transposed stores of one
+  // instruction write (by r alone those take four chunk places, an 8-way LDS bank
+  // conflict)
   auto swz = [](int r, int e, int re) {
     const int nchunk = re / 4, m = (nchunk < 16 ? nchunk : 16) - 1;
-    return r * re + (((e / 4) ^ (r & m)) * 4) + (e % 4);
+    return r * re + (((e / 4) ^ ((r ^ (r >> 4)) & m)) * 4) + (e % 4);
+  };
+  // the same for byte `pos` of row r, as a byte offset
+  auto swzb = [](int r, int pos, int re) {
+    const int nchunk = re / 4, m = (nchunk < 16 ? nchunk : 16) - 1;
+    return r * re * 4 + (((pos / 16) ^ ((r ^ (r >> 4)) & m)) * 16) + (pos % 16);
   };
 
   if (wv >= NCW) {
@@ -234,9 +238,12 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
     constexpr int NBLK = (BT / 4) * (D / 4);                // blocks per tile
     constexpr int BPL = TR ? NBLK / (64 * NP) : 1;          // blocks per producer lane
     static_assert(!TR || NBLK % (64 * NP) == 0, "blocks must split over the producers");
-    f32x4 stW[BPL][4], stK[BPL][4];
+    // The stored tiles are in the split pair layout (gdn2_common.h): a block row's
+    // four elements are 8 bytes of hi and 8 of lo, moved and transposed as they
+    // are, into the same layout of the transposed tile (no arithmetic)
+    Split4 stW[BPL][4], stK[BPL][4];
     auto tr_load_w = [&](int i) __attribute__((always_inline)) {
-      const float* w = reinterpret_cast<const float*>(a.W) + chunk_id(i) * BT * D;  // [t][d]
+      const char* w = reinterpret_cast<const char*>(a.W + chunk_id(i) * BT * D);  // [t][d]
       int ln = lane;   // one tile buffer: the block offsets are recomputed per
       if constexpr (NBUF == 1) asm volatile("" : "+v"(ln));   // staging, not kept live
 #pragma unroll
@@ -244,11 +251,11 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         const int b = (q * NP + p) * 64 + ln;
         const int wt4 = b / (D / 4), wd4 = b % (D / 4);     // W rows 4 wt4 + r, columns 4 wd4
 #pragma unroll
-        for (int r = 0; r < 4; ++r) stW[q][r] = load4f(w + (size_t)(4 * wt4 + r) * D + 4 * wd4);
+        for (int r = 0; r < 4; ++r) stW[q][r] = split_load4(w + (size_t)(4 * wt4 + r) * D * 4, 4 * wd4);
       }
     };
     auto tr_load_k = [&](int i) __attribute__((always_inline)) {
-      const float* k = reinterpret_cast<const float*>(a.KgT) + chunk_id(i) * D * BT;  // [d][t]
+      const char* k = reinterpret_cast<const char*>(a.KgT + chunk_id(i) * D * BT);  // [d][t]
       int ln = lane;   // one tile buffer: the block offsets are recomputed per
       if constexpr (NBUF == 1) asm volatile("" : "+v"(ln));   // staging, not kept live
 #pragma unroll
@@ -256,11 +263,20 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         const int b = (q * NP + p) * 64 + ln;
         const int kd4 = b / (BT / 4), kt4 = b % (BT / 4);   // kg^T rows 4 kd4 + r, columns 4 kt4
 #pragma unroll
-        for (int r = 0; r < 4; ++r) stK[q][r] = load4f(k + (size_t)(4 * kd4 + r) * BT + 4 * kt4);
+        for (int r = 0; r < 4; ++r) stK[q][r] = split_load4(k + (size_t)(4 * kd4 + r) * BT * 4, 4 * kt4);
       }
     };
+    // hi and lo of column c of a staged block as the 4-element runs of the
+    // transposed row, at element e of row r of a swizzled tile with `re` elements
+    // per row
+    auto put_t = [&](char* tile, int r, int e, int re, const Split4 (&s)[4], int c) __attribute__((always_inline)) {
+      const bf16x4 hi = {s[0].hi[c], s[1].hi[c], s[2].hi[c], s[3].hi[c]};
+      const bf16x4 lo = {s[0].lo[c], s[1].lo[c], s[2].lo[c], s[3].lo[c]};
+      const int pos = (e / 32) * 128 + split_pos(e % 32);     // unswizzled byte in the row
+      *reinterpret_cast<bf16x4*>(tile + swzb(r, pos, re)) = hi;
+      *reinterpret_cast<bf16x4*>(tile + swzb(r, pos + 64, re)) = lo;
+    };
     auto tr_store_w = [&](char* base) __attribute__((always_inline)) {
-      float* wt = reinterpret_cast<float*>(base);            // W^T [d][t]
       int ln = lane;   // one tile buffer: the block offsets are recomputed per
       if constexpr (NBUF == 1) asm volatile("" : "+v"(ln));   // staging, not kept live
 #pragma unroll
@@ -268,13 +284,10 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         const int b = (q * NP + p) * 64 + ln;
         const int wt4 = b / (D / 4), wd4 = b % (D / 4);
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          store4(&wt[swz(4 * wd4 + c, 4 * wt4, BT)],
-                 f32x4{stW[q][0][c], stW[q][1][c], stW[q][2][c], stW[q][3][c]});
+        for (int c = 0; c < 4; ++c) put_t(base, 4 * wd4 + c, 4 * wt4, BT, stW[q], c);   // W^T [d][t]
       }
     };
     auto tr_store_k = [&](char* base) __attribute__((always_inline)) {
-      float* kt = reinterpret_cast<float*>(base + WBYTES);   // kg [t][d]
       int ln = lane;   // one tile buffer: the block offsets are recomputed per
       if constexpr (NBUF == 1) asm volatile("" : "+v"(ln));   // staging, not kept live
 #pragma unroll
@@ -282,9 +295,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         const int b = (q * NP + p) * 64 + ln;
         const int kd4 = b / (BT / 4), kt4 = b % (BT / 4);
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          store4(&kt[swz(4 * kt4 + c, 4 * kd4, D)],
-                 f32x4{stK[q][0][c], stK[q][1][c], stK[q][2][c], stK[q][3][c]});
+        for (int c = 0; c < 4; ++c) put_t(base + WBYTES, 4 * kt4 + c, 4 * kd4, D, stK[q], c);   // kg [t][d]
       }
     };
     auto tr_load = [&](int i) __attribute__((always_inline)) {
@@ -459,11 +470,45 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       return;
     }
     // The next chunk's tiles and g_last move once A(i) has passed (their buffers
-    // were last read in chunk i-1) -- with TR the tile loads, into the producers'
-    // registers, already once this chunk's tiles are stored -- its gathers once
-    // B(i) has (single buffers, read between A(i) and B(i)); the touch comes
-    // last, so waiting for all but the touch waits for all of them.
-    constexpr int kEarly = TR ? kTiles : 0, kAfterA = TR ? kGl : kTiles | kGl;
+    // were last read in chunk i-1), its gathers once B(i) has (single buffers,
+    // read between A(i) and B(i)); the touch comes last, so waiting for all but
+    // the touch waits for all of them.
+    if constexpr (TR) {
+      // Through registers: chunk i's kg is stored before A(i) (the first product
+      // reads it after B(i)), its W after B(i), behind the compute waves' kg dh
+      // (the dh update reads it after X(i)); chunk i+1's tile loads then go out
+      // with its gathers, g_last once A(i) has freed its buffer.
+      for (int i = 0; i < n; i += 2) {
+        wait_step(i);
+        tr_store_k(sbuf0);
+        exp_gl(sGL0);
+        barrier();  // A(i)
+        if (i + 1 < n) issue(i + 1, sbuf1, sGL1, kGl);
+        barrier();  // B(i)
+        tr_store_w(sbuf0);
+        if (i + 1 < n) {
+          issue(i + 1, sbuf1, sGL1, kTiles | kGather);
+          if (i + 2 < n) touch(i + 2);
+          barrier();  // X(i)
+          wait_step(i + 1);
+          tr_store_k(sbuf1);
+          exp_gl(sGL1);
+          barrier();  // A(i+1)
+          if (i + 2 < n) issue(i + 2, sbuf0, sGL0, kGl);
+          barrier();  // B(i+1)
+          tr_store_w(sbuf1);
+          if (i + 2 < n) {
+            issue(i + 2, sbuf0, sGL0, kTiles | kGather);
+            if (i + 3 < n) touch(i + 3);
+          }
+          barrier();  // X(i+1)
+        } else {
+          barrier();  // X(i)
+        }
+      }
+      return;
+    }
+    constexpr int kEarly = 0, kAfterA = kTiles | kGl;
     for (int i = 0; i < n; i += 2) {
       wait_step(i);
       if constexpr (TR) tr_store(sbuf0);
@@ -586,8 +631,8 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       f32x4 part[NB];
 #pragma unroll
       for (int it = 0; it < NB; ++it) part[it] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (TR && kSplitScanB) {
-        // split form (gdn2_common.h): dh split once per chunk, kg pairs as read
+      if constexpr (TR) {
+        // split form: dh split once per chunk; the kg tile holds the split pairs
         static_assert(NDH % 2 == 0, "pairs of k-groups");
         Split8 dhs[NDH / 2];
 #pragma unroll
@@ -596,21 +641,17 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
         for (int q = 0; q < NDH / 2; ++q)
 #pragma unroll
           for (int it = 0; it < NB; ++it)
-            mma3(part[it], split8(xk(ks * NDH + 2 * q, it), xk(ks * NDH + 2 * q + 1, it)), dhs[q]);
+            mma3(part[it], split_read(xk(ks * NDH + 2 * q, it), xk(ks * NDH + 2 * q + 1, it)), dhs[q]);
       } else {
 #pragma unroll
       for (int j = 0; j < NDH; ++j) {
         const int at = ks * NDH + j;
 #pragma unroll
         for (int it = 0; it < NB; ++it) {
-          if constexpr (TR) {
-            mma(part[it], xk(at, it), dh[j]);
-          } else {
-            f32x4 x;
+          f32x4 x;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
-            mma(part[it], x, dh[j]);
-          }
+          for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
+          mma(part[it], x, dh[j]);
         }
       }
       }
@@ -631,14 +672,10 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       for (int it = 0; it < NB; ++it) {
 #pragma unroll
         for (int at = 0; at < NDT; ++at) {
-          if constexpr (TR) {
-            mma(dvn[it], xk(at, it), dh[at]);
-          } else {
-            f32x4 x;
+          f32x4 x;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
-            mma(dvn[it], x, dh[at]);
-          }
+          for (int e = 0; e < 4; ++e) x[e] = elem(sK, at * 16 + 4 * lg + e, it * 16 + li, BT);
+          mma(dvn[it], x, dh[at]);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) dvn[it][r] = sanitize(dvn[it][r]);
@@ -653,10 +690,9 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
 
     // dh <- e^{gl} dh + qdot - W^T dv_new: X[d][t] = W[t][d]
     if constexpr (QG && !QAHEAD) load_qd(i, qd);
-    // split form: dv_new split once per chunk, W^T pairs as read
-    constexpr bool SPB = TR && kSplitScanB;
-    Split8 dvs[SPB ? NB / 2 : 1];
-    if constexpr (SPB) {
+    // split form: dv_new split once per chunk; the W^T tile holds the split pairs
+    Split8 dvs[TR ? NB / 2 : 1];
+    if constexpr (TR) {
 #pragma unroll
       for (int q = 0; q < NB / 2; ++q) dvs[q] = split8(dvn[2 * q], dvn[2 * q + 1]);
     }
@@ -664,15 +700,12 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
     for (int j = 0; j < NDH; ++j) {
       const int at = ks * NDH + j;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (SPB) {
+      if constexpr (TR) {
 #pragma unroll
-        for (int q = 0; q < NB / 2; ++q) mma3(acc, split8(xw(2 * q, at), xw(2 * q + 1, at)), dvs[q]);
-      }
+        for (int q = 0; q < NB / 2; ++q) mma3(acc, split_read(xw(2 * q, at), xw(2 * q + 1, at)), dvs[q]);
+      } else {
 #pragma unroll
-      for (int it = 0; it < (SPB ? 0 : NB); ++it) {
-        if constexpr (TR) {
-          mma(acc, xw(it, at), dvn[it]);
-        } else {
+        for (int it = 0; it < NB; ++it) {
           f32x4 x;
 #pragma unroll
           for (int e = 0; e < 4; ++e) x[e] = elem(sW, it * 16 + 4 * lg + e, at * 16 + li, D);
@@ -2329,6 +2362,7 @@ hipError_t launch_stage_dhu(hipStream_t st, int B, int N, int H, const float* do
   float* QDOT = m.take(NC * D * D);
   float* DVPT = m.take(NC * D * SBT);
   float* KgT = m.take(NC * D * SBT);
+  float* Wsp = m.take(NC * SBT * D);
   float* DHT = m.take(NC * D * D);
   float* DVNT = m.take(NC * D * SBT);
   if (!ws) { *need = m.off; return hipSuccess; }
@@ -2342,8 +2376,11 @@ hipError_t launch_stage_dhu(hipStream_t st, int B, int N, int H, const float* do
     hipLaunchKernelGGL((bwd_b2<float, D, kB2Qdot>), dim3(NC), dim3(64 * b2_waves(D)), 0, st, ba);
     transpose_all(st, dv_partial, DVPT, NC, SBT, D);
     transpose_all(st, kg, KgT, NC, SBT, D);
+    // the scan's float32 tiles in the split pair layout, as fwd_prep writes them
+    split_runs(st, KgT, KgT, NC * D * SBT / 32);
+    split_runs(st, w_pseudo, Wsp, NC * SBT * D / 32);
   }
-  BStateArgs<float> sa{w_pseudo, KgT, gc_last, DVPT, QDOT, dht, N, DHT, DVNT, dh0, nullptr, 1, H};
+  BStateArgs<float> sa{Wsp, KgT, gc_last, DVPT, QDOT, dht, N, DHT, DVNT, dh0, nullptr, 1, H};
   constexpr int BW = 2, BK = bstate_ksplit<float, D>(), BP = BK > 1 ? 4 : 2;
   hipLaunchKernelGGL((bwd_state<float, SBT, D, BW, BP, BK>), dim3(BH * (D / (16 * BW))),
                      dim3(64 * (BW * BK + BP)), 0, st, sa);

@@ -119,6 +119,43 @@ __device__ __forceinline__ Split8 split8(const f32x4& a, const f32x4& b) {
 __device__ __forceinline__ Split8 split_read(const f32x4& chunk_hi, const f32x4& chunk_lo) {
   return Split8{__builtin_bit_cast(bf16x8, chunk_hi), __builtin_bit_cast(bf16x8, chunk_lo)};
 }
+// Byte offset, inside its 128-byte run, of the hi part of element e (0..31) of a
+// run in the split pair layout (the lo part is 64 bytes further): chunk
+// (e mod 16) / 4, slot 4 (e / 16) + e mod 4.  Four consecutive elements 4m .. 4m+3
+// are one aligned 8-byte half chunk.
+__host__ __device__ constexpr int split_pos(int e) {
+  return ((e % 16) / 4) * 16 + ((e / 16) * 4 + e % 4) * 2;
+}
+struct Split4 {
+  bf16x4 hi, lo;
+};
+__device__ __forceinline__ Split4 split4(const f32x4& a) {
+  Split4 s;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s.hi[e] = (bf16_t)a[e];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s.lo[e] = (bf16_t)(a[e] - (float)s.hi[e]);
+  return s;
+}
+// Four consecutive elements 4m .. 4m+3 (m = e / 4) of a row stored in the split
+// pair layout, `row` the row's first byte.
+__device__ __forceinline__ void split_store4(char* row, int e, const f32x4& v) {
+  const Split4 s = split4(v);
+  char* p = row + (e / 32) * 128 + split_pos(e % 32);
+  *reinterpret_cast<bf16x4*>(p) = s.hi;
+  *reinterpret_cast<bf16x4*>(p + 64) = s.lo;
+}
+__device__ __forceinline__ void split_store1(char* row, int e, float v) {
+  const bf16_t hi = (bf16_t)v, lo = (bf16_t)(v - (float)hi);
+  char* p = row + (e / 32) * 128 + split_pos(e % 32);
+  *reinterpret_cast<bf16_t*>(p) = hi;
+  *reinterpret_cast<bf16_t*>(p + 64) = lo;
+}
+// The four elements 4m .. 4m+3 of a row in the split pair layout, as hi and lo.
+__device__ __forceinline__ Split4 split_load4(const char* row, int e) {
+  const char* p = row + (e / 32) * 128 + split_pos(e % 32);
+  return Split4{*reinterpret_cast<const bf16x4*>(p), *reinterpret_cast<const bf16x4*>(p + 64)};
+}
 __device__ __forceinline__ void mma3(f32x4& acc, const Split8& x, const Split8& y) {
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.lo, y.hi, acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.hi, y.lo, acc, 0, 0, 0);

@@ -41,9 +41,9 @@ struct PrepArgs {
   int T_len, H, N;
   long long NC;   // number of chunks, B*H*N
   float scale;
-  T* W;
+  T* W;     // [cid][BT][D]; float32: in the split pair layout (kPrepFull)
   T* UT;
-  T* KgT;
+  T* KgT;   // [cid][D][BT]; float32: in the split pair layout (kPrepFull)
   T* Qg;
   T* Aqk;
   float* GL;
@@ -215,6 +215,9 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
     fwd_prep(PrepArgs<T, TG, TI> a) {
   static_assert(MODE == kPrepFull || (sizeof(T) == 4 && BT == 64),
                 "the stage modes run float32 tiles at chunk 64");
+  // float32 tiles of the forward: W and kg^T in the split pair layout of the
+  // float32 scans (gdn2_common.h), whose MFMA operands they are
+  constexpr bool SPF = sizeof(T) == 4 && MODE == kPrepFull;
   using Op = typename Tr<T>::Op;
   constexpr int KC = Tr<T>::KC, KS = Tr<T>::KS;
   constexpr int NB = BT / 16;             // 16-token row blocks
@@ -477,7 +480,11 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
           qg[e] = sanitize(qv * egc);
           if constexpr (MODE != kPrepScores) sKbdT[(d0 + ch) * TT_LD + t] = from_f<T>(bk * egc);
           const float kgv = sanitize(kv * ekh * sF1[I * DP + ch]);
-          if constexpr (MODE == kPrepFull) kgT[(size_t)(d0 + ch) * BT + kpos<T>(t)] = from_f<T>(kgv);
+          if constexpr (SPF) {
+            split_store1(reinterpret_cast<char*>(kgT + (size_t)(d0 + ch) * BT), t, kgv);
+          } else if constexpr (MODE == kPrepFull) {
+            kgT[(size_t)(d0 + ch) * BT + kpos<T>(t)] = from_f<T>(kgv);
+          }
           kgr[e] = kgv;
           kh[e] = kv * ekh;
           aq[i][x] = qv * eloc;
@@ -817,7 +824,12 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
           mma(accu, af, op_load<T>(&sWVT[(dt * 16 + li) * TT_LD + kg * KS + lg * KC]));
         }
       }
-      store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dg + 4 * lg), sanitize4(accw));
+      if constexpr (SPF) {
+        split_store4(reinterpret_cast<char*>(Wc + (size_t)(I * 16 + li) * D), dg + 4 * lg,
+                     sanitize4(accw));
+      } else {
+        store4(Wc + (size_t)(I * 16 + li) * D + kpos<T>(dg + 4 * lg), sanitize4(accw));
+      }
       if constexpr (MODE == kPrepWy) {   // u [t][d]
         T* uc = a.UT + (size_t)cid * BT * D;
 #pragma unroll
@@ -830,14 +842,6 @@ __global__ void __launch_bounds__(64 * prep_waves(BT), prep_min_blocks(sizeof(T)
 }
 
 // ---------------------------------------------------------------------------
-// Float32 scans form their two chained products (W h, kg^T v_new) in the split
-// form (gdn2_common.h: three bfloat16 MFMAs per 32-deep k step instead of eight
-// float32 ones), which shortens the serial chain per chunk.
-#ifndef GDN2_SPLIT_SCAN
-#define GDN2_SPLIT_SCAN 1
-#endif
-constexpr bool kSplitScan = GDN2_SPLIT_SCAN != 0;
-
 template <typename T>
 struct StateArgs {
   const T* W;
@@ -896,7 +900,11 @@ struct StateArgs {
 //
 // W / kg^T tiles are stored unpadded with the 16-byte chunks of row r
 // XOR-permuted by (r mod 16), so the 16 rows an MFMA operand read touches land
-// in distinct LDS banks.  u^T is gathered straight into the order the compute
+// in distinct LDS banks.  Float32 tiles arrive in the split pair layout
+// (written so by fwd_prep, gdn2_common.h), and the two products run in the split
+// form: three bfloat16 MFMAs per 32-deep k step instead of eight float32 ones,
+// with h and v_new split once per chunk; the DMA moves the 16-byte chunks as
+// they are.  u^T is gathered straight into the order the compute
 // lanes read it (one contiguous 1 KB block per wave and row block).  The two
 // halves of the W / kg^T double buffer are separate __shared__ arrays selected
 // at compile time (the chunk loop is unrolled by two), so the compiler can see
@@ -1458,8 +1466,9 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
         else return op_load<T>(&sW[swz(r, (ks * NKD + kk) * 32 + 8 * lg, D)]);
       };
       f32x4 acc[NB];
-      if constexpr (F32 && kSplitScan) {
-        // split form: h split once per chunk, each W operand pair as it is read
+      if constexpr (F32) {
+        // split form: h split once per chunk; the W tile holds the split pairs
+        // (chunks 2p, 2p+1 of a lane are one pair), all row blocks independent
         static_assert(NKD % 2 == 0, "pairs of k-groups");
         Split8 hs[NKD / 2];
 #pragma unroll
@@ -1470,25 +1479,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
         for (int p = 0; p < NKD / 2; ++p)
 #pragma unroll
           for (int it = 0; it < NB; ++it)
-            mma3(acc[it], split8(wop(it, 2 * p), wop(it, 2 * p + 1)), hs[p]);
-      } else if constexpr (F32) {
-        Op wc[NB], wn[NB];
-#pragma unroll
-        for (int it = 0; it < NB; ++it) {
-          acc[it] = f32x4{0.f, 0.f, 0.f, 0.f};
-          wc[it] = wop(it, 0);
-        }
-#pragma unroll
-        for (int kk = 0; kk < NKD; ++kk) {
-          if (kk + 1 < NKD) {
-#pragma unroll
-            for (int it = 0; it < NB; ++it) wn[it] = wop(it, kk + 1);
-          }
-#pragma unroll
-          for (int it = 0; it < NB; ++it) mma(acc[it], wc[it], hb[kk]);
-#pragma unroll
-          for (int it = 0; it < NB; ++it) wc[it] = wn[it];
-        }
+            mma3(acc[it], split_read(wop(it, 2 * p), wop(it, 2 * p + 1)), hs[p]);
       } else {
         // bfloat16: one accumulator chain at a time (a chain of dependent
         // 16x16x32 MFMAs issues faster than interleaved accumulators); the next
@@ -1559,12 +1550,10 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
         *reinterpret_cast<Op*>(vT + p * 32 + 8 * lg) = op_from_c(vn[2 * p], vn[2 * p + 1], (Op*)nullptr);
     }
 
-    // h <- e^{g_last} h + kg^T v_new: the NDT row tiles of h are independent
-    // accumulators, the k-step over tokens outermost (as above); the next
-    // k-step's kg^T operands are read ahead while NDT <= 8 (registers).
+    // h <- e^{g_last} h + kg^T v_new (the row tiles of h are independent
+    // accumulators)
     {
       constexpr int NKT = F32 ? NB : NB / 2;     // k-steps over t
-      constexpr bool AHEAD = NDT <= 8;
 #pragma unroll
       for (int i = 0; i < NDH; ++i) {
         const f32x4 egl = load4f(eglc + (ks * NDH + i) * 16 + 4 * lg);
@@ -1576,8 +1565,9 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
         if constexpr (F32) return load4f(&sK[swz(r, kk * 16 + 4 * lg, BT)]);
         else return op_load<T>(&sK[swz(r, kk * 32 + 8 * lg, BT)]);
       };
-      if constexpr (F32 && kSplitScan) {
-        // split form: v_new split once per chunk, each kg^T operand pair as read
+      if constexpr (F32) {
+        // split form: v_new split once per chunk; the kg^T tile holds the split
+        // pairs, all row tiles of h independent
         static_assert(NKT % 2 == 0, "pairs of k-groups");
         Split8 vs2[NKT / 2];
 #pragma unroll
@@ -1586,8 +1576,8 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
         for (int p = 0; p < NKT / 2; ++p)
 #pragma unroll
           for (int at = 0; at < NDH; ++at)
-            mma3(h[at], split8(kop(at, 2 * p), kop(at, 2 * p + 1)), vs2[p]);
-      } else if constexpr (!F32) {
+            mma3(h[at], split_read(kop(at, 2 * p), kop(at, 2 * p + 1)), vs2[p]);
+      } else {
         // bfloat16: one chain per row tile of h, as for W h above
         Op vb[NKT], kc2[NKT], kn2[NKT];
 #pragma unroll
@@ -1606,31 +1596,6 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP + NO)) fwd_state(StateArgs<
 #pragma unroll
           for (int kk = 0; kk < NKT; ++kk) kc2[kk] = kn2[kk];
         }
-      } else {
-      Op kc[NDH], kn[AHEAD ? NDH : 1];
-      if constexpr (AHEAD) {
-#pragma unroll
-        for (int at = 0; at < NDH; ++at) kc[at] = kop(at, 0);
-      }
-#pragma unroll
-      for (int kk = 0; kk < NKT; ++kk) {
-        Op vb;
-        if constexpr (F32) vb = vn[kk];
-        else vb = op_from_c(vn[2 * kk], vn[2 * kk + 1], (Op*)nullptr);
-        if constexpr (AHEAD) {
-          if (kk + 1 < NKT) {
-#pragma unroll
-            for (int at = 0; at < NDH; ++at) kn[at] = kop(at, kk + 1);
-          }
-#pragma unroll
-          for (int at = 0; at < NDH; ++at) mma(h[at], kc[at], vb);
-#pragma unroll
-          for (int at = 0; at < NDH; ++at) kc[at] = kn[at];
-        } else {
-#pragma unroll
-          for (int at = 0; at < NDH; ++at) mma(h[at], kop(at, kk), vb);
-        }
-      }
       }
       if (!mslice) {
         if (track) {
@@ -2085,14 +2050,18 @@ hipError_t launch_stage_combine(hipStream_t st, int B, int N, int H, const float
   const CombineLayout L = combine_layout(NC, BT, D);
   float* UT = reinterpret_cast<float*>(ws + L.UT);
   float* KgT = reinterpret_cast<float*>(ws + L.KgT);
+  float* Wsp = reinterpret_cast<float*>(ws + L.W);
   float* HT = reinterpret_cast<float*>(ws + L.HT);
   float* VnT = reinterpret_cast<float*>(ws + L.VnT);
   const int T_len = N * BT;
   transpose_all(st, u, UT, NC, BT, D);
   transpose_all(st, kg, KgT, NC, BT, D);
+  // the scan's float32 tiles in the split pair layout, as fwd_prep writes them
+  split_runs(st, KgT, KgT, NC * D * BT / 32);
+  split_runs(st, w_pseudo, Wsp, NC * BT * D / 32);
   constexpr int SW = 2, SP = 4, SK = state_ksplit<float, BT, D>();
   constexpr int NVS = D / (16 * SW);
-  StateArgs<float> sa{w_pseudo, UT, KgT, gc_last, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT,
+  StateArgs<float> sa{Wsp, UT, KgT, gc_last, h0, N, 1, N, 0, nullptr, nullptr, HT, VnT,
                       h_final, nullptr, H, qg, aqk, out, scale, T_len, nullptr};
   hipLaunchKernelGGL((fwd_state<float, BT, D, SW, SP, SK>), dim3((size_t)B * H * NVS),
                      dim3(64 * (SW * SK + SP)), 0, st, sa);

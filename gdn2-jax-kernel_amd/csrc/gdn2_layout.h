@@ -71,10 +71,11 @@ inline FwdLayout fwd_layout(size_t nchunks, int BT, int D, size_t elem, size_t s
   return L;
 }
 // Workspace of the stage entry point gdn2_chunk_combine (float32 tiles): u^T
-// and kg^T, the scan's [D][BT] copies of the caller's u and kg, and the h^T /
-// v_new^T tiles the scan writes for the output pass.
+// and kg^T, the scan's [D][BT] copies of the caller's u and kg, W in the scan's
+// split pair layout, and the h^T / v_new^T tiles the scan writes for the output
+// pass.
 struct CombineLayout {
-  size_t UT, KgT, HT, VnT, total;
+  size_t UT, KgT, W, HT, VnT, total;
 };
 inline CombineLayout combine_layout(size_t nchunks, int BT, int D) {
   CombineLayout L;
@@ -82,6 +83,7 @@ inline CombineLayout combine_layout(size_t nchunks, int BT, int D) {
   auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
   L.UT = take(nchunks * D * BT * 4);
   L.KgT = take(nchunks * D * BT * 4);
+  L.W = take(nchunks * BT * D * 4);
   L.HT = take(nchunks * (size_t)D * D * 4);
   L.VnT = take(nchunks * D * BT * 4);
   L.total = off;

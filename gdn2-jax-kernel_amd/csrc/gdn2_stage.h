@@ -32,4 +32,9 @@ void reverse_cumsum(hipStream_t st, const float* dgc, float* dg, size_t tiles, i
 // dst[i] = sanitize(src[i]) for n floats; src == nullptr writes zeros.
 void sanitized_copy(hipStream_t st, const float* src, float* dst, size_t n);
 
+// Rows of float32 tiles into the split pair layout of the float32 scans
+// (gdn2_common.h): `runs` runs of 32 floats, src == dst allowed (each run is
+// read whole before it is written).
+void split_runs(hipStream_t st, const float* src, float* dst, size_t runs);
+
 }  // namespace gdn2

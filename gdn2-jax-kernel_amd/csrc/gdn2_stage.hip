@@ -97,7 +97,25 @@ unsigned grid_for(size_t items) {
   return (unsigned)(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536);
 }
 
+// One run of 32 floats per thread into the split pair layout.
+__global__ void __launch_bounds__(256) split_run(const float* src, float* dst, size_t runs) {
+  for (size_t r = (size_t)blockIdx.x * 256 + threadIdx.x; r < runs;
+       r += (size_t)gridDim.x * 256) {
+    f32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = load4f(src + r * 32 + 4 * j);
+    char* row = reinterpret_cast<char*>(dst + r * 32);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) split_store4(row, 4 * j, v[j]);
+  }
+}
+
 }  // namespace
+
+void split_runs(hipStream_t st, const float* src, float* dst, size_t runs) {
+  if (runs > 0)
+    hipLaunchKernelGGL(split_run, dim3(grid_for(runs)), dim3(256), 0, st, src, dst, runs);
+}
 
 void transpose_all(hipStream_t st, const float* src, float* dst, size_t n, int R, int C) {
   if (n > 0)

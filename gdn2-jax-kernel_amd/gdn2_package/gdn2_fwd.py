@@ -285,16 +285,29 @@ def _residual_views(p: _Prepared, ws: torch.Tensor):
     # (gdn2_common.h kpos): undo it for the views
     chained = p.tile_dt == torch.bfloat16
     nat = lambda x, n: x[..., _kpos_index(n, x.device)] if chained else x
+    # float32 W and KgT are in the scans' split pair layout: decode them
+    spl = (lambda x: x) if chained else _split_decode
     return {
-        "w_pseudo": f(nat(views["W"].view(*shp, BT, D), D)),
+        "w_pseudo": f(spl(nat(views["W"].view(*shp, BT, D), D))),
         "u": f(nat(views["UT"].view(*shp, D, BT), BT).transpose(-1, -2)),
-        "kg": f(nat(views["KgT"].view(*shp, D, BT), BT).transpose(-1, -2)),
+        "kg": f(spl(nat(views["KgT"].view(*shp, D, BT), BT)).transpose(-1, -2)),
         "qg": f(views["Qg"].view(*shp, BT, D)),
         "Aqk": torch.where(causal, f(views["Aqk"].view(*shp, BT, BT)), 0.0),
         "gc_last": f(views["GL"].view(*shp, D)),
         "h_pre_all": f(nat(views["HT"].view(*shp, D, D), D).transpose(-1, -2)),
         "v_new_all": f(nat(views["VnT"].view(*shp, D, BT), BT).transpose(-1, -2)),
     }
+
+
+def _split_decode(x: torch.Tensor) -> torch.Tensor:
+    """Rows of a float32 tile stored in the split pair layout of the float32
+    scans (csrc/gdn2_common.h) as float32: each 128-byte run of 32 elements holds
+    the bfloat16 hi parts (bytes 0-63) and lo parts (64-127), chunk j of each
+    part the elements 4j..4j+3 and 16+4j..16+4j+3; the value is hi + lo."""
+    *lead, L = x.shape
+    parts = x.contiguous().view(torch.bfloat16).reshape(*lead, L // 32, 2, 4, 2, 4).float()
+    val = parts[..., 0, :, :, :] + parts[..., 1, :, :, :]          # (.., runs, j, half, slot)
+    return val.transpose(-3, -2).reshape(*lead, L)                  # element 16 half + 4 j + slot
 
 
 def _kpos_index(n: int, device) -> torch.Tensor:

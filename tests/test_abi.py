@@ -291,10 +291,11 @@ def test_stage_entry_points_reject_before_launch():
     wy = lambda d, a=0x3000: L.gdn2_recompute_wy(None, *d, *fake, a, *outs)
     assert wy((1, 512, 2, 64, 128, BF16, F32)) == _lib.ERR_CHUNK
     assert wy((1, 512, 2, 64, 64, F32, F32), a=None) == _lib.ERR_NULL
-    # combine: N chunks of 64; workspace = u^T, kg^T, h^T, v_new^T float32 tiles
+    # combine: N chunks of 64; workspace = u^T, kg^T, W (split pair layout), h^T,
+    # v_new^T float32 tiles
     nc, D = 2 * 2 * 8, 64
     need = L.gdn2_chunk_combine_workspace_bytes(2, 8, 2, D, 64)
-    assert need == 3 * nc * D * 64 * 4 + nc * D * D * 4
+    assert need == 4 * nc * D * 64 * 4 + nc * D * D * 4
     assert L.gdn2_chunk_combine_workspace_bytes(2, 8, 2, D, 128) == 0
     assert L.gdn2_chunk_combine_workspace_bytes(2, -1, 2, D, 64) == 0
     tiles = [0x100000 * (i + 1) for i in range(6)]
@@ -320,7 +321,7 @@ def test_backward_stage_entry_points_reject_before_launch():
     rows, sq = nc * 64 * D * 4, nc * D * D * 4
     ws = L.gdn2_bwd_stage_workspace_bytes
     assert ws(_lib.STAGE_DAV, B, N, H, D, 64) == 3 * rows
-    assert ws(_lib.STAGE_DHU, B, N, H, D, 64) == 4 * rows + 2 * sq
+    assert ws(_lib.STAGE_DHU, B, N, H, D, 64) == 5 * rows + 2 * sq   # + W, split pair layout
     assert ws(_lib.STAGE_WY, B, N, H, D, 64) == 18 * rows + 2 * sq + nc * D * 4
     assert ws(_lib.STAGE_INTRA, B, N, H, D, 64) == 4 * rows
     assert ws(9, B, N, H, D, 64) == 0 and ws(_lib.STAGE_DAV, B, N, H, D, 128) == 0
