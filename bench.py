@@ -364,10 +364,14 @@ def mfma_from(run_dir):
         short = next((k for k in ("fwd_prep", "fwd_state", "fwd_out", "bwd_b2", "bwd_state",
                                   "bwd_wy", "gram_bwd") if k in name), name)
         dt = "bf16" if ("DF16b" in name or "__bf16" in name or "bool" in name) else "fp32"
-        flops = 512 * (d.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0) + d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0))
+        f32 = 512 * d.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0)
+        b16 = 512 * d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0)
+        # float32 kernels: products in the split form run three bfloat16 MFMAs per
+        # float32 product, so their bfloat16 flops count a third as float32 work
+        flops = f32 + b16 / 3 if dt == "fp32" else f32 + b16
         peak = FP32_MFMA_PEAK if dt == "fp32" else 2516.6
         out[f"{short} ({dt})"] = {
-            "mfma_flops": flops, "ns": d["ns"],
+            "mfma_flops": flops, "f32_mfma_flops": f32, "bf16_mfma_flops": b16, "ns": d["ns"],
             "tflops": flops / d["ns"] / 1e3, "frac_of_peak": flops / d["ns"] / 1e3 / peak,
             "mfma_busy": d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0)
             / max(1.0, d.get("GRBM_GUI_ACTIVE", 0) / xcds * simds)}
