@@ -158,6 +158,44 @@ def test_chained_column_order(n):
         assert sorted(got[k] for k in ks) == list(range(8 * lg, 8 * lg + 8))
 
 
+@pytest.mark.parametrize("L", [64, 128, 256])
+def test_split_pair_layout_decode(L):
+    """The float32 scans' split pair layout (gdn2_common.h: per 32-element run of a
+    row, bytes 16j .. 16j+15 hold bf16 hi parts of elements 4j..4j+3 and
+    16+4j..16+4j+3, the lo parts 64 bytes further; lo = bf16(x - hi)).  Encoded
+    here element by element from that description (round to nearest even done on
+    the float32 bits) and decoded by the residual views' helper: the value is
+    hi + lo, within 2^-17 of x, and a planted swap of two slots is caught."""
+    import numpy as np
+    from gdn2_package.gdn2_fwd import _split_decode
+
+    def bf16_bits(x):
+        u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    def bf16_val(b):
+        return (b.astype(np.uint32) << 16).view(np.float32)
+
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((3, L)) * np.exp(rng.uniform(-8, 8, (3, L)))).astype(np.float32)
+    enc = np.zeros((3, L * 2), np.uint16)     # bf16 slots, L floats = 2 L halves
+    for r in range(3):
+        for e in range(L):
+            run, i = divmod(e, 32)
+            j, half, slot = (i % 16) // 4, i // 16, i % 4
+            pos = run * 64 + j * 8 + half * 4 + slot          # in bf16 units
+            hi = bf16_bits(x[r, e])
+            lo = bf16_bits(np.float32(x[r, e] - bf16_val(hi)))
+            enc[r, pos], enc[r, pos + 32] = hi, lo
+    got = _split_decode(torch.from_numpy(enc.view(np.float32).copy())).numpy()
+    assert np.all(np.abs(got - x) <= 2.0 ** -17 * np.abs(x))
+    assert np.abs(got - x).max() > 0            # hi + lo is not float32-exact
+    bad = enc.copy()
+    bad[:, [1, 5]] = bad[:, [5, 1]]             # element 1 and element 17 exchanged
+    wrong = _split_decode(torch.from_numpy(bad.view(np.float32).copy())).numpy()
+    assert not np.all(np.abs(wrong - x) <= 2.0 ** -17 * np.abs(x))
+
+
 def test_stage_diag_reports(monkeypatch, capsys):
     """GDN2_FWD_DIAG stage checks (gdn2_fwd.py:47-76): non-finite entries are
     counted with the largest finite magnitude; finite values above 1e6 are
