@@ -411,7 +411,7 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       // dvp gather and kg^T loads go out after B(i) (dvp(i) is in registers), its
       // kg is stored after X(i) (the first product has read kg(i)) and its W loads
       // issued; g_last after E(i) (the dh update has read e^{g_last}(i)); W and
-      // e^{g_last} are stored after A(i+1), before X(i+1) where the dh update
+      // e^{g_last} are stored after B(i+1), before X(i+1) where the dh update
       // starts reading them.  Register results are waited for by the compiler; the
       // LDS-DMA gathers before the barrier that publishes them.
       if (n > 0) {
@@ -426,10 +426,12 @@ __global__ void __launch_bounds__(64 * (NW * KS + NP)) bwd_state(BStateArgs<T> a
       for (int i = 0; i < n; ++i) {
         if (i == 0) wait_vmcnt<0>();   // chunk 0's gather, g_last and W
         barrier();  // A(i)
+        barrier();  // B(i)
+        // W(i) and e^{g_last}(i) are first read after X(i): stored behind the
+        // compute waves' kg dh (between A and B they would hold up B)
         if (i > 0) wait_step(i);       // g_last(i): only the touches may be outstanding
         tr_store_w(sbuf0);
         exp_gl(sGL0);
-        barrier();  // B(i)
         __builtin_amdgcn_sched_barrier(0);
         if (i + 1 < n) {
           gather_dv(i + 1);
