@@ -379,6 +379,70 @@ def mfma_from(run_dir):
     return out
 
 
+SQ_PASSES = (
+    ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY",
+     "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_VALU", "SQ_WAIT_INST_LDS"),
+    ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA", "SQ_INSTS_VMEM_RD",
+     "SQ_INSTS_VMEM_WR", "SQ_LDS_BANK_CONFLICT", "SQ_ACTIVE_INST_LDS"),
+)
+
+
+def sq_from(run_dirs):
+    """Where each kernel's waves spend their cycles, from --pmc-train-run counter
+    runs of the SQ_PASSES groups (one rocprofv3 run per group): the wave-cycle
+    counters SQ_WAIT_ANY (waiting on anything: a memory counter, a barrier, a
+    dependency), SQ_WAIT_INST_ANY (an issued instruction waiting for its
+    operands or a free unit), SQ_ACTIVE_INST_ANY / _VALU / _LDS (issuing) as
+    fractions of SQ_WAVE_CYCLES, and instructions per wave.  The last dispatch
+    of each kernel in the run is the one reported."""
+    import csv
+    per = {}
+    for run_dir in run_dirs:
+        files = sorted(Path(run_dir).rglob("*counter_collection.csv"))
+        if len(files) != 1:
+            raise SystemExit(f"expected one counter file under {run_dir}, found {len(files)}")
+        with open(files[0], newline="") as fh:
+            rows = [r for r in csv.DictReader(fh) if "gdn2" in r["Kernel_Name"]]
+
+        def key_of(name):
+            short = next((k for k in TRAIN_KERNELS if k in name), name)
+            return f"{short} ({'bf16' if ('DF16b' in name or '__bf16' in name) else 'fp32'})"
+        last = {}
+        for r in rows:
+            k = key_of(r["Kernel_Name"])
+            last[k] = max(last.get(k, -1), int(r["Dispatch_Id"]))
+        run = {}
+        for r in rows:
+            k = key_of(r["Kernel_Name"])
+            if int(r["Dispatch_Id"]) == last[k]:
+                d = run.setdefault(k, {})
+                d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        for k, d in run.items():
+            merged = per.setdefault(k, {})
+            for c, v in d.items():
+                merged.setdefault(c, v)
+    out = {}
+    for key, d in per.items():
+        wc = max(d.get("SQ_WAVE_CYCLES", 0.0), 1.0)
+        waves = max(d.get("SQ_WAVES", 0.0), 1.0)
+        out[key] = {
+            "wait_any": d.get("SQ_WAIT_ANY", 0.0) / wc,
+            "wait_inst_any": d.get("SQ_WAIT_INST_ANY", 0.0) / wc,
+            "active_any": d.get("SQ_ACTIVE_INST_ANY", 0.0) / wc,
+            "active_valu": d.get("SQ_ACTIVE_INST_VALU", 0.0) / wc,
+            "active_lds": d.get("SQ_ACTIVE_INST_LDS", 0.0) / wc,
+            "wait_inst_lds": d.get("SQ_WAIT_INST_LDS", 0.0) / wc,
+            "valu_per_wave": d.get("SQ_INSTS_VALU", 0.0) / waves,
+            "lds_per_wave": d.get("SQ_INSTS_LDS", 0.0) / waves,
+            "mfma_per_wave": d.get("SQ_INSTS_MFMA", 0.0) / waves,
+            "vmem_rd_per_wave": d.get("SQ_INSTS_VMEM_RD", 0.0) / waves,
+            "vmem_wr_per_wave": d.get("SQ_INSTS_VMEM_WR", 0.0) / waves,
+            "lds_bank_conflict_per_wave": d.get("SQ_LDS_BANK_CONFLICT", 0.0) / waves,
+            "waves": d.get("SQ_WAVES", 0.0)}
+    print(json.dumps(out, indent=1))
+    return out
+
+
 def _time(fn, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -688,7 +752,13 @@ def main():
                     help="reduce a --pmc-train-run MFMA counter run (per-kernel flops, utilisation)")
     ap.add_argument("--train-traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="reduce two --pmc-train-run counter runs to profiles/traffic_train_*")
+    ap.add_argument("--sq-from", nargs="+", metavar="DIR",
+                    help="reduce --pmc-train-run runs of the SQ_PASSES counter groups "
+                         "(wave-cycle shares, instructions per wave)")
     args = ap.parse_args()
+    if args.sq_from:
+        sq_from(args.sq_from)
+        return
     if args.mfma_from:
         mfma_from(args.mfma_from)
         return
