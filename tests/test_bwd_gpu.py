@@ -271,10 +271,11 @@ def test_bwd_d256_matches_oracle(dev, T, H, h0, dh, dtype):
 
 
 # ----------------------------------------------------------------------------- saturation
-@pytest.mark.parametrize("D,dos,dhs", [(64, 1e4, 0.0), (64, 3e3, 3e4), (128, 3e3, 3e4)])
+@pytest.mark.parametrize("D,dos,dhs", [(64, 1e4, 0.0), (64, 3e3, 3e4), (128, 3e3, 3e4),
+                                       (256, 3e3, 3e4)])
 def test_bwd_saturation_matches_reference_clipping(dev, D, dos, dhs):
     """Cotangents past the reference's clip (do x 1e4, or do x 3e3 with dh_final x
-    3e4; slow decay, unit v and scale): B2's dAqk / dv_partial, B1's dv_new and
+    3e4, D = 64, 128 and 256; slow decay, unit v and scale): B2's dAqk / dv_partial, B1's dv_new and
     dh carry (and its sanitized dh_final), B3's dA, dA A^T and outputs, B4's
     accumulators in the sub-block pair order and B5 all clip somewhere, and
     4-20 % of the gradients saturate.  The float32 trainable path matches the
@@ -293,8 +294,13 @@ def test_bwd_saturation_matches_reference_clipping(dev, D, dos, dhs):
     _, grads, _ = run_grads(xs, scale, do, dhn, h0=h0n, dev=dev)
     ref = O.chunked_bwd(*xs, scale, do, dhn, h0=h0n, BT=64, clip=True)
     whole = O.chunked_bwd(*xs, scale, do, dhn, h0=h0n, BT=64, clip=True, n_sub=None)
-    # B4's pair order matters here (in dq, dk or db)
-    assert max(np.abs(ref[i] - whole[i]).max() for i in (0, 1, 4)) > 100.0
+    # B4's pair order matters here (in dq, dk or db).  Not at D = 256, whose sums over
+    # twice the channels make it matter only from do x 1e5, where the float32 scans'
+    # split products (operands rounded to 2^-17) amplified 1e5-fold put dq past this
+    # bound (1.6-1.75, at D = 128 as at 256): this case pins bwd_wy_wide's and the
+    # D = 256 scans' clip points and the raw dh_final, the pair order is pinned above
+    pair = max(np.abs(ref[i] - whole[i]).max() for i in (0, 1, 4))
+    assert pair > 100.0 if D <= 128 else pair < 1e-6
     if dhs:
         san = O.chunked_bwd(*xs, scale, do, O.sanitize(dhn), h0=h0n, BT=64, clip=True)
         assert np.abs(ref[1] - san[1]).max() > 100.0        # and so does the raw dh_final
