@@ -309,3 +309,25 @@ def test_bwd_saturation_matches_reference_clipping(dev, D, dos, dhs):
         assert np.isfinite(g).all() and np.abs(g).max() <= 1e4, n
         ok, e = close(g * 1e-4, r * 1e-4, 1e-4)
         assert ok, (n, e * 1e4)
+
+
+# ----------------------------------------------------------------------------- empty
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.float32, 128),
+                                     (torch.bfloat16, 128), (torch.float32, 256)])
+def test_empty_sequence_training(dev, dtype, D):
+    """T = 0 through the trainable path: h_final = h0, every input gradient is
+    empty, and dh0 is the cotangent on h_final (the state passes through no chunk;
+    B1 starts its carry from the sanitized dh_final, which a value inside the clip
+    leaves unchanged)."""
+    B, H = 2, 2
+    xs = [torch.zeros((B, 0, H, D), device=dev, dtype=dtype if i < 5 else torch.float32)
+          .requires_grad_(True) for i in range(6)]
+    h0 = torch.randn((B, H, D, D), device=dev, requires_grad=True)
+    out, hf = gp().gdn2_pallas_forward_trainable(*xs, D ** -0.5, h0=h0)
+    assert out.shape == (B, 0, H, D) and torch.equal(hf.detach(), h0.detach())
+    dhf = torch.randn_like(hf)
+    grads = torch.autograd.grad((hf * dhf).sum() + out.sum(), xs + [h0])
+    torch.cuda.synchronize()
+    for x, g in zip(xs, grads[:6]):
+        assert g.shape == x.shape and g.dtype == x.dtype
+    assert torch.equal(grads[6], dhf)

@@ -235,16 +235,6 @@ def test_strong_decay_diagonal_blocks(dev, dtype, BT, D):
     assert close(o2.cpu().numpy(), ro, TOL[dtype])[0] and close(h2.cpu().numpy(), rh, TOL[dtype])[0]
 
 
-def test_empty_sequence(dev):
-    xs = [torch.zeros((2, 0, 3, 64), device=dev) for _ in range(6)]
-    h0 = torch.randn((2, 3, 64, 64), device=dev)
-    out, hf = gp().gdn2_pallas_forward(*xs, 0.1, h0=h0)
-    assert out.shape == (2, 0, 3, 64)
-    assert torch.equal(hf, h0)
-    out, hf = gp().gdn2_pallas_forward(*xs, 0.1)
-    assert torch.count_nonzero(hf).item() == 0
-
-
 def test_reference_all_ones_inputs_stay_finite(dev):
     """tests/test_pallas.py:28-41 feeds all-ones (2,512,4,128) with g=+1 (growing
     state); the reference's sanitize chain keeps outputs finite and within
@@ -529,3 +519,24 @@ def test_sanitize_map_on_the_initial_state(dev):
     got = hf.view(-1)[:len(vals)].cpu().tolist()
     assert got == [0.0, 1e4, -1e4, 1e4, -1e4, 9999.5, -5.0, 0.0], got
     assert torch.count_nonzero(hf.view(-1)[len(vals):]).item() == 0
+
+
+# ----------------------------------------------------------------------------- empty
+@pytest.mark.parametrize("dtype,BT,D", [(torch.float32, 64, 64), (torch.bfloat16, 128, 128),
+                                        (torch.bfloat16, 64, 128), (torch.float32, 64, 256)])
+def test_empty_sequence_forward(dev, dtype, BT, D):
+    """T = 0 (the reference's T % BT == 0 holds and its scan runs over no chunks):
+    out is (B, 0, H, D) and h_final is the entry state -- h0 as given (inside the
+    clip, so the stage sanitize leaves it unchanged), else zero -- on every path
+    (float32 with the scan writing its tiles, bfloat16 with the outputs formed in
+    the scan, D = 256)."""
+    B, H = 2, 3
+    xs = [torch.zeros((B, 0, H, D), device=dev, dtype=dtype) for _ in range(5)]
+    xs.append(torch.zeros((B, 0, H, D), device=dev))
+    h0 = torch.randn((B, H, D, D), device=dev)
+    out, hf = gp().gdn2_pallas_forward(*xs, D ** -0.5, h0=h0, chunk_size=BT)
+    torch.cuda.synchronize()
+    assert out.shape == (B, 0, H, D) and out.dtype == torch.float32
+    assert hf.shape == (B, H, D, D) and torch.equal(hf, h0)
+    out, hf = gp().gdn2_pallas_forward(*xs, D ** -0.5, chunk_size=BT)
+    assert out.shape == (B, 0, H, D) and torch.count_nonzero(hf).item() == 0
