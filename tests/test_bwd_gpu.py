@@ -331,3 +331,25 @@ def test_empty_sequence_training(dev, dtype, D):
     for x, g in zip(xs, grads[:6]):
         assert g.shape == x.shape and g.dtype == x.dtype
     assert torch.equal(grads[6], dhf)
+
+
+@pytest.mark.parametrize("D", [128, 256])
+def test_bwd_split_products_headroom_under_saturation(dev, D):
+    """The float32 scans' split products (operands as bfloat16 hi + lo, 2^-17)
+    under a cotangent ten times past the test above (do x 3e4; 32 % of dq at the
+    clip at D = 256): the forward state's rounding, amplified 3e4-fold into dq, must still
+    sit inside the saturation-scale bound |got - ref| <= 1 + 1e-4 |ref| (measured
+    about half of it; from do x 1e5 it does not, see the clip-point test)."""
+    B, T, H, scale = 1, 256, 2, 1.0
+    xs = O.make_inputs(B, T, H, D, seed=40, g_scale=0.05)
+    rng = np.random.default_rng(3)
+    do = (rng.standard_normal((B, T, H, D)) * 3e4).astype(np.float32)
+    dhn = (rng.standard_normal((B, H, D, D)) * 0.0).astype(np.float32)   # zero dh_final
+    h0n = rng.standard_normal((B, H, D, D)).astype(np.float32)
+    _, grads, _ = run_grads(xs, scale, do, dhn, h0=h0n, dev=dev)
+    ref = O.chunked_bwd(*xs, scale, do, dhn, h0=h0n, BT=64, clip=True)
+    assert 0.01 < np.mean(np.abs(ref[0]) == 1e4) < 0.5
+    for n, g, r in zip(NAMES, grads, ref):
+        assert np.isfinite(g).all() and np.abs(g).max() <= 1e4, n
+        ok, e = close(g * 1e-4, r * 1e-4, 1e-4)
+        assert ok, (n, e * 1e4)
